@@ -1,0 +1,167 @@
+"""Benchmark of the MGN MLP hot path on one MI355X.
+
+A step is one call of the fused edge MLP (384->128->128->128 + LayerNorm,
+fp16 I/O, fp32 accumulate) over the full BASELINE batch M = 1,048,576 with
+all inputs already resident in HBM.  Prints ONE JSON line (see README of the
+driver contract): rows/s, the HBM-roofline fraction of the kernel measured
+with HIP events on the launch stream, and the CPU oracle timed on a bounded
+sample on the host cores.
+
+  python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--workload edge|node]
+                  [--impl fused|pipelined] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "gpu-pipes_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "rows/sec + % fp16 MFMA peak, MGN edge MLP M=1M (1×MI355X)"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
+
+WORKLOADS = {
+    # name: (M, K, layernorm)
+    "edge": (1048576, 384, True),
+    "node": (262144, 256, True),
+}
+
+
+def algorithmic(M, K, ln):
+    """Bytes that must cross HBM per call and MFMA FLOPs per call."""
+    params = (K * 128 + 2 * 128 * 128) * 2 + 3 * 128 * 2 + (2 * 128 * 2 if ln else 0)
+    bytes_ = M * (K + 128) * 2 + params
+    flops = 2 * M * (K * 128 + 128 * 128 + 128 * 128)
+    return bytes_, flops
+
+
+def cpu_baseline(K, ln, budget_s=10.0):
+    """The CPU oracle (oracle/oracle.c, OpenMP over rows) on the config-0 shape."""
+    import numpy as np
+
+    import oracle
+    from gpipes.synth import mgn_params, normal_fp16
+
+    threads = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "16") or 16), 16)
+    oracle.set_num_threads(threads)
+    Ms = 16384
+    p = mgn_params(K, seed=0, layernorm=ln)
+    f = lambda t: None if t is None else t.float().numpy()  # noqa: E731
+    x = f(normal_fp16(Ms, K, seed=0))
+    args = [f(p[k]) for k in ("w1", "b1", "w2", "b2", "w3", "b3", "gamma", "beta")]
+    oracle.mgn_mlp(x, *args)  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        oracle.mgn_mlp(x, *args)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {
+        "value": Ms / med, "unit": "rows/s", "cores": threads, "kind": "port",
+        "sample": f"oracle/oracle.c MgnMlp fp32 on X[{Ms},{K}] (config-0 shape), "
+                  f"{len(times)} calls in {sum(times):.1f} s, median {med * 1e3:.2f} ms/call",
+    }
+
+
+def load_traffic(workload, impl):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as fh:
+            return json.load(fh).get(f"{workload}:{impl}")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="edge")
+    ap.add_argument("--impl", choices=["fused", "pipelined"], default="fused")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the path needs no cross-GPU exchange; rows shard "
+              f"trivially); --gpus {args.gpus} is not supported.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import gpipes
+    from gpipes.synth import mgn_params, normal_fp16
+
+    dev = torch.device("cuda:0")
+    M, K, ln = WORKLOADS[args.workload]
+    p = {k: (None if v is None else v.to(dev)) for k, v in mgn_params(K, seed=0, layernorm=ln).items()}
+    # Inputs resident in HBM.  The node batch (201 MB) would fit the 256 MB
+    # MALL, so two input/output buffer pairs are rotated to keep it honest.
+    nbuf = 2 if args.workload == "node" else 1
+    xs = [normal_fp16(M, K, seed=i, device=dev) for i in range(nbuf)]
+    outs = [torch.empty((M, 128), dtype=torch.float16, device=dev) for _ in range(nbuf)]
+
+    def step(i):
+        b = i % nbuf
+        gpipes.mgn_mlp_out(xs[b], p["w1"], p["b1"], p["w2"], p["b2"], p["w3"], p["b3"], p["gamma"],
+                           p["beta"], outs[b], impl=args.impl)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream(dev)  # the stream the kernels are launched on
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        step(i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    launch_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    avg_launch_ms = sum(launch_ms) / len(launch_ms)
+    ms_per_step = wall * 1e3 / args.steps
+    bytes_, flops = algorithmic(M, K, ln)
+    achieved_gbs = bytes_ / (avg_launch_ms * 1e-3) / 1e9
+    tflops = flops / (avg_launch_ms * 1e-3) / 1e12
+
+    rec = {
+        "metric": METRIC,
+        "value": M / (ms_per_step * 1e-3),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (X~N(0,1), nn.Linear default init, seed 0)",
+        "config": {"workload": f"mgn_{args.workload}_mlp", "M": M, "K": K,
+                   "layers": f"{K}-128-128-128" + ("+LN" if ln else ""), "impl": args.impl,
+                   "accumulate": "f32"},
+        "roofline": {
+            "bound": "hbm", "achieved": achieved_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": load_traffic(args.workload, args.impl),
+            "kernel_ms_avg": avg_launch_ms, "kernel_ms_median": launch_ms[len(launch_ms) // 2],
+            "algorithmic_bytes_per_launch": bytes_,
+        },
+        "mfma": {"achieved_tflops": tflops, "peak_tflops": MFMA_F16_PEAK_TFLOPS,
+                 "frac": tflops / MFMA_F16_PEAK_TFLOPS, "flops_per_launch": flops},
+        "cpu_baseline": None if args.no_cpu else cpu_baseline(K, ln),
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,89 @@
+// Device-side building blocks shared by every gpu-pipes kernel on gfx950.
+//
+// Everything here is written for CDNA4 wave64: MFMA operand fragments, the
+// s_waitcnt immediates used to overlap LDS-DMA prefetch with compute, and a
+// workgroup barrier that does not wait on in-flight global->LDS copies.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gp {
+
+typedef _Float16 half_t;
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f16x __attribute__((ext_vector_type(16)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+
+#define GP_LDS __attribute__((address_space(3)))
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] |
+// lgkmcnt[11:8] | vmcnt_hi[15:14]).  A field at its maximum means "do not
+// wait on this counter".
+// ---------------------------------------------------------------------------
+constexpr int waitcnt_imm(int vm, int exp, int lgkm) {
+  return (vm & 15) | ((exp & 7) << 4) | ((lgkm & 15) << 8) | (((vm >> 4) & 3) << 14);
+}
+constexpr int kWaitLgkm0 = waitcnt_imm(63, 7, 0);
+constexpr int kWaitAll = waitcnt_imm(0, 0, 0);
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt field is 6 bits");
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(N, 7, 15));
+}
+
+// Compiler-level fence: keeps the compiler from moving memory operations
+// across this point without emitting any hardware wait.
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
+// Workgroup barrier for LDS traffic only.  A HIP __syncthreads() carries a
+// workgroup release fence, and on gfx950 a release fence must also drain
+// every outstanding global->LDS DMA (vmcnt(0)), which would serialise the
+// X-tile prefetch with compute.  This barrier only makes this wave's own
+// ds_write results visible (lgkmcnt(0)) before s_barrier; callers wait for
+// their DMA explicitly with wait_vmcnt<N>() where needed.
+__device__ __forceinline__ void lds_barrier() {
+  compiler_fence();
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  __builtin_amdgcn_s_barrier();
+  compiler_fence();
+}
+
+// 16-byte global->LDS copy.  Lane i of the wave writes LDS bytes
+// [lds_base + 16 i, lds_base + 16 i + 16); lds_base must be wave-uniform.
+// The source address is per lane, so the LDS layout is chosen by picking
+// which global chunk each lane fetches.
+__device__ __forceinline__ void dma16(const void* gsrc, GP_LDS void* lds_base) {
+  __builtin_amdgcn_global_load_lds(gsrc, lds_base, 16, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// MFMA 32x32x16 f16 -> f32.  Operand layout (wave64):
+//   A[i][k]: lane = i + 32*(k/8), element k%8          (32 rows x 16 k)
+//   B[k][j]: lane = j + 32*(k/8), element k%8          (16 k x 32 cols)
+//   C[i][j]: lane = j + 32*((i/4)%2), element (i%4) + 4*(i/8)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f16x mfma32(h8 a, h8 b, f16x c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Row (M index) of accumulator element v held by a lane in half `lh` (= lane/32).
+__device__ __forceinline__ constexpr int c_row(int v, int lh) {
+  return 8 * (v / 4) + 4 * lh + (v % 4);
+}
+
+__device__ __forceinline__ float relu(float v) { return v > 0.f ? v : 0.f; }
+
+template <typename T>
+__device__ __forceinline__ T xor_lane32(T v) {
+  // exchange with the lane 32 positions away (the other half of the wave)
+  return __shfl_xor(v, 32, 64);
+}
+
+}  // namespace gp

@@ -1,0 +1,156 @@
+"""gpipes -- Python mirror of gpu-pipes' operator surface on MI355X (gfx950).
+
+The reference exposes its pipelined MLPs as a PyTorch extension
+(``cuda_ext.mgn_fullmlp(x, w1, b1, w2, b2, w3, b3, gamma, beta)`` and the
+``*_out`` forms, apps/mgn_fullmlp/pipelined/mgn_fullmlp_pl_ext.cu:24-93,
+apps/mgn_linears/pipelined/mgn_linears_pl_ext.cu:24-86).  This module keeps
+those names, argument order and layouts (weights [K, N] =
+``nn.Linear.weight.t().contiguous()``), and calls the HIP kernels through the
+C ABI of ``libgpipes.so`` (include/gpipes.h) on torch's current stream.
+
+Error behaviour: the reference raises RuntimeError for non-CUDA or
+non-contiguous tensors (TORCH_CHECK) and asserts on shapes; here every
+violation raises RuntimeError, and nothing aborts the process.
+
+There is no CPU fallback: if the library is missing, importing this module
+raises.
+"""
+import ctypes
+import os
+
+import torch
+
+__all__ = [
+    "lib", "mgn_fullmlp", "mgn_fullmlp_out", "mgn_linears", "mgn_linears_out",
+    "mgn_mlp", "mgn_mlp_out", "IMPL_FUSED", "IMPL_PIPELINED", "GpipesError",
+]
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libgpipes.so")
+
+GP_OK = 0
+IMPL_FUSED = 0
+IMPL_PIPELINED = 1
+_IMPLS = {"fused": IMPL_FUSED, "pipelined": IMPL_PIPELINED}
+
+
+class GpipesError(RuntimeError):
+    """A C ABI call returned a negative status."""
+
+    def __init__(self, code, msg):
+        super().__init__(f"gpipes error {code}: {msg}")
+        self.code = code
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is not built; run `python gpu-pipes_amd/build.py` "
+            "(or __graft_entry__.build()) first")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, i64, f32, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_int
+    L.gp_version.restype = i32
+    L.gp_last_error.restype = ctypes.c_char_p
+    L.gp_mgn_fullmlp_out.argtypes = [i64] + [vp] * 11
+    L.gp_mgn_fullmlp_out.restype = i32
+    L.gp_mgn_linears_out.argtypes = [i64] + [vp] * 9
+    L.gp_mgn_linears_out.restype = i32
+    L.gp_mgn_mlp_out.argtypes = [i64, i64] + [vp] * 9 + [f32, vp, i32, vp]
+    L.gp_mgn_mlp_out.restype = i32
+    return L
+
+
+lib = _load()
+
+
+def _check(rc):
+    if rc != GP_OK:
+        raise GpipesError(rc, lib.gp_last_error().decode())
+
+
+def _stream_ptr(t):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _check_input(name, t, shape=None):
+    # CHECK_CUDA / CHECK_CONTIGUOUS of mgn_fullmlp_pl_ext.cu:14-16, plus dtype/shape
+    if not isinstance(t, torch.Tensor):
+        raise RuntimeError(f"{name} must be a torch.Tensor")
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a CUDA tensor")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+    if t.dtype != torch.float16:
+        raise RuntimeError(f"{name} must be float16 (got {t.dtype})")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise RuntimeError(f"{name} must have shape {tuple(shape)} (got {tuple(t.shape)})")
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def mgn_mlp_out(x, w1, b1, w2, b2, w3, b3, gamma, beta, out, eps=1e-5, impl="fused"):
+    """MgnMlp(K, [128,128,128], layernorm=gamma is not None) into ``out``.
+
+    K = x.shape[1] in {128, 256, 384}; gamma/beta None -> no LayerNorm.
+    """
+    if x.dim() != 2:
+        raise RuntimeError("x must be 2-D [M, K]")
+    M, K = x.shape
+    _check_input("x", x)
+    _check_input("w1", w1, (K, 128))
+    _check_input("b1", b1, (128,))
+    _check_input("w2", w2, (128, 128))
+    _check_input("b2", b2, (128,))
+    _check_input("w3", w3, (128, 128))
+    _check_input("b3", b3, (128,))
+    if (gamma is None) != (beta is None):
+        raise RuntimeError("gamma and beta must both be given or both be None")
+    if gamma is not None:
+        _check_input("gamma", gamma, (128,))
+        _check_input("beta", beta, (128,))
+    _check_input("out", out, (M, 128))
+    devs = {t.device for t in (x, w1, b1, w2, b2, w3, b3, out) if t is not None}
+    if len(devs) != 1:
+        raise RuntimeError("all tensors must be on the same device")
+    impl_id = _IMPLS.get(impl, impl)
+    with torch.cuda.device(x.device):
+        rc = lib.gp_mgn_mlp_out(M, K, _ptr(x), _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2), _ptr(w3),
+                                _ptr(b3), _ptr(gamma), _ptr(beta), float(eps), _ptr(out), int(impl_id),
+                                ctypes.c_void_p(_stream_ptr(x)))
+    _check(rc)
+    return out
+
+
+def mgn_mlp(x, w1, b1, w2, b2, w3, b3, gamma=None, beta=None, eps=1e-5, impl="fused"):
+    out = torch.zeros((x.shape[0], 128), dtype=x.dtype, device=x.device)
+    return mgn_mlp_out(x, w1, b1, w2, b2, w3, b3, gamma, beta, out, eps=eps, impl=impl)
+
+
+def mgn_fullmlp_out(x, w1, b1, w2, b2, w3, b3, gamma, beta, out):
+    """Edge MLP 384->128->128->128 + LayerNorm(eps=1e-5) into ``out``
+    (mgn_fullmlp_pl_ext.cu:24-71)."""
+    _check_input("x", x)
+    if x.dim() != 2 or x.shape[1] != 384:
+        raise RuntimeError("x must be [M, 384]")
+    return mgn_mlp_out(x, w1, b1, w2, b2, w3, b3, gamma, beta, out, eps=1e-5)
+
+
+def mgn_fullmlp(x, w1, b1, w2, b2, w3, b3, gamma, beta):
+    """Allocating form: returns a new [M, 128] tensor (mgn_fullmlp_pl_ext.cu:74-88)."""
+    out = torch.zeros((x.shape[0], 128), dtype=x.dtype, device=x.device)
+    return mgn_fullmlp_out(x, w1, b1, w2, b2, w3, b3, gamma, beta, out)
+
+
+def mgn_linears_out(x, w1, b1, w2, b2, w3, b3, out):
+    """384->128->128->128 without LayerNorm (mgn_linears_pl_ext.cu:24-66)."""
+    _check_input("x", x)
+    if x.dim() != 2 or x.shape[1] != 384:
+        raise RuntimeError("x must be [M, 384]")
+    return mgn_mlp_out(x, w1, b1, w2, b2, w3, b3, None, None, out)
+
+
+def mgn_linears(x, w1, b1, w2, b2, w3, b3):
+    out = torch.zeros((x.shape[0], 128), dtype=x.dtype, device=x.device)
+    return mgn_linears_out(x, w1, b1, w2, b2, w3, b3, out)

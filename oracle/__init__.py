@@ -1,0 +1,135 @@
+"""CPU oracle for the gpu-pipes fused-MLP path -- TEST INFRASTRUCTURE ONLY.
+
+Thin numpy wrappers over liboracle.so (oracle/oracle.c), the plain-C fp32
+restatement of the reference's MLP chain.  Only tests/, __graft_entry__.smoke()
+and bench.py's cpu_baseline leg may import this package; the product library
+(gpu-pipes_amd/) never does.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SIGMOID = 0, 1, 2, 3
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} missing; run python gpu-pipes_amd/build.py")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i64, f32, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_int
+        L.oracle_h2f.argtypes = [ctypes.c_uint16]
+        L.oracle_h2f.restype = f32
+        L.oracle_f2h.argtypes = [f32]
+        L.oracle_f2h.restype = ctypes.c_uint16
+        L.oracle_h2f_array.argtypes = [i64, vp, vp]
+        L.oracle_f2h_array.argtypes = [i64, vp, vp]
+        L.oracle_linear.argtypes = [i64, i64, i64, vp, vp, vp, i32, vp]
+        L.oracle_layer_norm.argtypes = [i64, i64, vp, vp, vp, f32, vp]
+        L.oracle_mgn_mlp.argtypes = [i64, i64] + [vp] * 9 + [f32, vp, vp]
+        L.oracle_add.argtypes = [i64, vp, vp, vp]
+        L.oracle_concat.argtypes = [i64, i64, i64, vp, vp, vp]
+        L.oracle_num_threads.restype = i32
+        L.oracle_set_num_threads.argtypes = [i32]
+        _lib = L
+    return _lib
+
+
+def _f32(a):
+    if a is None:
+        return None
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def h2f(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().oracle_h2f_array(h.size, _p(h), _p(out))
+    return out
+
+
+def f2h(f):
+    f = _f32(f)
+    out = np.empty(f.shape, np.uint16)
+    lib().oracle_f2h_array(f.size, _p(f), _p(out))
+    return out
+
+
+def linear(x, w, b, act=ACT_NONE):
+    x, w, b = _f32(x), _f32(w), _f32(b)
+    M, K = x.shape
+    N = w.shape[1]
+    y = np.empty((M, N), np.float32)
+    lib().oracle_linear(M, K, N, _p(x), _p(w), _p(b), act, _p(y))
+    return y
+
+
+def layer_norm(x, gamma=None, beta=None, eps=1e-5):
+    x = _f32(x)
+    M, D = x.shape
+    y = np.empty_like(x)
+    lib().oracle_layer_norm(M, D, _p(x), _p(_f32(gamma)), _p(_f32(beta)), eps, _p(y))
+    return y
+
+
+def mgn_mlp(x, w1, b1, w2, b2, w3, b3, gamma=None, beta=None, eps=1e-5):
+    """MgnMlp forward (common/mlps.py:3-20) in fp32; inputs any float dtype."""
+    x = _f32(x)
+    M, K = x.shape
+    ws = [_f32(a) for a in (w1, b1, w2, b2, w3, b3)]
+    g, bt = _f32(gamma), _f32(beta)
+    out = np.empty((M, 128), np.float32)
+    work = np.empty((2 * M * 128,), np.float32)
+    lib().oracle_mgn_mlp(M, K, _p(x), *[_p(a) for a in ws], _p(g), _p(bt), eps, _p(out), _p(work))
+    return out
+
+
+def add(a, b):
+    a, b = _f32(a), _f32(b)
+    c = np.empty_like(a)
+    lib().oracle_add(a.size, _p(a), _p(b), _p(c))
+    return c
+
+
+def concat(a, b):
+    a, b = _f32(a), _f32(b)
+    M, N0 = a.shape
+    N1 = b.shape[1]
+    c = np.empty((M, N0 + N1), np.float32)
+    lib().oracle_concat(M, N0, N1, _p(a), _p(b), _p(c))
+    return c
+
+
+def num_threads():
+    return lib().oracle_num_threads()
+
+
+def set_num_threads(n):
+    lib().oracle_set_num_threads(int(n))
+
+
+def errors(actual, expected):
+    """(max-abs error, relative-L2 error) of actual vs expected (float64 math)."""
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(expected, dtype=np.float64)
+    d = a - e
+    max_abs = float(np.max(np.abs(d))) if d.size else 0.0
+    den = float(np.linalg.norm(e))
+    rel = float(np.linalg.norm(d) / den) if den > 0 else float(np.linalg.norm(d))
+    return max_abs, rel
+
+
+# Parity bar for fp16 I/O against the fp32 oracle (workload definition).
+MAX_ABS_TOL = 2e-2
+REL_L2_TOL = 5e-3

@@ -1,0 +1,116 @@
+"""Generate the golden fixtures under tests/golden/ (run from the repo root).
+
+The reference ships no fixture files and its validation scripts assert nothing
+(apps/*/pipelined/val.py only print errors), so the vectors are produced
+here from first principles:
+
+* inputs: X ~ N(0,1) and torch.nn default-initialised MgnMlp parameters
+  (nn.Linear / nn.LayerNorm built in the order of common/mlps.py:3-20),
+  everything rounded to fp16 exactly as the kernels receive it;
+* expected outputs: the torch.nn library modules (Linear, ReLU, LayerNorm)
+  evaluated in float64 on the fp16-rounded values -- an implementation
+  independent of both the C oracle and the HIP kernels.
+
+The LayerNorm fixture uses the literal 128-value input row that the
+reference's own LayerNorm check types in (misc_tests/layer_norm/torch_val.py:88-105,
+repeated over 128 rows there, gamma = 1, beta = 0); its expected output is
+F.layer_norm in float64.
+
+Usage: python tests/golden/gen_fixtures.py
+"""
+import hashlib
+import json
+import os
+import sys
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, os.path.join(ROOT, "gpu-pipes_amd"))
+from gpipes.synth import mgn_params, normal_fp16  # noqa: E402
+
+M_FIX = 256
+
+# misc_tests/layer_norm/torch_val.py:88-105 (fp16 in the reference)
+LN_ROW = [
+    0.0584, -0.0362, -0.0660, 0.0422, 0.0275, -0.0063, 0.0683, 0.0086,
+    0.0682, 0.0531, -0.0416, -0.0233, 0.1115, 0.0872, 0.0444, -0.1655,
+    -0.0645, -0.0249, -0.1387, 0.0323, 0.0275, 0.0374, -0.0202, -0.1707,
+    -0.0095, 0.0696, -0.0305, -0.0340, -0.1326, -0.0438, 0.1910, 0.0103,
+    -0.0041, -0.0133, 0.0273, -0.0519, -0.0641, -0.0294, 0.1016, -0.0116,
+    0.2269, -0.0229, -0.0088, -0.0543, 0.1884, 0.2455, -0.0098, 0.0155,
+    0.0209, 0.0940, -0.0056, 0.2769, 0.0936, 0.0133, -0.1065, 0.1091,
+    0.0047, 0.0628, 0.0091, -0.0368, 0.0240, 0.0104, -0.0033, 0.1326,
+    -0.1333, 0.2052, 0.0168, 0.1188, -0.2090, -0.1128, -0.1947, -0.1901,
+    0.0079, -0.0408, 0.0222, 0.0292, 0.0156, 0.0968, 0.0820, -0.0456,
+    -0.1573, 0.0282, -0.0734, 0.0977, -0.0263, -0.2069, 0.0491, 0.1038,
+    -0.0596, -0.1426, 0.0345, -0.1094, 0.0271, -0.1213, 0.1202, -0.0337,
+    -0.0151, -0.0343, -0.0700, -0.2043, -0.0188, 0.0386, 0.0837, 0.0340,
+    -0.0264, 0.0816, -0.0600, -0.0872, -0.0091, 0.0435, -0.0995, 0.0306,
+    0.1932, 0.0959, 0.0385, -0.0917, 0.0891, 0.1542, 0.0395, 0.1276,
+    0.0145, -0.0723, 0.0550, 0.0746, -0.0141, 0.0147, 0.2205, -0.0380,
+]
+
+
+def torch_mgn_f64(x16, p, eps):
+    """MgnMlp forward with torch.nn library modules in float64."""
+    K = x16.shape[1]
+    seq = [torch.nn.Linear(K, 128), torch.nn.ReLU(), torch.nn.Linear(128, 128), torch.nn.ReLU(),
+           torch.nn.Linear(128, 128)]
+    if p["gamma"] is not None:
+        seq.append(torch.nn.LayerNorm(128, eps=eps))
+    net = torch.nn.Sequential(*seq).double()
+    with torch.no_grad():
+        for idx, (w, b) in zip((0, 2, 4), (("w1", "b1"), ("w2", "b2"), ("w3", "b3"))):
+            net[idx].weight.copy_(p[w].double().t())
+            net[idx].bias.copy_(p[b].double())
+        if p["gamma"] is not None:
+            net[5].weight.copy_(p["gamma"].double())
+            net[5].bias.copy_(p["beta"].double())
+        return net(x16.double())
+
+
+def make_mgn_fixture(name, K, layernorm, seed, affine_random, eps=1e-5):
+    p = mgn_params(K, seed=seed, layernorm=layernorm, affine_random=affine_random)
+    x = normal_fp16(M_FIX, K, seed=seed + 1000)
+    y = torch_mgn_f64(x, p, eps)
+    arrs = {"x": x.numpy(), "expected": y.numpy().astype(np.float64), "eps": np.float64(eps)}
+    for k, v in p.items():
+        if v is not None:
+            arrs[k] = v.numpy()
+    path = os.path.join(HERE, f"{name}.npz")
+    np.savez_compressed(path, **arrs)
+    return path
+
+
+def make_ln_fixture():
+    row = torch.tensor(LN_ROW, dtype=torch.float16)
+    x = row.repeat(128, 1)
+    y = torch.nn.functional.layer_norm(x.double(), [128], weight=torch.ones(128, dtype=torch.float64),
+                                       bias=torch.zeros(128, dtype=torch.float64), eps=1e-5)
+    path = os.path.join(HERE, "layer_norm_row.npz")
+    np.savez_compressed(path, x=x.numpy(), expected=y.numpy(), eps=np.float64(1e-5))
+    return path
+
+
+def main():
+    paths = [
+        make_mgn_fixture("mgn_edge_ln", 384, True, seed=0, affine_random=False),
+        make_mgn_fixture("mgn_edge_ln_affine", 384, True, seed=1, affine_random=True),
+        make_mgn_fixture("mgn_edge_linears", 384, False, seed=2, affine_random=False),
+        make_mgn_fixture("mgn_node_ln", 256, True, seed=3, affine_random=True),
+        make_ln_fixture(),
+    ]
+    manifest = {}
+    for pth in paths:
+        with open(pth, "rb") as f:
+            manifest[os.path.basename(pth)] = hashlib.sha256(f.read()).hexdigest()
+    with open(os.path.join(HERE, "MANIFEST.json"), "w") as f:
+        json.dump(manifest, f, indent=1, sort_keys=True)
+    print(json.dumps(manifest, indent=1))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,80 @@
+"""C ABI checks that need no GPU: the library loads, exports every symbol that
+include/gpipes.h declares, and rejects bad arguments before touching a device."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT
+
+import gpipes
+
+HEADERS = [os.path.join(ROOT, "include", "gpipes.h")]
+
+
+def declared_symbols():
+    syms = set()
+    for h in HEADERS:
+        txt = open(h).read()
+        txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+        syms |= set(re.findall(r"\b(gp_[a-z0-9_]+)\s*\(", txt))
+    return sorted(syms)
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    for s in ("gp_mgn_fullmlp_out", "gp_mgn_linears_out", "gp_mgn_mlp_out", "gp_last_error", "gp_version"):
+        assert s in syms
+
+
+@pytest.mark.parametrize("sym", declared_symbols())
+def test_library_exports(sym):
+    assert hasattr(gpipes.lib, sym), f"{sym} declared in include/ but not exported"
+
+
+def test_version():
+    assert gpipes.lib.gp_version() >= 0x000100
+
+
+def _call(M=16, K=384, x=16, w=16, b=16, g=16, bt=16, eps=1e-5, out=16, impl=0):
+    """Call gp_mgn_mlp_out with fake (never dereferenced) pointers."""
+    vp = ctypes.c_void_p
+    P = lambda v: vp(v) if v else None  # noqa: E731
+    return gpipes.lib.gp_mgn_mlp_out(M, K, P(x), P(w), P(b), P(w), P(b), P(w), P(b), P(g), P(bt),
+                                     eps, P(out), impl, None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(K=100), -2), (dict(K=512), -2), (dict(M=-1), -1), (dict(w=0), -1), (dict(b=0), -1),
+    (dict(g=0), -1), (dict(x=0), -1), (dict(out=0), -1), (dict(x=24), -3), (dict(out=8), -3),
+    (dict(w=40), -3), (dict(impl=7), -1), (dict(eps=-1.0), -1), (dict(eps=float("nan")), -1),
+])
+def test_argument_errors(kw, code):
+    rc = _call(**kw)
+    assert rc == code
+    assert gpipes.lib.gp_last_error().decode() != ""
+
+
+def test_empty_batch_is_a_noop():
+    assert _call(M=0, x=0, out=0) == 0
+    assert gpipes.lib.gp_last_error().decode() == ""
+
+
+def test_fullmlp_requires_affine():
+    vp = ctypes.c_void_p
+    rc = gpipes.lib.gp_mgn_fullmlp_out(16, vp(16), vp(16), vp(16), vp(16), vp(16), vp(16), vp(16), None,
+                                       None, vp(16), None)
+    assert rc == -1
+
+
+def test_python_mirror_rejects_cpu_and_bad_tensors():
+    x = torch.zeros(4, 384, dtype=torch.float16)
+    w1 = torch.zeros(384, 128, dtype=torch.float16)
+    w = torch.zeros(128, 128, dtype=torch.float16)
+    b = torch.zeros(128, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        gpipes.mgn_fullmlp(x, w1, b, w, b, w, b, b, b)
+    with pytest.raises(RuntimeError):
+        gpipes.mgn_linears(torch.zeros(4, 256, dtype=torch.float16), w1, b, w, b, w, b)

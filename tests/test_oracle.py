@@ -1,0 +1,208 @@
+"""Pin the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+
+Each oracle function is checked against something that is not a retyping of
+its own formula:
+  * fp16 conversion    -- numpy's IEEE binary16 conversion, all 65536 patterns
+  * linear (+act)      -- torch.nn.functional (library) in float64; K != N so a
+                          transposed weight fails
+  * layer_norm         -- torch.nn.functional.layer_norm in float64, closed
+                          forms (constant row -> beta, alternating +-a -> +-1),
+                          and the literal row of misc_tests/layer_norm/torch_val.py:88-105
+  * mgn_mlp            -- golden fixtures made by torch.nn modules in float64,
+                          closed forms (zero weights -> beta; identity weights ->
+                          LN(relu(x[:, :128]))), and planted mistakes that must fail
+  * add / concat       -- numpy
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from conftest import load_golden
+
+RNG = np.random.default_rng(1234)
+
+
+def test_h2f_all_patterns():
+    bits = np.arange(65536, dtype=np.uint16)
+    got = oracle.h2f(bits)
+    ref = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_f2h_round_to_nearest_even():
+    vals = np.concatenate([
+        RNG.standard_normal(200000).astype(np.float32) * np.float32(10.0),
+        (RNG.standard_normal(50000) * 1e-5).astype(np.float32),            # subnormal range
+        (RNG.standard_normal(50000) * 3e4).astype(np.float32),             # near overflow
+        np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e9, -1e9, np.inf, -np.inf,
+                  2.0 ** -24, 2.0 ** -25, 2.0 ** -25 * 1.0001, 2.0 ** -26], np.float32),
+    ])
+    # exact ties between adjacent fp16 values
+    h = RNG.integers(0, 0x7bff, 20000).astype(np.uint16)
+    lo = h.view(np.float16).astype(np.float64)
+    hi = (h + 1).view(np.float16).astype(np.float64)
+    vals = np.concatenate([vals, ((lo + hi) / 2).astype(np.float32)])
+    got = oracle.f2h(vals)
+    ref = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, ref)
+    nanb = oracle.f2h(np.array([np.nan], np.float32))
+    assert np.isnan(nanb.view(np.float16)[0])
+
+
+@pytest.mark.parametrize("act,tfn", [
+    (oracle.ACT_NONE, lambda t: t),
+    (oracle.ACT_RELU, torch.relu),
+    (oracle.ACT_GELU_TANH, lambda t: F.gelu(t, approximate="tanh")),
+    (oracle.ACT_SIGMOID, torch.sigmoid),
+])
+def test_linear_vs_torch(act, tfn):
+    M, K, N = 37, 96, 48
+    x = RNG.standard_normal((M, K)).astype(np.float32)
+    w = RNG.standard_normal((K, N)).astype(np.float32) / np.sqrt(K)
+    b = RNG.standard_normal(N).astype(np.float32)
+    got = oracle.linear(x, w, b, act)
+    ref = tfn(F.linear(torch.from_numpy(x).double(), torch.from_numpy(w).double().t(),
+                       torch.from_numpy(b).double())).numpy()
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+
+
+def test_linear_no_bias_and_k1():
+    x = RNG.standard_normal((5, 1)).astype(np.float32)
+    w = RNG.standard_normal((1, 7)).astype(np.float32)
+    got = oracle.linear(x, w, None)
+    np.testing.assert_allclose(got, x @ w, rtol=1e-6)
+
+
+@pytest.mark.parametrize("eps", [1e-5, 1e-12])
+def test_layer_norm_vs_torch(eps):
+    M, D = 64, 128
+    x = (RNG.standard_normal((M, D)) * 3 + 1.5).astype(np.float32)
+    g = RNG.uniform(0.5, 1.5, D).astype(np.float32)
+    b = RNG.uniform(-1, 1, D).astype(np.float32)
+    got = oracle.layer_norm(x, g, b, eps)
+    ref = F.layer_norm(torch.from_numpy(x).double(), [D], torch.from_numpy(g).double(),
+                       torch.from_numpy(b).double(), eps).numpy()
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=2e-5)
+
+
+def test_layer_norm_closed_forms():
+    D = 128
+    # constant row: variance 0, output is exactly beta
+    beta = RNG.uniform(-1, 1, D).astype(np.float32)
+    x = np.full((3, D), 0.375, np.float32)  # sums exactly in fp32
+    np.testing.assert_array_equal(oracle.layer_norm(x, np.ones(D, np.float32), beta), np.broadcast_to(beta, x.shape))
+    # alternating +-a: mean 0, var a^2 -> +-a/sqrt(a^2+eps)
+    for a in (1.0, 0.25, 7.0):
+        row = np.where(np.arange(D) % 2 == 0, a, -a).astype(np.float32)[None]
+        want = row / np.sqrt(a * a + 1e-5)
+        np.testing.assert_allclose(oracle.layer_norm(row), want, rtol=1e-6)
+
+
+def test_layer_norm_reference_row():
+    z = load_golden("layer_norm_row.npz")
+    x = z["x"].astype(np.float32)
+    got = oracle.layer_norm(x, eps=float(z["eps"]))
+    np.testing.assert_allclose(got, z["expected"], rtol=1e-5, atol=2e-5)
+    # normalised row: zero mean, variance v / (v + eps) for the input variance v
+    v = x[0].astype(np.float64).var()
+    assert abs(got[0].mean()) < 1e-5
+    assert abs(got[0].var() - v / (v + 1e-5)) < 1e-5
+
+
+FIXTURES = ["mgn_edge_ln.npz", "mgn_edge_ln_affine.npz", "mgn_edge_linears.npz", "mgn_node_ln.npz"]
+
+
+def _run_fixture(z, **override):
+    p = {k: z[k].astype(np.float32) for k in ("x", "w1", "b1", "w2", "b2", "w3", "b3")}
+    p["gamma"] = z["gamma"].astype(np.float32) if "gamma" in z else None
+    p["beta"] = z["beta"].astype(np.float32) if "beta" in z else None
+    p.update(override)
+    return oracle.mgn_mlp(p["x"], p["w1"], p["b1"], p["w2"], p["b2"], p["w3"], p["b3"],
+                          p["gamma"], p["beta"], eps=float(z["eps"]))
+
+
+@pytest.mark.parametrize("name", FIXTURES)
+def test_mgn_mlp_golden(name):
+    z = load_golden(name)
+    got = _run_fixture(z)
+    np.testing.assert_allclose(got, z["expected"], rtol=1e-4, atol=1e-4)
+    max_abs, rel = oracle.errors(got, z["expected"])
+    assert max_abs < 1e-4 and rel < 1e-5
+
+
+@pytest.mark.parametrize("mutant", ["no_relu1", "relu3", "w1_rows_swapped", "b3_dropped", "eps_wrong"])
+def test_mgn_mlp_golden_rejects_planted_mistakes(mutant):
+    """A plausible oracle mistake must fail the same fixture check."""
+    z = load_golden("mgn_edge_ln_affine.npz")
+    x = z["x"].astype(np.float32)
+    w1, b1 = z["w1"].astype(np.float32), z["b1"].astype(np.float32)
+    w2, b2 = z["w2"].astype(np.float32), z["b2"].astype(np.float32)
+    w3, b3 = z["w3"].astype(np.float32), z["b3"].astype(np.float32)
+    g, bt = z["gamma"].astype(np.float32), z["beta"].astype(np.float32)
+    if mutant == "no_relu1":
+        h = oracle.linear(x, w1, b1)
+        h = oracle.linear(h, w2, b2, oracle.ACT_RELU)
+        got = oracle.layer_norm(oracle.linear(h, w3, b3), g, bt)
+    elif mutant == "relu3":
+        h = oracle.linear(oracle.linear(x, w1, b1, oracle.ACT_RELU), w2, b2, oracle.ACT_RELU)
+        got = oracle.layer_norm(oracle.linear(h, w3, b3, oracle.ACT_RELU), g, bt)
+    elif mutant == "w1_rows_swapped":
+        got = _run_fixture(z, w1=np.roll(w1, 1, axis=0))
+    elif mutant == "b3_dropped":
+        got = _run_fixture(z, b3=np.zeros_like(b3))
+    else:
+        got = oracle.layer_norm(oracle.linear(oracle.linear(oracle.linear(x, w1, b1, 1), w2, b2, 1), w3, b3),
+                                g, bt, eps=1e-1)
+    max_abs, rel = oracle.errors(got, z["expected"])
+    assert max_abs > oracle.MAX_ABS_TOL or rel > oracle.REL_L2_TOL, (mutant, max_abs, rel)
+
+
+def test_mgn_mlp_zero_weights():
+    """W = 0: every row becomes LN(b3); with a constant b3 that is exactly beta."""
+    K = 384
+    x = RNG.standard_normal((9, K)).astype(np.float32)
+    z = np.zeros
+    b3 = RNG.standard_normal(128).astype(np.float32)
+    beta = RNG.uniform(-1, 1, 128).astype(np.float32)
+    gamma = RNG.uniform(0.5, 1.5, 128).astype(np.float32)
+    args = (x, z((K, 128), np.float32), RNG.standard_normal(128), z((128, 128), np.float32),
+            RNG.standard_normal(128), z((128, 128), np.float32))
+    out = oracle.mgn_mlp(*args, b3, gamma, beta)
+    ref = F.layer_norm(torch.from_numpy(b3).double()[None], [128], torch.from_numpy(gamma).double(),
+                       torch.from_numpy(beta).double()).numpy()
+    np.testing.assert_allclose(out, np.broadcast_to(ref, out.shape), rtol=1e-5, atol=1e-5)
+    out_c = oracle.mgn_mlp(*args, np.full(128, -0.625, np.float32), gamma, beta)
+    np.testing.assert_array_equal(out_c, np.broadcast_to(beta, out_c.shape))
+
+
+def test_mgn_mlp_identity_weights():
+    K = 384
+    x = RNG.standard_normal((33, K)).astype(np.float32)
+    w1 = np.zeros((K, 128), np.float32)
+    w1[:128] = np.eye(128)
+    eye = np.eye(128, dtype=np.float32)
+    zb = np.zeros(128, np.float32)
+    out = oracle.mgn_mlp(x, w1, zb, eye, zb, eye, zb, np.ones(128), zb)
+    ref = F.layer_norm(torch.relu(torch.from_numpy(x[:, :128]).double()), [128]).numpy()
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-5)
+    out_nl = oracle.mgn_mlp(x, w1, zb, eye, zb, eye, zb)
+    np.testing.assert_array_equal(out_nl, np.maximum(x[:, :128], 0))
+
+
+def test_add_concat():
+    a = RNG.standard_normal((17, 64)).astype(np.float32)
+    b = RNG.standard_normal((17, 64)).astype(np.float32)
+    np.testing.assert_array_equal(oracle.add(a, b), a + b)
+    c = RNG.standard_normal((17, 32)).astype(np.float32)
+    np.testing.assert_array_equal(oracle.concat(a, c), np.concatenate([a, c], axis=1))
+
+
+def test_errors_helper():
+    e = np.array([3.0, 4.0])
+    assert oracle.errors(e, e) == (0.0, 0.0)
+    ma, rel = oracle.errors(np.array([3.0, 4.5]), e)
+    assert ma == pytest.approx(0.5) and rel == pytest.approx(0.1)
