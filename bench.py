@@ -86,6 +86,9 @@ def main():
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="edge")
     ap.add_argument("--impl", choices=["fused", "pipelined"], default="fused")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--copy-ref", action="store_true",
+                    help="first run one plain 1 GiB device copy (a known-size reference kernel "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -111,6 +114,13 @@ def main():
         b = i % nbuf
         gpipes.mgn_mlp_out(xs[b], p["w1"], p["b1"], p["w2"], p["b2"], p["w3"], p["b3"], p["gamma"],
                            p["beta"], outs[b], impl=args.impl)
+
+    if args.copy_ref:
+        src = torch.ones(1 << 29, dtype=torch.float16, device=dev)  # 1 GiB
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     for i in range(args.warmup):
         step(i)

@@ -42,6 +42,14 @@ __device__ __forceinline__ void wait_vmcnt() {
 // across this point without emitting any hardware wait.
 __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
 
+// Returns v unchanged, but hides its value from the optimiser so that
+// expressions derived from it are recomputed where used instead of being
+// hoisted out of loops and kept live in registers.
+__device__ __forceinline__ int opaque(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // Workgroup barrier for LDS traffic only.  A HIP __syncthreads() carries a
 // workgroup release fence, and on gfx950 a release fence must also drain
 // every outstanding global->LDS DMA (vmcnt(0)), which would serialise the
@@ -61,6 +69,19 @@ __device__ __forceinline__ void lds_barrier() {
 // which global chunk each lane fetches.
 __device__ __forceinline__ void dma16(const void* gsrc, GP_LDS void* lds_base) {
   __builtin_amdgcn_global_load_lds(gsrc, lds_base, 16, 0, 0);
+}
+
+// Raw buffer descriptor over [base, base + nbytes) (gfx9 word 3: 0x00020000).
+// Buffer accesses at offsets >= nbytes are discarded by the hardware range
+// check: loads return zero, stores are dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, nbytes, 0x00020000);
+}
+
+// 16-byte buffer->LDS copy: lane i fetches rsrc[voffset .. voffset+16) into
+// LDS bytes [lds_base + 16 i, lds_base + 16 i + 16).
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t rsrc, int voffset, GP_LDS void* lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds_base, 16, voffset, 0, 0, 0);
 }
 
 // ---------------------------------------------------------------------------
