@@ -63,6 +63,51 @@ __device__ __forceinline__ void lds_barrier() {
   compiler_fence();
 }
 
+// ---------------------------------------------------------------------------
+// LDS counters for synchronising a subset of the waves of a workgroup
+// (s_barrier always involves every wave).  Counters only ever increase;
+// a waiter spins until the counter reaches its target.  Each wave first
+// drains its own LDS traffic (lgkmcnt(0)) so that everything it wrote
+// before signalling is visible to the waves that observe the signal.
+// ---------------------------------------------------------------------------
+constexpr int kSpinLimit = 1 << 20;  // ~0.1 s: a broken protocol ends instead of hanging
+
+__device__ __forceinline__ int lds_load_relaxed(GP_LDS int* c) {
+  return __hip_atomic_load((int*)c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Add 1 to an LDS counter once per wave, after this wave's LDS writes.
+__device__ __forceinline__ void lds_signal(GP_LDS int* c, int lane) {
+  compiler_fence();
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  if (lane == 0) __hip_atomic_fetch_add((int*)c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  compiler_fence();
+}
+
+// Spin until an LDS counter is >= target (every lane reads the same word).
+// If the bound runs out, the sticky abort word is set and every later wait of
+// the workgroup returns at once, so the kernel always terminates.
+__device__ __forceinline__ void lds_wait_geq(GP_LDS int* c, int target, GP_LDS int* abort) {
+  compiler_fence();
+  for (int it = 0;; ++it) {
+    if (lds_load_relaxed(c) >= target || lds_load_relaxed(abort) != 0) break;
+    if (it == kSpinLimit) {
+      __hip_atomic_store((int*)abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  compiler_fence();
+}
+
+// Barrier among the `nw` waves that share counter c; `gen` is this wave's
+// running target (starts at 0, advanced by nw per barrier).
+__device__ __forceinline__ void group_barrier(GP_LDS int* c, int& gen, int nw, int lane, GP_LDS int* abort) {
+  gen += nw;
+  lds_signal(c, lane);
+  lds_wait_geq(c, gen, abort);
+}
+
 // 16-byte global->LDS copy.  Lane i of the wave writes LDS bytes
 // [lds_base + 16 i, lds_base + 16 i + 16); lds_base must be wave-uniform.
 // The source address is per lane, so the LDS layout is chosen by picking

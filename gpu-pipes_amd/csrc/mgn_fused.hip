@@ -7,28 +7,32 @@
 // (the same chain without LayerNorm).  The oracle semantics are those of
 // common/mlps.py:3-20 (MgnMlp), computed here with fp32 accumulation.
 //
-// MI355X design (one workgroup of 8 waves per CU, persistent over 64-row tiles):
-//  * Wave w owns output features [32n, 32n+32) (n = w % 4) of every layer for
-//    the 32-row block m = w / 4 of each tile, so each SIMD runs two waves with
-//    the same weights: while one waits on LDS, the other issues MFMAs.
-//  * Weights stay resident for the whole kernel in AGPRs (MFMA takes its A
-//    operand from AGPRs on gfx950): W1[:,32n:32n+32] as K/16 fragments plus the
-//    W2 and W3 slices (8 fragments each) -- 160 registers per wave.
-//  * Each X tile (64 rows x K fp16) is streamed HBM->LDS with global_load_lds
-//    (16 B per lane, whole 1 KiB wave transactions), double-buffered so the
-//    next tile is in flight while this one is computed.  LDS chunks are
-//    XOR-swizzled per row so the MFMA B-operand reads are bank-conflict free.
-//  * The chain is computed transposed, Y^T = W^T X^T, with
+// MI355X design: one persistent workgroup of 8 waves per CU walks 64-row tiles.
+// The reference's stage blocks become wave-specialised stages inside the CU:
+//  * Stage A (waves 0-3, one per SIMD): layer 1.  Wave n keeps the W1 slice
+//    for output features [32n, 32n+32) resident in AGPRs (K/16 MFMA A
+//    fragments), streams X tiles HBM->LDS with buffer_load ... lds (16 B per
+//    lane, whole 1 KiB wave transactions, double-buffered, XOR-swizzled so
+//    the MFMA B-operand reads are bank-conflict free), and writes
+//    relu(X W1 + b1) in fp16 to one of two LDS handoff tiles.
+//  * Stage B (waves 4-7, one per SIMD): layers 2 and 3 plus LayerNorm.  Layer
+//    2 is split by feature (wave r computes features [32r, 32r+32) of all 64
+//    rows from the handoff tile, W2 slice resident), its output is exchanged
+//    through LDS, and layer 3 is split by row: wave r computes all 128
+//    features of rows [16r, 16r+16) with v_mfma_f32_16x16x32_f16 and the whole
+//    W3 resident in AGPRs.  Every row's 128 outputs then sit in four lanes of
+//    one wave, so the LayerNorm (two-pass mean / variance, as the reference's
+//    common/layer_norm_v2.cuh:42-70) is computed in-wave with two lane
+//    exchanges and no cross-wave synchronisation.
+//  * The handoff replaces the reference's global-memory queue
+//    (common/mpmcq.cuh): a two-slot LDS ring with monotonic "full"/"free"
+//    counters, so activations never leave the CU and stages A and B of
+//    different tiles run concurrently on every SIMD (one A and one B wave per
+//    SIMD share the matrix core).  All in-loop synchronisation is LDS
+//    counters (one A-wave barrier per tile, one-sided waits elsewhere);
+//    s_barrier is used only in the prologue.
+//  * All chains are computed transposed, Y^T = W^T X^T, with
 //    v_mfma_f32_32x32x16_f16; the bias is the accumulator's initial value.
-//    Layer outputs (ReLU + fp16 rounding in the epilogue) are exchanged between
-//    the four feature slices through two small LDS tiles; they never leave the
-//    CU.  Layer 3 stays fp32 into the LayerNorm.
-//  * LayerNorm is fused: each wave reduces its 32 features per row (in-lane +
-//    one cross-half exchange), and the four partial (mean, M2) pairs of a row
-//    are combined with Chan's parallel-variance formula through LDS.
-//  * The finished output tile is staged in LDS and written out as whole rows at
-//    the start of the next tile, so the wait for the next X tile never waits on
-//    fresh stores.
 #include "gp_device.hpp"
 #include "gp_kernels.hpp"
 
@@ -37,11 +41,10 @@ namespace fused {
 
 constexpr int TM = 64;          // rows per tile (two 32-row MFMA blocks)
 constexpr int D = 128;          // hidden width of every MGN layer
-constexpr int NWAVES = 8;       // 4 feature slices x 2 row blocks
+constexpr int NWAVES = 8;       // 4 layer-1 waves + 4 layer-2/3/LN waves
 constexpr int NTHREADS = NWAVES * kWave;
 constexpr int ACT_STRIDE = D * 2 + 16;   // padded LDS row (bytes) of a 128-wide fp16 tile
 constexpr int SLAB_STRIDE = 64 * 2 + 16; // padded LDS row (bytes) of a transposed 64-k weight slab
-constexpr int ACT_BYTES = (TM * ACT_STRIDE > D * SLAB_STRIDE) ? TM * ACT_STRIDE : D * SLAB_STRIDE;
 
 template <int K>
 struct Cfg {
@@ -49,9 +52,10 @@ struct Cfg {
   static constexpr int KS1 = K / 16;                 // MFMA k-steps of layer 1
   static constexpr int CPR = K / 8;                  // 16-byte chunks per X row
   static constexpr int XTILE = TM * K * 2;           // bytes per X tile
+  static constexpr int XBUF = XTILE > D * SLAB_STRIDE ? XTILE : D * SLAB_STRIDE;  // also weight-slab scratch
   static constexpr int DMA_INSTR = XTILE / 1024;     // wave-wide 1 KiB copies per tile
-  static constexpr int DMA_PER_WAVE = DMA_INSTR / NWAVES;
-  static_assert(DMA_INSTR % NWAVES == 0, "tile must split evenly over waves");
+  static constexpr int DMA_PER_WAVE = DMA_INSTR / 4; // issued by the four A waves
+  static_assert(DMA_INSTR % 4 == 0, "tile must split evenly over the A waves");
 };
 
 struct Params {
@@ -69,30 +73,15 @@ struct Params {
   float eps;
 };
 
-// Issue this wave's share of the copy of X tile `tile` into an LDS buffer.
-// LDS chunk slot q = 64*i + lane holds row r = q / CPR, physical chunk p = q % CPR,
-// which is logical chunk c = p ^ (r & 15) of that row.  The copy goes through a
-// buffer descriptor whose base is the tile and whose size ends at row M, so
-// rows past M are zero-filled by the hardware range check (their results are
-// never stored) and every per-lane offset is a 32-bit value.
-template <int K>
-__device__ __forceinline__ void issue_x_tile(const half_t* __restrict__ x, int64_t M, int64_t tile,
-                                             GP_LDS char* buf, int wave, int lane) {
-  using C = Cfg<K>;
-  const int64_t row0 = tile * TM;
-  const int64_t left = (M - row0) * (K * 2);
-  const int nbytes = left < C::XTILE ? (int)left : C::XTILE;
-  const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(x + row0 * K, nbytes);
-#pragma unroll
-  for (int ii = 0; ii < C::DMA_PER_WAVE; ++ii) {
-    const int i = ii * NWAVES + wave;
-    const int q = i * kWave + lane;
-    const int r = q / C::CPR;
-    const int p = q - r * C::CPR;
-    const int c = p ^ (r & 15);
-    dma16_buf(rsrc, (r * K + c * 8) * 2, buf + i * 1024);
-  }
-}
+// LDS synchronisation words (monotonic counters, one count per wave per tile).
+struct Sync {
+  int a_bar;    // barrier among the A waves
+  int h_full;   // handoff tile written by the A waves
+  int h_free;   // handoff tile read by the B waves
+  int x2_full;  // layer-2 output tile written by the B waves
+  int x2_free;  // layer-2 output tile read by the B waves
+  int abort;    // set when a wait exceeds its spin bound
+};
 
 // Accumulator initialised with the bias: C element 4g+e of a lane holds the
 // bias of feature fq + 8g + e (every row of the block shares it).
@@ -107,21 +96,27 @@ __device__ __forceinline__ f16x bias_frag(const float* bias, int fq) {
   return c;
 }
 
-// One 32-row block: acc += W^T(fragments wf[0..KS)) * B, B fragments read from
-// LDS through ld(s) two k-steps ahead of their MFMA.
+// Two 32-row blocks sharing the A operand (weight fragments wf[0..KS)); B
+// fragments come from LDS through ld(rb, s), fetched two k-steps ahead.
 template <int KS, typename LD>
-__device__ __forceinline__ void gemm_blk(const h8* wf, LD ld, f16x& acc) {
-  h8 q[2];
-  q[0] = ld(0);
-  q[1] = ld(1);
+__device__ __forceinline__ void gemm_2blk(const h8* wf, LD ld, f16x& acc0, f16x& acc1) {
+  h8 q0[2], q1[2];
+  q0[0] = ld(0, 0);
+  q1[0] = ld(1, 0);
+  q0[1] = ld(0, 1);
+  q1[1] = ld(1, 1);
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    acc = mfma32(wf[s], q[s & 1], acc);
-    if (s + 2 < KS) q[s & 1] = ld(s + 2);
+    acc0 = mfma32(wf[s], q0[s & 1], acc0);
+    acc1 = mfma32(wf[s], q1[s & 1], acc1);
+    if (s + 2 < KS) {
+      q0[s & 1] = ld(0, s + 2);
+      q1[s & 1] = ld(1, s + 2);
+    }
   }
 }
 
-// ReLU + fp16 rounding of the accumulator into this lane's row of an LDS
+// ReLU + fp16 rounding of an accumulator into this lane's row of an LDS
 // activation tile.  relu(round(x)) == round(relu(x)), so ReLU runs on the
 // packed fp16 values.
 __device__ __forceinline__ void store_relu_row(GP_LDS char* act_row, int fq, const f16x& a) {
@@ -134,37 +129,81 @@ __device__ __forceinline__ void store_relu_row(GP_LDS char* act_row, int fq, con
   }
 }
 
+// Prologue shared by both stages: weights are row-major [K][128]; 64-k slabs
+// are transposed through two LDS scratch tiles ([feature][k], SLAB_STRIDE
+// bytes per feature) so every MFMA fragment is one 16-byte read.  Slab
+// j < K/64 holds W1 rows [64j, 64j+64), then two slabs of W2 and two of W3.
+// All eight waves copy every slab (wave w copies feature octets w and w+8 of
+// the 64 rows); take(j, buf) then reads whatever fragments the caller needs.
+template <int K, typename Take>
+__device__ __forceinline__ void stage_weights(const Params& p, GP_LDS char* buf0, GP_LDS char* buf1, int wave,
+                                              int lane, Take take) {
+  constexpr int NS1 = K / 64;
+  constexpr int NS = NS1 + 4;
+  auto slab_src = [&](int j) -> const half_t* {
+    return j < NS1 ? p.w1 + (64 * j) * D : (j < NS1 + 2 ? p.w2 + 64 * (j - NS1) * D : p.w3 + 64 * (j - NS1 - 2) * D);
+  };
+  h8 va[2], vb[2];
+  auto load_slab = [&](int j, h8(&v)[2]) {
+    const half_t* W = slab_src(j);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) v[i] = *(const h8*)(W + lane * D + 8 * (wave + 8 * i));
+  };
+  auto put_slab = [&](GP_LDS char* buf, const h8(&v)[2]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        *(GP_LDS half_t*)(buf + (8 * (wave + 8 * i) + e) * SLAB_STRIDE + lane * 2) = v[i][e];
+  };
+  load_slab(0, va);
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    GP_LDS char* buf = (j & 1) ? buf1 : buf0;
+    if (j + 1 < NS) load_slab(j + 1, (j & 1) ? va : vb);
+    put_slab(buf, (j & 1) ? vb : va);
+    lds_barrier();
+    take(j, buf);
+  }
+  lds_barrier();  // the scratch tiles are reused afterwards
+}
+
+// 16-byte fragment of a transposed slab: feature f, slab-local k offset kk.
+__device__ __forceinline__ h8 slab_frag(GP_LDS char* buf, int f, int kk) {
+  return *(const GP_LDS h8*)(buf + f * SLAB_STRIDE + kk * 2);
+}
+
+__device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
 template <int K, bool LN>
 __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void mgn_fused_kernel(Params p) {
   using C = Cfg<K>;
-  __shared__ __attribute__((aligned(1024))) char xs0[C::XTILE];
-  __shared__ __attribute__((aligned(1024))) char xs1[C::XTILE];
-  __shared__ __attribute__((aligned(16))) char act1[ACT_BYTES];
-  __shared__ __attribute__((aligned(16))) char act2[ACT_BYTES];
-  __shared__ __attribute__((aligned(16))) char ostage[TM * ACT_STRIDE];  // finished output tile
-  __shared__ __attribute__((aligned(16))) f2 lnpart[TM][4];
+  __shared__ __attribute__((aligned(1024))) char xs0[C::XBUF];
+  __shared__ __attribute__((aligned(1024))) char xs1[C::XBUF];
+  __shared__ __attribute__((aligned(16))) char hand0[TM * ACT_STRIDE];  // layer-1 output, slot 0
+  __shared__ __attribute__((aligned(16))) char hand1[TM * ACT_STRIDE];  // layer-1 output, slot 1
+  __shared__ __attribute__((aligned(16))) char act2[TM * ACT_STRIDE];   // layer-2 output
   __shared__ __attribute__((aligned(16))) float prm[5][D];  // b1, b2, b3, gamma, beta
+  __shared__ Sync sy;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
-  const int lr = lane & 31;   // row within the 32-row block (B / C column)
-  const int lh = lane >> 5;   // half of the k-chunk / feature quad
-  const int n = wave & 3;     // feature slice
-  const int m = wave >> 2;    // row block
+  const int lr = lane & 31;   // row within a 32-row block (32x32 B / C column)
+  const int lh = lane >> 5;   // half of the k-chunk / feature quad (32x32 layout)
+  const int n = wave & 3;     // feature slice (A, B layer 2) / row block (B layer 3)
+  const bool stage_a = wave < 4;
 
   const int64_t M = p.M;
   const int64_t ntiles = (M + TM - 1) / TM;
   const int64_t G = gridDim.x;
-  int64_t t = blockIdx.x;
-  if (t >= ntiles) return;
+  const int64_t t0 = blockIdx.x;
+  if (t0 >= ntiles) return;
+  const int nt = (int)((ntiles - 1 - t0) / G + 1);  // tiles of this workgroup
 
-  // Start streaming the first two tiles before anything else.
-  issue_x_tile<K>(p.x, M, t, (GP_LDS char*)xs0, wave, lane);
-  if (t + G < ntiles) issue_x_tile<K>(p.x, M, t + G, (GP_LDS char*)xs1, wave, lane);
-
-  // Bias / LayerNorm parameters -> LDS (fp32).
   if (tid < D) {
     prm[0][tid] = (float)p.b1[tid];
     prm[1][tid] = (float)p.b2[tid];
@@ -174,179 +213,179 @@ void mgn_fused_kernel(Params p) {
       prm[4][tid] = (float)p.beta[tid];
     }
   }
+  if (tid == 0) sy = Sync{0, 0, 0, 0, 0, 0};
 
-  // Weight fragments: A operand = W^T, lane holds W[k0 + 8*lh + e][32*n + lr].
-  // W is row-major [K][128]; 64-k slabs are transposed through LDS (the two
-  // activation tiles, double-buffered) so every fragment is one 16-byte read.
-  const int fcol = 32 * n + lr;
-  h8 w1f[C::KS1];
-  h8 w2f[D / 16];
-  h8 w3f[D / 16];
-  {
-    constexpr int NS1 = K / 64;
-    constexpr int NS = NS1 + 4;  // W1 slabs, then two for W2, two for W3
-    auto slab_src = [&](int j) -> const half_t* {
-      return j < NS1 ? p.w1 + (64 * j) * D : (j < NS1 + 2 ? p.w2 + 64 * (j - NS1) * D : p.w3 + 64 * (j - NS1 - 2) * D);
+  const int fq = 32 * n + 4 * lh;  // 32x32 accumulator group g covers features fq + 8g + (0..3)
+  const int arow0 = lr * ACT_STRIDE, arow1 = (32 + lr) * ACT_STRIDE;
+  GP_LDS int* const ab = (GP_LDS int*)&sy.abort;
+  constexpr int NS1 = K / 64;
+
+  if (stage_a) {
+    // ------------------------------------------------------------- stage A
+    // W1 fragment for k-step s: lane holds W1[16s + 8*lh + e][32n + lr].
+    h8 w1f[C::KS1];
+    stage_weights<K>(p, (GP_LDS char*)xs0, (GP_LDS char*)xs1, wave, lane, [&](int j, GP_LDS char* buf) {
+      if (j < NS1)
+#pragma unroll
+        for (int sl = 0; sl < 4; ++sl) w1f[4 * j + sl] = slab_frag(buf, 32 * n + lr, 16 * sl + 8 * lh);
+    });
+#pragma unroll
+    for (int s = 0; s < C::KS1; ++s) asm volatile("" : "+a"(w1f[s]));
+
+    // X tiles are copied HBM->LDS by the four A waves (wave n issues the
+    // 1 KiB wave copies n, n+4, ...).  LDS chunk slot q = 64*i + lane holds
+    // row r = q / CPR, physical chunk p = q % CPR, which is logical chunk
+    // c = p ^ (r & 15) of that row.  The copy goes through a buffer descriptor
+    // whose base is the tile and whose size ends at row M, so rows past M are
+    // zero-filled by the hardware range check (their results are never
+    // stored).  voff[] are this lane's byte offsets within the tile.
+    int voff[C::DMA_PER_WAVE];
+#pragma unroll
+    for (int ii = 0; ii < C::DMA_PER_WAVE; ++ii) {
+      const int q = (ii * 4 + n) * kWave + lane;
+      const int r = q / C::CPR;
+      const int c = (q - r * C::CPR) ^ (r & 15);
+      voff[ii] = (r * K + c * 8) * 2;
+    }
+    auto issue = [&](int k, GP_LDS char* buf) {
+      const int64_t row0 = (t0 + (int64_t)k * G) * TM;
+      const int64_t left = (M - row0) * (K * 2);
+      const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(p.x + row0 * K, left < C::XTILE ? (int)left : C::XTILE);
+#pragma unroll
+      for (int ii = 0; ii < C::DMA_PER_WAVE; ++ii) dma16_buf(rsrc, voff[ii], buf + (ii * 4 + n) * 1024);
     };
-    // 64 rows x 16 feature octets per slab: wave w copies octets w and w + 8.
-    h8 va[2], vb[2];
-    auto load_slab = [&](int j, h8(&v)[2]) {
-      const half_t* W = slab_src(j);
-#pragma unroll
-      for (int i = 0; i < 2; ++i) v[i] = *(const h8*)(W + lane * D + 8 * (wave + 8 * i));
+    issue(0, (GP_LDS char*)xs0);
+
+    const int xa = lh ^ (lr & 15);  // chunk (2s+lh) of rows lr, lr+32 lands at (2s ^ xa) in its 16-group
+    const int xrow = lr * (K * 2);
+    int abar = 0;
+
+    auto tile_a = [&](GP_LDS char* xs, GP_LDS char* xnext, GP_LDS char* hand, int k) {
+      // X(k) is the only copy in flight.  After the barrier it has landed for
+      // every A wave and every A wave is done with tile k-1, whose buffer is
+      // refilled with X(k+1) at once.
+      wait_vmcnt<0>();
+      group_barrier((GP_LDS int*)&sy.a_bar, abar, 4, lane, ab);
+      if (k + 1 < nt) issue(k + 1, xnext);
+
+      f16x acc0 = bias_frag(prm[0], fq), acc1 = acc0;
+      gemm_2blk<C::KS1>(w1f, [&](int rb, int s) {
+        const int off = ((2 * s) & ~15) * 16 + (((2 * s) ^ xa) & 15) * 16;
+        return *(const GP_LDS h8*)(xs + xrow + rb * (32 * K * 2) + off);
+      }, acc0, acc1);
+
+      // Handoff slot k%2 was last read by stage B for tile k-2.
+      if (k >= 2) lds_wait_geq((GP_LDS int*)&sy.h_free, 4 * (k - 1), ab);
+      store_relu_row(hand + arow0, fq, acc0);
+      store_relu_row(hand + arow1, fq, acc1);
+      lds_signal((GP_LDS int*)&sy.h_full, lane);
     };
-    auto put_slab = [&](GP_LDS char* buf, const h8(&v)[2]) {
+
+    for (int k = 0; k < nt; k += 2) {
+      tile_a((GP_LDS char*)xs0, (GP_LDS char*)xs1, (GP_LDS char*)hand0, k);
+      if (k + 1 < nt) tile_a((GP_LDS char*)xs1, (GP_LDS char*)xs0, (GP_LDS char*)hand1, k + 1);
+    }
+  } else {
+    // ------------------------------------------------------------- stage B
+    // W2 (32x32x16 A operand): lane holds W2[16s + 8*lh + e][32n + lr].
+    // W3 (16x16x32 A operand) for feature block fb, k-step ks: lane holds
+    // W3[32ks + 8*(lane/16) + e][16fb + lane%16] -- all 128 features.
+    const int l16 = lane & 15, q4 = lane >> 4;
+    h8 w2f[D / 16];
+    h8 w3f[8][4];
+    stage_weights<K>(p, (GP_LDS char*)xs0, (GP_LDS char*)xs1, wave, lane, [&](int j, GP_LDS char* buf) {
+      if (j >= NS1 && j < NS1 + 2) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+        for (int sl = 0; sl < 4; ++sl) w2f[4 * (j - NS1) + sl] = slab_frag(buf, 32 * n + lr, 16 * sl + 8 * lh);
+      } else if (j >= NS1 + 2) {
+        const int half = j - NS1 - 2;  // k in [64 half, 64 half + 64)
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          *(GP_LDS half_t*)(buf + (8 * (wave + 8 * i) + e) * SLAB_STRIDE + lane * 2) = v[i][e];
+        for (int fb = 0; fb < 8; ++fb)
+#pragma unroll
+          for (int kl = 0; kl < 2; ++kl) w3f[fb][2 * half + kl] = slab_frag(buf, 16 * fb + l16, 32 * kl + 8 * q4);
+      }
+    });
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) asm volatile("" : "+v"(w2f[s]));
+#pragma unroll
+    for (int fb = 0; fb < 8; ++fb)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) asm volatile("" : "+a"(w3f[fb][ks]));
+
+    const int xrow3 = (16 * n + l16) * ACT_STRIDE;  // this lane's layer-3 row in act2
+
+    auto tile_b = [&](GP_LDS char* hand, int k) {
+      lds_wait_geq((GP_LDS int*)&sy.h_full, 4 * (k + 1), ab);
+
+      // layer 2, features [32n, 32n+32) of all 64 rows, from the handoff tile
+      f16x acc0 = bias_frag(prm[1], fq), acc1 = acc0;
+      gemm_2blk<D / 16>(w2f, [&](int rb, int s) {
+        return *(const GP_LDS h8*)(hand + (rb ? arow1 : arow0) + (2 * s + lh) * 16);
+      }, acc0, acc1);
+      lds_signal((GP_LDS int*)&sy.h_free, lane);  // B operands are in registers: release the slot
+
+      // exchange: act2 was last read (layer 3) for tile k-1
+      if (k >= 1) lds_wait_geq((GP_LDS int*)&sy.x2_free, 4 * k, ab);
+      store_relu_row((GP_LDS char*)act2 + arow0, fq, acc0);
+      store_relu_row((GP_LDS char*)act2 + arow1, fq, acc1);
+      lds_signal((GP_LDS int*)&sy.x2_full, lane);
+      lds_wait_geq((GP_LDS int*)&sy.x2_full, 4 * (k + 1), ab);
+
+      // layer 3, all features of rows [16n, 16n+16)
+      h8 bf[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) bf[ks] = *(const GP_LDS h8*)((GP_LDS char*)act2 + xrow3 + (32 * ks + 8 * q4) * 2);
+      lds_signal((GP_LDS int*)&sy.x2_free, lane);
+      f4 y[8];
+#pragma unroll
+      for (int fb = 0; fb < 8; ++fb) {
+        y[fb] = *(const f4*)&prm[2][16 * fb + 4 * q4];  // bias of features 16fb + 4q4 + (0..3)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) y[fb] = mfma16(w3f[fb][ks], bf[ks], y[fb]);
+      }
+
+      const int64_t grow = (t0 + (int64_t)k * G) * TM + 16 * n + l16;
+      half_t* o = p.out + grow * D + 4 * q4;
+      if constexpr (LN) {
+        // Lanes l16, l16+16, l16+32, l16+48 hold the row's 128 features.
+        float s = 0.f;
+#pragma unroll
+        for (int fb = 0; fb < 8; ++fb) s += (y[fb][0] + y[fb][1]) + (y[fb][2] + y[fb][3]);
+        s += __shfl_xor(s, 16, 64);
+        s += __shfl_xor(s, 32, 64);
+        const float mu = s * (1.f / D);
+        float v = 0.f;
+#pragma unroll
+        for (int fb = 0; fb < 8; ++fb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float d = y[fb][e] - mu;
+            v = __builtin_fmaf(d, d, v);
+          }
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        const float rstd = rsqrtf(v * (1.f / D) + p.eps);
+#pragma unroll
+        for (int fb = 0; fb < 8; ++fb) {
+          const f4 gm = *(const f4*)&prm[3][16 * fb + 4 * q4];
+          const f4 bt = *(const f4*)&prm[4][16 * fb + 4 * q4];
+          f4 z;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) z[e] = __builtin_fmaf((y[fb][e] - mu) * rstd, gm[e], bt[e]);
+          if (grow < M) *(h4*)(o + 16 * fb) = __builtin_convertvector(z, h4);
+        }
+      } else {
+#pragma unroll
+        for (int fb = 0; fb < 8; ++fb)
+          if (grow < M) *(h4*)(o + 16 * fb) = __builtin_convertvector(y[fb], h4);
+      }
     };
-    load_slab(0, va);
-#pragma unroll
-    for (int j = 0; j < NS; ++j) {
-      GP_LDS char* buf = (j & 1) ? (GP_LDS char*)act2 : (GP_LDS char*)act1;
-      if (j + 1 < NS) load_slab(j + 1, (j & 1) ? va : vb);
-      put_slab(buf, (j & 1) ? vb : va);
-      lds_barrier();
-#pragma unroll
-      for (int sl = 0; sl < 4; ++sl) {
-        const h8 f = *(const GP_LDS h8*)(buf + fcol * SLAB_STRIDE + (16 * sl + 8 * lh) * 2);
-        if (j < NS1) w1f[4 * j + sl] = f;
-        else if (j < NS1 + 2) w2f[4 * (j - NS1) + sl] = f;
-        else w3f[4 * (j - NS1 - 2) + sl] = f;
-      }
+
+    for (int k = 0; k < nt; k += 2) {
+      tile_b((GP_LDS char*)hand0, k);
+      if (k + 1 < nt) tile_b((GP_LDS char*)hand1, k + 1);
     }
-    // the activation tiles are reused below: every wave must be done reading
-    lds_barrier();
   }
-  // Register placement with two waves per SIMD (128 VGPRs + 128 AGPRs each):
-  // W1 and W3 live in AGPRs (MFMA reads its A operand from AGPRs on gfx950),
-  // W2, the accumulator and the LDS operand pipeline in VGPRs.
-#pragma unroll
-  for (int s = 0; s < C::KS1; ++s) asm volatile("" : "+a"(w1f[s]));
-#pragma unroll
-  for (int s = 0; s < D / 16; ++s) {
-    asm volatile("" : "+v"(w2f[s]));
-    asm volatile("" : "+a"(w3f[s]));
-  }
-
-  // Per-lane LDS addressing for this wave's row block.
-  const int row = 32 * m + lr;                  // tile row covered by this lane's accumulator column
-  const int xa = lh ^ (lr & 15);                // chunk (2s+lh) lands at (2s ^ xa) within its 16-group
-  const int xrow = row * (K * 2);
-  const int arow = row * ACT_STRIDE;
-  const int fq = 32 * n + 4 * lh;               // features of accumulator group g: fq + 8g + (0..3)
-
-  // The finished output tile waits in LDS and is stored at the top of the
-  // next tile as whole 256-byte rows (thread t copies 16-byte chunks t, t+512).
-  int64_t pend_tile = -1;
-  auto store_pending = [&]() {
-    if (pend_tile < 0) return;
-    const int tid_l = opaque(tid);  // recompute the offsets per tile rather than keep them live
-#pragma unroll
-    for (int j = 0; j < (TM * D * 2 / 16) / NTHREADS; ++j) {
-      const int c = tid_l + NTHREADS * j;
-      const int r = c >> 4, col = (c & 15) * 8;
-      const int64_t grow = pend_tile * TM + r;
-      const h8 v = *(const GP_LDS h8*)((GP_LDS char*)ostage + r * ACT_STRIDE + col * 2);
-      if (grow < M) *(h8*)(p.out + grow * D + col) = v;
-    }
-  };
-  auto put_out = [&](int g, h4 v) { *(GP_LDS h4*)((GP_LDS char*)ostage + arow + (fq + 8 * g) * 2) = v; };
-
-  auto process = [&](GP_LDS char* xs, int64_t tile, bool next_inflight, bool issue_next, int64_t next_tile) {
-    // 1. this tile's X has landed (only the following tile's copies may remain).
-    if (next_inflight) wait_vmcnt<C::DMA_PER_WAVE>();
-    else wait_vmcnt<0>();
-    lds_barrier();
-    store_pending();
-
-    // 2. layer 1: acc = b1 + W1^T X^T over K.
-    f16x acc = bias_frag(prm[0], fq);
-    gemm_blk<C::KS1>(w1f, [&](int s) {
-      const int off = ((2 * s) & ~15) * 16 + (((2 * s) ^ xa) & 15) * 16;
-      return *(const GP_LDS h8*)(xs + xrow + off);
-    }, acc);
-    store_relu_row((GP_LDS char*)act1 + arow, fq, acc);
-    lds_barrier();
-    // The X buffer is free again: start the copy of the tile two steps ahead.
-    if (issue_next) issue_x_tile<K>(p.x, M, next_tile, xs, wave, opaque(lane));
-
-    // 3. layer 2
-    acc = bias_frag(prm[1], fq);
-    gemm_blk<D / 16>(w2f, [&](int s) {
-      return *(const GP_LDS h8*)((GP_LDS char*)act1 + arow + (2 * s + lh) * 16);
-    }, acc);
-    store_relu_row((GP_LDS char*)act2 + arow, fq, acc);
-    lds_barrier();
-
-    // 4. layer 3 (+ bias), fp32 kept for the LayerNorm
-    acc = bias_frag(prm[2], fq);
-    gemm_blk<D / 16>(w3f, [&](int s) {
-      return *(const GP_LDS h8*)((GP_LDS char*)act2 + arow + (2 * s + lh) * 16);
-    }, acc);
-
-    if constexpr (LN) {
-      // Statistics of this wave's 32 features of the row.
-      float s0 = 0.f;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) s0 += acc[v];
-      s0 += xor_lane32(s0);
-      const float m0 = s0 * (1.f / 32.f);
-      float q0 = 0.f;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const float d0 = acc[v] - m0;
-        q0 = __builtin_fmaf(d0, d0, q0);
-      }
-      q0 += xor_lane32(q0);
-      if (lh == 0) lnpart[row][n] = f2{m0, q0};
-      lds_barrier();
-      // Combine the four (mean, M2) partials of the row (Chan et al.).
-      const f4 pa = *(const f4*)&lnpart[row][0];
-      const f4 pb = *(const f4*)&lnpart[row][2];
-      const float mu = 0.25f * ((pa[0] + pa[2]) + (pb[0] + pb[2]));
-      const float da = pa[0] - mu, db = pa[2] - mu, dc = pb[0] - mu, dd = pb[2] - mu;
-      const float m2 = (pa[1] + pa[3]) + (pb[1] + pb[3]) + 32.f * (da * da + db * db + dc * dc + dd * dd);
-      const float rstd = 1.f / sqrtf(m2 * (1.f / D) + p.eps);
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f4 gm = *(const f4*)&prm[3][fq + 8 * g];
-        const f4 bt = *(const f4*)&prm[4][fq + 8 * g];
-        f4 y;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = __builtin_fmaf((acc[4 * g + e] - mu) * rstd, gm[e], bt[e]);
-        put_out(g, __builtin_convertvector(y, h4));
-      }
-    } else {
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        put_out(g, __builtin_convertvector((f4){acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]}, h4));
-    }
-    pend_tile = tile;
-  };
-
-  // Tiles alternate between the two X buffers; the loop is unrolled by two so
-  // each buffer is a distinct LDS object at every access.
-  for (;;) {
-    {
-      const bool inflight = t + G < ntiles;
-      const bool issue = t + 2 * G < ntiles;
-      process((GP_LDS char*)xs0, t, inflight, issue, t + 2 * G);
-    }
-    t += G;
-    if (t >= ntiles) break;
-    {
-      const bool inflight = t + G < ntiles;
-      const bool issue = t + 2 * G < ntiles;
-      process((GP_LDS char*)xs1, t, inflight, issue, t + 2 * G);
-    }
-    t += G;
-    if (t >= ntiles) break;
-  }
-  lds_barrier();
-  store_pending();
 }
 
 }  // namespace fused
