@@ -173,6 +173,18 @@ __device__ __forceinline__ h8 slab_frag(GP_LDS char* buf, int f, int kk) {
   return *(const GP_LDS h8*)(buf + f * SLAB_STRIDE + kk * 2);
 }
 
+// Sum of a value over the four lanes l, l^16, l^32, l^48 (the lanes that
+// share l % 16), returned in all of them: v_permlane16_swap / 32_swap exchange
+// rows of 16 lanes without going through LDS.
+__device__ __forceinline__ float sum_lanes_16_32(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float y = __builtin_bit_cast(float, (unsigned)a[0]) + __builtin_bit_cast(float, (unsigned)a[1]);
+  const unsigned w = __builtin_bit_cast(unsigned, y);
+  const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  return __builtin_bit_cast(float, (unsigned)b[0]) + __builtin_bit_cast(float, (unsigned)b[1]);
+}
+
 __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
@@ -351,9 +363,7 @@ void mgn_fused_kernel(Params p) {
         float s = 0.f;
 #pragma unroll
         for (int fb = 0; fb < 8; ++fb) s += (y[fb][0] + y[fb][1]) + (y[fb][2] + y[fb][3]);
-        s += __shfl_xor(s, 16, 64);
-        s += __shfl_xor(s, 32, 64);
-        const float mu = s * (1.f / D);
+        const float mu = sum_lanes_16_32(s) * (1.f / D);
         float v = 0.f;
 #pragma unroll
         for (int fb = 0; fb < 8; ++fb)
@@ -362,16 +372,15 @@ void mgn_fused_kernel(Params p) {
             const float d = y[fb][e] - mu;
             v = __builtin_fmaf(d, d, v);
           }
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        const float rstd = rsqrtf(v * (1.f / D) + p.eps);
+        const float rstd = rsqrtf(sum_lanes_16_32(v) * (1.f / D) + p.eps);
+        const float nmr = -mu * rstd;
 #pragma unroll
         for (int fb = 0; fb < 8; ++fb) {
           const f4 gm = *(const f4*)&prm[3][16 * fb + 4 * q4];
           const f4 bt = *(const f4*)&prm[4][16 * fb + 4 * q4];
           f4 z;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) z[e] = __builtin_fmaf((y[fb][e] - mu) * rstd, gm[e], bt[e]);
+          for (int e = 0; e < 4; ++e) z[e] = __builtin_fmaf(__builtin_fmaf(y[fb][e], rstd, nmr), gm[e], bt[e]);
           if (grow < M) *(h4*)(o + 16 * fb) = __builtin_convertvector(z, h4);
         }
       } else {
