@@ -30,7 +30,7 @@ HIP_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
-SOURCES = ["mgn_fused.hip", "mgn_pipelined.hip", "stages.hip", "capi.cpp"]
+SOURCES = ["mgn_fused.hip", "mgn_pipelined.hip", "stages.hip", "capi.cpp", "arena.cpp"]
 
 
 def _run(cmd, verbose):

@@ -1,0 +1,66 @@
+// Queue arenas for the pipelined kernels.
+//
+// The reference keeps one process-global queue buffer per app, allocated on
+// first use and never freed (mgn_fullmlp_pl.cuh:255-266), shared by every
+// stream and device.  Here an arena is kept per (device, stream): launches on
+// one stream are ordered by the stream, launches on different streams use
+// different arenas.  An arena is zeroed once when allocated; afterwards every
+// launch gets a fresh epoch number and the device code treats counters of
+// older epochs as zero, so no per-launch reset is needed.
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "../../include/gpipes.h"
+#include "gp_host.hpp"
+
+namespace gp {
+
+namespace {
+struct ArenaRec {
+  void* base = nullptr;
+  size_t bytes = 0;
+  uint32_t epoch = 0;  // last epoch handed out
+};
+std::mutex g_mu;
+std::map<std::pair<int, hipStream_t>, ArenaRec> g_arenas;
+}  // namespace
+
+int arena_acquire(int dev, hipStream_t stream, size_t bytes, void** base, uint32_t* epoch) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  ArenaRec& a = g_arenas[{dev, stream}];
+  if (a.bytes < bytes) {
+    if (a.base) {
+      // the old arena may still be in use by work queued on this stream
+      hipError_t e = hipStreamSynchronize(stream);
+      if (e != hipSuccess) return fail_hip(e, "hipStreamSynchronize (arena growth)");
+      e = hipFree(a.base);
+      if (e != hipSuccess) return fail_hip(e, "hipFree (arena growth)");
+      a.base = nullptr;
+      a.bytes = 0;
+    }
+    hipError_t e = hipMalloc(&a.base, bytes);
+    if (e != hipSuccess) return fail_hip(e, "hipMalloc (queue arena)");
+    e = hipMemsetAsync(a.base, 0, bytes, stream);
+    if (e != hipSuccess) return fail_hip(e, "hipMemsetAsync (queue arena)");
+    a.bytes = bytes;
+    a.epoch = 0;
+  }
+  if (++a.epoch == 0) a.epoch = 1;  // epoch 0 is the zeroed state
+  *base = a.base;
+  *epoch = a.epoch;
+  return GP_OK;
+}
+
+int arena_last(int dev, hipStream_t stream, void** base, uint32_t* epoch) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_arenas.find({dev, stream});
+  if (it == g_arenas.end() || !it->second.base) return fail(GP_ERR_INVALID_ARG, "no pipelined launch on this stream");
+  *base = it->second.base;
+  *epoch = it->second.epoch;
+  return GP_OK;
+}
+
+}  // namespace gp

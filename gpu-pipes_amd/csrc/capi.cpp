@@ -67,7 +67,15 @@ int current_device_info(int* dev_out, int* num_cus) {
   return GP_OK;
 }
 
-static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// Host view of the pipeline control block (layout of PipeCtl, pipeline.hpp):
+// 16 ticket counters and the barrier counter, 128 bytes each, then the
+// launch error word.
+struct PipeCtlView {
+  char counters[17 * 128];
+  unsigned long long err;
+};
 
 int check_mgn_args(const MgnArgs& a) {
   if (a.M < 0) return fail(GP_ERR_INVALID_ARG, "M must be >= 0 (got %lld)", (long long)a.M);
@@ -93,7 +101,7 @@ int run_mgn(const MgnArgs& a, int impl, hipStream_t stream) {
   clear_error();
   int rc = check_mgn_args(a);
   if (rc != GP_OK) return rc;
-  if (impl != GP_IMPL_FUSED && impl != GP_IMPL_PIPELINED)
+  if (impl != GP_IMPL_FUSED && impl != GP_IMPL_PIPELINED && impl != GP_IMPL_PIPELINED_SPLIT_LN)
     return fail(GP_ERR_INVALID_ARG, "unknown impl %d", impl);
   if (a.M == 0) return GP_OK;
   int dev = 0, ncu = 0;
@@ -105,7 +113,23 @@ int run_mgn(const MgnArgs& a, int impl, hipStream_t stream) {
     if (e != hipSuccess) return fail_hip(e, "mgn_fused launch");
     return GP_OK;
   }
-  return mgn_pipelined_run(a, dev, ncu, stream);
+  return mgn_pipelined_run(a, impl == GP_IMPL_PIPELINED_SPLIT_LN, dev, ncu, stream);
+}
+
+// Common prologue of the stage-level entry points.
+static int stage_prologue(int64_t M, int* dev, int* ncu) {
+  clear_error();
+  if (M < 0) return fail(GP_ERR_INVALID_ARG, "M must be >= 0 (got %lld)", (long long)M);
+  if (M > (int64_t(1) << 40)) return fail(GP_ERR_SHAPE, "M too large (%lld)", (long long)M);
+  if (M == 0) return 1;  // nothing to do
+  int rc = current_device_info(dev, ncu);
+  return rc;
+}
+
+static int need(const void* p, const char* name, bool align = true) {
+  if (!p) return fail(GP_ERR_INVALID_ARG, "%s is NULL", name);
+  if (align && !aligned16(p)) return fail(GP_ERR_ALIGN, "%s must be 16-byte aligned", name);
+  return GP_OK;
 }
 
 }  // namespace gp
@@ -123,6 +147,100 @@ int gp_mgn_mlp_out(int64_t M, int64_t K, const void* x, const void* w1, const vo
                    float eps, void* out, int impl, void* stream) {
   MgnArgs a{M, K, x, w1, b1, w2, b2, w3, b3, gamma, beta, eps, out};
   return run_mgn(a, impl, (hipStream_t)stream);
+}
+
+int gp_linear_out(int64_t M, int64_t K, const void* x, const void* w, const void* b, const void* acc, int act,
+                  void* out, void* stream) {
+  int dev = 0, ncu = 0;
+  if (K != 128 && K != 256 && K != 384) return fail(GP_ERR_SHAPE, "K must be 128, 256 or 384 (got %lld)", (long long)K);
+  if (act < GP_ACT_NONE || act > GP_ACT_SIGMOID) return fail(GP_ERR_INVALID_ARG, "unknown act %d", act);
+  int rc = need(w, "w");
+  if (rc) return rc;
+  rc = stage_prologue(M, &dev, &ncu);
+  if (rc) return rc < 0 ? rc : GP_OK;
+  if ((rc = need(x, "x")) || (rc = need(out, "out"))) return rc;
+  if (acc && !aligned16(acc)) return fail(GP_ERR_ALIGN, "acc must be 16-byte aligned");
+  LinearArgs a{M, K, x, w, b, acc, nullptr, nullptr, 0.f, act, out};
+  hipError_t e = linear_launch(a, ncu, (hipStream_t)stream);
+  return e == hipSuccess ? GP_OK : fail_hip(e, "linear launch");
+}
+
+int gp_linear_layer_norm_out(int64_t M, int64_t K, const void* x, const void* w, const void* b, const void* gamma,
+                             const void* beta, float eps, void* out, void* stream) {
+  int dev = 0, ncu = 0;
+  if (K != 128 && K != 256 && K != 384) return fail(GP_ERR_SHAPE, "K must be 128, 256 or 384 (got %lld)", (long long)K);
+  int rc = need(w, "w");
+  if (rc) return rc;
+  if ((rc = need(gamma, "gamma", false)) || (rc = need(beta, "beta", false))) return rc;
+  if (!(eps >= 0.f)) return fail(GP_ERR_INVALID_ARG, "eps must be >= 0");
+  rc = stage_prologue(M, &dev, &ncu);
+  if (rc) return rc < 0 ? rc : GP_OK;
+  if ((rc = need(x, "x")) || (rc = need(out, "out"))) return rc;
+  LinearArgs a{M, K, x, w, b, nullptr, gamma, beta, eps, GP_ACT_NONE, out};
+  hipError_t e = linear_launch(a, ncu, (hipStream_t)stream);
+  return e == hipSuccess ? GP_OK : fail_hip(e, "linear+LayerNorm launch");
+}
+
+int gp_layer_norm_out(int64_t M, int64_t D, const void* x, const void* gamma, const void* beta, float eps, void* out,
+                      void* stream) {
+  int dev = 0, ncu = 0;
+  if (D != 128 && D != 256 && D != 512 && D != 1024)
+    return fail(GP_ERR_SHAPE, "D must be 128, 256, 512 or 1024 (got %lld)", (long long)D);
+  if (!(eps >= 0.f)) return fail(GP_ERR_INVALID_ARG, "eps must be >= 0");
+  int rc = stage_prologue(M, &dev, &ncu);
+  if (rc) return rc < 0 ? rc : GP_OK;
+  if ((rc = need(x, "x")) || (rc = need(out, "out"))) return rc;
+  hipError_t e = layer_norm_launch(M, D, x, gamma, beta, eps, out, ncu, (hipStream_t)stream);
+  return e == hipSuccess ? GP_OK : fail_hip(e, "layer_norm launch");
+}
+
+int gp_add_out(int64_t M, int64_t N, const void* a, const void* b, void* c, void* stream) {
+  int dev = 0, ncu = 0;
+  if (N <= 0 || N % 8 || N > (1 << 20)) return fail(GP_ERR_SHAPE, "N must be a positive multiple of 8");
+  int rc = stage_prologue(M, &dev, &ncu);
+  if (rc) return rc < 0 ? rc : GP_OK;
+  if ((rc = need(a, "a")) || (rc = need(b, "b")) || (rc = need(c, "c"))) return rc;
+  hipError_t e = add_launch(M, N, a, b, c, ncu, (hipStream_t)stream);
+  return e == hipSuccess ? GP_OK : fail_hip(e, "add launch");
+}
+
+int gp_concat_out(int64_t M, int64_t N0, int64_t N1, const void* a, const void* b, void* c, void* stream) {
+  int dev = 0, ncu = 0;
+  if (N0 <= 0 || N1 <= 0 || N0 % 8 || N1 % 8 || N0 + N1 > (1 << 20))
+    return fail(GP_ERR_SHAPE, "N0 and N1 must be positive multiples of 8");
+  int rc = stage_prologue(M, &dev, &ncu);
+  if (rc) return rc < 0 ? rc : GP_OK;
+  if ((rc = need(a, "a")) || (rc = need(b, "b")) || (rc = need(c, "c"))) return rc;
+  hipError_t e = concat_launch(M, N0, N1, a, b, c, ncu, (hipStream_t)stream);
+  return e == hipSuccess ? GP_OK : fail_hip(e, "concat launch");
+}
+
+int gp_pipe_ident(int64_t M, const void* x, void* out, int max_pipes, void* stream) {
+  int dev = 0, ncu = 0;
+  int rc = stage_prologue(M, &dev, &ncu);
+  if (rc) return rc < 0 ? rc : GP_OK;
+  if ((rc = need(x, "x")) || (rc = need(out, "out"))) return rc;
+  return pipe_ident_run(M, x, out, max_pipes, dev, ncu, (hipStream_t)stream);
+}
+
+int gp_pipeline_check(void* stream) {
+  clear_error();
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail_hip(e, "hipGetDevice");
+  void* base = nullptr;
+  uint32_t epoch = 0;
+  int rc = arena_last(dev, (hipStream_t)stream, &base, &epoch);
+  if (rc != GP_OK) return rc;
+  e = hipStreamSynchronize((hipStream_t)stream);
+  if (e != hipSuccess) return fail_hip(e, "hipStreamSynchronize");
+  unsigned long long err = 0;
+  e = hipMemcpy(&err, &((PipeCtlView*)base)->err, sizeof(err), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return fail_hip(e, "hipMemcpy (pipeline status)");
+  if ((uint32_t)(err >> 32) == epoch && (uint32_t)err != 0)
+    return fail(GP_ERR_TIMEOUT, "the last pipelined launch failed: %s (error bits 0x%x)",
+                (err & 1) ? "a queue wait timed out" : "no complete pipeline fitted on one XCD", (unsigned)err);
+  return GP_OK;
 }
 
 int gp_mgn_fullmlp_out(int64_t M, const void* x, const void* w1, const void* b1, const void* w2,

@@ -19,6 +19,15 @@ int current_device_info(int* dev_out, int* num_cus);
 int check_mgn_args(const MgnArgs& a);
 
 // Stage-chained implementation (workgroup stages linked by L2 ring queues).
-int mgn_pipelined_run(const MgnArgs& a, int dev, int num_cus, hipStream_t stream);
+// split_ln: the reference's layout with separate LayerNorm workers.
+int mgn_pipelined_run(const MgnArgs& a, bool split_ln, int dev, int num_cus, hipStream_t stream);
+
+// Identity pipelines through ring queues (tests the queue protocol).
+int pipe_ident_run(int64_t M, const void* x, void* out, int max_pipes, int dev, int num_cus, hipStream_t stream);
+
+// Queue arenas, one per (device, stream), zeroed once; each call returns a
+// new launch epoch.  arena_last returns the arena and epoch of the last call.
+int arena_acquire(int dev, hipStream_t stream, size_t bytes, void** base, uint32_t* epoch);
+int arena_last(int dev, hipStream_t stream, void** base, uint32_t* epoch);
 
 }  // namespace gp

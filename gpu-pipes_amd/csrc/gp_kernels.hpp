@@ -28,4 +28,25 @@ struct MgnArgs {
 // Persistent fused kernel (all layers in one workgroup per CU).
 hipError_t mgn_fused_launch(const MgnArgs& a, int num_cus, hipStream_t stream);
 
+// One GEMM stage over M rows: out = act(x W + b [+ acc]) or LayerNorm(x W + b).
+struct LinearArgs {
+  int64_t M;
+  int64_t K;          // 128, 256 or 384 (N is 128)
+  const void* x;      // [M, K]
+  const void* w;      // [K, 128]
+  const void* b;      // [128] or nullptr
+  const void* acc;    // [M, 128] accumulator input or nullptr
+  const void* gamma;  // LayerNorm epilogue when non-null
+  const void* beta;
+  float eps;
+  int act;            // GP_ACT_* (ignored with LayerNorm)
+  void* out;          // [M, 128]
+};
+hipError_t linear_launch(const LinearArgs& a, int num_cus, hipStream_t stream);
+hipError_t layer_norm_launch(int64_t M, int64_t D, const void* x, const void* gamma, const void* beta, float eps,
+                             void* out, int num_cus, hipStream_t stream);
+hipError_t add_launch(int64_t M, int64_t N, const void* a, const void* b, void* c, int num_cus, hipStream_t stream);
+hipError_t concat_launch(int64_t M, int64_t N0, int64_t N1, const void* a, const void* b, void* c, int num_cus,
+                         hipStream_t stream);
+
 }  // namespace gp

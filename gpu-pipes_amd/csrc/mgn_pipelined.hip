@@ -1,9 +1,136 @@
-// Stage-chained MGN MLP (workgroup stages linked by L2 ring queues).
-#include "gp_host.hpp"
+// Stage-chained MeshGraphNet MLP: one workgroup per stage, stages linked by
+// L2-resident ring queues -- the reference's pipelined form.
+//
+// Reference: apps/mgn_fullmlp/pipelined/mgn_fullmlp_pl.cuh:23-273 and
+// apps/mgn_linears/pipelined/mgn_linears_pl.cuh:22-212.  Per pipeline:
+//   X -> [Linear K->128 + ReLU] -q12-> [Linear + ReLU] -q23-> [Linear (+ LN)] -> out
+// with, in the split layout, the reference's LayerNorm workers:
+//   ... -q23-> [Linear] -lnq-> 5 x [LayerNorm] (round-robin split queue) -> out
+// (mlp0_sm0 :83-101, mlp1_sm0 :146-160, mlp2_sm0 :162-181, ln_sm :183-203).
+//
+// MI355X: stage roles come from the XCD-aware assignment (pipeline.hpp), so
+// every queue's producer and consumer share an L2; the launch is cooperative
+// (all workgroups resident, as spin-waiting stages require); pipelines take
+// tiles g, g+P, ... of any M, with the partial last tile carried by the
+// queue's row count.  Stage bodies are the library's stage functions.
+#include <hip/hip_runtime.h>
+
 #include "../../include/gpipes.h"
+#include "gp_host.hpp"
+#include "pipeline.hpp"
+#include "stages.hpp"
 
 namespace gp {
-int mgn_pipelined_run(const MgnArgs&, int, int, hipStream_t) {
-  return fail(GP_ERR_INVALID_ARG, "GP_IMPL_PIPELINED is not built in this version");
+namespace mgnpl {
+
+constexpr int MBLK = 128;
+constexpr int D = 128;
+constexpr int NLN = 5;  // LayerNorm workers per pipeline in the split layout (mgn_fullmlp_pl.cuh:28)
+
+using QEntry = QueueEntry2D<MBLK, D>;
+using Queue = RingQueue<QEntry, 2>;              // q12, q23 (qlen = 2, mgn_fullmlp_pl.cuh:32)
+using LnQueue = RingQueue<QEntry, NLN + 1>;      // lnq (ln_qlen = n_ln_cols + 1, :33)
+
+struct Queues {
+  Queue q12;
+  Queue q23;
+  LnQueue lnq;
+};
+
+struct Args {
+  MgnArgs m;
+  PipeCtl* ctl;
+  Queues* queues;
+  QueueCtx ctx;
+};
+
+template <int K, bool LN, bool SPLIT>
+__global__ __launch_bounds__(kStageThreads) void mgn_pipelined_kernel(Args a) {
+  constexpr int S = SPLIT ? 3 + NLN : 3;
+  const Role r = assign_role(a.ctl, S, a.ctx);
+  if (r.pipe < 0) return;
+  const MgnArgs& m = a.m;
+  Queues* qs = a.queues + r.pipe;
+  const int64_t T = (m.M + MBLK - 1) / MBLK, NP = r.npipes, g = r.pipe;
+  const int nt = g < T ? (int)((T - 1 - g) / NP + 1) : 0;
+  half_t* out = (half_t*)m.out;
+  const TensorView gamma{(half_t*)m.gamma, 1, 1}, beta{(half_t*)m.beta, 1, 1};
+  NullReader ar;
+
+  if (r.stage == 0) {
+    MemoryReader ir((half_t*)m.x + g * MBLK * K, NP * MBLK * K, K, MBLK, m.M - g * MBLK, NP * MBLK);
+    QueueWriter<Queue> ow(&qs->q12, &a.ctx);
+    pipe_gemm_bias_relu<MBLK, K>({(half_t*)m.w1, D, K}, {(half_t*)m.b1, 1, 1}, ir, ar, ow, nt);
+  } else if (r.stage == 1) {
+    QueueReader<Queue> ir(&qs->q12, &a.ctx);
+    QueueWriter<Queue> ow(&qs->q23, &a.ctx);
+    pipe_gemm_bias_relu<MBLK, D>({(half_t*)m.w2, D, D}, {(half_t*)m.b2, 1, 1}, ir, ar, ow, nt);
+  } else if (r.stage == 2) {
+    QueueReader<Queue> ir(&qs->q23, &a.ctx);
+    const TensorView w3{(half_t*)m.w3, D, D}, b3{(half_t*)m.b3, 1, 1};
+    if constexpr (SPLIT) {
+      QueueWriter<LnQueue> ow(&qs->lnq, &a.ctx);
+      pipe_gemm_bias<MBLK, D>(w3, b3, ir, ar, ow, nt);
+    } else {
+      MemoryWriter ow(out + g * MBLK * D, NP * MBLK * D, D);
+      if constexpr (LN) pipe_gemm_bias_layer_norm<MBLK, D>(w3, b3, gamma, beta, m.eps, ir, ar, ow, nt);
+      else pipe_gemm_bias<MBLK, D>(w3, b3, ir, ar, ow, nt);
+    }
+  } else if constexpr (SPLIT) {
+    // LayerNorm worker w takes queue sequence numbers w, w + NLN, ...
+    const int w = r.stage - 3;
+    const int cnt = nt > w ? (nt - w + NLN - 1) / NLN : 0;
+    SplitQueueReader<LnQueue> ir(&qs->lnq, &a.ctx, w, NLN);
+    MemoryWriter ow(out + (g + (int64_t)w * NP) * MBLK * D, (int64_t)NLN * NP * MBLK * D, D);
+    pipe_layer_norm<MBLK, D>(gamma, beta, ir, ow, cnt, m.eps);
+  }
 }
+
+template <int K, bool LN, bool SPLIT>
+static int run(const MgnArgs& m, int dev, int num_cus, hipStream_t s) {
+  constexpr int S = SPLIT ? 3 + NLN : 3;
+  constexpr int lds = gemm_stage_lds<MBLK, K>() + kGemmParamLds;
+  auto kern = mgn_pipelined_kernel<K, LN, SPLIT>;
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (e != hipSuccess) return fail_hip(e, "hipFuncSetAttribute");
+  int per_cu = 0;
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kStageThreads, lds);
+  if (e != hipSuccess) return fail_hip(e, "occupancy query");
+  const int grid = per_cu * num_cus;
+  if (grid < S) return fail(GP_ERR_NO_DEVICE, "not enough co-resident workgroups for one pipeline");
+  const size_t bytes = sizeof(PipeCtl) + (size_t)(grid / S) * sizeof(Queues);
+  void* base = nullptr;
+  uint32_t epoch = 0;
+  int rc = arena_acquire(dev, s, bytes, &base, &epoch);
+  if (rc != GP_OK) return rc;
+  Args a;
+  a.m = m;
+  a.ctl = (PipeCtl*)base;
+  a.queues = (Queues*)((char*)base + sizeof(PipeCtl));
+  a.ctx = QueueCtx{epoch, &a.ctl->err.v};
+  void* args[] = {&a};
+  e = hipLaunchCooperativeKernel((const void*)kern, dim3(grid), dim3(kStageThreads), args, lds, s);
+  if (e != hipSuccess) return fail_hip(e, "mgn_pipelined cooperative launch");
+  return GP_OK;
+}
+
+template <int K>
+static int run_k(const MgnArgs& m, bool split, int dev, int ncu, hipStream_t s) {
+  const bool ln = m.gamma != nullptr;
+  if (split) return run<K, true, true>(m, dev, ncu, s);
+  return ln ? run<K, true, false>(m, dev, ncu, s) : run<K, false, false>(m, dev, ncu, s);
+}
+
+}  // namespace mgnpl
+
+int mgn_pipelined_run(const MgnArgs& a, bool split_ln, int dev, int num_cus, hipStream_t stream) {
+  if (split_ln && a.gamma == nullptr) return fail(GP_ERR_INVALID_ARG, "the split-LayerNorm layout needs gamma/beta");
+  switch (a.K) {
+    case 384: return mgnpl::run_k<384>(a, split_ln, dev, num_cus, stream);
+    case 256: return mgnpl::run_k<256>(a, split_ln, dev, num_cus, stream);
+    case 128: return mgnpl::run_k<128>(a, split_ln, dev, num_cus, stream);
+    default: return fail(GP_ERR_SHAPE, "K must be 128, 256 or 384");
+  }
+}
+
 }  // namespace gp

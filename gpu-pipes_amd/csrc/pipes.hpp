@@ -1,0 +1,360 @@
+// Stage-chaining API for gfx950: tile views, readers / writers and the
+// inter-workgroup ring queue.
+//
+// Reference: common/pipes.cuh:7-108 (MemoryReader, read_striped_input,
+// NullReader, QueueReader, SplitQueueReader, MemoryWriter, QueueWriter,
+// SplitQueueWriter, NullWriter), common/mpmcq.cuh:10-115 (QueueSlot,
+// MpmcRingQueue) and common/common.cuh:3-6 (TensorView).  The names, the
+// acquire / release call pattern and the round-robin split semantics are the
+// reference's; the queue protocol is redesigned for MI355X:
+//
+//  * Every reader / writer call is workgroup-collective (all threads call it);
+//    one thread spins and the result is broadcast with a barrier.  The
+//    reference's per-warp spinning (mpmcq.cuh:79-88) has no wave64 analogue.
+//  * A slot has two monotonic 64-bit counters, "full" (producer commits) and
+//    "empty" (consumer commits), each on its own 128-byte line, tagged with the
+//    launch epoch in the high 32 bits.  Nothing is ever reset, so there is no
+//    reset race (mpmcq.cuh:42-54, 68-75) and back-to-back launches need no
+//    memset: a counter from an older epoch reads as zero.
+//  * Release: the producer's payload stores are complete in L2 (vmcnt(0) in
+//    every wave, then a barrier) before the commit atomic.  Acquire: after the
+//    consumer observes the counter it invalidates its CU's L1 (buffer_inv sc1)
+//    so payload loads are served by L2.  The reference has no fences at all
+//    (mpmcq.cuh:34-40).  Producer and consumer must share an XCD (one L2):
+//    the pipelined kernels assign stage roles by the hardware XCC id.
+//  * Waits are bounded: on timeout an error word is set and every later wait
+//    of the launch returns at once, so a broken pipeline ends instead of
+//    hanging; the host reports it as GP_ERR_TIMEOUT.
+//  * TensorView carries the number of valid rows, so the last, partial tile of
+//    an arbitrary M is handled (the reference drops it, mgn_fullmlp_pl.cuh:84).
+#pragma once
+
+#include "gp_device.hpp"
+
+namespace gp {
+
+// common/common.cuh:3-6: non-owning fp16 tile view.  `stride` is the row
+// stride in elements (0 = one row broadcast to all rows, e.g. a bias);
+// `rows` is the number of valid rows of the tile.
+struct TensorView {
+  half_t* data;
+  int stride;
+  int rows;
+};
+
+// ---------------------------------------------------------------------------
+// Launch context shared by every queue of a kernel launch.
+// ---------------------------------------------------------------------------
+struct QueueCtx {
+  uint32_t epoch;            // launch epoch (never 0)
+  unsigned long long* err;   // (epoch << 32) | error bits; bits of this epoch abort all waits
+};
+
+constexpr int kQueueSpinLimit = 1 << 22;  // polls of ~1 us before a wait gives up
+constexpr unsigned kErrTimeout = 1;
+constexpr unsigned kErrNoPipes = 2;  // the launch held no complete pipeline
+
+__device__ __forceinline__ bool q_aborted(const QueueCtx& c) {
+  const unsigned long long v = __hip_atomic_load(c.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return (uint32_t)(v >> 32) == c.epoch && (uint32_t)v != 0;
+}
+
+__device__ __forceinline__ void q_fail(const QueueCtx& c, unsigned bits) {
+  __hip_atomic_fetch_max(c.err, (unsigned long long)c.epoch << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(kWaitAll);
+  __hip_atomic_fetch_or(c.err, (unsigned long long)bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct alignas(128) QCounter {
+  unsigned long long v;  // (epoch << 32) | count
+  char pad[120];
+};
+
+__device__ __forceinline__ uint32_t qcount(unsigned long long v, uint32_t epoch) {
+  return (uint32_t)(v >> 32) == epoch ? (uint32_t)v : 0u;
+}
+
+// Count one commit on `c` in this epoch (thread-level; called by one thread).
+// The max lifts a counter left by an older launch to (epoch << 32) | 0; it
+// must be complete before the add, so the wave waits for it in between.
+__device__ __forceinline__ void qcommit(QCounter* c, uint32_t epoch) {
+  const unsigned long long base = (unsigned long long)epoch << 32;
+  __hip_atomic_fetch_max(&c->v, base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(kWaitAll);
+  __hip_atomic_fetch_add(&c->v, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(kWaitAll);
+}
+
+// Workgroup-collective: wait until count(c) >= target.  Returns false if the
+// launch was aborted (timeout here or elsewhere).
+__device__ __forceinline__ bool qwait(QCounter* c, uint32_t target, const QueueCtx& ctx) {
+  __shared__ int ok;
+  if (threadIdx.x == 0) {
+    int r = 1;
+    for (int it = 0;; ++it) {
+      const unsigned long long v = __hip_atomic_load(&c->v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (qcount(v, ctx.epoch) >= target) break;
+      if (q_aborted(ctx)) {
+        r = 0;
+        break;
+      }
+      if (it == kQueueSpinLimit) {
+        q_fail(ctx, kErrTimeout);
+        r = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(4);
+    }
+    ok = r;
+  }
+  __syncthreads();
+  const bool res = ok != 0;
+  __syncthreads();  // `ok` is reused by the next wait
+  return res;
+}
+
+// Acquire side: an agent-scope acquire fence (on gfx950: wait for the counter
+// load, then buffer_inv sc1) drops this CU's L1 lines, so the payload loads
+// that follow are served by L2.
+__device__ __forceinline__ void l1_invalidate() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+
+// Release side, workgroup-collective: every store of every wave is complete
+// in L2 once this returns.
+__device__ __forceinline__ void stores_complete() {
+  __builtin_amdgcn_s_waitcnt(kWaitAll);
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Queue payloads
+// ---------------------------------------------------------------------------
+// mgn_fullmlp_pl.cuh:13-21: a queue entry is an [M][D] fp16 tile.
+template <int MBLK, int D>
+struct QueueEntry2D {
+  half_t buf[MBLK][D];
+  __device__ half_t* as_ptr() { return &buf[0][0]; }
+  __device__ TensorView as_view(int rows) { return {as_ptr(), D, rows < 0 ? 0 : (rows > MBLK ? MBLK : rows)}; }
+};
+
+template <typename Entry>
+struct alignas(128) QueueSlot {
+  QCounter full;   // producer commits
+  QCounter empty;  // consumer commits
+  int rows;        // valid rows of the payload
+  char pad[124];
+  Entry data;
+};
+
+// Ring of N slots with NP producers and NC consumers per sequence number
+// (mpmcq.cuh:66-115).  Sequence s lives in slot s % N, round s / N.
+template <typename Entry, int N, int NP = 1, int NC = 1>
+struct RingQueue {
+  using Item = Entry;
+  QueueSlot<Entry> slots[N];
+
+  __device__ QueueSlot<Entry>& slot(int64_t seq) { return slots[seq % N]; }
+
+  // Wait until the slot of `seq` has been drained by the previous round.
+  __device__ Entry* write_wait(int64_t seq, const QueueCtx& ctx) {
+    QueueSlot<Entry>& s = slot(seq);
+    qwait(&s.empty, (uint32_t)(seq / N) * NC, ctx);
+    return &s.data;
+  }
+  __device__ void write_commit(int64_t seq, int rows, const QueueCtx& ctx) {
+    QueueSlot<Entry>& s = slot(seq);
+    if (threadIdx.x == 0) s.rows = rows;
+    stores_complete();
+    if (threadIdx.x == 0) qcommit(&s.full, ctx.epoch);
+  }
+  // Wait until all NP producers of `seq` have committed; returns the payload.
+  __device__ Entry* read_wait(int64_t seq, int* rows, const QueueCtx& ctx) {
+    QueueSlot<Entry>& s = slot(seq);
+    qwait(&s.full, (uint32_t)(seq / N + 1) * NP, ctx);
+    l1_invalidate();
+    *rows = *(volatile int*)&s.rows;
+    return &s.data;
+  }
+  __device__ void read_commit(int64_t seq, const QueueCtx& ctx) {
+    stores_complete();  // this workgroup's loads of the payload have returned
+    if (threadIdx.x == 0) qcommit(&slot(seq).empty, ctx.epoch);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Readers.  Concept: TensorView read_acquire(); void read_release(); void reset().
+// kFromQueue tells a stage that the tile lives in another workgroup's output
+// (the stage then orders its own payload loads after the acquire).
+// ---------------------------------------------------------------------------
+
+// pipes.cuh:7-19.  Walks tiles of `tile_rows` rows: tile i starts at
+// base + i * stride elements; `rows_left` bounds the valid rows.
+struct MemoryReader {
+  static constexpr bool kFromQueue = false;
+  half_t* base;
+  int64_t stride;
+  int tile_stride;
+  int tile_rows;
+  int64_t rows_left0;
+  int64_t row_step;
+  int64_t offset = 0;
+  int64_t rows_left = 0;
+
+  __device__ MemoryReader(half_t* base_, int64_t stride_, int tile_stride_, int tile_rows_ = 1 << 30,
+                          int64_t rows_left_ = int64_t(1) << 62, int64_t row_step_ = 0)
+      : base(base_), stride(stride_), tile_stride(tile_stride_), tile_rows(tile_rows_), rows_left0(rows_left_),
+        row_step(row_step_ ? row_step_ : tile_rows_), rows_left(rows_left_) {}
+
+  __device__ TensorView read_acquire() {
+    const int64_t r = rows_left < tile_rows ? rows_left : tile_rows;
+    return {base + offset, tile_stride, (int)(r > 0 ? r : 0)};
+  }
+  __device__ void read_release() {
+    offset += stride;
+    rows_left -= row_step;
+  }
+  __device__ void reset() {
+    offset = 0;
+    rows_left = rows_left0;
+  }
+};
+
+// pipes.cuh:21-25: the contiguous chunk of pipeline row `row`.
+__device__ inline MemoryReader read_striped_input(half_t* base, int row, int num_iters, int mblk, int d,
+                                                  int64_t total_rows) {
+  const int64_t first = (int64_t)row * num_iters * mblk;
+  return MemoryReader(base + first * d, (int64_t)mblk * d, d, mblk, total_rows - first);
+}
+
+// pipes.cuh:27-31
+struct NullReader {
+  static constexpr bool kFromQueue = false;
+  __device__ TensorView read_acquire() { return {nullptr, 0, 0}; }
+  __device__ void read_release() {}
+  __device__ void reset() {}
+};
+
+// pipes.cuh:33-43
+template <typename QT>
+struct QueueReader {
+  static constexpr bool kFromQueue = true;
+  using Queue = QT;
+  Queue* q;
+  const QueueCtx* ctx;
+  int64_t seq_n = 0;
+
+  __device__ QueueReader(Queue* q_, const QueueCtx* ctx_) : q(q_), ctx(ctx_) {}
+  __device__ TensorView read_acquire() {
+    int rows = 0;
+    auto* e = q->read_wait(seq_n, &rows, *ctx);
+    return e->as_view(rows);
+  }
+  __device__ void read_release() {
+    q->read_commit(seq_n, *ctx);
+    ++seq_n;
+  }
+  __device__ void reset() { seq_n = 0; }
+};
+
+// pipes.cuh:45-58: worker `seq_off` of `seq_stride` takes sequence numbers
+// seq_off, seq_off + seq_stride, ...
+template <typename QT>
+struct SplitQueueReader {
+  static constexpr bool kFromQueue = true;
+  using Queue = QT;
+  Queue* q;
+  const QueueCtx* ctx;
+  int64_t seq_n;
+  int64_t seq_off;
+  int64_t seq_stride;
+
+  __device__ SplitQueueReader(Queue* q_, const QueueCtx* ctx_, int64_t off, int64_t stride)
+      : q(q_), ctx(ctx_), seq_n(off), seq_off(off), seq_stride(stride) {}
+  __device__ TensorView read_acquire() {
+    int rows = 0;
+    auto* e = q->read_wait(seq_n, &rows, *ctx);
+    return e->as_view(rows);
+  }
+  __device__ void read_release() {
+    q->read_commit(seq_n, *ctx);
+    seq_n += seq_stride;
+  }
+  __device__ void reset() { seq_n = seq_off; }
+};
+
+// ---------------------------------------------------------------------------
+// Writers.  Concept: TensorView write_acquire(int rows); void write_release();
+// void reset().  write_acquire takes the number of valid rows being produced.
+// ---------------------------------------------------------------------------
+
+// pipes.cuh:60-72
+struct MemoryWriter {
+  half_t* base;
+  int64_t stride;
+  int tile_stride;
+  int64_t offset = 0;
+  int rows = 0;
+
+  __device__ MemoryWriter(half_t* base_, int64_t stride_, int tile_stride_)
+      : base(base_), stride(stride_), tile_stride(tile_stride_) {}
+  __device__ TensorView write_acquire(int rows_) {
+    rows = rows_;
+    return {base + offset, tile_stride, rows_};
+  }
+  __device__ void write_release() { offset += stride; }
+  __device__ void reset() { offset = 0; }
+};
+
+// pipes.cuh:74-84 (the reference resets the queue in the constructor, :80;
+// epoch-tagged counters make that unnecessary).
+template <typename QT>
+struct QueueWriter {
+  using Queue = QT;
+  Queue* q;
+  const QueueCtx* ctx;
+  int64_t seq_n = 0;
+  int rows = 0;
+
+  __device__ QueueWriter(Queue* q_, const QueueCtx* ctx_) : q(q_), ctx(ctx_) {}
+  __device__ TensorView write_acquire(int rows_) {
+    rows = rows_;
+    return q->write_wait(seq_n, *ctx)->as_view(rows_);
+  }
+  __device__ void write_release() {
+    q->write_commit(seq_n, rows, *ctx);
+    ++seq_n;
+  }
+  __device__ void reset() { seq_n = 0; }
+};
+
+// pipes.cuh:86-102
+template <typename QT>
+struct SplitQueueWriter {
+  using Queue = QT;
+  Queue* q;
+  const QueueCtx* ctx;
+  int64_t seq_n;
+  int64_t seq_off;
+  int64_t seq_stride;
+  int rows = 0;
+
+  __device__ SplitQueueWriter(Queue* q_, const QueueCtx* ctx_, int64_t off, int64_t stride)
+      : q(q_), ctx(ctx_), seq_n(off), seq_off(off), seq_stride(stride) {}
+  __device__ TensorView write_acquire(int rows_) {
+    rows = rows_;
+    return q->write_wait(seq_n, *ctx)->as_view(rows_);
+  }
+  __device__ void write_release() {
+    q->write_commit(seq_n, rows, *ctx);
+    seq_n += seq_stride;
+  }
+  __device__ void reset() { seq_n = seq_off; }
+};
+
+// pipes.cuh:104-108
+struct NullWriter {
+  __device__ TensorView write_acquire(int) { return {nullptr, 0, 0}; }
+  __device__ void write_release() {}
+  __device__ void reset() {}
+};
+
+}  // namespace gp

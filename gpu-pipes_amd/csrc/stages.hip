@@ -1,2 +1,237 @@
-// Stage kernels (pipe_gemm*, pipe_layer_norm, pipe_add, pipe_concat).
+// Stage-level kernels: the library's stage functions run over whole matrices
+// (the reference's bulk-sync building blocks, and its identity pipeline).
+//
+//  * linear_kernel      one pipe_gemm_* stage per workgroup over M rows
+//                       (the bulk-sync GEMM of common/bulksync_gemm.cuh:13-110,
+//                       fp32 accumulation instead of fp16);
+//  * layer_norm_kernel  pipe_layer_norm over M rows (host_layer_norm,
+//                       common/layer_norm_v2.cuh:129-147);
+//  * add_kernel         pipe_add (host_add2, common/elemwise_add.cuh:42-54);
+//  * concat_kernel      pipe_concat (host_concat2, common/concat.cuh:50-69);
+//  * ident_kernel       two-stage pipelines sender -> ring queue -> receiver
+//                       (misc_tests/pipeval/pipe_val_ext.cu:65-149).
+// Workgroups are persistent: workgroup b of G handles tiles b, b+G, ...
+#include <hip/hip_runtime.h>
+
+#include "../../include/gpipes.h"
 #include "gp_host.hpp"
+#include "pipeline.hpp"
+#include "stages.hpp"
+
+namespace gp {
+
+constexpr int MBLK = 128;  // rows per tile, as the reference's mblk
+
+struct TileWalk {
+  int64_t ntiles;
+  int nt;  // tiles of this workgroup
+};
+
+__device__ __forceinline__ TileWalk tile_walk(int64_t M) {
+  const int64_t ntiles = (M + MBLK - 1) / MBLK;
+  const int64_t b = blockIdx.x;
+  return {ntiles, b < ntiles ? (int)((ntiles - 1 - b) / gridDim.x + 1) : 0};
+}
+
+// Reader over this workgroup's tiles of a row-major [M][width] matrix.
+__device__ __forceinline__ MemoryReader tiles_in(const void* base, int64_t M, int width) {
+  const int64_t b = blockIdx.x, G = gridDim.x;
+  return MemoryReader(base ? (half_t*)base + b * MBLK * width : nullptr, G * MBLK * width, width, MBLK, M - b * MBLK,
+                      G * MBLK);
+}
+__device__ __forceinline__ MemoryWriter tiles_out(void* base, int width) {
+  const int64_t b = blockIdx.x, G = gridDim.x;
+  return MemoryWriter((half_t*)base + b * MBLK * width, G * MBLK * width, width);
+}
+
+// Memory reader that yields null views when its base is null (optional
+// accumulator input of pipe_gemm).
+struct OptionalReader : MemoryReader {
+  using MemoryReader::MemoryReader;
+  __device__ TensorView read_acquire() {
+    TensorView v = MemoryReader::read_acquire();
+    if (base == nullptr) v.data = nullptr;
+    return v;
+  }
+};
+
+template <int K, int ACT, bool LN>
+__global__ __launch_bounds__(kStageThreads) void linear_kernel(LinearArgs a) {
+  const TileWalk tw = tile_walk(a.M);
+  if (tw.nt == 0) return;
+  MemoryReader ir = tiles_in(a.x, a.M, K);
+  MemoryReader acc0 = tiles_in(a.acc, a.M, 128);
+  OptionalReader ar(acc0.base, acc0.stride, acc0.tile_stride, acc0.tile_rows, acc0.rows_left0, acc0.row_step);
+  MemoryWriter ow = tiles_out(a.out, 128);
+  const TensorView w{(half_t*)a.w, 128, K}, b{(half_t*)a.b, 1, 1};
+  if constexpr (LN) {
+    const TensorView g{(half_t*)a.gamma, 1, 1}, be{(half_t*)a.beta, 1, 1};
+    pipe_gemm_bias_layer_norm<MBLK, K>(w, b, g, be, a.eps, ir, ar, ow, tw.nt);
+  } else {
+    pipe_gemm_bias_act<MBLK, K, ACT>(w, b, ir, ar, ow, tw.nt);
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kStageThreads) void layer_norm_kernel(const half_t* x, const half_t* gamma,
+                                                                   const half_t* beta, float eps, half_t* out,
+                                                                   int64_t M) {
+  const TileWalk tw = tile_walk(M);
+  if (tw.nt == 0) return;
+  MemoryReader ir = tiles_in(x, M, D);
+  MemoryWriter ow = tiles_out(out, D);
+  pipe_layer_norm<MBLK, D>({(half_t*)gamma, 1, 1}, {(half_t*)beta, 1, 1}, ir, ow, tw.nt, eps);
+}
+
+__global__ __launch_bounds__(kStageThreads) void add_kernel(const half_t* a, const half_t* b, half_t* c, int64_t M,
+                                                            int n) {
+  const TileWalk tw = tile_walk(M);
+  if (tw.nt == 0) return;
+  MemoryReader r0 = tiles_in(a, M, n), r1 = tiles_in(b, M, n);
+  MemoryWriter ow = tiles_out(c, n);
+  pipe_add_n(r0, r1, ow, tw.nt, n);
+}
+
+__global__ __launch_bounds__(kStageThreads) void concat_kernel(const half_t* a, const half_t* b, half_t* c, int64_t M,
+                                                               int n0, int n1) {
+  const TileWalk tw = tile_walk(M);
+  if (tw.nt == 0) return;
+  MemoryReader r0 = tiles_in(a, M, n0), r1 = tiles_in(b, M, n1);
+  MemoryWriter ow = tiles_out(c, n0 + n1);
+  pipe_concat_n(r0, r1, ow, tw.nt, n0, n1);
+}
+
+// ---------------------------------------------------------------------------
+// Identity pipelines: stage 0 copies its tiles of x into a ring queue, stage 1
+// copies them out of the queue into out.  Pipeline g of P moves tiles g, g+P, ...
+// ---------------------------------------------------------------------------
+using IdentEntry = QueueEntry2D<MBLK, 128>;
+using IdentQueue = RingQueue<IdentEntry, 2>;
+
+struct IdentArgs {
+  const half_t* x;
+  half_t* out;
+  int64_t M;
+  PipeCtl* ctl;
+  IdentQueue* queues;
+  QueueCtx ctx;
+  int max_pipes;
+};
+
+__global__ __launch_bounds__(kStageThreads) void ident_kernel(IdentArgs a) {
+  const Role r = assign_role(a.ctl, 2, a.ctx, a.max_pipes);
+  if (r.pipe < 0) return;
+  const int64_t T = (a.M + MBLK - 1) / MBLK, P = r.npipes, g = r.pipe;
+  const int nt = g < T ? (int)((T - 1 - g) / P + 1) : 0;
+  IdentQueue* q = a.queues + g;
+  if (r.stage == 0) {
+    MemoryReader ir((half_t*)a.x + g * MBLK * 128, P * MBLK * 128, 128, MBLK, a.M - g * MBLK, P * MBLK);
+    QueueWriter<IdentQueue> ow(q, &a.ctx);
+    pipe_copy_n(ir, ow, nt, 128);
+  } else {
+    QueueReader<IdentQueue> ir(q, &a.ctx);
+    MemoryWriter ow(a.out + g * MBLK * 128, P * MBLK * 128, 128);
+    pipe_copy_n(ir, ow, nt, 128);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+static int persistent_grid(int64_t M, int num_cus, int per_cu) {
+  const int64_t ntiles = (M + MBLK - 1) / MBLK;
+  const int64_t g = (int64_t)num_cus * per_cu;
+  return (int)(ntiles < g ? ntiles : g);
+}
+
+template <int K, int ACT, bool LN>
+static hipError_t launch_linear(const LinearArgs& a, int num_cus, hipStream_t s) {
+  constexpr int lds = gemm_stage_lds<MBLK, K>() + kGemmParamLds;
+  auto kern = linear_kernel<K, ACT, LN>;
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(persistent_grid(a.M, num_cus, 1)), dim3(kStageThreads), lds, s, a);
+  return hipGetLastError();
+}
+
+template <int K>
+static hipError_t linear_dispatch_k(const LinearArgs& a, int num_cus, hipStream_t s) {
+  if (a.gamma) return launch_linear<K, ACT_NONE, true>(a, num_cus, s);
+  switch (a.act) {
+    case ACT_NONE: return launch_linear<K, ACT_NONE, false>(a, num_cus, s);
+    case ACT_RELU: return launch_linear<K, ACT_RELU, false>(a, num_cus, s);
+    case ACT_GELU_TANH: return launch_linear<K, ACT_GELU_TANH, false>(a, num_cus, s);
+    case ACT_SIGMOID: return launch_linear<K, ACT_SIGMOID, false>(a, num_cus, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t linear_launch(const LinearArgs& a, int num_cus, hipStream_t s) {
+  switch (a.K) {
+    case 128: return linear_dispatch_k<128>(a, num_cus, s);
+    case 256: return linear_dispatch_k<256>(a, num_cus, s);
+    case 384: return linear_dispatch_k<384>(a, num_cus, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t layer_norm_launch(int64_t M, int64_t D, const void* x, const void* gamma, const void* beta, float eps,
+                             void* out, int num_cus, hipStream_t s) {
+  const dim3 grid(persistent_grid(M, num_cus, 4)), block(kStageThreads);
+  const half_t *hx = (const half_t*)x, *hg = (const half_t*)gamma, *hb = (const half_t*)beta;
+  half_t* ho = (half_t*)out;
+  switch (D) {
+    case 128: hipLaunchKernelGGL(layer_norm_kernel<128>, grid, block, 0, s, hx, hg, hb, eps, ho, M); break;
+    case 256: hipLaunchKernelGGL(layer_norm_kernel<256>, grid, block, 0, s, hx, hg, hb, eps, ho, M); break;
+    case 512: hipLaunchKernelGGL(layer_norm_kernel<512>, grid, block, 0, s, hx, hg, hb, eps, ho, M); break;
+    case 1024: hipLaunchKernelGGL(layer_norm_kernel<1024>, grid, block, 0, s, hx, hg, hb, eps, ho, M); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t add_launch(int64_t M, int64_t N, const void* a, const void* b, void* c, int num_cus, hipStream_t s) {
+  hipLaunchKernelGGL(add_kernel, dim3(persistent_grid(M, num_cus, 4)), dim3(kStageThreads), 0, s, (const half_t*)a,
+                     (const half_t*)b, (half_t*)c, M, (int)N);
+  return hipGetLastError();
+}
+
+hipError_t concat_launch(int64_t M, int64_t N0, int64_t N1, const void* a, const void* b, void* c, int num_cus,
+                         hipStream_t s) {
+  hipLaunchKernelGGL(concat_kernel, dim3(persistent_grid(M, num_cus, 4)), dim3(kStageThreads), 0, s,
+                     (const half_t*)a, (const half_t*)b, (half_t*)c, M, (int)N0, (int)N1);
+  return hipGetLastError();
+}
+
+int pipe_ident_run(int64_t M, const void* x, void* out, int max_pipes, int dev, int num_cus, hipStream_t s) {
+  int per_cu = 0;
+  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ident_kernel, kStageThreads, 0);
+  if (e != hipSuccess) return fail_hip(e, "occupancy query");
+  int grid = per_cu * num_cus;
+  if (max_pipes > 0) {
+    // Workgroups are spread round-robin over the XCDs and a pipeline needs
+    // both its workgroups on one XCD: launch whole rounds of kXcdHint * 2.
+    const int64_t rounds = (max_pipes + kXcdHint - 1) / kXcdHint;
+    if (rounds * kXcdHint * 2 < grid) grid = (int)(rounds * kXcdHint * 2);
+  }
+  if (grid < 2) return fail(GP_ERR_NO_DEVICE, "not enough co-resident workgroups for a pipeline");
+  const size_t bytes = sizeof(PipeCtl) + (size_t)(grid / 2) * sizeof(IdentQueue);
+  void* base = nullptr;
+  uint32_t epoch = 0;
+  int rc = arena_acquire(dev, s, bytes, &base, &epoch);
+  if (rc != GP_OK) return rc;
+  IdentArgs a;
+  a.x = (const half_t*)x;
+  a.out = (half_t*)out;
+  a.M = M;
+  a.ctl = (PipeCtl*)base;
+  a.queues = (IdentQueue*)((char*)base + sizeof(PipeCtl));
+  a.ctx = QueueCtx{epoch, &a.ctl->err.v};
+  a.max_pipes = max_pipes;
+  void* args[] = {&a};
+  e = hipLaunchCooperativeKernel((const void*)ident_kernel, dim3(grid), dim3(kStageThreads), args, 0, s);
+  if (e != hipSuccess) return fail_hip(e, "ident_kernel cooperative launch");
+  return GP_OK;
+}
+
+}  // namespace gp

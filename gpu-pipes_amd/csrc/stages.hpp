@@ -1,0 +1,413 @@
+// Pipeline stage functions for gfx950 (workgroup-collective device functions).
+//
+// Reference stages: common/pipe_gemm_bias_relu.cuh:85-192,
+// common/pipe_gemm_bias.cuh:85-191, common/pipe_gemm.cuh:78-183 (GEMM with an
+// accumulator tile from an AccumReader), common/pipe_gemm_bias_layer_norm.cuh:
+// 100-249 (GEMM + bias then LayerNorm in the same block), common/
+// pipe_layer_norm.cuh:13-60 + common/layer_norm_v2.cuh:16-73 (LayerNorm),
+// common/pipe_add.cuh:13-40 and common/pipe_concat.cuh:48-74.  Each stage
+// keeps the reference's calling convention -- (weights, bias, input reader,
+// accumulator reader, output writer, num_iters) -- and loops acquire /
+// compute / release over its tiles.
+//
+// MI355X implementation: a stage runs in a workgroup of 256 threads (four
+// wave64s).  GEMM stages keep the whole weight matrix resident in registers
+// for all tiles (the reference re-streams it through shared memory for every
+// tile, pipe_gemm_bias_relu.cuh:119-124): wave w owns output features
+// [32w, 32w+32) and holds W[:, 32w:32w+32]^T as MFMA A fragments; input
+// tiles are copied into LDS with buffer_load ... lds (XOR-swizzled rows, rows
+// past the tile's valid count zero-filled) and multiplied with
+// v_mfma_f32_32x32x16_f16, accumulating in fp32 (the reference accumulates in
+// fp16, pipe_gemm_bias_relu.cuh:43).  The bias is the accumulator's initial
+// value, the activation / LayerNorm are applied in the epilogue.
+//
+// Dynamic LDS: every stage uses the kernel's dynamic shared memory from
+// offset 0; stage_lds_bytes<...>() gives the requirement.
+#pragma once
+
+#include "gp_device.hpp"
+#include "pipes.hpp"
+
+namespace gp {
+
+enum Act : int { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU_TANH = 2, ACT_SIGMOID = 3 };
+
+__device__ __forceinline__ float apply_act(float v, int act) {
+  if (act == ACT_RELU) return v > 0.f ? v : 0.f;
+  if (act == ACT_GELU_TANH) {
+    const float c = 0.7978845608028654f;  // sqrt(2/pi)
+    return 0.5f * v * (1.f + tanhf(c * (v + 0.044715f * v * v * v)));
+  }
+  if (act == ACT_SIGMOID) return 1.f / (1.f + expf(-v));
+  return v;
+}
+
+__device__ __forceinline__ GP_LDS char* dyn_lds() {
+  extern __shared__ __attribute__((aligned(1024))) char gp_dyn_smem[];
+  return (GP_LDS char*)gp_dyn_smem;
+}
+
+constexpr int kStageThreads = 256;
+constexpr int kSlabStride = 64 * 2 + 16;  // padded LDS row of a transposed 64-k weight slab
+
+// LDS bytes of a GEMM stage with an MBLK x K input tile and N = 128 outputs.
+template <int MBLK, int K>
+constexpr int gemm_stage_lds() {
+  return MBLK * K * 2 > 128 * kSlabStride ? MBLK * K * 2 : 128 * kSlabStride;
+}
+constexpr int kGemmParamLds = 3 * 128 * 4 + 128 * 4 * 8;  // bias/gamma/beta + LN partials (MBLK <= 128)
+
+// Copy rows [0, MBLK) x K halves of a tile view into LDS.  LDS row r holds
+// 16-byte chunk c at chunk position (c & ~15) | ((c ^ r) & 15), so the 16
+// rows read by one ds_read_b128 phase hit 16 different bank groups.  Rows at
+// or past v.rows lie outside the buffer descriptor and arrive as zeros.
+template <int MBLK, int K>
+__device__ __forceinline__ void load_tile_swz(const TensorView& v, GP_LDS char* dst) {
+  static_assert(K % 128 == 0, "K must be a multiple of 128");
+  constexpr int CPR = K / 8;
+  constexpr int NI = MBLK * K * 2 / 1024;
+  static_assert(NI % 4 == 0, "tile must split over four waves");
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int rows = v.rows < MBLK ? (v.rows > 0 ? v.rows : 0) : MBLK;
+  const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(v.data, rows * v.stride * 2);
+#pragma unroll
+  for (int ii = 0; ii < NI / 4; ++ii) {
+    const int i = ii * 4 + wave;
+    const int q = i * kWave + lane;
+    const int r = q / CPR;
+    const int c = (q - r * CPR) ^ (r & 15);
+    dma16_buf(rsrc, r * v.stride * 2 + c * 16, dst + i * 1024);
+  }
+}
+
+// Load a weight matrix W [K][128] (row stride w.stride elements) into MFMA A
+// fragments: wf[s] of wave w, lane l holds W[16s + 8(l/32) + e][32w + l%32].
+// 64-k slabs are transposed through LDS scratch (>= 128 * kSlabStride bytes).
+template <int K>
+__device__ __forceinline__ void load_weight_frags(const TensorView& w, GP_LDS char* scratch, h8 (&wf)[K / 16]) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int lr = lane & 31, lh = lane >> 5;
+#pragma unroll
+  for (int j = 0; j < K / 64; ++j) {
+    // 64 rows x 16 feature octets: wave w copies octets w, w+4, w+8, w+12
+    h8 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = *(const h8*)(w.data + (int64_t)(64 * j + lane) * w.stride + 8 * (wave + 4 * i));
+    __syncthreads();  // previous slab fully read
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        *(GP_LDS half_t*)(scratch + (8 * (wave + 4 * i) + e) * kSlabStride + lane * 2) = v[i][e];
+    __syncthreads();
+#pragma unroll
+    for (int sl = 0; sl < 4; ++sl)
+      wf[4 * j + sl] = *(const GP_LDS h8*)(scratch + (32 * wave + lr) * kSlabStride + (16 * sl + 8 * lh) * 2);
+  }
+  __syncthreads();
+}
+
+// Parameter vectors (fp16 in memory, stride 0 or 1) -> fp32 LDS array.
+__device__ __forceinline__ void load_param(const TensorView& p, GP_LDS float* dst, int n) {
+  for (int i = threadIdx.x; i < n; i += kStageThreads) dst[i] = p.data ? (float)p.data[p.stride ? i : 0] : 0.f;
+}
+
+template <int MBLK, int K, int ACT, bool LN, typename IR, typename AR, typename OW>
+__device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView gamma, TensorView beta, float eps,
+                                IR& ir, AR& ar, OW& ow, int num_iters) {
+  constexpr int N = 128;
+  constexpr int RB = MBLK / 32;
+  static_assert(MBLK % 32 == 0 && MBLK <= 128, "MBLK must be 32, 64, 96 or 128");
+  GP_LDS char* xs = dyn_lds();
+  GP_LDS float* prm = (GP_LDS float*)(xs + gemm_stage_lds<MBLK, K>());
+  GP_LDS f2* lnpart = (GP_LDS f2*)(prm + 3 * N);  // [MBLK][4]
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int lr = lane & 31, lh = lane >> 5;
+  const int fq = 32 * wave + 4 * lh;  // accumulator group g covers features fq + 8g + (0..3)
+
+  h8 wf[K / 16];
+  load_weight_frags<K>(weight, xs, wf);
+  load_param(bias, prm, N);
+  if (LN) {
+    load_param(gamma, prm + N, N);
+    load_param(beta, prm + 2 * N, N);
+  }
+  __syncthreads();
+
+  const int xa = lh ^ (lr & 15);
+  for (int it = 0; it < num_iters; ++it) {
+    const TensorView in = ir.read_acquire();
+    load_tile_swz<MBLK, K>(in, xs);
+    __builtin_amdgcn_s_waitcnt(kWaitAll);
+    __syncthreads();
+    ir.read_release();  // the tile is in LDS: hand the input slot back at once
+
+    // accumulators start at bias (+ the accumulator tile, pipe_gemm.cuh:128-146)
+    f16x acc[RB];
+    const TensorView at = ar.read_acquire();
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[rb][4 * g + e] = prm[fq + 8 * g + e];
+      if (at.data != nullptr) {
+        const int r = 32 * rb + lr;
+        if (r < at.rows) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const h4 a4 = *(const h4*)(at.data + (int64_t)r * at.stride + fq + 8 * g);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[rb][4 * g + e] += (float)a4[e];
+          }
+        }
+      }
+    }
+    ar.read_release();
+
+#pragma unroll
+    for (int s = 0; s < K / 16; ++s) {
+      const int off = ((2 * s) & ~15) * 16 + (((2 * s) ^ xa) & 15) * 16;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const h8 b = *(const GP_LDS h8*)(xs + (32 * rb + lr) * (K * 2) + off);
+        acc[rb] = mfma32(wf[s], b, acc[rb]);
+      }
+    }
+
+    if constexpr (LN) {
+      // per-wave (mean, M2) over 32 features, combined over the four waves
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        float s0 = 0.f;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s0 += acc[rb][v];
+        s0 += xor_lane32(s0);
+        const float m0 = s0 * (1.f / 32.f);
+        float q0 = 0.f;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float d = acc[rb][v] - m0;
+          q0 = __builtin_fmaf(d, d, q0);
+        }
+        q0 += xor_lane32(q0);
+        if (lh == 0) lnpart[(32 * rb + lr) * 4 + wave] = f2{m0, q0};
+      }
+      __syncthreads();
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const GP_LDS f2* pr = lnpart + (32 * rb + lr) * 4;
+        const f2 p0 = pr[0], p1 = pr[1], p2 = pr[2], p3 = pr[3];
+        const float mu = 0.25f * ((p0[0] + p1[0]) + (p2[0] + p3[0]));
+        const float d0 = p0[0] - mu, d1 = p1[0] - mu, d2 = p2[0] - mu, d3 = p3[0] - mu;
+        const float m2 = (p0[1] + p1[1]) + (p2[1] + p3[1]) + 32.f * (d0 * d0 + d1 * d1 + d2 * d2 + d3 * d3);
+        const float rstd = rsqrtf(m2 * (1.f / N) + eps);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int f = fq + 8 * g + e;
+            acc[rb][4 * g + e] = (acc[rb][4 * g + e] - mu) * rstd * prm[N + f] + prm[2 * N + f];
+          }
+      }
+    }
+
+    const TensorView ot = ow.write_acquire(in.rows);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int r = 32 * rb + lr;
+      if (r < ot.rows) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          f4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = LN ? acc[rb][4 * g + e] : apply_act(acc[rb][4 * g + e], ACT);
+          *(h4*)(ot.data + (int64_t)r * ot.stride + fq + 8 * g) = __builtin_convertvector(v, h4);
+        }
+      }
+    }
+    ow.write_release();
+    __syncthreads();  // LDS tile / LN partials are reused by the next iteration
+  }
+}
+
+// pipe_gemm_bias_relu.cuh:85-192: out = relu(in . W + b).
+template <int MBLK, int K, typename IR, typename AR, typename OW>
+__device__ void pipe_gemm_bias_relu(TensorView weight, TensorView bias, IR& ir, AR& ar, OW& ow, int num_iters) {
+  gemm_stage_impl<MBLK, K, ACT_RELU, false>(weight, bias, {}, {}, 0.f, ir, ar, ow, num_iters);
+}
+
+// pipe_gemm_bias.cuh:85-191: out = in . W + b.
+template <int MBLK, int K, typename IR, typename AR, typename OW>
+__device__ void pipe_gemm_bias(TensorView weight, TensorView bias, IR& ir, AR& ar, OW& ow, int num_iters) {
+  gemm_stage_impl<MBLK, K, ACT_NONE, false>(weight, bias, {}, {}, 0.f, ir, ar, ow, num_iters);
+}
+
+// pipe_gemm.cuh:78-183: out = in . W (+ accumulator tile from ar).
+template <int MBLK, int K, typename IR, typename AR, typename OW>
+__device__ void pipe_gemm(TensorView weight, IR& ir, AR& ar, OW& ow, int num_iters) {
+  gemm_stage_impl<MBLK, K, ACT_NONE, false>(weight, {}, {}, {}, 0.f, ir, ar, ow, num_iters);
+}
+
+// Generic activation epilogue (GELU / sigmoid heads of the later apps).
+template <int MBLK, int K, int ACT, typename IR, typename AR, typename OW>
+__device__ void pipe_gemm_bias_act(TensorView weight, TensorView bias, IR& ir, AR& ar, OW& ow, int num_iters) {
+  gemm_stage_impl<MBLK, K, ACT, false>(weight, bias, {}, {}, 0.f, ir, ar, ow, num_iters);
+}
+
+// pipe_gemm_bias_layer_norm.cuh:100-249: out = LayerNorm(in . W + b) * gamma + beta.
+template <int MBLK, int K, typename IR, typename AR, typename OW>
+__device__ void pipe_gemm_bias_layer_norm(TensorView weight, TensorView bias, TensorView gamma, TensorView beta,
+                                          float eps, IR& ir, AR& ar, OW& ow, int num_iters) {
+  gemm_stage_impl<MBLK, K, ACT_NONE, true>(weight, bias, gamma, beta, eps, ir, ar, ow, num_iters);
+}
+
+// ---------------------------------------------------------------------------
+// pipe_layer_norm.cuh:13-60 with layer_norm_v2.cuh:16-73: LayerNorm over D
+// features of each row, fp32 math, fp16 I/O, two-pass variance.  Sixteen
+// lanes share a row (D/16 features each, 16-byte vectors), so one wave
+// covers four rows per step; the reductions are 16-lane butterflies.
+// ---------------------------------------------------------------------------
+template <int MBLK, int D, typename IR, typename OW>
+__device__ void pipe_layer_norm(TensorView gamma, TensorView beta, IR& ir, OW& ow, int num_iters, float eps) {
+  static_assert(D % 128 == 0 && D <= 1024, "D must be a multiple of 128, at most 1024");
+  constexpr int NV = D / 128;  // 16-byte vectors per lane per row
+  const int tid = threadIdx.x;
+  const int g16 = tid & 15;    // lane within the row group
+  const int rsub = tid >> 4;   // row within a 16-row pass
+  float gm[NV][8], bt[NV][8];
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int f = 128 * j + 8 * g16 + e;
+      gm[j][e] = gamma.data ? (float)gamma.data[gamma.stride ? f : 0] : 1.f;
+      bt[j][e] = beta.data ? (float)beta.data[beta.stride ? f : 0] : 0.f;
+    }
+  for (int it = 0; it < num_iters; ++it) {
+    const TensorView in = ir.read_acquire();
+    const TensorView ot = ow.write_acquire(in.rows);
+    for (int r0 = 0; r0 < MBLK; r0 += kStageThreads / 16) {
+      const int r = r0 + rsub;
+      const bool valid = r < in.rows;
+      float x[NV][8];
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        h8 v = {};
+        if (valid) v = *(const h8*)(in.data + (int64_t)r * in.stride + 128 * j + 8 * g16);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          x[j][e] = (float)v[e];
+          s += x[j][e];
+        }
+      }
+#pragma unroll
+      for (int m = 8; m >= 1; m >>= 1) s += __shfl_xor(s, m, 16);
+      const float mean = s * (1.f / D);
+      float q = 0.f;
+#pragma unroll
+      for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = x[j][e] - mean;
+          q = __builtin_fmaf(d, d, q);
+        }
+#pragma unroll
+      for (int m = 8; m >= 1; m >>= 1) q += __shfl_xor(q, m, 16);
+      const float rstd = rsqrtf(q * (1.f / D) + eps);
+      if (valid) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+          h8 o;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = (half_t)((x[j][e] - mean) * rstd * gm[j][e] + bt[j][e]);
+          *(h8*)(ot.data + (int64_t)r * ot.stride + 128 * j + 8 * g16) = o;
+        }
+      }
+    }
+    ir.read_release();
+    ow.write_release();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// pipe_add.cuh:13-40 (elemwise_add.cuh:5-21): c = a + b, n halves per row.
+// fp16 addition of two fp16 values is the correctly rounded real sum, i.e.
+// identical to adding in fp32 and rounding once.
+// ---------------------------------------------------------------------------
+template <typename IR0, typename IR1, typename OW>
+__device__ void pipe_add_n(IR0& ir0, IR1& ir1, OW& ow, int num_iters, int n) {
+  const int vpr = n / 8;  // 16-byte vectors per row
+  for (int it = 0; it < num_iters; ++it) {
+    const TensorView a = ir0.read_acquire();
+    const TensorView b = ir1.read_acquire();
+    const int rows = a.rows < b.rows ? a.rows : b.rows;
+    const TensorView c = ow.write_acquire(rows);
+    for (int i = threadIdx.x; i < rows * vpr; i += kStageThreads) {
+      const int r = i / vpr, v = i - r * vpr;
+      const h8 x = *(const h8*)(a.data + (int64_t)r * a.stride + 8 * v);
+      const h8 y = *(const h8*)(b.data + (int64_t)r * b.stride + 8 * v);
+      *(h8*)(c.data + (int64_t)r * c.stride + 8 * v) = x + y;
+    }
+    ir0.read_release();
+    ir1.read_release();
+    ow.write_release();
+  }
+}
+
+template <int MBLK, int N, typename IR0, typename IR1, typename OW>
+__device__ void pipe_add(IR0& ir0, IR1& ir1, OW& ow, int num_iters) {
+  static_assert(N % 8 == 0, "N must be a multiple of 8");
+  pipe_add_n(ir0, ir1, ow, num_iters, N);
+}
+
+// ---------------------------------------------------------------------------
+// pipe_concat.cuh:48-74 (concat2_internal :6-39): c[r] = [a[r] | b[r]] with
+// 16-byte copies; n0 and n1 halves must be multiples of 8 (pipe_concat.cuh:13-14).
+// ---------------------------------------------------------------------------
+template <typename IR0, typename IR1, typename OW>
+__device__ void pipe_concat_n(IR0& ir0, IR1& ir1, OW& ow, int num_iters, int n0, int n1) {
+  const int v0 = n0 / 8, vo = (n0 + n1) / 8;
+  for (int it = 0; it < num_iters; ++it) {
+    const TensorView a = ir0.read_acquire();
+    const TensorView b = ir1.read_acquire();
+    const int rows = a.rows < b.rows ? a.rows : b.rows;
+    const TensorView c = ow.write_acquire(rows);
+    for (int i = threadIdx.x; i < rows * vo; i += kStageThreads) {
+      const int r = i / vo, v = i - r * vo;
+      const h8 x = v < v0 ? *(const h8*)(a.data + (int64_t)r * a.stride + 8 * v)
+                          : *(const h8*)(b.data + (int64_t)r * b.stride + 8 * (v - v0));
+      *(h8*)(c.data + (int64_t)r * c.stride + 8 * v) = x;
+    }
+    ir0.read_release();
+    ir1.read_release();
+    ow.write_release();
+  }
+}
+
+template <int MBLK, int N0, int N1, typename IR0, typename IR1, typename OW>
+__device__ void pipe_concat(IR0& ir0, IR1& ir1, OW& ow, int num_iters) {
+  static_assert(N0 % 8 == 0 && N1 % 8 == 0, "N0 * 2 and N1 * 2 must be multiples of 16 bytes");
+  pipe_concat_n(ir0, ir1, ow, num_iters, N0, N1);
+}
+
+// Copy stage (the sender / receiver of the reference's identity pipeline,
+// misc_tests/pipeval/pipe_val_ext.cu:65-108): out tile = in tile, n halves per row.
+template <typename IR, typename OW>
+__device__ void pipe_copy_n(IR& ir, OW& ow, int num_iters, int n) {
+  const int vpr = n / 8;
+  for (int it = 0; it < num_iters; ++it) {
+    const TensorView a = ir.read_acquire();
+    const TensorView c = ow.write_acquire(a.rows);
+    for (int i = threadIdx.x; i < a.rows * vpr; i += kStageThreads) {
+      const int r = i / vpr, v = i - r * vpr;
+      *(h8*)(c.data + (int64_t)r * c.stride + 8 * v) = *(const h8*)(a.data + (int64_t)r * a.stride + 8 * v);
+    }
+    ir.read_release();
+    ow.write_release();
+  }
+}
+
+}  // namespace gp

@@ -22,7 +22,9 @@ import torch
 
 __all__ = [
     "lib", "mgn_fullmlp", "mgn_fullmlp_out", "mgn_linears", "mgn_linears_out",
-    "mgn_mlp", "mgn_mlp_out", "IMPL_FUSED", "IMPL_PIPELINED", "GpipesError",
+    "mgn_mlp", "mgn_mlp_out", "IMPL_FUSED", "IMPL_PIPELINED", "IMPL_PIPELINED_SPLIT_LN", "GpipesError",
+    "linear_out", "linear_layer_norm_out", "layer_norm_out", "add_out", "concat_out", "pipe_ident",
+    "pipeline_check", "ACTS",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -31,7 +33,9 @@ LIB_PATH = os.path.join(_HERE, "libgpipes.so")
 GP_OK = 0
 IMPL_FUSED = 0
 IMPL_PIPELINED = 1
-_IMPLS = {"fused": IMPL_FUSED, "pipelined": IMPL_PIPELINED}
+IMPL_PIPELINED_SPLIT_LN = 2
+_IMPLS = {"fused": IMPL_FUSED, "pipelined": IMPL_PIPELINED, "pipelined_split_ln": IMPL_PIPELINED_SPLIT_LN}
+ACTS = {"none": 0, "relu": 1, "gelu_tanh": 2, "sigmoid": 3}
 
 
 class GpipesError(RuntimeError):
@@ -57,6 +61,16 @@ def _load():
     L.gp_mgn_linears_out.restype = i32
     L.gp_mgn_mlp_out.argtypes = [i64, i64] + [vp] * 9 + [f32, vp, i32, vp]
     L.gp_mgn_mlp_out.restype = i32
+    L.gp_linear_out.argtypes = [i64, i64, vp, vp, vp, vp, i32, vp, vp]
+    L.gp_linear_layer_norm_out.argtypes = [i64, i64] + [vp] * 5 + [f32, vp, vp]
+    L.gp_layer_norm_out.argtypes = [i64, i64, vp, vp, vp, f32, vp, vp]
+    L.gp_add_out.argtypes = [i64, i64, vp, vp, vp, vp]
+    L.gp_concat_out.argtypes = [i64, i64, i64, vp, vp, vp, vp]
+    L.gp_pipe_ident.argtypes = [i64, vp, vp, i32, vp]
+    L.gp_pipeline_check.argtypes = [vp]
+    for name in ("gp_linear_out", "gp_linear_layer_norm_out", "gp_layer_norm_out", "gp_add_out",
+                 "gp_concat_out", "gp_pipe_ident", "gp_pipeline_check"):
+        getattr(L, name).restype = i32
     return L
 
 
@@ -154,3 +168,115 @@ def mgn_linears_out(x, w1, b1, w2, b2, w3, b3, out):
 def mgn_linears(x, w1, b1, w2, b2, w3, b3):
     out = torch.zeros((x.shape[0], 128), dtype=x.dtype, device=x.device)
     return mgn_linears_out(x, w1, b1, w2, b2, w3, b3, out)
+
+
+# ---------------------------------------------------------------------------
+# Stage-level operations (one library stage over a whole matrix)
+# ---------------------------------------------------------------------------
+
+def _opt(name, t, shape):
+    if t is None:
+        return None
+    _check_input(name, t, shape)
+    return t
+
+
+def _stream(t):
+    return ctypes.c_void_p(_stream_ptr(t))
+
+
+def linear_out(x, w, b=None, acc=None, act="none", out=None):
+    """out[M,128] = act(x @ w + b [+ acc]) -- pipe_gemm_bias_relu / pipe_gemm_bias / pipe_gemm."""
+    _check_input("x", x)
+    M, K = x.shape
+    _check_input("w", w, (K, 128))
+    _opt("b", b, (128,))
+    _opt("acc", acc, (M, 128))
+    if out is None:
+        out = torch.empty((M, 128), dtype=torch.float16, device=x.device)
+    _check_input("out", out, (M, 128))
+    with torch.cuda.device(x.device):
+        _check(lib.gp_linear_out(M, K, _ptr(x), _ptr(w), _ptr(b), _ptr(acc), ACTS.get(act, act), _ptr(out),
+                                 _stream(x)))
+    return out
+
+
+def linear_layer_norm_out(x, w, b, gamma, beta, eps=1e-5, out=None):
+    """out = LayerNorm(x @ w + b) * gamma + beta -- pipe_gemm_bias_layer_norm."""
+    _check_input("x", x)
+    M, K = x.shape
+    _check_input("w", w, (K, 128))
+    _opt("b", b, (128,))
+    _check_input("gamma", gamma, (128,))
+    _check_input("beta", beta, (128,))
+    if out is None:
+        out = torch.empty((M, 128), dtype=torch.float16, device=x.device)
+    _check_input("out", out, (M, 128))
+    with torch.cuda.device(x.device):
+        _check(lib.gp_linear_layer_norm_out(M, K, _ptr(x), _ptr(w), _ptr(b), _ptr(gamma), _ptr(beta), float(eps),
+                                            _ptr(out), _stream(x)))
+    return out
+
+
+def layer_norm_out(x, gamma=None, beta=None, eps=1e-5, out=None):
+    """LayerNorm over the last dimension (host_layer_norm / pipe_layer_norm)."""
+    _check_input("x", x)
+    M, D = x.shape
+    _opt("gamma", gamma, (D,))
+    _opt("beta", beta, (D,))
+    if out is None:
+        out = torch.empty_like(x)
+    _check_input("out", out, (M, D))
+    with torch.cuda.device(x.device):
+        _check(lib.gp_layer_norm_out(M, D, _ptr(x), _ptr(gamma), _ptr(beta), float(eps), _ptr(out), _stream(x)))
+    return out
+
+
+def add_out(a, b, out=None):
+    """c = a + b (host_add2 / pipe_add)."""
+    _check_input("a", a)
+    M, N = a.shape
+    _check_input("b", b, (M, N))
+    if out is None:
+        out = torch.empty_like(a)
+    _check_input("out", out, (M, N))
+    with torch.cuda.device(a.device):
+        _check(lib.gp_add_out(M, N, _ptr(a), _ptr(b), _ptr(out), _stream(a)))
+    return out
+
+
+def concat_out(a, b, out=None):
+    """c = [a | b] row-wise (host_concat2 / pipe_concat)."""
+    _check_input("a", a)
+    M, N0 = a.shape
+    _check_input("b", b)
+    if b.shape[0] != M:
+        raise RuntimeError("a and b must have the same number of rows")
+    N1 = b.shape[1]
+    if out is None:
+        out = torch.empty((M, N0 + N1), dtype=a.dtype, device=a.device)
+    _check_input("out", out, (M, N0 + N1))
+    with torch.cuda.device(a.device):
+        _check(lib.gp_concat_out(M, N0, N1, _ptr(a), _ptr(b), _ptr(out), _stream(a)))
+    return out
+
+
+def pipe_ident(x, max_pipes=0, out=None):
+    """Copy x[M,128] through ring-queue pipelines (the reference's pipeval ident)."""
+    _check_input("x", x)
+    M, D = x.shape
+    if D != 128:
+        raise RuntimeError("pipe_ident moves 128-wide rows")
+    if out is None:
+        out = torch.zeros_like(x)
+    _check_input("out", out, (M, D))
+    with torch.cuda.device(x.device):
+        _check(lib.gp_pipe_ident(M, _ptr(x), _ptr(out), int(max_pipes), _stream(x)))
+    return out
+
+
+def pipeline_check(device=None):
+    """Wait for the current stream; raise GpipesError if its last pipelined launch timed out."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    with torch.cuda.device(dev):
+        _check(lib.gp_pipeline_check(ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))

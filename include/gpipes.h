@@ -28,12 +28,23 @@ extern "C" {
 #define GP_ERR_SHAPE (-2)       /* a dimension the kernels do not support      */
 #define GP_ERR_ALIGN (-3)       /* pointer not 16-byte aligned                 */
 #define GP_ERR_HIP (-4)         /* HIP runtime / launch failure                */
-#define GP_ERR_TIMEOUT (-5)     /* a queue wait exceeded its spin bound        */
+#define GP_ERR_TIMEOUT (-5)     /* a pipelined launch failed on the device: a   */
+                                /* queue wait exceeded its spin bound, or no    */
+                                /* pipeline fitted on one XCD                   */
 #define GP_ERR_NO_DEVICE (-6)   /* no usable gfx950 device                     */
 
 /* Implementation selector for gp_mgn_mlp_out. */
-#define GP_IMPL_FUSED 0     /* persistent fused kernel (default, fastest)   */
-#define GP_IMPL_PIPELINED 1 /* stage-chained kernel with L2 ring queues      */
+#define GP_IMPL_FUSED 0              /* persistent fused kernel (default, fastest)        */
+#define GP_IMPL_PIPELINED 1          /* stage workgroups linked by L2 ring queues;         */
+                                     /* layer 3 and LayerNorm fused in one stage            */
+#define GP_IMPL_PIPELINED_SPLIT_LN 2 /* the reference's layout: layer 3 feeds five         */
+                                     /* LayerNorm workers through a round-robin split queue */
+
+/* Activations of gp_linear_out. */
+#define GP_ACT_NONE 0
+#define GP_ACT_RELU 1
+#define GP_ACT_GELU_TANH 2
+#define GP_ACT_SIGMOID 3
 
 /* Library version as 0xMMmmpp. */
 int gp_version(void);
@@ -64,7 +75,8 @@ int gp_mgn_linears_out(int64_t M, const void* x, const void* w1, const void* b1,
 /*
  * Generic MGN-shaped MLP (common/mlps.py:3-20, MgnMlp(K, [128,128,128],
  * layernorm=gamma!=NULL)): K in {128, 256, 384}; gamma == NULL (and beta ==
- * NULL) skips the LayerNorm.  `impl` is GP_IMPL_FUSED or GP_IMPL_PIPELINED.
+ * NULL) skips the LayerNorm.  `impl` is one of GP_IMPL_*.  The pipelined
+ * implementations report a queue-wait timeout through gp_pipeline_check().
  * The node MLP of MeshGraphNet is K = 256.  Both entry points above are this
  * call with K = 384.
  */
@@ -72,6 +84,69 @@ int gp_mgn_mlp_out(int64_t M, int64_t K, const void* x, const void* w1, const vo
                    const void* w2, const void* b2, const void* w3, const void* b3,
                    const void* gamma, const void* beta, float eps, void* out, int impl,
                    void* stream);
+
+/* ------------------------------------------------------------------------
+ * Stage-level entry points: one stage function of the library run over a
+ * whole matrix (tiles of 128 rows, persistent workgroups).
+ * ------------------------------------------------------------------------ */
+
+/*
+ * out[M,128] = act(x[M,K] . w[K,128] + b [+ acc[M,128]]), fp32 accumulation.
+ * K in {128, 256, 384}; b and acc may be NULL; act is GP_ACT_*.
+ * The stage of common/pipe_gemm_bias_relu.cuh:85-192 (act = RELU),
+ * common/pipe_gemm_bias.cuh:85-191 (act = NONE) and common/pipe_gemm.cuh:78-183
+ * (acc = the AccumReader tile, b = NULL); as a whole-matrix call it also
+ * replaces bulksync_gemm<M,N,K,RELU>, common/bulksync_gemm.cuh:13-110.
+ */
+int gp_linear_out(int64_t M, int64_t K, const void* x, const void* w, const void* b, const void* acc, int act,
+                  void* out, void* stream);
+
+/*
+ * out = LayerNorm(x . w + b) * gamma + beta over the 128 outputs: the stage
+ * intended by common/pipe_gemm_bias_layer_norm.cuh:100-249.
+ */
+int gp_linear_layer_norm_out(int64_t M, int64_t K, const void* x, const void* w, const void* b,
+                             const void* gamma, const void* beta, float eps, void* out, void* stream);
+
+/*
+ * out[M,D] = LayerNorm(x[M,D]) * gamma + beta, biased variance, eps as given;
+ * D in {128, 256, 512, 1024}; gamma / beta NULL mean 1 / 0.
+ * Replaces host_layer_norm<D>(M, x, gamma, beta, out),
+ * common/layer_norm_v2.cuh:129-147 (the pipe_layer_norm stage,
+ * common/pipe_layer_norm.cuh:13-60).
+ */
+int gp_layer_norm_out(int64_t M, int64_t D, const void* x, const void* gamma, const void* beta, float eps,
+                      void* out, void* stream);
+
+/*
+ * c[M,N] = a + b elementwise; N a multiple of 8.  Replaces host_add2,
+ * common/elemwise_add.cuh:42-54 (the pipe_add stage, common/pipe_add.cuh:13-40).
+ */
+int gp_add_out(int64_t M, int64_t N, const void* a, const void* b, void* c, void* stream);
+
+/*
+ * c[M,N0+N1] = [a[M,N0] | b[M,N1]] row-wise; N0, N1 multiples of 8.
+ * Replaces host_concat2, common/concat.cuh:50-69 (the pipe_concat stage,
+ * common/pipe_concat.cuh:48-74).
+ */
+int gp_concat_out(int64_t M, int64_t N0, int64_t N1, const void* a, const void* b, void* c, void* stream);
+
+/*
+ * Identity pipelines: sender workgroups copy 128-row tiles of x[M,128] into
+ * ring queues, receiver workgroups copy them out to out[M,128].  At most
+ * max_pipes pipelines (<= 0: as many as fit).  The queue round trip of
+ * misc_tests/pipeval/pipe_val_ext.cu:65-149 (ident).
+ */
+int gp_pipe_ident(int64_t M, const void* x, void* out, int max_pipes, void* stream);
+
+/*
+ * Waits for `stream`, then reports whether the last pipelined launch on it
+ * (GP_IMPL_PIPELINED*, gp_pipe_ident) failed on the device (GP_ERR_TIMEOUT: a
+ * queue wait timed out, or no pipeline's workgroups shared an XCD) or
+ * completed (GP_OK).  The reference has no such check:
+ * a stuck queue spins forever (common/mpmcq.cuh:83,104).
+ */
+int gp_pipeline_check(void* stream);
 
 #ifdef __cplusplus
 }
