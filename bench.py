@@ -8,7 +8,7 @@ with HIP events on the launch stream, and the CPU oracle timed on a bounded
 sample on the host cores.
 
   python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--workload edge|node]
-                  [--impl fused|pipelined] [--no-cpu]
+                  [--impl fused|pipelined|pipelined_split_ln] [--no-cpu]
 """
 import argparse
 import json
@@ -84,7 +84,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="edge")
-    ap.add_argument("--impl", choices=["fused", "pipelined"], default="fused")
+    ap.add_argument("--impl", choices=["fused", "pipelined", "pipelined_split_ln"], default="fused")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-ref", action="store_true",
                     help="first run one plain 1 GiB device copy (a known-size reference kernel "
