@@ -1,11 +1,12 @@
 """Benchmark of the MGN MLP hot path on one MI355X.
 
 A step is one call of the fused edge MLP (384->128->128->128 + LayerNorm,
-fp16 I/O, fp32 accumulate) over the full BASELINE batch M = 1,048,576 with
-all inputs already resident in HBM.  Prints ONE JSON line (see README of the
-driver contract): rows/s, the HBM-roofline fraction of the kernel measured
-with HIP events on the launch stream, and the CPU oracle timed on a bounded
-sample on the host cores.
+fp16 I/O, fp32 accumulate) over the full headline batch M = 1,048,576 with
+all inputs already resident in HBM.  Prints ONE JSON line: rows/s, the
+HBM-roofline fraction of the kernel measured with HIP events on the launch
+stream, the HBM traffic per launch measured with rocprofv3 counters
+(profiles/traffic.json), and the CPU oracle timed on a bounded sample on the
+host cores.
 
   python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--workload edge|node]
                   [--impl fused|pipelined|pipelined_split_ln] [--no-cpu]

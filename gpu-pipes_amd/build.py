@@ -3,6 +3,7 @@
 Both are compiled in-tree so the shared objects travel with the source tree:
   gpu-pipes_amd/gpipes/libgpipes.so   HIP kernels + C ABI (include/gpipes.h)
   oracle/liboracle.so                 CPU restatement used only by tests/bench
+  gpu-pipes_amd/apps/mgn_mlp_cc       C++ driver of the operator (links libgpipes.so)
 
 Usage: python gpu-pipes_amd/build.py [--verbose]
 """
@@ -74,8 +75,23 @@ def build_oracle(verbose=False):
     return ORACLE_LIB
 
 
+APPS = ["mgn_mlp_cc"]
+
+
+def build_apps(verbose=False):
+    outs = []
+    for app in APPS:
+        exe = os.path.join(PKG, "apps", app)
+        _run([HIPCC, "-O2", "-std=c++17", os.path.join(PKG, "apps", app + ".cpp"), "-o", exe + ".tmp",
+              "-L" + os.path.dirname(LIB), "-lgpipes", "-Wl,-rpath,$ORIGIN/../gpipes"], verbose)
+        os.replace(exe + ".tmp", exe)
+        outs.append(exe)
+    return outs
+
+
 def build(verbose=False):
-    return build_library(verbose), build_oracle(verbose)
+    lib = build_library(verbose)
+    return lib, build_oracle(verbose), build_apps(verbose)
 
 
 if __name__ == "__main__":

@@ -1,0 +1,91 @@
+/*
+ * gpipes.hpp -- C++ wrappers over the C ABI of gpipes.h with the reference's
+ * operator names and argument order.
+ *
+ * The reference's host entry points are functions such as
+ *   void mgn_fullmlp_out(x, w1, b1, w2, b2, w3, b3, gamma, beta, out)
+ * (apps/mgn_fullmlp/pipelined/mgn_fullmlp_pl_ext.cu:24-71) that report errors
+ * by throwing (TORCH_CHECK).  These wrappers keep that shape for C++ callers
+ * that hold raw device pointers: the row count comes first, the stream last
+ * (default: the null stream), and a failing call throws gpipes::Error with
+ * the library's message.  Header-only; link against libgpipes.so.
+ */
+#ifndef GPIPES_HPP
+#define GPIPES_HPP
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "gpipes.h"
+
+namespace gpipes {
+
+class Error : public std::runtime_error {
+ public:
+  Error(int code, const std::string& what) : std::runtime_error(what), code_(code) {}
+  int code() const { return code_; }
+
+ private:
+  int code_;
+};
+
+inline void check(int rc) {
+  if (rc != GP_OK) throw Error(rc, "gpipes error " + std::to_string(rc) + ": " + gp_last_error());
+}
+
+// mgn_fullmlp_pl_ext.cu:24-71
+inline void mgn_fullmlp_out(int64_t M, const void* x, const void* w1, const void* b1, const void* w2, const void* b2,
+                            const void* w3, const void* b3, const void* gamma, const void* beta, void* out,
+                            void* stream = nullptr) {
+  check(gp_mgn_fullmlp_out(M, x, w1, b1, w2, b2, w3, b3, gamma, beta, out, stream));
+}
+
+// mgn_linears_pl_ext.cu:24-66
+inline void mgn_linears_out(int64_t M, const void* x, const void* w1, const void* b1, const void* w2, const void* b2,
+                            const void* w3, const void* b3, void* out, void* stream = nullptr) {
+  check(gp_mgn_linears_out(M, x, w1, b1, w2, b2, w3, b3, out, stream));
+}
+
+// common/mlps.py:3-20, MgnMlp(K, [128, 128, 128], layernorm = gamma != nullptr)
+inline void mgn_mlp_out(int64_t M, int64_t K, const void* x, const void* w1, const void* b1, const void* w2,
+                        const void* b2, const void* w3, const void* b3, const void* gamma, const void* beta, void* out,
+                        float eps = 1e-5f, int impl = GP_IMPL_FUSED, void* stream = nullptr) {
+  check(gp_mgn_mlp_out(M, K, x, w1, b1, w2, b2, w3, b3, gamma, beta, eps, out, impl, stream));
+}
+
+// common/pipe_gemm_bias_relu.cuh:85-192, pipe_gemm_bias.cuh:85-191, pipe_gemm.cuh:78-183
+inline void linear_out(int64_t M, int64_t K, const void* x, const void* w, const void* b, const void* acc, int act,
+                       void* out, void* stream = nullptr) {
+  check(gp_linear_out(M, K, x, w, b, acc, act, out, stream));
+}
+
+// common/pipe_gemm_bias_layer_norm.cuh:100-249
+inline void linear_layer_norm_out(int64_t M, int64_t K, const void* x, const void* w, const void* b, const void* gamma,
+                                  const void* beta, float eps, void* out, void* stream = nullptr) {
+  check(gp_linear_layer_norm_out(M, K, x, w, b, gamma, beta, eps, out, stream));
+}
+
+// common/layer_norm_v2.cuh:129-147 (host_layer_norm)
+inline void layer_norm_out(int64_t M, int64_t D, const void* x, const void* gamma, const void* beta, float eps,
+                           void* out, void* stream = nullptr) {
+  check(gp_layer_norm_out(M, D, x, gamma, beta, eps, out, stream));
+}
+
+// common/elemwise_add.cuh:42-54 (host_add2)
+inline void add_out(int64_t M, int64_t N, const void* a, const void* b, void* c, void* stream = nullptr) {
+  check(gp_add_out(M, N, a, b, c, stream));
+}
+
+// common/concat.cuh:50-69 (host_concat2)
+inline void concat_out(int64_t M, int64_t N0, int64_t N1, const void* a, const void* b, void* c,
+                       void* stream = nullptr) {
+  check(gp_concat_out(M, N0, N1, a, b, c, stream));
+}
+
+// Waits for `stream` and throws if its last pipelined launch failed on the device.
+inline void pipeline_check(void* stream = nullptr) { check(gp_pipeline_check(stream)); }
+
+}  // namespace gpipes
+
+#endif  // GPIPES_HPP

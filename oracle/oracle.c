@@ -7,10 +7,11 @@
  * loads or calls it.  Only tests/, __graft_entry__.smoke() and bench.py's
  * cpu_baseline leg may use it.
  *
- * Every function names the reference lines it follows.  How each one is pinned
- * (closed forms, torch.nn library modules, float64 brute force, the reference's
- * literal LayerNorm row) is described in oracle/README.md and checked by
- * tests/test_oracle.py.
+ * Every function names the reference lines it follows.  Each one is pinned by
+ * tests/test_oracle.py against checks that do not retype its formula: numpy's
+ * binary16 conversion over all 65536 patterns, torch.nn library modules in
+ * float64, closed forms, the reference's literal LayerNorm row, and planted
+ * mistakes that must fail.
  */
 #include "oracle.h"
 
@@ -92,7 +93,7 @@ static float act_apply(float v, int act) {
   switch (act) {
     case ORACLE_ACT_RELU: /* torch.nn.ReLU, common/mlps.py:9-11 */
       return v > 0.f ? v : 0.f;
-    case ORACLE_ACT_GELU_TANH: { /* GELU(approximate='tanh'), BASELINE config 2 */
+    case ORACLE_ACT_GELU_TANH: { /* GELU(approximate='tanh'), the BERT FFN activation */
       const float c = 0.7978845608028654f; /* sqrt(2/pi) */
       return 0.5f * v * (1.f + tanhf(c * (v + 0.044715f * v * v * v)));
     }
@@ -108,8 +109,8 @@ static float act_apply(float v, int act) {
  * The reference feeds nn.Linear.weight.t().contiguous() as W
  * (apps/mgn_fullmlp/pipelined/val.py:17-19) and applies the epilogue
  * relu(acc + b) (common/pipe_gemm_bias_relu.cuh:173-188) or acc + b
- * (common/pipe_gemm_bias.cuh:32-37).  Accumulation is fp32 here, as BASELINE
- * requires (the reference GPU path accumulates in fp16,
+ * (common/pipe_gemm_bias.cuh:32-37).  Accumulation is fp32 here, as the parity bar
+ * assumes (the reference GPU path accumulates in fp16,
  * common/pipe_gemm_bias_relu.cuh:43).
  */
 void oracle_linear(int64_t M, int64_t K, int64_t N, const float* x, const float* w, const float* b,

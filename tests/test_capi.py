@@ -78,3 +78,32 @@ def test_python_mirror_rejects_cpu_and_bad_tensors():
         gpipes.mgn_fullmlp(x, w1, b, w, b, w, b, b, b)
     with pytest.raises(RuntimeError):
         gpipes.mgn_linears(torch.zeros(4, 256, dtype=torch.float16), w1, b, w, b, w, b)
+
+
+def test_cpp_wrappers_throw_with_message(tmp_path):
+    """include/gpipes.hpp: the reference-named C++ wrappers turn a negative
+    status into gpipes::Error carrying the library's message (no GPU needed:
+    the arguments are rejected before any device call)."""
+    import subprocess
+    src = tmp_path / "t.cpp"
+    src.write_text(r'''
+#include <cstdio>
+#include "gpipes.hpp"
+int main() {
+  try {
+    gpipes::mgn_fullmlp_out(16, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
+  } catch (const gpipes::Error& e) {
+    std::printf("%d|%s\n", e.code(), e.what());
+    return 0;
+  }
+  return 1;
+}
+''')
+    exe = tmp_path / "t"
+    libdir = os.path.dirname(gpipes.LIB_PATH)
+    subprocess.run(["g++", "-std=c++17", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe),
+                    "-L", libdir, "-lgpipes", f"-Wl,-rpath,{libdir}"], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    code, msg = r.stdout.strip().split("|", 1)
+    assert int(code) < 0 and "gpipes error" in msg

@@ -1,7 +1,7 @@
 """GPU parity of the MGN MLP kernels against the CPU oracle (oracle/oracle.c).
 
 Bar (fp16 I/O, fp32 accumulate): max-abs <= 2e-2 and relative-L2 <= 5e-3
-against the fp32 oracle on identical fp16-rounded inputs.  At full BASELINE
+against the fp32 oracle on identical fp16-rounded inputs.  At the full headline
 size the oracle checks a row sample, and size-independent properties cover
 every row: permutation equivariance (bit-exact), per-row LayerNorm moments,
 determinism, and untouched memory past the output.
@@ -67,7 +67,7 @@ def test_random_shapes(cuda, K, ln, M):
 
 
 def test_config0_shape(cuda):
-    """edge MLP, M = 16384, gamma = 1, beta = 0."""
+    """The CPU-reference shape: edge MLP, M = 16384, gamma = 1, beta = 0."""
     M, K = 16384, 384
     p = mgn_params(K, seed=0)
     x = normal_fp16(M, K, seed=0)
@@ -115,7 +115,7 @@ def test_nondefault_stream_and_repeat(cuda):
 
 @pytest.mark.parametrize("which", ["edge", "node"])
 def test_full_size_sampled_and_invariants(cuda, which):
-    """BASELINE config 1 sizes: edge M=1,048,576 K=384; node M=262,144 K=256."""
+    """Headline sizes: edge M=1,048,576 K=384; node M=262,144 K=256."""
     M, K = (1048576, 384) if which == "edge" else (262144, 256)
     p = to_dev(mgn_params(K, seed=11), cuda)
     x = normal_fp16(M, K, seed=12, device=cuda)

@@ -62,7 +62,7 @@ def test_split_needs_layernorm(cuda):
 
 @pytest.mark.parametrize("impl", IMPLS)
 def test_full_size_edge(cuda, impl):
-    """BASELINE config 1 size through the queue pipelines: sampled rows vs the
+    """Headline edge size through the queue pipelines: sampled rows vs the
     oracle, and a second launch bit-identical to the first (the tile-to-pipeline
     assignment may change between launches; the per-row arithmetic may not)."""
     M, K = 1048576, 384
