@@ -12,8 +12,9 @@
 //  * Stage A (waves 0-3, one per SIMD): layer 1.  Wave n keeps the W1 slice
 //    for output features [32n, 32n+32) resident in AGPRs (K/16 MFMA A
 //    fragments), streams X tiles HBM->LDS with buffer_load ... lds (16 B per
-//    lane, whole 1 KiB wave transactions, double-buffered, XOR-swizzled so
-//    the MFMA B-operand reads are bank-conflict free), and writes
+//    lane, whole 1 KiB wave transactions, non-temporal so the stream does not
+//    evict L2, double-buffered, XOR-swizzled so the MFMA B-operand reads are
+//    bank-conflict free), and writes
 //    relu(X W1 + b1) in fp16 to one of two LDS handoff tiles.
 //  * Stage B (waves 4-7, one per SIMD): layers 2 and 3 plus LayerNorm.  Layer
 //    2 is split by feature (wave r computes features [32r, 32r+32) of all 64
@@ -45,6 +46,8 @@ constexpr int NWAVES = 8;       // 4 layer-1 waves + 4 layer-2/3/LN waves
 constexpr int NTHREADS = NWAVES * kWave;
 constexpr int ACT_STRIDE = D * 2 + 16;   // padded LDS row (bytes) of a 128-wide fp16 tile
 constexpr int SLAB_STRIDE = 64 * 2 + 16; // padded LDS row (bytes) of a transposed 64-k weight slab
+constexpr int PF_L1 = 4;                 // layer-1 B-fragment prefetch depth (k-steps)
+constexpr int PF_L2 = 2;                 // layer-2 B-fragment prefetch depth (k-steps)
 
 template <int K>
 struct Cfg {
@@ -97,21 +100,31 @@ __device__ __forceinline__ f16x bias_frag(const float* bias, int fq) {
 }
 
 // Two 32-row blocks sharing the A operand (weight fragments wf[0..KS)); B
-// fragments come from LDS through ld(rb, s), fetched two k-steps ahead.
-template <int KS, typename LD>
+// fragments come from LDS through ld(rb, s), fetched PF k-steps ahead.  The
+// scheduling barriers fix the issue order (2*PF reads, then per k-step two
+// MFMAs followed by the two reads of step s + PF), so 2*PF LDS reads stay in
+// flight behind every MFMA instead of the one or two the default schedule
+// leaves.  NPRE counts LDS reads the caller issues just before (the bias
+// fragments), which the scheduler places in the first group.
+template <int KS, int PF, int NPRE, typename LD>
 __device__ __forceinline__ void gemm_2blk(const h8* wf, LD ld, f16x& acc0, f16x& acc1) {
-  h8 q0[2], q1[2];
-  q0[0] = ld(0, 0);
-  q1[0] = ld(1, 0);
-  q0[1] = ld(0, 1);
-  q1[1] = ld(1, 1);
+  static_assert(PF >= 1 && PF <= KS, "prefetch depth");
+  h8 q0[PF], q1[PF];
+#pragma unroll
+  for (int p = 0; p < PF; ++p) {
+    q0[p] = ld(0, p);
+    q1[p] = ld(1, p);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x100, 2 * PF + NPRE, 0);
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    acc0 = mfma32(wf[s], q0[s & 1], acc0);
-    acc1 = mfma32(wf[s], q1[s & 1], acc1);
-    if (s + 2 < KS) {
-      q0[s & 1] = ld(0, s + 2);
-      q1[s & 1] = ld(1, s + 2);
+    acc0 = mfma32(wf[s], q0[s % PF], acc0);
+    acc1 = mfma32(wf[s], q1[s % PF], acc1);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    if (s + PF < KS) {
+      q0[s % PF] = ld(0, s + PF);
+      q1[s % PF] = ld(1, s + PF);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
   }
 }
@@ -264,7 +277,7 @@ void mgn_fused_kernel(Params p) {
       const int64_t left = (M - row0) * (K * 2);
       const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(p.x + row0 * K, left < C::XTILE ? (int)left : C::XTILE);
 #pragma unroll
-      for (int ii = 0; ii < C::DMA_PER_WAVE; ++ii) dma16_buf(rsrc, voff[ii], buf + (ii * 4 + n) * 1024);
+      for (int ii = 0; ii < C::DMA_PER_WAVE; ++ii) dma16_buf_nt(rsrc, voff[ii], buf + (ii * 4 + n) * 1024);
     };
     issue(0, (GP_LDS char*)xs0);
 
@@ -281,7 +294,7 @@ void mgn_fused_kernel(Params p) {
       if (k + 1 < nt) issue(k + 1, xnext);
 
       f16x acc0 = bias_frag(prm[0], fq), acc1 = acc0;
-      gemm_2blk<C::KS1>(w1f, [&](int rb, int s) {
+      gemm_2blk<C::KS1, PF_L1, 4>(w1f, [&](int rb, int s) {
         const int off = ((2 * s) & ~15) * 16 + (((2 * s) ^ xa) & 15) * 16;
         return *(const GP_LDS h8*)(xs + xrow + rb * (32 * K * 2) + off);
       }, acc0, acc1);
@@ -326,12 +339,17 @@ void mgn_fused_kernel(Params p) {
 
     const int xrow3 = (16 * n + l16) * ACT_STRIDE;  // this lane's layer-3 row in act2
 
+    // Each SIMD runs one A and one B wave.  B is the consumer and carries
+    // the waits of the layer-2 -> layer-3 exchange: giving it issue priority
+    // keeps the four B waves in step, and A fills the gaps.
+    __builtin_amdgcn_s_setprio(1);
+
     auto tile_b = [&](GP_LDS char* hand, int k) {
       lds_wait_geq((GP_LDS int*)&sy.h_full, 4 * (k + 1), ab);
 
       // layer 2, features [32n, 32n+32) of all 64 rows, from the handoff tile
       f16x acc0 = bias_frag(prm[1], fq), acc1 = acc0;
-      gemm_2blk<D / 16>(w2f, [&](int rb, int s) {
+      gemm_2blk<D / 16, PF_L2, 4>(w2f, [&](int rb, int s) {
         return *(const GP_LDS h8*)(hand + (rb ? arow1 : arow0) + (2 * s + lh) * 16);
       }, acc0, acc1);
       lds_signal((GP_LDS int*)&sy.h_free, lane);  // B operands are in registers: release the slot
