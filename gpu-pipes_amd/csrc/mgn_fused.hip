@@ -106,9 +106,9 @@ __device__ __forceinline__ f16x bias_frag(const float* bias, int fq) {
 // flight behind every MFMA instead of the one or two the default schedule
 // leaves.  NPRE counts LDS reads the caller issues just before (the bias
 // fragments), which the scheduler places in the first group.
-template <int KS, int PF, int NPRE, typename LD>
-__device__ __forceinline__ void gemm_2blk(const h8* wf, LD ld, f16x& acc0, f16x& acc1) {
-  static_assert(PF >= 1 && PF <= KS, "prefetch depth");
+template <int KS, int PF, int NPRE, int NHOOK, typename LD, typename HOOK>
+__device__ __forceinline__ void gemm_2blk(const h8* wf, LD ld, f16x& acc0, f16x& acc1, HOOK hook) {
+  static_assert(PF >= 1 && PF <= KS && NHOOK <= KS, "prefetch depth / hook steps");
   h8 q0[PF], q1[PF];
 #pragma unroll
   for (int p = 0; p < PF; ++p) {
@@ -126,7 +126,16 @@ __device__ __forceinline__ void gemm_2blk(const h8* wf, LD ld, f16x& acc0, f16x&
       q1[s % PF] = ld(1, s + PF);
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
+    if (s < NHOOK) {
+      hook(s);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
   }
+}
+
+template <int KS, int PF, int NPRE, typename LD>
+__device__ __forceinline__ void gemm_2blk(const h8* wf, LD ld, f16x& acc0, f16x& acc1) {
+  gemm_2blk<KS, PF, NPRE, 0>(wf, ld, acc0, acc1, [](int) {});
 }
 
 // ReLU + fp16 rounding of an accumulator into this lane's row of an LDS
@@ -272,10 +281,16 @@ void mgn_fused_kernel(Params p) {
       const int c = (q - r * C::CPR) ^ (r & 15);
       voff[ii] = (r * K + c * 8) * 2;
     }
-    auto issue = [&](int k, GP_LDS char* buf) {
+    // Descriptor of tile k (empty past the last tile: a copy through it
+    // writes zeros to LDS without touching memory).
+    auto tile_rsrc = [&](int k) {
       const int64_t row0 = (t0 + (int64_t)k * G) * TM;
       const int64_t left = (M - row0) * (K * 2);
-      const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(p.x + row0 * K, left < C::XTILE ? (int)left : C::XTILE);
+      const int bytes = left <= 0 ? 0 : (left < C::XTILE ? (int)left : C::XTILE);
+      return make_rsrc(p.x + (left > 0 ? row0 * K : 0), bytes);
+    };
+    auto issue = [&](int k, GP_LDS char* buf) {
+      const __amdgpu_buffer_rsrc_t rsrc = tile_rsrc(k);
 #pragma unroll
       for (int ii = 0; ii < C::DMA_PER_WAVE; ++ii) dma16_buf_nt(rsrc, voff[ii], buf + (ii * 4 + n) * 1024);
     };
@@ -291,13 +306,14 @@ void mgn_fused_kernel(Params p) {
       // refilled with X(k+1) at once.
       wait_vmcnt<0>();
       group_barrier((GP_LDS int*)&sy.a_bar, abar, 4, lane, ab);
-      if (k + 1 < nt) issue(k + 1, xnext);
-
+      // Layer 1; the copies of X(k+1) into xnext are issued between its
+      // MFMAs, so a busy memory pipeline stalls the copies, not the MFMAs.
+      const __amdgpu_buffer_rsrc_t nrsrc = tile_rsrc(k + 1);
       f16x acc0 = bias_frag(prm[0], fq), acc1 = acc0;
-      gemm_2blk<C::KS1, PF_L1, 4>(w1f, [&](int rb, int s) {
+      gemm_2blk<C::KS1, PF_L1, 4, C::DMA_PER_WAVE>(w1f, [&](int rb, int s) {
         const int off = ((2 * s) & ~15) * 16 + (((2 * s) ^ xa) & 15) * 16;
         return *(const GP_LDS h8*)(xs + xrow + rb * (32 * K * 2) + off);
-      }, acc0, acc1);
+      }, acc0, acc1, [&](int ii) { dma16_buf_nt(nrsrc, voff[ii], xnext + (ii * 4 + n) * 1024); });
 
       // Handoff slot k%2 was last read by stage B for tile k-2.
       if (k >= 2) lds_wait_geq((GP_LDS int*)&sy.h_free, 4 * (k - 1), ab);
@@ -310,6 +326,7 @@ void mgn_fused_kernel(Params p) {
       tile_a((GP_LDS char*)xs0, (GP_LDS char*)xs1, (GP_LDS char*)hand0, k);
       if (k + 1 < nt) tile_a((GP_LDS char*)xs1, (GP_LDS char*)xs0, (GP_LDS char*)hand1, k + 1);
     }
+    wait_vmcnt<0>();  // the (empty) copy issued during the last tile has landed before the waves exit
   } else {
     // ------------------------------------------------------------- stage B
     // W2 (32x32x16 A operand): lane holds W2[16s + 8*lh + e][32n + lr].
