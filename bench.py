@@ -30,13 +30,22 @@ WORKLOADS = {
     # name: (M, K, layernorm)
     "edge": (1048576, 384, True),
     "node": (262144, 256, True),
+    # edge MLP with the gather front end: M edges over GATHER_NODES nodes,
+    # X rows gathered as [nf[src] | ef | nf[dst]] (int64 indices)
+    "edge_gather": (1048576, 384, True),
 }
+GATHER_NODES = 262144
 
 
-def algorithmic(M, K, ln):
-    """Bytes that must cross HBM per call and MFMA FLOPs per call."""
+def algorithmic(M, K, ln, gather_nodes=0, idx_bytes=8):
+    """Bytes that must cross HBM per call and MFMA FLOPs per call.  With the
+    gather front end the input is the edge features (256 B/row), two indices
+    per row and the node table (read at least once), not the [M, K] matrix."""
     params = (K * 128 + 2 * 128 * 128) * 2 + 3 * 128 * 2 + (2 * 128 * 2 if ln else 0)
-    bytes_ = M * (K + 128) * 2 + params
+    if gather_nodes:
+        bytes_ = M * (128 * 2 + 2 * idx_bytes + 128 * 2) + gather_nodes * 128 * 2 + params
+    else:
+        bytes_ = M * (K + 128) * 2 + params
     flops = 2 * M * (K * 128 + 128 * 128 + 128 * 128)
     return bytes_, flops
 
@@ -108,20 +117,35 @@ def main():
     # Inputs resident in HBM.  The node batch (201 MB) would fit the 256 MB
     # MALL, so two input/output buffer pairs are rotated to keep it honest.
     nbuf = 2 if args.workload == "node" else 1
-    xs = [normal_fp16(M, K, seed=i, device=dev) for i in range(nbuf)]
+    gather = args.workload == "edge_gather"
+    if gather:
+        if args.impl != "fused":
+            print("the gather front end exists for the fused kernel only", file=sys.stderr)
+            sys.exit(2)
+        g = torch.Generator().manual_seed(0)
+        nf = normal_fp16(GATHER_NODES, 128, seed=1, device=dev)
+        xs = [normal_fp16(M, 128, seed=0, device=dev)]  # edge features
+        src = torch.randint(0, GATHER_NODES, (M,), generator=g).to(dev)
+        dst = torch.randint(0, GATHER_NODES, (M,), generator=g).to(dev)
+    else:
+        xs = [normal_fp16(M, K, seed=i, device=dev) for i in range(nbuf)]
     outs = [torch.empty((M, 128), dtype=torch.float16, device=dev) for _ in range(nbuf)]
 
     def step(i):
         b = i % nbuf
-        gpipes.mgn_mlp_out(xs[b], p["w1"], p["b1"], p["w2"], p["b2"], p["w3"], p["b3"], p["gamma"],
-                           p["beta"], outs[b], impl=args.impl)
+        if gather:
+            gpipes.mgn_edge_gather_out(nf, xs[0], src, dst, p["w1"], p["b1"], p["w2"], p["b2"], p["w3"], p["b3"],
+                                       p["gamma"], p["beta"], outs[0])
+        else:
+            gpipes.mgn_mlp_out(xs[b], p["w1"], p["b1"], p["w2"], p["b2"], p["w3"], p["b3"], p["gamma"],
+                               p["beta"], outs[b], impl=args.impl)
 
     if args.copy_ref:
-        src = torch.ones(1 << 29, dtype=torch.float16, device=dev)  # 1 GiB
-        dst = torch.empty_like(src)
-        dst.copy_(src)
+        ref_in = torch.ones(1 << 29, dtype=torch.float16, device=dev)  # 1 GiB
+        ref_out = torch.empty_like(ref_in)
+        ref_out.copy_(ref_in)
         torch.cuda.synchronize()
-        del src, dst
+        del ref_in, ref_out
 
     for i in range(args.warmup):
         step(i)
@@ -141,7 +165,7 @@ def main():
     launch_ms = sorted(a.elapsed_time(b) for a, b in ev)
     avg_launch_ms = sum(launch_ms) / len(launch_ms)
     ms_per_step = wall * 1e3 / args.steps
-    bytes_, flops = algorithmic(M, K, ln)
+    bytes_, flops = algorithmic(M, K, ln, GATHER_NODES if gather else 0)
     achieved_gbs = bytes_ / (avg_launch_ms * 1e-3) / 1e9
     tflops = flops / (avg_launch_ms * 1e-3) / 1e12
 
@@ -159,6 +183,7 @@ def main():
         "dtype": "f16",
         "data": "synthetic (X~N(0,1), nn.Linear default init, seed 0)",
         "config": {"workload": f"mgn_{args.workload}_mlp", "M": M, "K": K,
+                   **({"nodes": GATHER_NODES, "index": "int64"} if gather else {}),
                    "layers": f"{K}-128-128-128" + ("+LN" if ln else ""), "impl": args.impl,
                    "accumulate": "f32"},
         "roofline": {

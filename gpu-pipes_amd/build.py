@@ -61,7 +61,8 @@ def build_library(verbose=False):
     with cf.ThreadPoolExecutor(max_workers=min(len(jobs), 8)) as ex:
         list(ex.map(lambda c: _run(c, verbose), jobs))
     tmp = LIB + ".tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs, verbose)
+    # --no-undefined: a kernel whose host stub was not emitted fails here, not at load time
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", tmp] + objs, verbose)
     os.replace(tmp, LIB)
     return LIB
 

@@ -257,4 +257,32 @@ int gp_mgn_linears_out(int64_t M, const void* x, const void* w1, const void* b1,
   return run_mgn(a, GP_IMPL_FUSED, (hipStream_t)stream);
 }
 
+int gp_mgn_edge_gather_out(int64_t E, int64_t N, const void* nf, const void* ef, const void* src, const void* dst,
+                           int idx_bytes, const void* w1, const void* b1, const void* w2, const void* b2,
+                           const void* w3, const void* b3, const void* gamma, const void* beta, float eps, void* out,
+                           void* stream) {
+  clear_error();
+  if (idx_bytes != 4 && idx_bytes != 8) return fail(GP_ERR_INVALID_ARG, "idx_bytes must be 4 or 8 (got %d)", idx_bytes);
+  if (E < 0 || N < 0) return fail(GP_ERR_INVALID_ARG, "E and N must be >= 0");
+  if (E > 0 && N < 1) return fail(GP_ERR_SHAPE, "a non-empty edge set needs N >= 1 nodes");
+  if (N * 256 > (int64_t(1) << 31) - 16) return fail(GP_ERR_SHAPE, "N too large (%lld nodes; at most 8388607)", (long long)N);
+  MgnArgs a{E, 384, ef, w1, b1, w2, b2, w3, b3, gamma, beta, eps, out};
+  a.nf = nf;
+  a.N = N;
+  a.src = src;
+  a.dst = dst;
+  a.idx_bytes = idx_bytes;
+  int rc = check_mgn_args(a);
+  if (rc != GP_OK) return rc;
+  if (E == 0) return GP_OK;
+  if (!nf || !src || !dst) return fail(GP_ERR_INVALID_ARG, "nf, src and dst must be non-NULL when E > 0");
+  if (!aligned16(nf) || !aligned16(src) || !aligned16(dst))
+    return fail(GP_ERR_ALIGN, "nf, src and dst must be 16-byte aligned");
+  int dev = 0, ncu = 0;
+  rc = current_device_info(&dev, &ncu);
+  if (rc != GP_OK) return rc;
+  hipError_t e = mgn_fused_launch(a, ncu, (hipStream_t)stream);
+  return e == hipSuccess ? GP_OK : fail_hip(e, "mgn_edge_gather launch");
+}
+
 }  // extern "C"

@@ -23,6 +23,13 @@ struct MgnArgs {
   const void* beta;
   float eps;
   void* out;
+  // Gather front end (nf != nullptr): x is the edge features [M][128] and
+  // row e of the MLP input is [nf[src[e]] | x[e] | nf[dst[e]]].
+  const void* nf = nullptr;
+  int64_t N = 0;
+  const void* src = nullptr;
+  const void* dst = nullptr;
+  int idx_bytes = 0;  // 4 (int32) or 8 (int64)
 };
 
 // Persistent fused kernel (all layers in one workgroup per CU).

@@ -74,6 +74,12 @@ struct Params {
   half_t* out;
   int64_t M;
   float eps;
+  // Gather front end (GATHER kernels only): X row e is
+  // [nf[src[e]] | x[e] | nf[dst[e]]], nf is [N][128], indices are int32 or int64.
+  const half_t* nf;
+  int64_t N;
+  const void* src;
+  const void* dst;
 };
 
 // LDS synchronisation words (monotonic counters, one count per wave per tile).
@@ -211,10 +217,19 @@ __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-template <int K, bool LN>
+template <int K, bool LN, int GATHER_IDX = 0>  // GATHER_IDX: 0 = X given; 4 / 8 = gather, index bytes
 __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void mgn_fused_kernel(Params p) {
   using C = Cfg<K>;
+  constexpr bool GATHER = GATHER_IDX != 0;
+  static_assert(!GATHER || K == 3 * D, "the gather front end builds 384-wide rows");
+  // LDS layout of an X tile: row r, 16-byte logical chunk c (of K/8) lives at
+  // (c / 16) * XSEG + r * XROW + ((c ^ r) & 15) * 16 -- XOR-swizzled within
+  // groups of 16 chunks.  A plain tile is row-major (XROW = 2K, XSEG = 256);
+  // a gathered tile is segment-major (XROW = 256, XSEG = 64 * 256), so every
+  // 1 KiB copy comes from one source array.
+  constexpr int XROW = GATHER ? 256 : K * 2;
+  constexpr int XSEG = GATHER ? TM * 256 : 256;
   __shared__ __attribute__((aligned(1024))) char xs0[C::XBUF];
   __shared__ __attribute__((aligned(1024))) char xs1[C::XBUF];
   __shared__ __attribute__((aligned(16))) char hand0[TM * ACT_STRIDE];  // layer-1 output, slot 0
@@ -222,6 +237,7 @@ void mgn_fused_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) char act2[TM * ACT_STRIDE];   // layer-2 output
   __shared__ __attribute__((aligned(16))) float prm[5][D];  // b1, b2, b3, gamma, beta
   __shared__ Sync sy;
+  __shared__ __attribute__((aligned(16))) char idxs[GATHER ? 2 : 1][GATHER ? 2048 : 16];  // gather indices: [tile & 1][src | dst]
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -283,22 +299,87 @@ void mgn_fused_kernel(Params p) {
     }
     // Descriptor of tile k (empty past the last tile: a copy through it
     // writes zeros to LDS without touching memory).
+    // (Gather: the tile of x, whose rows are 128 wide.)
+    constexpr int XW = GATHER ? D : K;  // x row width (halves)
     auto tile_rsrc = [&](int k) {
       const int64_t row0 = (t0 + (int64_t)k * G) * TM;
-      const int64_t left = (M - row0) * (K * 2);
-      const int bytes = left <= 0 ? 0 : (left < C::XTILE ? (int)left : C::XTILE);
-      return make_rsrc(p.x + (left > 0 ? row0 * K : 0), bytes);
+      const int64_t left = (M - row0) * (XW * 2);
+      const int bytes = left <= 0 ? 0 : (left < TM * XW * 2 ? (int)left : TM * XW * 2);
+      return make_rsrc(p.x + (left > 0 ? row0 * XW : 0), bytes);
     };
     auto issue = [&](int k, GP_LDS char* buf) {
       const __amdgpu_buffer_rsrc_t rsrc = tile_rsrc(k);
 #pragma unroll
       for (int ii = 0; ii < C::DMA_PER_WAVE; ++ii) dma16_buf_nt(rsrc, voff[ii], buf + (ii * 4 + n) * 1024);
     };
-    issue(0, (GP_LDS char*)xs0);
+
+    int abar = 0;
+    int& abar0 = abar;
+    // ---- gather front end ----
+    // Copy ii (0..11) of wave n moves segment ii / 4 (0: nf[src], 1: x, 2:
+    // nf[dst]) of tile rows 16 (ii & 3) + r0 (r0 = 4n + lane / 16, four rows
+    // per copy), logical chunk gc of each row.  The gathered rows' byte
+    // offsets in nf (goff) are computed once per tile from the indices, which
+    // are copied into LDS (idxs) two tiles ahead by wave 0.  An index outside
+    // [0, N) selects an offset past the table: the range check returns zeros.
+    const int r0 = 4 * n + (lane >> 4);
+    const int gc = (lane & 15) ^ (r0 & 15);
+    const __amdgpu_buffer_rsrc_t nf_rsrc = make_rsrc(p.nf, GATHER ? (int)(p.N * (D * 2)) : 0);
+    int goff[GATHER ? 8 : 1];  // [src q0..q3, dst q0..q3]
+    auto row_index_bytes = [&](int k, int which, int q) {  // nf byte offset of the gathered row
+      const GP_LDS char* ib = (const GP_LDS char*)idxs[k & 1] + which * 1024 + (16 * q + r0) * GATHER_IDX;
+      const unsigned lo = *(const GP_LDS unsigned*)ib;
+      const unsigned hi = GATHER_IDX == 8 ? *(const GP_LDS unsigned*)(ib + 4) : 0u;
+      const bool ok = hi == 0u && lo < (unsigned)p.N;
+      return ok ? (int)(lo * (unsigned)(D * 2) + gc * 16) : (int)0xFFFFFFF0u;
+    };
+    auto gather_offsets = [&](int k) {
+      if constexpr (GATHER) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          goff[q] = row_index_bytes(k, 0, q);
+          goff[4 + q] = row_index_bytes(k, 1, q);
+        }
+      }
+    };
+    auto gather_copy = [&](int ii, __amdgpu_buffer_rsrc_t xrsrc, GP_LDS char* buf) {
+      const int seg = ii >> 2, q = ii & 3;
+      GP_LDS char* dst = buf + seg * XSEG + (16 * q + 4 * n) * 256;
+      if (seg == 1)
+        dma16_buf_nt(xrsrc, (16 * q + r0) * 256 + gc * 16, dst);
+      else
+        dma16_buf(nf_rsrc, goff[(seg >> 1) * 4 + q], dst);
+    };
+    // Indices of tile k's 64 rows: src into idxs[k & 1][0..), dst at +1024
+    // (64 x GATHER_IDX bytes each; lanes past the tile copy zeros into the
+    // unused upper part).
+    auto index_copy = [&](int k, int which) {
+      const int64_t row0 = (t0 + (int64_t)k * G) * TM;
+      const int64_t left = (M - row0) * GATHER_IDX;
+      const int bytes = left <= 0 ? 0 : (left < TM * GATHER_IDX ? (int)left : TM * GATHER_IDX);
+      const char* base = (const char*)(which ? p.dst : p.src) + (left > 0 ? row0 * GATHER_IDX : 0);
+      dma16_buf_nt(make_rsrc(base, bytes), lane * 16, (GP_LDS char*)idxs[k & 1] + which * 1024);
+    };
+
+    if constexpr (GATHER) {
+      if (n == 0) {
+        index_copy(0, 0);
+        index_copy(0, 1);
+        index_copy(1, 0);
+        index_copy(1, 1);
+      }
+      wait_vmcnt<0>();
+      group_barrier((GP_LDS int*)&sy.a_bar, abar0, 4, lane, ab);
+      gather_offsets(0);
+      const __amdgpu_buffer_rsrc_t rsrc = tile_rsrc(0);
+#pragma unroll
+      for (int ii = 0; ii < C::DMA_PER_WAVE; ++ii) gather_copy(ii, rsrc, (GP_LDS char*)xs0);
+    } else {
+      issue(0, (GP_LDS char*)xs0);
+    }
 
     const int xa = lh ^ (lr & 15);  // chunk (2s+lh) of rows lr, lr+32 lands at (2s ^ xa) in its 16-group
-    const int xrow = lr * (K * 2);
-    int abar = 0;
+    const int xrow = lr * XROW;
 
     auto tile_a = [&](GP_LDS char* xs, GP_LDS char* xnext, GP_LDS char* hand, int k) {
       // X(k) is the only copy in flight.  After the barrier it has landed for
@@ -308,12 +389,22 @@ void mgn_fused_kernel(Params p) {
       group_barrier((GP_LDS int*)&sy.a_bar, abar, 4, lane, ab);
       // Layer 1; the copies of X(k+1) into xnext are issued between its
       // MFMAs, so a busy memory pipeline stalls the copies, not the MFMAs.
+      // (Gather: tile k+1's indices landed with X(k); tile k+2's are copied
+      // into the index buffer tile k's indices used.)
+      gather_offsets(k + 1);
       const __amdgpu_buffer_rsrc_t nrsrc = tile_rsrc(k + 1);
       f16x acc0 = bias_frag(prm[0], fq), acc1 = acc0;
       gemm_2blk<C::KS1, PF_L1, 4, C::DMA_PER_WAVE>(w1f, [&](int rb, int s) {
-        const int off = ((2 * s) & ~15) * 16 + (((2 * s) ^ xa) & 15) * 16;
-        return *(const GP_LDS h8*)(xs + xrow + rb * (32 * K * 2) + off);
-      }, acc0, acc1, [&](int ii) { dma16_buf_nt(nrsrc, voff[ii], xnext + (ii * 4 + n) * 1024); });
+        const int off = (s >> 3) * XSEG + (((2 * s) ^ xa) & 15) * 16;
+        return *(const GP_LDS h8*)(xs + xrow + rb * (32 * XROW) + off);
+      }, acc0, acc1, [&](int ii) {
+        if constexpr (GATHER) {
+          gather_copy(ii, nrsrc, xnext);
+          if (n == 0 && ii < 2) index_copy(k + 2, ii);
+        } else {
+          dma16_buf_nt(nrsrc, voff[ii], xnext + (ii * 4 + n) * 1024);
+        }
+      });
 
       // Handoff slot k%2 was last read by stage B for tile k-2.
       if (k >= 2) lds_wait_geq((GP_LDS int*)&sy.h_free, 4 * (k - 1), ab);
@@ -437,12 +528,12 @@ void mgn_fused_kernel(Params p) {
 // ---------------------------------------------------------------------------
 // Host launcher
 // ---------------------------------------------------------------------------
-template <int K, bool LN>
+template <int K, bool LN, int GI = 0>
 static hipError_t launch_fused(const MgnArgs& a, int grid, hipStream_t stream) {
   fused::Params p{(const half_t*)a.x,  (const half_t*)a.w1, (const half_t*)a.b1, (const half_t*)a.w2,
                   (const half_t*)a.b2, (const half_t*)a.w3, (const half_t*)a.b3, (const half_t*)a.gamma,
-                  (const half_t*)a.beta, (half_t*)a.out, a.M, a.eps};
-  hipLaunchKernelGGL((fused::mgn_fused_kernel<K, LN>), dim3(grid), dim3(fused::NTHREADS), 0, stream, p);
+                  (const half_t*)a.beta, (half_t*)a.out, a.M, a.eps, (const half_t*)a.nf, a.N, a.src, a.dst};
+  hipLaunchKernelGGL((fused::mgn_fused_kernel<K, LN, GI>), dim3(grid), dim3(fused::NTHREADS), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -450,6 +541,14 @@ hipError_t mgn_fused_launch(const MgnArgs& a, int num_cus, hipStream_t stream) {
   const int64_t ntiles = (a.M + fused::TM - 1) / fused::TM;
   const int grid = (int)(ntiles < num_cus ? ntiles : num_cus);
   const bool ln = a.gamma != nullptr;
+  if (a.nf != nullptr) {  // gather front end (K = 384 = 3 x 128)
+    if (a.K != 384) return hipErrorInvalidValue;
+    if (a.idx_bytes == 4)
+      return ln ? launch_fused<384, true, 4>(a, grid, stream) : launch_fused<384, false, 4>(a, grid, stream);
+    if (a.idx_bytes == 8)
+      return ln ? launch_fused<384, true, 8>(a, grid, stream) : launch_fused<384, false, 8>(a, grid, stream);
+    return hipErrorInvalidValue;
+  }
   switch (a.K) {
     case 384: return ln ? launch_fused<384, true>(a, grid, stream) : launch_fused<384, false>(a, grid, stream);
     case 256: return ln ? launch_fused<256, true>(a, grid, stream) : launch_fused<256, false>(a, grid, stream);

@@ -24,7 +24,7 @@ __all__ = [
     "lib", "mgn_fullmlp", "mgn_fullmlp_out", "mgn_linears", "mgn_linears_out",
     "mgn_mlp", "mgn_mlp_out", "IMPL_FUSED", "IMPL_PIPELINED", "IMPL_PIPELINED_SPLIT_LN", "GpipesError",
     "linear_out", "linear_layer_norm_out", "layer_norm_out", "add_out", "concat_out", "pipe_ident",
-    "pipeline_check", "ACTS",
+    "pipeline_check", "ACTS", "mgn_edge_gather", "mgn_edge_gather_out",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -68,6 +68,8 @@ def _load():
     L.gp_concat_out.argtypes = [i64, i64, i64, vp, vp, vp, vp]
     L.gp_pipe_ident.argtypes = [i64, vp, vp, i32, vp]
     L.gp_pipeline_check.argtypes = [vp]
+    L.gp_mgn_edge_gather_out.argtypes = [i64, i64, vp, vp, vp, vp, i32] + [vp] * 8 + [f32, vp, vp]
+    L.gp_mgn_edge_gather_out.restype = i32
     for name in ("gp_linear_out", "gp_linear_layer_norm_out", "gp_layer_norm_out", "gp_add_out",
                  "gp_concat_out", "gp_pipe_ident", "gp_pipeline_check"):
         getattr(L, name).restype = i32
@@ -280,3 +282,39 @@ def pipeline_check(device=None):
     dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
     with torch.cuda.device(dev):
         _check(lib.gp_pipeline_check(ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
+
+
+def mgn_edge_gather_out(nf, ef, src, dst, w1, b1, w2, b2, w3, b3, gamma, beta, out, eps=1e-5):
+    """Edge update of update_edges (graphmodel/mgn_dp.py:28-32) with the gather fused in:
+    out[e] = MgnMlp([nf[src[e]] | ef[e] | nf[dst[e]]]).  src / dst: int32 or int64 [E]."""
+    _check_input("nf", nf)
+    _check_input("ef", ef)
+    if nf.dim() != 2 or nf.shape[1] != 128 or ef.dim() != 2 or ef.shape[1] != 128:
+        raise RuntimeError("nf and ef must be [*, 128]")
+    E, N = ef.shape[0], nf.shape[0]
+    for name, t in (("src", src), ("dst", dst)):
+        if not isinstance(t, torch.Tensor) or not t.is_cuda or not t.is_contiguous():
+            raise RuntimeError(f"{name} must be a contiguous CUDA tensor")
+        if t.dtype not in (torch.int32, torch.int64) or tuple(t.shape) != (E,):
+            raise RuntimeError(f"{name} must be int32 or int64 of shape ({E},)")
+    if src.dtype != dst.dtype:
+        raise RuntimeError("src and dst must have the same dtype")
+    _check_input("w1", w1, (384, 128))
+    for name, t, shp in (("b1", b1, (128,)), ("w2", w2, (128, 128)), ("b2", b2, (128,)), ("w3", w3, (128, 128)),
+                         ("b3", b3, (128,))):
+        _check_input(name, t, shp)
+    if (gamma is None) != (beta is None):
+        raise RuntimeError("gamma and beta must both be given or both be None")
+    _opt("gamma", gamma, (128,))
+    _opt("beta", beta, (128,))
+    _check_input("out", out, (E, 128))
+    with torch.cuda.device(ef.device):
+        _check(lib.gp_mgn_edge_gather_out(E, N, _ptr(nf), _ptr(ef), _ptr(src), _ptr(dst), src.element_size(),
+                                          _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2), _ptr(w3), _ptr(b3), _ptr(gamma),
+                                          _ptr(beta), float(eps), _ptr(out), _stream(ef)))
+    return out
+
+
+def mgn_edge_gather(nf, ef, src, dst, w1, b1, w2, b2, w3, b3, gamma=None, beta=None, eps=1e-5):
+    out = torch.empty((ef.shape[0], 128), dtype=torch.float16, device=ef.device)
+    return mgn_edge_gather_out(nf, ef, src, dst, w1, b1, w2, b2, w3, b3, gamma, beta, out, eps=eps)

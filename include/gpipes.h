@@ -85,6 +85,22 @@ int gp_mgn_mlp_out(int64_t M, int64_t K, const void* x, const void* w1, const vo
                    const void* gamma, const void* beta, float eps, void* out, int impl,
                    void* stream);
 
+/*
+ * MeshGraphNet edge update with the gather front end fused in:
+ *   out[e] = MLP([nf[src[e]] | ef[e] | nf[dst[e]]]),  e < E,
+ * the edge MLP of gp_mgn_fullmlp_out (K = 384; gamma == NULL skips the
+ * LayerNorm) whose input rows are gathered from the node table nf[N,128] and
+ * the edge features ef[E,128] while they are copied into the kernel, so the
+ * concatenated [E,384] input never exists in memory.  src / dst are int32
+ * (idx_bytes = 4) or int64 (idx_bytes = 8); an index outside [0, N) gathers
+ * zeros.  N <= 8388607.  Replaces the index / index / concat / mlp sequence
+ * of update_edges, graphmodel/mgn_dp.py:28-32.
+ */
+int gp_mgn_edge_gather_out(int64_t E, int64_t N, const void* nf, const void* ef, const void* src, const void* dst,
+                           int idx_bytes, const void* w1, const void* b1, const void* w2, const void* b2,
+                           const void* w3, const void* b3, const void* gamma, const void* beta, float eps, void* out,
+                           void* stream);
+
 /* ------------------------------------------------------------------------
  * Stage-level entry points: one stage function of the library run over a
  * whole matrix (tiles of 128 rows, persistent workgroups).
