@@ -6,7 +6,10 @@
 // one stream are ordered by the stream, launches on different streams use
 // different arenas.  An arena is zeroed once when allocated; afterwards every
 // launch gets a fresh epoch number and the device code treats counters of
-// older epochs as zero, so no per-launch reset is needed.
+// older epochs as zero, so no per-launch reset is needed -- as long as the
+// launches share a queue layout.  A launch with a different layout (another
+// kernel, whose payload may lie where this one's counters are) zeroes the
+// arena once first.
 #include <hip/hip_runtime.h>
 
 #include <map>
@@ -22,15 +25,24 @@ namespace {
 struct ArenaRec {
   void* base = nullptr;
   size_t bytes = 0;
-  uint32_t epoch = 0;  // last epoch handed out
+  uint32_t epoch = 0;   // last epoch handed out
+  uint32_t layout = 0;  // queue layout of the last launch (0: none)
 };
 std::mutex g_mu;
 std::map<std::pair<int, hipStream_t>, ArenaRec> g_arenas;
 }  // namespace
 
-int arena_acquire(int dev, hipStream_t stream, size_t bytes, void** base, uint32_t* epoch) {
+int arena_acquire(int dev, hipStream_t stream, size_t bytes, uint32_t layout, void** base, uint32_t* epoch) {
   std::lock_guard<std::mutex> lk(g_mu);
   ArenaRec& a = g_arenas[{dev, stream}];
+  if (a.bytes >= bytes && a.layout != layout) {
+    // Another kernel's queue layout used this memory: its payload bytes could
+    // sit where this layout keeps counters, so the arena is zeroed again
+    // (ordered on the stream, after the previous launch).
+    hipError_t e = hipMemsetAsync(a.base, 0, a.bytes, stream);
+    if (e != hipSuccess) return fail_hip(e, "hipMemsetAsync (queue arena)");
+  }
+  a.layout = layout;
   if (a.bytes < bytes) {
     if (a.base) {
       // the old arena may still be in use by work queued on this stream

@@ -220,7 +220,18 @@ int gp_pipe_ident(int64_t M, const void* x, void* out, int max_pipes, void* stre
   int rc = stage_prologue(M, &dev, &ncu);
   if (rc) return rc < 0 ? rc : GP_OK;
   if ((rc = need(x, "x")) || (rc = need(out, "out"))) return rc;
-  return pipe_ident_run(M, x, out, max_pipes, dev, ncu, (hipStream_t)stream);
+  return pipe_route_run(M, x, out, nullptr, GP_ROUTE_IDENT, max_pipes, dev, ncu, (hipStream_t)stream);
+}
+
+int gp_pipe_route(int64_t M, const void* x, void* out, void* out2, int route, int max_pipes, void* stream) {
+  int dev = 0, ncu = 0;
+  if (route != GP_ROUTE_IDENT && route != GP_ROUTE_BROADCAST && route != GP_ROUTE_SPLIT)
+    return fail(GP_ERR_INVALID_ARG, "unknown route %d", route);
+  int rc = stage_prologue(M, &dev, &ncu);
+  if (rc) return rc < 0 ? rc : GP_OK;
+  if ((rc = need(x, "x")) || (rc = need(out, "out"))) return rc;
+  if (route == GP_ROUTE_BROADCAST && (rc = need(out2, "out2"))) return rc;
+  return pipe_route_run(M, x, out, out2, route, max_pipes, dev, ncu, (hipStream_t)stream);
 }
 
 int gp_pipeline_check(void* stream) {

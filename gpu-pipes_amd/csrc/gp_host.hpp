@@ -23,11 +23,15 @@ int check_mgn_args(const MgnArgs& a);
 int mgn_pipelined_run(const MgnArgs& a, bool split_ln, int dev, int num_cus, hipStream_t stream);
 
 // Identity pipelines through ring queues (tests the queue protocol).
-int pipe_ident_run(int64_t M, const void* x, void* out, int max_pipes, int dev, int num_cus, hipStream_t stream);
+int pipe_route_run(int64_t M, const void* x, void* out, void* out2, int route, int max_pipes, int dev, int num_cus,
+                   hipStream_t stream);
 
-// Queue arenas, one per (device, stream), zeroed once; each call returns a
-// new launch epoch.  arena_last returns the arena and epoch of the last call.
-int arena_acquire(int dev, hipStream_t stream, size_t bytes, void** base, uint32_t* epoch);
+// Queue arenas, one per (device, stream), zeroed when allocated and when the
+// queue layout changes; each call returns a new launch epoch.  arena_last
+// returns the arena and epoch of the last call.
+constexpr uint32_t kArenaLayoutMgn = 1;    // mgn_pipelined Queues
+constexpr uint32_t kArenaLayoutRoute = 2;  // route kernels (+1 for the split layout)
+int arena_acquire(int dev, hipStream_t stream, size_t bytes, uint32_t layout, void** base, uint32_t* epoch);
 int arena_last(int dev, hipStream_t stream, void** base, uint32_t* epoch);
 
 }  // namespace gp

@@ -101,7 +101,7 @@ static int run(const MgnArgs& m, int dev, int num_cus, hipStream_t s) {
   const size_t bytes = sizeof(PipeCtl) + (size_t)(grid / S) * sizeof(Queues);
   void* base = nullptr;
   uint32_t epoch = 0;
-  int rc = arena_acquire(dev, s, bytes, &base, &epoch);
+  int rc = arena_acquire(dev, s, bytes, kArenaLayoutMgn, &base, &epoch);
   if (rc != GP_OK) return rc;
   Args a;
   a.m = m;

@@ -8,8 +8,9 @@
 //                       common/layer_norm_v2.cuh:129-147);
 //  * add_kernel         pipe_add (host_add2, common/elemwise_add.cuh:42-54);
 //  * concat_kernel      pipe_concat (host_concat2, common/concat.cuh:50-69);
-//  * ident_kernel       two-stage pipelines sender -> ring queue -> receiver
-//                       (misc_tests/pipeval/pipe_val_ext.cu:65-149).
+//  * route_kernel       copy pipelines over the reference's queue topologies:
+//                       1:1 (misc_tests/pipeval/pipe_val_ext.cu:65-149),
+//                       one producer / two consumers, and split / merge.
 // Workgroups are persistent: workgroup b of G handles tiles b, b+G, ...
 #include <hip/hip_runtime.h>
 
@@ -102,36 +103,92 @@ __global__ __launch_bounds__(kStageThreads) void concat_kernel(const half_t* a, 
 }
 
 // ---------------------------------------------------------------------------
-// Identity pipelines: stage 0 copies its tiles of x into a ring queue, stage 1
-// copies them out of the queue into out.  Pipeline g of P moves tiles g, g+P, ...
+// Copy pipelines over the queue topologies of the reference's apps.  Every
+// stage copies 128-row tiles; pipeline g of P moves tiles g, g+P, ...
+//  * ROUTE_IDENT (2 stages): x -> q -> out
+//    (misc_tests/pipeval/pipe_val_ext.cu:65-149).
+//  * ROUTE_BROADCAST (3 stages): x -> q (one producer, two consumers) -> out
+//    and -> out2, the MpmcRingQueue<E, N, 1, 2> of
+//    apps/bert_addln_ffn/pipelined/bert_addln_ffn_pl.cuh:55 and
+//    apps/nerf_a/pipelined/nerf_a_pl.cuh:55.
+//  * ROUTE_SPLIT (5 stages): x -> q0 -> 3 workers (SplitQueueReader, round
+//    robin) -> q1 (SplitQueueWriter, round robin) -> one reader in sequence
+//    order -> out, the split write of bert_addln_ffn_pl.cuh:121.
 // ---------------------------------------------------------------------------
-using IdentEntry = QueueEntry2D<MBLK, 128>;
-using IdentQueue = RingQueue<IdentEntry, 2>;
+using RouteEntry = QueueEntry2D<MBLK, 128>;
+using IdentQueue = RingQueue<RouteEntry, 2>;
+using BcastQueue = RingQueue<RouteEntry, 2, 1, 2>;
+constexpr int kSplitWorkers = 3;
+using SplitQueue = RingQueue<RouteEntry, kSplitWorkers + 1>;
 
-struct IdentArgs {
+struct RouteQueues {
+  union {
+    IdentQueue ident;
+    BcastQueue bcast;
+    struct {
+      SplitQueue q0, q1;
+    } split;
+  };
+};
+
+struct RouteArgs {
   const half_t* x;
   half_t* out;
+  half_t* out2;
   int64_t M;
   PipeCtl* ctl;
-  IdentQueue* queues;
+  RouteQueues* queues;
   QueueCtx ctx;
   int max_pipes;
 };
 
-__global__ __launch_bounds__(kStageThreads) void ident_kernel(IdentArgs a) {
-  const Role r = assign_role(a.ctl, 2, a.ctx, a.max_pipes);
+template <int ROUTE>
+__global__ __launch_bounds__(kStageThreads) void route_kernel(RouteArgs a) {
+  constexpr int S = ROUTE == GP_ROUTE_IDENT ? 2 : (ROUTE == GP_ROUTE_BROADCAST ? 3 : 2 + kSplitWorkers);
+  const Role r = assign_role(a.ctl, S, a.ctx, a.max_pipes);
   if (r.pipe < 0) return;
   const int64_t T = (a.M + MBLK - 1) / MBLK, P = r.npipes, g = r.pipe;
   const int nt = g < T ? (int)((T - 1 - g) / P + 1) : 0;
-  IdentQueue* q = a.queues + g;
-  if (r.stage == 0) {
-    MemoryReader ir((half_t*)a.x + g * MBLK * 128, P * MBLK * 128, 128, MBLK, a.M - g * MBLK, P * MBLK);
-    QueueWriter<IdentQueue> ow(q, &a.ctx);
-    pipe_copy_n(ir, ow, nt, 128);
+  RouteQueues* q = a.queues + g;
+  const int64_t tile = (int64_t)MBLK * 128;
+  auto input = [&]() { return MemoryReader((half_t*)a.x + g * tile, P * tile, 128, MBLK, a.M - g * MBLK, P * MBLK); };
+  auto output = [&](half_t* base) { return MemoryWriter(base + g * tile, P * tile, 128); };
+  if constexpr (ROUTE == GP_ROUTE_IDENT) {
+    if (r.stage == 0) {
+      MemoryReader ir = input();
+      QueueWriter<IdentQueue> ow(&q->ident, &a.ctx);
+      pipe_copy_n(ir, ow, nt, 128);
+    } else {
+      QueueReader<IdentQueue> ir(&q->ident, &a.ctx);
+      MemoryWriter ow = output(a.out);
+      pipe_copy_n(ir, ow, nt, 128);
+    }
+  } else if constexpr (ROUTE == GP_ROUTE_BROADCAST) {
+    if (r.stage == 0) {
+      MemoryReader ir = input();
+      QueueWriter<BcastQueue> ow(&q->bcast, &a.ctx);
+      pipe_copy_n(ir, ow, nt, 128);
+    } else {
+      QueueReader<BcastQueue> ir(&q->bcast, &a.ctx);
+      MemoryWriter ow = output(r.stage == 1 ? a.out : a.out2);
+      pipe_copy_n(ir, ow, nt, 128);
+    }
   } else {
-    QueueReader<IdentQueue> ir(q, &a.ctx);
-    MemoryWriter ow(a.out + g * MBLK * 128, P * MBLK * 128, 128);
-    pipe_copy_n(ir, ow, nt, 128);
+    if (r.stage == 0) {
+      MemoryReader ir = input();
+      QueueWriter<SplitQueue> ow(&q->split.q0, &a.ctx);
+      pipe_copy_n(ir, ow, nt, 128);
+    } else if (r.stage <= kSplitWorkers) {
+      const int w = r.stage - 1;
+      const int cnt = nt > w ? (nt - w + kSplitWorkers - 1) / kSplitWorkers : 0;
+      SplitQueueReader<SplitQueue> ir(&q->split.q0, &a.ctx, w, kSplitWorkers);
+      SplitQueueWriter<SplitQueue> ow(&q->split.q1, &a.ctx, w, kSplitWorkers);
+      pipe_copy_n(ir, ow, cnt, 128);
+    } else {
+      QueueReader<SplitQueue> ir(&q->split.q1, &a.ctx);
+      MemoryWriter ow = output(a.out);
+      pipe_copy_n(ir, ow, nt, 128);
+    }
   }
 }
 
@@ -203,35 +260,50 @@ hipError_t concat_launch(int64_t M, int64_t N0, int64_t N1, const void* a, const
   return hipGetLastError();
 }
 
-int pipe_ident_run(int64_t M, const void* x, void* out, int max_pipes, int dev, int num_cus, hipStream_t s) {
+template <int ROUTE>
+static int route_launch(int64_t M, const void* x, void* out, void* out2, int max_pipes, int dev, int num_cus,
+                        hipStream_t s) {
+  constexpr int S = ROUTE == GP_ROUTE_IDENT ? 2 : (ROUTE == GP_ROUTE_BROADCAST ? 3 : 2 + kSplitWorkers);
+  auto kern = route_kernel<ROUTE>;
   int per_cu = 0;
-  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ident_kernel, kStageThreads, 0);
+  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kStageThreads, 0);
   if (e != hipSuccess) return fail_hip(e, "occupancy query");
   int grid = per_cu * num_cus;
   if (max_pipes > 0) {
     // Workgroups are spread round-robin over the XCDs and a pipeline needs
-    // both its workgroups on one XCD: launch whole rounds of kXcdHint * 2.
+    // all its workgroups on one XCD: launch whole rounds of kXcdHint * S.
     const int64_t rounds = (max_pipes + kXcdHint - 1) / kXcdHint;
-    if (rounds * kXcdHint * 2 < grid) grid = (int)(rounds * kXcdHint * 2);
+    if (rounds * kXcdHint * S < grid) grid = (int)(rounds * kXcdHint * S);
   }
-  if (grid < 2) return fail(GP_ERR_NO_DEVICE, "not enough co-resident workgroups for a pipeline");
-  const size_t bytes = sizeof(PipeCtl) + (size_t)(grid / 2) * sizeof(IdentQueue);
+  if (grid < S) return fail(GP_ERR_NO_DEVICE, "not enough co-resident workgroups for a pipeline");
+  const size_t bytes = sizeof(PipeCtl) + (size_t)(grid / S) * sizeof(RouteQueues);
   void* base = nullptr;
   uint32_t epoch = 0;
-  int rc = arena_acquire(dev, s, bytes, &base, &epoch);
+  int rc = arena_acquire(dev, s, bytes, kArenaLayoutRoute + (ROUTE == GP_ROUTE_SPLIT), &base, &epoch);
   if (rc != GP_OK) return rc;
-  IdentArgs a;
+  RouteArgs a;
   a.x = (const half_t*)x;
   a.out = (half_t*)out;
+  a.out2 = (half_t*)out2;
   a.M = M;
   a.ctl = (PipeCtl*)base;
-  a.queues = (IdentQueue*)((char*)base + sizeof(PipeCtl));
+  a.queues = (RouteQueues*)((char*)base + sizeof(PipeCtl));
   a.ctx = QueueCtx{epoch, &a.ctl->err.v};
   a.max_pipes = max_pipes;
   void* args[] = {&a};
-  e = hipLaunchCooperativeKernel((const void*)ident_kernel, dim3(grid), dim3(kStageThreads), args, 0, s);
-  if (e != hipSuccess) return fail_hip(e, "ident_kernel cooperative launch");
+  e = hipLaunchCooperativeKernel((const void*)kern, dim3(grid), dim3(kStageThreads), args, 0, s);
+  if (e != hipSuccess) return fail_hip(e, "route_kernel cooperative launch");
   return GP_OK;
+}
+
+int pipe_route_run(int64_t M, const void* x, void* out, void* out2, int route, int max_pipes, int dev, int num_cus,
+                   hipStream_t s) {
+  switch (route) {
+    case GP_ROUTE_IDENT: return route_launch<GP_ROUTE_IDENT>(M, x, out, out2, max_pipes, dev, num_cus, s);
+    case GP_ROUTE_BROADCAST: return route_launch<GP_ROUTE_BROADCAST>(M, x, out, out2, max_pipes, dev, num_cus, s);
+    case GP_ROUTE_SPLIT: return route_launch<GP_ROUTE_SPLIT>(M, x, out, out2, max_pipes, dev, num_cus, s);
+    default: return fail(GP_ERR_INVALID_ARG, "unknown route %d", route);
+  }
 }
 
 }  // namespace gp

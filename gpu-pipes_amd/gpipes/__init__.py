@@ -24,7 +24,7 @@ __all__ = [
     "lib", "mgn_fullmlp", "mgn_fullmlp_out", "mgn_linears", "mgn_linears_out",
     "mgn_mlp", "mgn_mlp_out", "IMPL_FUSED", "IMPL_PIPELINED", "IMPL_PIPELINED_SPLIT_LN", "GpipesError",
     "linear_out", "linear_layer_norm_out", "layer_norm_out", "add_out", "concat_out", "pipe_ident",
-    "pipeline_check", "ACTS", "mgn_edge_gather", "mgn_edge_gather_out",
+    "pipeline_check", "ACTS", "mgn_edge_gather", "mgn_edge_gather_out", "pipe_route", "ROUTES",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -36,6 +36,7 @@ IMPL_PIPELINED = 1
 IMPL_PIPELINED_SPLIT_LN = 2
 _IMPLS = {"fused": IMPL_FUSED, "pipelined": IMPL_PIPELINED, "pipelined_split_ln": IMPL_PIPELINED_SPLIT_LN}
 ACTS = {"none": 0, "relu": 1, "gelu_tanh": 2, "sigmoid": 3}
+ROUTES = {"ident": 0, "broadcast": 1, "split": 2}
 
 
 class GpipesError(RuntimeError):
@@ -67,6 +68,8 @@ def _load():
     L.gp_add_out.argtypes = [i64, i64, vp, vp, vp, vp]
     L.gp_concat_out.argtypes = [i64, i64, i64, vp, vp, vp, vp]
     L.gp_pipe_ident.argtypes = [i64, vp, vp, i32, vp]
+    L.gp_pipe_route.argtypes = [i64, vp, vp, vp, i32, i32, vp]
+    L.gp_pipe_route.restype = i32
     L.gp_pipeline_check.argtypes = [vp]
     L.gp_mgn_edge_gather_out.argtypes = [i64, i64, vp, vp, vp, vp, i32] + [vp] * 8 + [f32, vp, vp]
     L.gp_mgn_edge_gather_out.restype = i32
@@ -275,6 +278,21 @@ def pipe_ident(x, max_pipes=0, out=None):
     with torch.cuda.device(x.device):
         _check(lib.gp_pipe_ident(M, _ptr(x), _ptr(out), int(max_pipes), _stream(x)))
     return out
+
+
+def pipe_route(x, route="ident", max_pipes=0):
+    """Copy x[M,128] through a queue topology (ident / broadcast / split); returns
+    (out, out2) -- out2 is None except for the two-consumer broadcast."""
+    _check_input("x", x)
+    M, D = x.shape
+    if D != 128:
+        raise RuntimeError("pipe_route moves 128-wide rows")
+    rid = ROUTES.get(route, route)
+    out = torch.zeros_like(x)
+    out2 = torch.zeros_like(x) if rid == ROUTES["broadcast"] else None
+    with torch.cuda.device(x.device):
+        _check(lib.gp_pipe_route(M, _ptr(x), _ptr(out), _ptr(out2), int(rid), int(max_pipes), _stream(x)))
+    return out, out2
 
 
 def pipeline_check(device=None):

@@ -151,9 +151,25 @@ int gp_concat_out(int64_t M, int64_t N0, int64_t N1, const void* a, const void* 
  * Identity pipelines: sender workgroups copy 128-row tiles of x[M,128] into
  * ring queues, receiver workgroups copy them out to out[M,128].  At most
  * max_pipes pipelines (<= 0: as many as fit).  The queue round trip of
- * misc_tests/pipeval/pipe_val_ext.cu:65-149 (ident).
+ * misc_tests/pipeval/pipe_val_ext.cu:65-149 (ident).  Same as
+ * gp_pipe_route(M, x, out, NULL, GP_ROUTE_IDENT, max_pipes, stream).
  */
 int gp_pipe_ident(int64_t M, const void* x, void* out, int max_pipes, void* stream);
+
+/* Queue topologies of gp_pipe_route. */
+#define GP_ROUTE_IDENT 0     /* x -> queue -> out                                            */
+#define GP_ROUTE_BROADCAST 1 /* x -> queue with two consumers -> out and out2                */
+                             /* (MpmcRingQueue<E, N, 1, 2>, bert_addln_ffn_pl.cuh:55)        */
+#define GP_ROUTE_SPLIT 2     /* x -> queue -> 3 workers round robin (SplitQueueReader) ->    */
+                             /* queue written round robin (SplitQueueWriter,                 */
+                             /* bert_addln_ffn_pl.cuh:121) -> out in sequence order          */
+
+/*
+ * Copy pipelines over the queue topologies the reference's apps use; out
+ * (and out2 for GP_ROUTE_BROADCAST) must equal x bit for bit.  The exercise
+ * of the queue library's multi-consumer and split reader / writer paths.
+ */
+int gp_pipe_route(int64_t M, const void* x, void* out, void* out2, int route, int max_pipes, void* stream);
 
 /*
  * Waits for `stream`, then reports whether the last pipelined launch on it

@@ -127,3 +127,35 @@ def test_pipe_ident_back_to_back(cuda):
         y = gpipes.pipe_ident(x, max_pipes=[0, 2, 7, 1, 0][i])
         gpipes.pipeline_check()
         assert torch.equal(y.view(torch.int16), x.view(torch.int16)), i
+
+
+@pytest.mark.parametrize("route", ["ident", "broadcast", "split"])
+@pytest.mark.parametrize("M", [1, 129, 100003, 1048576])
+@pytest.mark.parametrize("max_pipes", [1, 0])
+def test_pipe_route_bit_exact(cuda, route, M, max_pipes):
+    """Queue topologies: 1:1, one producer / two consumers, split / merge."""
+    x = torch.randn((M, 128), device=cuda, generator=torch.Generator(device=cuda).manual_seed(M + 1)).to(torch.float16)
+    out, out2 = gpipes.pipe_route(x, route, max_pipes=max_pipes)
+    gpipes.pipeline_check()
+    assert torch.equal(out.view(torch.int16), x.view(torch.int16))
+    if route == "broadcast":
+        assert torch.equal(out2.view(torch.int16), x.view(torch.int16))
+
+
+def test_arena_shared_by_different_queue_layouts(cuda):
+    """Launches with different queue layouts on one stream share the arena."""
+    from gpipes.synth import mgn_params, normal_fp16
+    x = torch.randn((70000, 128), device=cuda).to(torch.float16)
+    p = {k: (None if v is None else v.to(cuda)) for k, v in mgn_params(384, seed=2).items()}
+    xe = normal_fp16(5000, 384, seed=3, device=cuda)
+    ref = gpipes.mgn_mlp(xe, p["w1"], p["b1"], p["w2"], p["b2"], p["w3"], p["b3"], p["gamma"], p["beta"],
+                         impl="pipelined")
+    gpipes.pipeline_check()
+    for route in ["split", "ident", "broadcast", "split", "ident"]:
+        out, _ = gpipes.pipe_route(x, route)
+        gpipes.pipeline_check()
+        assert torch.equal(out, x), route
+        y = gpipes.mgn_mlp(xe, p["w1"], p["b1"], p["w2"], p["b2"], p["w3"], p["b3"], p["gamma"], p["beta"],
+                           impl="pipelined")
+        gpipes.pipeline_check()
+        assert torch.equal(y, ref), route
