@@ -26,12 +26,14 @@ HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     # keep packed-fp32 VALU forms out of the generated code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # MFMA accumulators in VGPRs: the AGPR file holds the resident weights
-    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wno-unused-command-line-argument",
 ]
+# MFMA accumulators in VGPRs: the AGPR file holds the resident weights of the
+# MLP kernels.  The wide GEMM keeps its 256 accumulators in AGPRs instead.
+VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 
-SOURCES = ["mgn_fused.hip", "mgn_pipelined.hip", "stages.hip", "capi.cpp", "arena.cpp"]
+SOURCES = ["mgn_fused.hip", "mgn_pipelined.hip", "stages.hip", "gemm.hip", "capi.cpp", "ffn.cpp", "arena.cpp"]
+SOURCE_FLAGS = {"gemm.hip": []}
 
 
 def _run(cmd, verbose):
@@ -57,7 +59,8 @@ def build_library(verbose=False):
         obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
         lang = ["-x", "hip"] if src.endswith(".hip") else []
-        jobs.append([HIPCC] + HIP_FLAGS + lang + ["-c", path, "-o", obj])
+        extra = SOURCE_FLAGS.get(src, VGPR_FORM)
+        jobs.append([HIPCC] + HIP_FLAGS + extra + lang + ["-c", path, "-o", obj])
     with cf.ThreadPoolExecutor(max_workers=min(len(jobs), 8)) as ex:
         list(ex.map(lambda c: _run(c, verbose), jobs))
     tmp = LIB + ".tmp"

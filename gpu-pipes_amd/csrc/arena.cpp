@@ -10,6 +10,10 @@
 // launches share a queue layout.  A launch with a different layout (another
 // kernel, whose payload may lie where this one's counters are) zeroes the
 // arena once first.
+//
+// Workspaces hold the intermediates of the unpipelined wide operators (the
+// BERT FFN's transposed weights and activation chunks): one per (device,
+// stream), grown on demand, never zeroed.
 #include <hip/hip_runtime.h>
 
 #include <map>
@@ -63,6 +67,34 @@ int arena_acquire(int dev, hipStream_t stream, size_t bytes, uint32_t layout, vo
   if (++a.epoch == 0) a.epoch = 1;  // epoch 0 is the zeroed state
   *base = a.base;
   *epoch = a.epoch;
+  return GP_OK;
+}
+
+namespace {
+struct WorkRec {
+  void* base = nullptr;
+  size_t bytes = 0;
+};
+std::map<std::pair<int, hipStream_t>, WorkRec> g_work;
+}  // namespace
+
+int workspace_acquire(int dev, hipStream_t stream, size_t bytes, void** base) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  WorkRec& w = g_work[{dev, stream}];
+  if (w.bytes < bytes) {
+    if (w.base) {
+      hipError_t e = hipStreamSynchronize(stream);  // earlier launches may still use it
+      if (e != hipSuccess) return fail_hip(e, "hipStreamSynchronize (workspace growth)");
+      e = hipFree(w.base);
+      if (e != hipSuccess) return fail_hip(e, "hipFree (workspace growth)");
+      w.base = nullptr;
+      w.bytes = 0;
+    }
+    hipError_t e = hipMalloc(&w.base, bytes);
+    if (e != hipSuccess) return fail_hip(e, "hipMalloc (workspace)");
+    w.bytes = bytes;
+  }
+  *base = w.base;
   return GP_OK;
 }
 

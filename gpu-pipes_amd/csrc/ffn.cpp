@@ -1,0 +1,136 @@
+// C ABI of the wide operators: the GEMM stage with any N / K (gp_gemm_out)
+// and the BERT feed-forward block (gp_bert_ffn_out).
+//
+// The reference's pipelined BERT FFN (apps/bert_ffn/pipelined/bert_ffn_pl.cuh:
+// 79-162) chains GEMM + bias + ReLU -> GEMM + bias with the residual as
+// accumulator -> LayerNorm workers through queues, sized for H = 128 and
+// FF = 512.  At BERT-large width the two GEMMs are compute-bound and their
+// weights cannot be held on chip, so here the block is three launches per row
+// chunk: GEMM1 with a bias + activation epilogue, GEMM2 with a bias +
+// residual epilogue, and the LayerNorm stage -- the shape of the reference's
+// bulk-sync variant (apps/bert_ffn/bulksync/bert_ffn_bs.cuh:12-27) with the add
+// fused.  Rows are processed in chunks so the FF-wide activations of one chunk
+// (128 MB at 16384 x 4096) can stay in the 256 MB Infinity Cache between the
+// two GEMMs rather than make a round trip through HBM.
+#include <hip/hip_runtime.h>
+
+#include "../../include/gpipes.h"
+#include "gp_host.hpp"
+#include "gp_kernels.hpp"
+
+namespace gp {
+namespace {
+
+constexpr int64_t kMaxDim = 16384;
+constexpr int64_t kMaxRows = (int64_t(1) << 31) - 1;  // GEMM tile indices are 32-bit
+// 16384 rows: GEMM1 has 1024 tiles and GEMM2 256 tiles per chunk at
+// BERT-large width, whole multiples of the 256 CUs.
+constexpr int64_t kFfnChunkRows = 16384;
+
+size_t round_up(size_t v) { return (v + 255) & ~size_t(255); }
+
+int check_act(int act) {
+  if (act != GP_ACT_NONE && act != GP_ACT_RELU && act != GP_ACT_GELU_TANH && act != GP_ACT_SIGMOID)
+    return fail(GP_ERR_INVALID_ARG, "unknown activation %d", act);
+  return GP_OK;
+}
+
+int need16(const void* p, const char* name) {
+  if (!p) return fail(GP_ERR_INVALID_ARG, "%s is NULL", name);
+  if (!aligned16(p)) return fail(GP_ERR_ALIGN, "%s must be 16-byte aligned", name);
+  return GP_OK;
+}
+
+int opt16(const void* p, const char* name) {
+  if (p && !aligned16(p)) return fail(GP_ERR_ALIGN, "%s must be 16-byte aligned", name);
+  return GP_OK;
+}
+
+const char* at_row(const void* base, int64_t row, int64_t width) { return (const char*)base + row * width * 2; }
+
+}  // namespace
+}  // namespace gp
+
+using namespace gp;
+
+extern "C" {
+
+int gp_gemm_out(int64_t M, int64_t N, int64_t K, const void* x, const void* w, const void* b, const void* r,
+                int act, void* out, void* stream) {
+  clear_error();
+  int rc;
+  if (M < 0) return fail(GP_ERR_INVALID_ARG, "M must be >= 0 (got %lld)", (long long)M);
+  if (N < 128 || N > kMaxDim || N % 128)
+    return fail(GP_ERR_SHAPE, "N must be a multiple of 128 in [128, %lld] (got %lld)", (long long)kMaxDim,
+                (long long)N);
+  if (K < 64 || K > kMaxDim || K % 64)
+    return fail(GP_ERR_SHAPE, "K must be a multiple of 64 in [64, %lld] (got %lld)", (long long)kMaxDim,
+                (long long)K);
+  if (M > kMaxRows) return fail(GP_ERR_SHAPE, "M too large (%lld)", (long long)M);
+  if ((rc = check_act(act))) return rc;
+  if (r && act != GP_ACT_NONE) return fail(GP_ERR_INVALID_ARG, "a residual input requires act = GP_ACT_NONE");
+  if ((rc = need16(w, "w")) || (rc = opt16(b, "b")) || (rc = opt16(r, "r"))) return rc;
+  if (M == 0) return GP_OK;
+  if ((rc = need16(x, "x")) || (rc = need16(out, "out"))) return rc;
+  int dev = 0, ncu = 0;
+  if ((rc = current_device_info(&dev, &ncu))) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  void* ws = nullptr;
+  if ((rc = workspace_acquire(dev, s, (size_t)N * K * 2, &ws))) return rc;
+  hipError_t e = transpose_launch(w, ws, K, N, s);
+  if (e != hipSuccess) return fail_hip(e, "transpose launch");
+  e = gemm_launch({M, N, K, x, ws, b, r, act, out}, ncu, s);
+  return e == hipSuccess ? GP_OK : fail_hip(e, "gemm launch");
+}
+
+int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void* w1, const void* b1,
+                    const void* w2, const void* b2, const void* gamma, const void* beta, float eps, int act,
+                    void* out, void* stream) {
+  clear_error();
+  int rc;
+  if (M < 0) return fail(GP_ERR_INVALID_ARG, "M must be >= 0 (got %lld)", (long long)M);
+  if (H != 128 && H != 256 && H != 512 && H != 1024)
+    return fail(GP_ERR_SHAPE, "H must be 128, 256, 512 or 1024 (got %lld)", (long long)H);
+  if (FF < 128 || FF > kMaxDim || FF % 128)
+    return fail(GP_ERR_SHAPE, "FF must be a multiple of 128 in [128, %lld] (got %lld)", (long long)kMaxDim,
+                (long long)FF);
+  if (M > kMaxRows) return fail(GP_ERR_SHAPE, "M too large (%lld)", (long long)M);
+  if ((rc = check_act(act))) return rc;
+  if (!(eps >= 0.f)) return fail(GP_ERR_INVALID_ARG, "eps must be >= 0");
+  if ((rc = need16(w1, "w1")) || (rc = need16(w2, "w2")) || (rc = opt16(b1, "b1")) || (rc = opt16(b2, "b2")) ||
+      (rc = opt16(gamma, "gamma")) || (rc = opt16(beta, "beta")))
+    return rc;
+  if (M == 0) return GP_OK;
+  if ((rc = need16(x, "x")) || (rc = need16(out, "out"))) return rc;
+  int dev = 0, ncu = 0;
+  if ((rc = current_device_info(&dev, &ncu))) return rc;
+  hipStream_t s = (hipStream_t)stream;
+
+  // Workspace: w1^T [FF][H], w2^T [H][FF], then one chunk of activations
+  // [CH][FF] and of pre-LayerNorm rows [CH][H].
+  const int64_t CH = M < kFfnChunkRows ? M : kFfnChunkRows;
+  const size_t o_w2t = round_up((size_t)FF * H * 2);
+  const size_t o_act = o_w2t + round_up((size_t)FF * H * 2);
+  const size_t o_y = o_act + round_up((size_t)CH * FF * 2);
+  const size_t total = o_y + round_up((size_t)CH * H * 2);
+  char* ws = nullptr;
+  if ((rc = workspace_acquire(dev, s, total, (void**)&ws))) return rc;
+  void *w1t = ws, *w2t = ws + o_w2t, *hbuf = ws + o_act, *ybuf = ws + o_y;
+
+  hipError_t e = transpose_launch(w1, w1t, H, FF, s);
+  if (e == hipSuccess) e = transpose_launch(w2, w2t, FF, H, s);
+  if (e != hipSuccess) return fail_hip(e, "transpose launch");
+  for (int64_t r0 = 0; r0 < M; r0 += CH) {
+    const int64_t rows = M - r0 < CH ? M - r0 : CH;
+    const void* xc = at_row(x, r0, H);
+    e = gemm_launch({rows, FF, H, xc, w1t, b1, nullptr, act, hbuf}, ncu, s);
+    if (e != hipSuccess) return fail_hip(e, "FFN GEMM1 launch");
+    e = gemm_launch({rows, H, FF, hbuf, w2t, b2, xc, GP_ACT_NONE, ybuf}, ncu, s);
+    if (e != hipSuccess) return fail_hip(e, "FFN GEMM2 launch");
+    e = layer_norm_launch(rows, H, ybuf, gamma, beta, eps, (char*)out + r0 * H * 2, ncu, s);
+    if (e != hipSuccess) return fail_hip(e, "FFN LayerNorm launch");
+  }
+  return GP_OK;
+}
+
+}  // extern "C"

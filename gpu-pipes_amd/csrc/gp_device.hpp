@@ -134,6 +134,17 @@ __device__ __forceinline__ void dma16_buf_nt(__amdgpu_buffer_rsrc_t rsrc, int vo
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds_base, 16, voffset, 0, 0, 2);
 }
 
+// 8-byte buffer load / store of four fp16 values at byte offset `off`.
+// Accesses at or beyond the descriptor's range read zero / are dropped, which
+// is how partial tiles are bounded without per-row branches.
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ h4 buf_load_h4(__amdgpu_buffer_rsrc_t rsrc, int off) {
+  return __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rsrc, off, 0, 0));
+}
+__device__ __forceinline__ void buf_store_h4(__amdgpu_buffer_rsrc_t rsrc, int off, h4 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), rsrc, off, 0, 0);
+}
+
 // ---------------------------------------------------------------------------
 // MFMA 32x32x16 f16 -> f32.  Operand layout (wave64):
 //   A[i][k]: lane = i + 32*(k/8), element k%8          (32 rows x 16 k)

@@ -34,4 +34,10 @@ constexpr uint32_t kArenaLayoutRoute = 2;  // route kernels (+1 for the split la
 int arena_acquire(int dev, hipStream_t stream, size_t bytes, uint32_t layout, void** base, uint32_t* epoch);
 int arena_last(int dev, hipStream_t stream, void** base, uint32_t* epoch);
 
+// Scratch memory of the wide operators, one per (device, stream), grown on
+// demand (a grow synchronises the stream); contents are not preserved.
+int workspace_acquire(int dev, hipStream_t stream, size_t bytes, void** base);
+
+bool aligned16(const void* p);
+
 }  // namespace gp

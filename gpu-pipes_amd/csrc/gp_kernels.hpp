@@ -53,6 +53,23 @@ hipError_t linear_launch(const LinearArgs& a, int num_cus, hipStream_t stream);
 hipError_t layer_norm_launch(int64_t M, int64_t D, const void* x, const void* gamma, const void* beta, float eps,
                              void* out, int num_cus, hipStream_t stream);
 hipError_t add_launch(int64_t M, int64_t N, const void* a, const void* b, void* c, int num_cus, hipStream_t stream);
+
+// Wide GEMM stage: out = act(x W + b) or x W + b + r, any N multiple of 128,
+// K multiple of 32, with W passed transposed (wt = W^T, [N, K]).
+struct GemmArgs {
+  int64_t M;
+  int64_t N;
+  int64_t K;
+  const void* x;   // [M, K]
+  const void* wt;  // [N, K]
+  const void* b;   // [N] or nullptr
+  const void* r;   // [M, N] residual or nullptr (then act must be ACT_NONE)
+  int act;
+  void* out;       // [M, N]
+};
+hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t stream);
+// out[N, K] = in[K, N]; K and N multiples of 64.
+hipError_t transpose_launch(const void* in, void* out, int64_t K, int64_t N, hipStream_t stream);
 hipError_t concat_launch(int64_t M, int64_t N0, int64_t N1, const void* a, const void* b, void* c, int num_cus,
                          hipStream_t stream);
 

@@ -32,12 +32,22 @@ namespace gp {
 
 enum Act : int { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU_TANH = 2, ACT_SIGMOID = 3 };
 
+// GELU with the tanh approximation, 0.5 v (1 + tanh(u)), u = sqrt(2/pi)(v + 0.044715 v^3),
+// evaluated through the identity 0.5 (1 + tanh(u)) = 1 / (1 + e^(-2u)):
+//   v / (1 + 2^(v (c0 + c1 v^2))),  c0 = -2 sqrt(2/pi) log2(e),  c1 = 0.044715 c0,
+// five VALU operations and two transcendentals (v_exp_f32, v_rcp_f32).  For
+// v -> -inf the power overflows to +inf and the result is -0; for v -> +inf it
+// is v.  Relative error is a few ulp of fp32.
+__device__ __forceinline__ float gelu_tanh(float v) {
+  constexpr float c0 = -2.f * 0.7978845608028654f * 1.4426950408889634f;
+  constexpr float c1 = 0.044715f * c0;
+  const float z = v * __builtin_fmaf(c1, v * v, c0);
+  return v * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(z));
+}
+
 __device__ __forceinline__ float apply_act(float v, int act) {
   if (act == ACT_RELU) return v > 0.f ? v : 0.f;
-  if (act == ACT_GELU_TANH) {
-    const float c = 0.7978845608028654f;  // sqrt(2/pi)
-    return 0.5f * v * (1.f + tanhf(c * (v + 0.044715f * v * v * v)));
-  }
+  if (act == ACT_GELU_TANH) return gelu_tanh(v);
   if (act == ACT_SIGMOID) return 1.f / (1.f + expf(-v));
   return v;
 }

@@ -25,6 +25,7 @@ __all__ = [
     "mgn_mlp", "mgn_mlp_out", "IMPL_FUSED", "IMPL_PIPELINED", "IMPL_PIPELINED_SPLIT_LN", "GpipesError",
     "linear_out", "linear_layer_norm_out", "layer_norm_out", "add_out", "concat_out", "pipe_ident",
     "pipeline_check", "ACTS", "mgn_edge_gather", "mgn_edge_gather_out", "pipe_route", "ROUTES",
+    "gemm_out", "bert_ffn", "bert_ffn_out",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -73,7 +74,9 @@ def _load():
     L.gp_pipeline_check.argtypes = [vp]
     L.gp_mgn_edge_gather_out.argtypes = [i64, i64, vp, vp, vp, vp, i32] + [vp] * 8 + [f32, vp, vp]
     L.gp_mgn_edge_gather_out.restype = i32
-    for name in ("gp_linear_out", "gp_linear_layer_norm_out", "gp_layer_norm_out", "gp_add_out",
+    L.gp_gemm_out.argtypes = [i64, i64, i64, vp, vp, vp, vp, i32, vp, vp]
+    L.gp_bert_ffn_out.argtypes = [i64, i64, i64] + [vp] * 7 + [f32, i32, vp, vp]
+    for name in ("gp_gemm_out", "gp_bert_ffn_out", "gp_linear_out", "gp_linear_layer_norm_out", "gp_layer_norm_out", "gp_add_out",
                  "gp_concat_out", "gp_pipe_ident", "gp_pipeline_check"):
         getattr(L, name).restype = i32
     return L
@@ -336,3 +339,58 @@ def mgn_edge_gather_out(nf, ef, src, dst, w1, b1, w2, b2, w3, b3, gamma, beta, o
 def mgn_edge_gather(nf, ef, src, dst, w1, b1, w2, b2, w3, b3, gamma=None, beta=None, eps=1e-5):
     out = torch.empty((ef.shape[0], 128), dtype=torch.float16, device=ef.device)
     return mgn_edge_gather_out(nf, ef, src, dst, w1, b1, w2, b2, w3, b3, gamma, beta, out, eps=eps)
+
+
+def gemm_out(x, w, b=None, r=None, act="none", out=None):
+    """out[M,N] = act(x @ w + b), or x @ w + b + r -- the wide GEMM stage (any N multiple of
+    128, K multiple of 64): the N-split PipeGemmBiasRelu / PipeGemmBias blocks of
+    apps/bert_ffn/pipelined/bert_ffn_pl.cuh:79-99 and bulksync_gemm."""
+    _check_input("x", x)
+    M, K = x.shape
+    _check_input("w", w)
+    if w.dim() != 2 or w.shape[0] != K:
+        raise RuntimeError(f"w must be [{K}, N]")
+    N = w.shape[1]
+    _opt("b", b, (N,))
+    _opt("r", r, (M, N))
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    _check_input("out", out, (M, N))
+    with torch.cuda.device(x.device):
+        _check(lib.gp_gemm_out(M, N, K, _ptr(x), _ptr(w), _ptr(b), _ptr(r), ACTS.get(act, act), _ptr(out),
+                               _stream(x)))
+    return out
+
+
+def bert_ffn_out(x, w1, b1, w2, b2, ga, be, out, eps=1e-5, act="relu"):
+    """LayerNorm(Linear2(act(Linear1(x))) + x) into ``out`` -- bert_ffn_out of
+    apps/bert_ffn/pipelined/bert_ffn_pl_ext.cu:24-56 (there H = 128, FF = 512, ReLU,
+    eps 1e-5), for H in {128, 256, 512, 1024} and FF a multiple of 128.  Weights
+    [in, out] = ``nn.Linear.weight.t().contiguous()``; ga / be may be None (1 / 0)."""
+    _check_input("x", x)
+    if x.dim() != 2:
+        raise RuntimeError("x must be 2-D [M, H]")
+    M, H = x.shape
+    _check_input("w1", w1)
+    if w1.dim() != 2 or w1.shape[0] != H:
+        raise RuntimeError(f"w1 must be [{H}, FF]")
+    FF = w1.shape[1]
+    _opt("b1", b1, (FF,))
+    _check_input("w2", w2, (FF, H))
+    _opt("b2", b2, (H,))
+    _opt("ga", ga, (H,))
+    _opt("be", be, (H,))
+    _check_input("out", out, (M, H))
+    devs = {t.device for t in (x, w1, b1, w2, b2, ga, be, out) if t is not None}
+    if len(devs) != 1:
+        raise RuntimeError("all tensors must be on the same device")
+    with torch.cuda.device(x.device):
+        _check(lib.gp_bert_ffn_out(M, H, FF, _ptr(x), _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2), _ptr(ga), _ptr(be),
+                                   float(eps), ACTS.get(act, act), _ptr(out), _stream(x)))
+    return out
+
+
+def bert_ffn(x, w1, b1, w2, b2, ga, be, eps=1e-5, act="relu"):
+    """Allocating form (bert_ffn_pl_ext.cu:59-72)."""
+    out = torch.zeros_like(x)
+    return bert_ffn_out(x, w1, b1, w2, b2, ga, be, out, eps=eps, act=act)

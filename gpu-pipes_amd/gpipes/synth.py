@@ -1,4 +1,4 @@
-"""Deterministic synthetic inputs for the MGN MLP workloads.
+"""Deterministic synthetic inputs for the MGN MLP and BERT FFN workloads.
 
 Parameters follow torch.nn defaults, which is what the workload definition
 asks for: Linear weights Kaiming-uniform(a=sqrt(5)) = U(+-1/sqrt(fan_in)),
@@ -33,6 +33,34 @@ def mgn_params(K, seed=0, layernorm=True, device="cpu", affine_random=False):
         "beta": h(lnm.bias) if lnm is not None else None,
     }
     return p
+
+
+def bert_params(H, FF, seed=0, init="bert", device="cpu", affine_random=False):
+    """Parameters of the BERT FFN block (Linear(H, FF), Linear(FF, H), LayerNorm(H))
+    in kernel layout.  init="bert": weights ~ N(0, 0.02), biases 0 (the BERT-large
+    workload); init="torch": nn.Linear defaults, as apps/bert_ffn/torch/model.py:3-11
+    builds them.  LayerNorm gamma = 1, beta = 0 unless affine_random."""
+    with torch.random.fork_rng(devices=[]):
+        torch.manual_seed(seed)
+        l1 = torch.nn.Linear(H, FF)
+        l2 = torch.nn.Linear(FF, H)
+        lnm = torch.nn.LayerNorm(H)
+        with torch.no_grad():
+            if init == "bert":
+                for lin in (l1, l2):
+                    lin.weight.normal_(0.0, 0.02)
+                    lin.bias.zero_()
+            elif init != "torch":
+                raise ValueError(f"unknown init {init!r}")
+            if affine_random:
+                lnm.weight.uniform_(0.5, 1.5)
+                lnm.bias.uniform_(-0.5, 0.5)
+
+    def h(t):
+        return t.detach().to(torch.float16).contiguous().to(device)
+
+    return {"w1": h(l1.weight.t()), "b1": h(l1.bias), "w2": h(l2.weight.t()), "b2": h(l2.bias),
+            "gamma": h(lnm.weight), "beta": h(lnm.bias)}
 
 
 def normal_fp16(M, K, seed=0, device="cpu"):

@@ -101,6 +101,24 @@ int gp_mgn_edge_gather_out(int64_t E, int64_t N, const void* nf, const void* ef,
                            const void* w3, const void* b3, const void* gamma, const void* beta, float eps, void* out,
                            void* stream);
 
+/*
+ * BERT feed-forward block with residual add and LayerNorm:
+ *   out[M,H] = LayerNorm(act(x . w1 + b1) . w2 + b2 + x) * gamma + beta
+ * with w1 [H,FF], b1 [FF], w2 [FF,H], b2 [H], gamma / beta [H] (NULL: 1 / 0),
+ * act GP_ACT_RELU (the reference app) or GP_ACT_GELU_TANH (BERT-large), eps
+ * as given.  H in {128, 256, 512, 1024}; FF a multiple of 128, at most 16384.
+ * Replaces bert_ffn_out(x, w1, b1, w2, b2, ga, be, out),
+ * apps/bert_ffn/pipelined/bert_ffn_pl_ext.cu:24-56 (H = 128, FF = 512, ReLU,
+ * eps 1e-5 fixed), and the bulk-sync chain gemm / gemm / add / LayerNorm of
+ * apps/bert_ffn/bulksync/bert_ffn_bs.cuh:12-27.  The FF-wide activations pass
+ * through a workspace kept per (device, stream), allocated on first use and
+ * grown when needed (a grow synchronises the stream).  Any M >= 0 (the
+ * reference needs M to be a multiple of its pipeline rows x 128).
+ */
+int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void* w1, const void* b1,
+                    const void* w2, const void* b2, const void* gamma, const void* beta, float eps, int act,
+                    void* out, void* stream);
+
 /* ------------------------------------------------------------------------
  * Stage-level entry points: one stage function of the library run over a
  * whole matrix (tiles of 128 rows, persistent workgroups).
@@ -123,6 +141,19 @@ int gp_linear_out(int64_t M, int64_t K, const void* x, const void* w, const void
  */
 int gp_linear_layer_norm_out(int64_t M, int64_t K, const void* x, const void* w, const void* b,
                              const void* gamma, const void* beta, float eps, void* out, void* stream);
+
+/*
+ * The wide GEMM stage: out[M,N] = act(x[M,K] . w[K,N] + b), or, with r
+ * non-NULL, x . w + b + r[M,N] (act must then be GP_ACT_NONE).  N a multiple
+ * of 128, K a multiple of 64 (both at most 16384); b may be NULL.  The
+ * PipeGemmBiasRelu / PipeGemmBias blocks composed along N and K with the
+ * residual as accumulator (apps/bert_ffn/pipelined/bert_ffn_pl.cuh:79-99,
+ * common/pipe_gemm.cuh:128-146), and bulksync_gemm<M,N,K,RELU>
+ * (common/bulksync_gemm.cuh:13-110) beyond the 128-wide stage of
+ * gp_linear_out.  w is transposed into the per-stream workspace on each call.
+ */
+int gp_gemm_out(int64_t M, int64_t N, int64_t K, const void* x, const void* w, const void* b, const void* r,
+                int act, void* out, void* stream);
 
 /*
  * out[M,D] = LayerNorm(x[M,D]) * gamma + beta, biased variance, eps as given;

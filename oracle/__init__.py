@@ -34,6 +34,7 @@ def lib():
         L.oracle_linear.argtypes = [i64, i64, i64, vp, vp, vp, i32, vp]
         L.oracle_layer_norm.argtypes = [i64, i64, vp, vp, vp, f32, vp]
         L.oracle_mgn_mlp.argtypes = [i64, i64] + [vp] * 9 + [f32, vp, vp]
+        L.oracle_bert_ffn.argtypes = [i64, i64, i64] + [vp] * 7 + [i32, f32, vp, vp]
         L.oracle_add.argtypes = [i64, vp, vp, vp]
         L.oracle_concat.argtypes = [i64, i64, i64, vp, vp, vp]
         L.oracle_num_threads.restype = i32
@@ -92,6 +93,21 @@ def mgn_mlp(x, w1, b1, w2, b2, w3, b3, gamma=None, beta=None, eps=1e-5):
     out = np.empty((M, 128), np.float32)
     work = np.empty((2 * M * 128,), np.float32)
     lib().oracle_mgn_mlp(M, K, _p(x), *[_p(a) for a in ws], _p(g), _p(bt), eps, _p(out), _p(work))
+    return out
+
+
+def bert_ffn(x, w1, b1, w2, b2, gamma=None, beta=None, act=ACT_RELU, eps=1e-5):
+    """BertFfn forward, LayerNorm(Linear2(act(Linear1(x))) + x), in fp32.
+
+    apps/bert_ffn/torch/model.py:3-14; weights stored [in, out].
+    """
+    x = _f32(x)
+    M, H = x.shape
+    FF = np.asarray(w1).shape[1]
+    ws = [_f32(a) for a in (w1, b1, w2, b2, gamma, beta)]
+    out = np.empty((M, H), np.float32)
+    work = np.empty((M * (FF + H),), np.float32)
+    lib().oracle_bert_ffn(M, H, FF, _p(x), *[_p(a) for a in ws], act, eps, _p(out), _p(work))
     return out
 
 

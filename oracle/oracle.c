@@ -182,6 +182,26 @@ void oracle_mgn_mlp(int64_t M, int64_t K, const float* x, const float* w1, const
   }
 }
 
+/*
+ * BertFfn forward, apps/bert_ffn/torch/model.py:3-14: ln(ffn(x) + x) with
+ * ffn = Linear(H, FF) -> activation -> Linear(FF, H).  The reference app uses
+ * ReLU and LayerNorm eps 1e-5 (model.py:8,11; common/layer_norm_v2.cuh:62);
+ * the BERT-large workload uses GELU(tanh) and eps 1e-12, so both are
+ * parameters.  In the reference's pipelined kernel the residual enters as the
+ * accumulator of the second GEMM (apps/bert_ffn/pipelined/bert_ffn_pl.cuh:
+ * 90-99), which is the same sum.  `work` must hold M*FF + M*H floats.
+ */
+void oracle_bert_ffn(int64_t M, int64_t H, int64_t FF, const float* x, const float* w1, const float* b1,
+                     const float* w2, const float* b2, const float* gamma, const float* beta, int act,
+                     float eps, float* out, float* work) {
+  float* h = work;
+  float* y = work + M * FF;
+  oracle_linear(M, H, FF, x, w1, b1, act, h);
+  oracle_linear(M, FF, H, h, w2, b2, ORACLE_ACT_NONE, y);
+  for (int64_t i = 0; i < M * H; ++i) y[i] += x[i];
+  oracle_layer_norm(M, H, y, gamma, beta, eps, out);
+}
+
 /* c = a + b elementwise, common/elemwise_add.cuh:5-21 (fp32 here). */
 void oracle_add(int64_t n, const float* a, const float* b, float* c) {
   for (int64_t i = 0; i < n; ++i) c[i] = a[i] + b[i];

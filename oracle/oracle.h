@@ -25,6 +25,9 @@ void oracle_layer_norm(int64_t M, int64_t D, const float* x, const float* gamma,
 void oracle_mgn_mlp(int64_t M, int64_t K, const float* x, const float* w1, const float* b1,
                     const float* w2, const float* b2, const float* w3, const float* b3,
                     const float* gamma, const float* beta, float eps, float* out, float* work);
+void oracle_bert_ffn(int64_t M, int64_t H, int64_t FF, const float* x, const float* w1, const float* b1,
+                     const float* w2, const float* b2, const float* gamma, const float* beta, int act,
+                     float eps, float* out, float* work);
 void oracle_add(int64_t n, const float* a, const float* b, float* c);
 void oracle_concat(int64_t M, int64_t N0, int64_t N1, const float* a, const float* b, float* c);
 

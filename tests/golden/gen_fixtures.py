@@ -11,6 +11,13 @@ here from first principles:
   evaluated in float64 on the fp16-rounded values -- an implementation
   independent of both the C oracle and the HIP kernels.
 
+The BERT FFN fixtures follow the module structure of
+apps/bert_ffn/torch/model.py:3-14 (Linear -> activation -> Linear, + x,
+LayerNorm), once with the reference app's shape and defaults (H 128, FF 512,
+ReLU, eps 1e-5, nn.Linear init) and once with the BERT-large recipe (GELU(tanh),
+eps 1e-12, N(0, 0.02) weights, zero biases) at a small width; expected outputs
+are again the torch.nn modules in float64.
+
 The LayerNorm fixture uses the literal 128-value input row that the
 reference's own LayerNorm check types in (misc_tests/layer_norm/torch_val.py:88-105,
 repeated over 128 rows there, gamma = 1, beta = 0); its expected output is
@@ -29,7 +36,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, os.path.join(ROOT, "gpu-pipes_amd"))
-from gpipes.synth import mgn_params, normal_fp16  # noqa: E402
+from gpipes.synth import bert_params, mgn_params, normal_fp16  # noqa: E402
 
 M_FIX = 256
 
@@ -85,6 +92,38 @@ def make_mgn_fixture(name, K, layernorm, seed, affine_random, eps=1e-5):
     return path
 
 
+def torch_bert_ffn_f64(x16, p, act, eps):
+    """BERT FFN block, LayerNorm(Linear2(act(Linear1(x))) + x), with torch.nn
+    library modules in float64 (the module structure of
+    apps/bert_ffn/torch/model.py:3-14, activation and eps as given)."""
+    H, FF = p["w1"].shape
+    a = torch.nn.ReLU() if act == "relu" else torch.nn.GELU(approximate="tanh")
+    ffn = torch.nn.Sequential(torch.nn.Linear(H, FF), a, torch.nn.Linear(FF, H)).double()
+    ln = torch.nn.LayerNorm(H, eps=eps).double()
+    with torch.no_grad():
+        ffn[0].weight.copy_(p["w1"].double().t())
+        ffn[0].bias.copy_(p["b1"].double())
+        ffn[2].weight.copy_(p["w2"].double().t())
+        ffn[2].bias.copy_(p["b2"].double())
+        ln.weight.copy_(p["gamma"].double())
+        ln.bias.copy_(p["beta"].double())
+        xd = x16.double()
+        return ln(ffn(xd) + xd)
+
+
+def make_bert_fixture(name, M, H, FF, act, eps, init, seed, affine_random):
+    p = bert_params(H, FF, seed=seed, init=init, affine_random=affine_random)
+    x = normal_fp16(M, H, seed=seed + 1000)
+    y = torch_bert_ffn_f64(x, p, act, eps)
+    arrs = {"x": x.numpy(), "expected": y.numpy().astype(np.float32), "eps": np.float64(eps),
+            "act": np.array(act)}
+    for k, v in p.items():
+        arrs[k] = v.numpy()
+    path = os.path.join(HERE, f"{name}.npz")
+    np.savez_compressed(path, **arrs)
+    return path
+
+
 def make_ln_fixture():
     row = torch.tensor(LN_ROW, dtype=torch.float16)
     x = row.repeat(128, 1)
@@ -102,6 +141,11 @@ def main():
         make_mgn_fixture("mgn_edge_linears", 384, False, seed=2, affine_random=False),
         make_mgn_fixture("mgn_node_ln", 256, True, seed=3, affine_random=True),
         make_ln_fixture(),
+        # the reference app's shape and defaults (H 128, FF 512, ReLU, eps 1e-5)
+        make_bert_fixture("bert_ffn_relu", 256, 128, 512, "relu", 1e-5, "torch", seed=10, affine_random=False),
+        # the BERT-large recipe (GELU(tanh), eps 1e-12, N(0, 0.02) weights) at a small width
+        make_bert_fixture("bert_ffn_gelu", 128, 256, 512, "gelu_tanh", 1e-12, "bert", seed=11,
+                          affine_random=True),
     ]
     manifest = {}
     for pth in paths:

@@ -1,0 +1,151 @@
+"""GPU parity of the wide GEMM stage (gp_gemm_out) and the BERT FFN block
+(gp_bert_ffn_out): LayerNorm(Linear2(act(Linear1(x))) + x).
+
+Checked against the golden fixtures (torch.nn modules in float64) and the CPU
+oracle at the fp16 I/O bar (max-abs 2e-2, relative-L2 5e-3).  At the full
+BERT-large size (M = 65,536) the oracle checks a sample of rows, and two
+size-independent properties are asserted: every row is computed independently,
+so the rows of a small batch are bit-identical to the same rows inside a large
+(chunked) batch; and with gamma = 1, beta = 0 every output row has mean 0 and
+variance var / (var + eps) of its pre-LayerNorm row (~1).
+"""
+import numpy as np
+import pytest
+import torch
+
+import gpipes
+import oracle
+from conftest import load_golden
+from gpipes.synth import bert_params, normal_fp16
+
+pytestmark = pytest.mark.gpu
+
+ACT_ID = {"relu": oracle.ACT_RELU, "gelu_tanh": oracle.ACT_GELU_TANH, "none": oracle.ACT_NONE,
+          "sigmoid": oracle.ACT_SIGMOID}
+
+
+def assert_parity(got, want, what):
+    max_abs, rel = oracle.errors(got, want)
+    print(f"[parity] {what}: max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
+    assert max_abs <= oracle.MAX_ABS_TOL and rel <= oracle.REL_L2_TOL, (what, max_abs, rel)
+
+
+def f(t):
+    return None if t is None else t.detach().float().cpu().numpy()
+
+
+def dev(p, cuda):
+    return {k: (None if v is None else v.to(cuda)) for k, v in p.items()}
+
+
+def ffn(x, p, act, eps):
+    return gpipes.bert_ffn(x, p["w1"], p["b1"], p["w2"], p["b2"], p["gamma"], p["beta"], eps=eps, act=act)
+
+
+def oracle_ffn(x, p, act, eps):
+    return oracle.bert_ffn(f(x), f(p["w1"]), f(p["b1"]), f(p["w2"]), f(p["b2"]), f(p["gamma"]), f(p["beta"]),
+                           act=ACT_ID[act], eps=eps)
+
+
+# ------------------------------------------------------------------ golden fixtures
+@pytest.mark.parametrize("name", ["bert_ffn_relu.npz", "bert_ffn_gelu.npz"])
+def test_bert_ffn_golden(cuda, name):
+    z = load_golden(name)
+    p = {k: torch.from_numpy(z[k]).to(cuda) for k in ("w1", "b1", "w2", "b2", "gamma", "beta")}
+    y = ffn(torch.from_numpy(z["x"]).to(cuda), p, str(z["act"]), float(z["eps"]))
+    assert_parity(f(y), z["expected"], f"golden {name}")
+
+
+def test_bert_ffn_reference_signature(cuda):
+    """bert_ffn(x, w1, b1, w2, b2, ga, be) with the reference app's defaults
+    (apps/bert_ffn/pipelined/val.py:8-22: M = 64 x 512, H 128, FF 512, ReLU)."""
+    M = 64 * 512
+    p = dev(bert_params(128, 512, seed=3, init="torch"), cuda)
+    x = normal_fp16(M, 128, seed=4, device=cuda)
+    y = gpipes.bert_ffn(x, p["w1"], p["b1"], p["w2"], p["b2"], p["gamma"], p["beta"])
+    assert_parity(f(y), oracle_ffn(x, p, "relu", 1e-5), "reference app shape")
+
+
+# ------------------------------------------------------------------ shapes vs oracle
+@pytest.mark.parametrize("M,H,FF,act", [
+    (1, 128, 512, "relu"), (300, 128, 512, "relu"), (257, 256, 1024, "gelu_tanh"), (129, 512, 2048, "gelu_tanh"),
+    (1000, 1024, 4096, "gelu_tanh"), (77, 1024, 128, "relu"), (513, 128, 384, "gelu_tanh"),
+])
+def test_bert_ffn_vs_oracle(cuda, M, H, FF, act):
+    p = dev(bert_params(H, FF, seed=M + H, init="bert", affine_random=True), cuda)
+    x = normal_fp16(M, H, seed=M, device=cuda)
+    eps = 1e-12 if act == "gelu_tanh" else 1e-5
+    assert_parity(f(ffn(x, p, act, eps)), oracle_ffn(x, p, act, eps), f"bert_ffn M={M} H={H} FF={FF} {act}")
+
+
+def test_bert_ffn_no_affine_no_bias(cuda):
+    M, H, FF = 200, 256, 512
+    p = dev(bert_params(H, FF, seed=5, init="torch"), cuda)
+    x = normal_fp16(M, H, seed=6, device=cuda)
+    y = gpipes.bert_ffn(x, p["w1"], None, p["w2"], None, None, None, eps=1e-12, act="gelu_tanh")
+    want = oracle.bert_ffn(f(x), f(p["w1"]), None, f(p["w2"]), None, None, None, act=oracle.ACT_GELU_TANH,
+                           eps=1e-12)
+    assert_parity(f(y), want, "no biases, no affine")
+
+
+# ------------------------------------------------------------------ full size (config 2)
+def test_bert_large_full_size(cuda):
+    """M = 65,536 (128 x 512 tokens), H 1024, FF 4096, GELU(tanh), eps 1e-12: four
+    16,384-row chunks.  Oracle on sampled rows (first, chunk edges, last), bit
+    identity of a small batch with the same rows of the large one, and the
+    LayerNorm row statistics."""
+    M, H, FF = 65536, 1024, 4096
+    p = dev(bert_params(H, FF, seed=0, init="bert"), cuda)
+    x = normal_fp16(M, H, seed=0, device=cuda)
+    y = ffn(x, p, "gelu_tanh", 1e-12)
+    torch.cuda.synchronize()
+    rows = np.r_[0:64, 16320:16448, 32700:32800, M - 64:M]
+    assert_parity(f(y)[rows], oracle_ffn(x[rows], p, "gelu_tanh", 1e-12), "BERT-large sampled rows")
+    small = ffn(x[:1000].contiguous(), p, "gelu_tanh", 1e-12)
+    assert torch.equal(small.view(torch.int16), y[:1000].view(torch.int16))
+    tail = ffn(x[16000:17000].contiguous(), p, "gelu_tanh", 1e-12)  # crosses a chunk edge in the big batch
+    assert torch.equal(tail.view(torch.int16), y[16000:17000].view(torch.int16))
+    yf = y.float()
+    assert torch.isfinite(yf).all()
+    assert yf.mean(dim=1).abs().max().item() < 1e-2
+    assert (yf.var(dim=1, unbiased=False) - 1).abs().max().item() < 2e-2
+
+
+# ------------------------------------------------------------------ wide GEMM stage
+@pytest.mark.parametrize("M,N,K", [(1, 128, 64), (255, 256, 128), (257, 384, 1024), (1000, 4096, 1024),
+                                   (513, 1024, 4096), (64, 128, 4096)])
+@pytest.mark.parametrize("act", ["none", "relu", "gelu_tanh", "sigmoid"])
+def test_gemm_vs_oracle(cuda, M, N, K, act):
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    x = torch.randn((M, K), generator=g).to(torch.float16)
+    w = (torch.randn((K, N), generator=g) / np.sqrt(K)).to(torch.float16)
+    b = (torch.randn((N,), generator=g) * 0.5).to(torch.float16)
+    y = gpipes.gemm_out(x.to(cuda), w.to(cuda), b.to(cuda), act=act)
+    assert_parity(f(y), oracle.linear(f(x), f(w), f(b), ACT_ID[act]), f"gemm M={M} N={N} K={K} {act}")
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 128, 512), (1000, 1024, 4096)])
+def test_gemm_residual(cuda, M, N, K):
+    g = torch.Generator().manual_seed(M + N)
+    x = torch.randn((M, K), generator=g).to(torch.float16)
+    w = (torch.randn((K, N), generator=g) / np.sqrt(K)).to(torch.float16)
+    b = (torch.randn((N,), generator=g) * 0.5).to(torch.float16)
+    r = torch.randn((M, N), generator=g).to(torch.float16)
+    y = gpipes.gemm_out(x.to(cuda), w.to(cuda), b.to(cuda), r.to(cuda))
+    assert_parity(f(y), oracle.linear(f(x), f(w), f(b)) + f(r), f"gemm+residual M={M} N={N} K={K}")
+    y0 = gpipes.gemm_out(x.to(cuda), w.to(cuda), None, r.to(cuda))
+    assert_parity(f(y0), oracle.linear(f(x), f(w), None) + f(r), f"gemm+residual no bias M={M}")
+
+
+def test_gemm_identity_weight_is_exact(cuda):
+    """x . I (+ 0) passes every fp16 value through the fp32 accumulator unchanged."""
+    M, K = 700, 256
+    x = normal_fp16(M, K, seed=9, device=cuda)
+    x = torch.where(x.abs() < 2.0 ** -14, torch.zeros_like(x), x)  # no fp16 subnormals
+    eye = torch.eye(K, dtype=torch.float16, device=cuda)
+    y = gpipes.gemm_out(x, eye)
+    assert torch.equal(y.view(torch.int16), x.view(torch.int16))
+    # a column permutation is exact as well: catches a transposed or shuffled operand
+    perm = torch.randperm(K, generator=torch.Generator().manual_seed(1)).to(cuda)
+    y = gpipes.gemm_out(x, eye[:, perm].contiguous())
+    assert torch.equal(y.view(torch.int16), x[:, perm].contiguous().view(torch.int16))

@@ -107,3 +107,39 @@ int main() {
     assert r.returncode == 0, r.stderr
     code, msg = r.stdout.strip().split("|", 1)
     assert int(code) < 0 and "gpipes error" in msg
+
+
+def _ffn(M=16, H=1024, FF=4096, x=16, w1=16, b1=16, w2=16, b2=16, g=16, bt=16, eps=1e-12, act=2, out=16):
+    """Call gp_bert_ffn_out with fake (never dereferenced) pointers."""
+    vp = ctypes.c_void_p
+    P = lambda v: vp(v) if v else None  # noqa: E731
+    return gpipes.lib.gp_bert_ffn_out(M, H, FF, P(x), P(w1), P(b1), P(w2), P(b2), P(g), P(bt), eps, act, P(out),
+                                      None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(H=768), -2), (dict(H=64), -2), (dict(FF=100), -2), (dict(FF=32768), -2), (dict(FF=0), -2),
+    (dict(M=-1), -1), (dict(w1=0), -1), (dict(w2=0), -1), (dict(x=0), -1), (dict(out=0), -1),
+    (dict(act=9), -1), (dict(eps=-1.0), -1), (dict(eps=float("nan")), -1),
+    (dict(x=24), -3), (dict(out=8), -3), (dict(w1=40), -3), (dict(b2=8), -3), (dict(g=8), -3),
+])
+def test_bert_ffn_argument_errors(kw, code):
+    assert _ffn(**kw) == code
+    assert gpipes.lib.gp_last_error().decode() != ""
+
+
+def test_bert_ffn_empty_batch_is_a_noop():
+    assert _ffn(M=0, x=0, out=0) == 0
+    assert gpipes.lib.gp_last_error().decode() == ""
+
+
+@pytest.mark.parametrize("M,N,K,x,w,r,act,out,code", [
+    (16, 100, 128, 16, 16, 0, 0, 16, -2), (16, 128, 96, 16, 16, 0, 0, 16, -2), (16, 32768, 128, 16, 16, 0, 0, 16, -2),
+    (-1, 128, 128, 16, 16, 0, 0, 16, -1), (16, 128, 128, 16, 0, 0, 0, 16, -1), (16, 128, 128, 16, 16, 16, 1, 16, -1),
+    (16, 128, 128, 8, 16, 0, 0, 16, -3), (16, 128, 128, 16, 16, 8, 0, 16, -3), (16, 128, 128, 16, 16, 0, 7, 16, -1),
+    (0, 128, 128, 0, 16, 0, 0, 0, 0),
+])
+def test_gemm_argument_errors(M, N, K, x, w, r, act, out, code):
+    vp = ctypes.c_void_p
+    P = lambda v: vp(v) if v else None  # noqa: E731
+    assert gpipes.lib.gp_gemm_out(M, N, K, P(x), P(w), None, P(r), act, P(out), None) == code

@@ -11,6 +11,12 @@ its own formula:
   * mgn_mlp            -- golden fixtures made by torch.nn modules in float64,
                           closed forms (zero weights -> beta; identity weights ->
                           LN(relu(x[:, :128]))), and planted mistakes that must fail
+  * bert_ffn           -- golden fixtures made by torch.nn modules in float64
+                          (ReLU / eps 1e-5 and GELU(tanh) / eps 1e-12), closed forms
+                          (w2 = 0 -> LN(x + b2); constant rows -> beta; GELU(tanh)
+                          told apart from erf GELU), planted mistakes (no residual,
+                          residual after LN, transposed w2, ReLU for GELU, wrong
+                          eps) that must fail
   * add / concat       -- numpy
 """
 import numpy as np
@@ -206,3 +212,76 @@ def test_errors_helper():
     assert oracle.errors(e, e) == (0.0, 0.0)
     ma, rel = oracle.errors(np.array([3.0, 4.5]), e)
     assert ma == pytest.approx(0.5) and rel == pytest.approx(0.1)
+
+
+BERT_FIXTURES = ["bert_ffn_relu.npz", "bert_ffn_gelu.npz"]
+
+
+def _bert_args(z):
+    p = {k: z[k].astype(np.float32) for k in ("x", "w1", "b1", "w2", "b2", "gamma", "beta")}
+    act = oracle.ACT_RELU if str(z["act"]) == "relu" else oracle.ACT_GELU_TANH
+    return p, act, float(z["eps"])
+
+
+@pytest.mark.parametrize("name", BERT_FIXTURES)
+def test_bert_ffn_golden(name):
+    z = load_golden(name)
+    p, act, eps = _bert_args(z)
+    got = oracle.bert_ffn(p["x"], p["w1"], p["b1"], p["w2"], p["b2"], p["gamma"], p["beta"], act=act, eps=eps)
+    max_abs, rel = oracle.errors(got, z["expected"])
+    assert max_abs < 2e-4 and rel < 1e-5, (max_abs, rel)
+
+
+@pytest.mark.parametrize("mutant", ["no_residual", "residual_after_ln", "w2_transposed_blocks", "relu_for_gelu",
+                                    "eps_1e-5_instead"])
+def test_bert_ffn_golden_rejects_planted_mistakes(mutant):
+    """Plausible oracle mistakes must fail the GELU / eps 1e-12 fixture at the parity bar."""
+    z = load_golden("bert_ffn_gelu.npz")
+    p, act, eps = _bert_args(z)
+    x, w1, b1, w2, b2, g, bt = (p[k] for k in ("x", "w1", "b1", "w2", "b2", "gamma", "beta"))
+    h = oracle.linear(x, w1, b1, act)
+    if mutant == "no_residual":
+        got = oracle.layer_norm(oracle.linear(h, w2, b2), g, bt, eps)
+    elif mutant == "residual_after_ln":
+        got = oracle.layer_norm(oracle.linear(h, w2, b2), g, bt, eps) + x
+    elif mutant == "w2_transposed_blocks":
+        FF, H = w2.shape  # read w2 as if it were stored [H, FF] in blocks
+        got = oracle.bert_ffn(x, w1, b1, w2.reshape(H, FF).T.copy(), b2, g, bt, act=act, eps=eps)
+    elif mutant == "relu_for_gelu":
+        got = oracle.bert_ffn(x, w1, b1, w2, b2, g, bt, act=oracle.ACT_RELU, eps=eps)
+    else:
+        # eps too large for rows whose pre-LN variance is tiny: make them tiny
+        got = oracle.bert_ffn(x * 1e-3, w1, b1, w2, b2, g, bt, act=act, eps=1e-5)
+        want = oracle.bert_ffn(x * 1e-3, w1, b1, w2, b2, g, bt, act=act, eps=eps)
+        max_abs, rel = oracle.errors(got, want)
+        assert max_abs > oracle.MAX_ABS_TOL or rel > oracle.REL_L2_TOL, (mutant, max_abs, rel)
+        return
+    max_abs, rel = oracle.errors(got, z["expected"])
+    assert max_abs > oracle.MAX_ABS_TOL or rel > oracle.REL_L2_TOL, (mutant, max_abs, rel)
+
+
+def test_bert_ffn_closed_forms():
+    M, H, FF = 24, 128, 256
+    x = RNG.standard_normal((M, H)).astype(np.float32)
+    w1 = RNG.standard_normal((H, FF)).astype(np.float32) * 0.05
+    b1 = RNG.standard_normal(FF).astype(np.float32)
+    b2 = RNG.standard_normal(H).astype(np.float32)
+    g = RNG.uniform(0.5, 1.5, H).astype(np.float32)
+    bt = RNG.uniform(-0.5, 0.5, H).astype(np.float32)
+    zero_w2 = np.zeros((FF, H), np.float32)
+    # w2 = 0: the FFN contributes only b2, so out = LN(x + b2)
+    for act in (oracle.ACT_RELU, oracle.ACT_GELU_TANH):
+        got = oracle.bert_ffn(x, w1, b1, zero_w2, b2, g, bt, act=act, eps=1e-12)
+        ref = F.layer_norm(torch.from_numpy(x + b2).double(), [H], torch.from_numpy(g).double(),
+                           torch.from_numpy(bt).double(), 1e-12).numpy()
+        np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+    # constant x rows and b2 = 0, w2 = 0: variance 0, output exactly beta
+    xc = np.full((3, H), 0.25, np.float32)
+    got = oracle.bert_ffn(xc, w1, b1, zero_w2, np.zeros(H, np.float32), g, bt, act=oracle.ACT_RELU)
+    np.testing.assert_array_equal(got, np.broadcast_to(bt, got.shape))
+    # the hidden activation is GELU(tanh), told apart from exact-erf GELU (which the
+    # end-to-end parity bar cannot resolve: the two differ by < 1e-3)
+    h = oracle.linear(x, w1, b1, oracle.ACT_GELU_TANH)
+    pre = torch.from_numpy(x).double() @ torch.from_numpy(w1).double() + torch.from_numpy(b1).double()
+    np.testing.assert_allclose(h, F.gelu(pre, approximate="tanh").numpy(), rtol=1e-5, atol=1e-6)
+    assert np.abs(h - F.gelu(pre).numpy()).max() > 1e-5
