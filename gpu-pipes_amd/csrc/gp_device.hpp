@@ -128,6 +128,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
 __device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t rsrc, int voffset, GP_LDS void* lds_base) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds_base, 16, voffset, 0, 0, 0);
 }
+// The same with a wave-uniform byte offset in an SGPR (soffset) added to the
+// per-lane voffset.
+__device__ __forceinline__ void dma16_buf_so(__amdgpu_buffer_rsrc_t rsrc, int voffset, int soffset,
+                                             GP_LDS void* lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds_base, 16, voffset, soffset, 0, 0);
+}
 // The same with the non-temporal cache policy (nt): for data read exactly
 // once, which should not displace reusable lines from L2.
 __device__ __forceinline__ void dma16_buf_nt(__amdgpu_buffer_rsrc_t rsrc, int voffset, GP_LDS void* lds_base) {

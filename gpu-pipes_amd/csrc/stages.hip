@@ -4,14 +4,14 @@
 //  * linear_kernel      one pipe_gemm_* stage per workgroup over M rows
 //                       (the bulk-sync GEMM of common/bulksync_gemm.cuh:13-110,
 //                       fp32 accumulation instead of fp16);
-//  * layer_norm_kernel  pipe_layer_norm over M rows (host_layer_norm,
-//                       common/layer_norm_v2.cuh:129-147);
+//  * layer_norm_rows_kernel  LayerNorm over M rows (host_layer_norm,
+//                       common/layer_norm_v2.cuh:129-147), one wave per row;
 //  * add_kernel         pipe_add (host_add2, common/elemwise_add.cuh:42-54);
 //  * concat_kernel      pipe_concat (host_concat2, common/concat.cuh:50-69);
 //  * route_kernel       copy pipelines over the reference's queue topologies:
 //                       1:1 (misc_tests/pipeval/pipe_val_ext.cu:65-149),
 //                       one producer / two consumers, and split / merge.
-// Workgroups are persistent: workgroup b of G handles tiles b, b+G, ...
+// Stage workgroups are persistent: workgroup b of G handles tiles b, b+G, ...
 #include <hip/hip_runtime.h>
 
 #include "../../include/gpipes.h"
@@ -71,17 +71,6 @@ __global__ __launch_bounds__(kStageThreads) void linear_kernel(LinearArgs a) {
   } else {
     pipe_gemm_bias_act<MBLK, K, ACT>(w, b, ir, ar, ow, tw.nt);
   }
-}
-
-template <int D>
-__global__ __launch_bounds__(kStageThreads) void layer_norm_kernel(const half_t* x, const half_t* gamma,
-                                                                   const half_t* beta, float eps, half_t* out,
-                                                                   int64_t M) {
-  const TileWalk tw = tile_walk(M);
-  if (tw.nt == 0) return;
-  MemoryReader ir = tiles_in(x, M, D);
-  MemoryWriter ow = tiles_out(out, D);
-  pipe_layer_norm<MBLK, D>({(half_t*)gamma, 1, 1}, {(half_t*)beta, 1, 1}, ir, ow, tw.nt, eps);
 }
 
 __global__ __launch_bounds__(kStageThreads) void add_kernel(const half_t* a, const half_t* b, half_t* c, int64_t M,
@@ -232,16 +221,66 @@ hipError_t linear_launch(const LinearArgs& a, int num_cus, hipStream_t s) {
   }
 }
 
+// Whole-matrix LayerNorm (host_layer_norm, common/layer_norm_v2.cuh:129-147)
+// with the same arithmetic as pipe_layer_norm, laid out for bandwidth: one
+// wave per row, D/64 consecutive features per lane (one 4- to 32-byte
+// vector), 64-lane butterfly reductions, and up to 32 waves per CU so that
+// many rows' loads are in flight (the kernel is HBM-bound).
+template <int D>
+__global__ __launch_bounds__(kStageThreads) void layer_norm_rows_kernel(const half_t* x, const half_t* gamma,
+                                                                        const half_t* beta, float eps, half_t* out,
+                                                                        int64_t M) {
+  constexpr int EPL = D / kWave;
+  typedef _Float16 hv __attribute__((ext_vector_type(EPL)));
+  const int lane = threadIdx.x & 63;
+  const int64_t step = (int64_t)gridDim.x * (kStageThreads / kWave);
+  hv gv, bv;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    gv[e] = (half_t)1.f;
+    bv[e] = (half_t)0.f;
+  }
+  if (gamma) gv = *(const hv*)(gamma + lane * EPL);
+  if (beta) bv = *(const hv*)(beta + lane * EPL);
+  for (int64_t r = (int64_t)blockIdx.x * (kStageThreads / kWave) + (threadIdx.x >> 6); r < M; r += step) {
+    const hv v = *(const hv*)(x + r * D + lane * EPL);
+    float f[EPL], s = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      f[e] = (float)v[e];
+      s += f[e];
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, kWave);
+    const float mean = s * (1.f / D);
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const float d = f[e] - mean;
+      q = __builtin_fmaf(d, d, q);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) q += __shfl_xor(q, m, kWave);
+    const float rstd = rsqrtf(q * (1.f / D) + eps);
+    hv o;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) o[e] = (half_t)((f[e] - mean) * rstd * (float)gv[e] + (float)bv[e]);
+    *(hv*)(out + r * D + lane * EPL) = o;
+  }
+}
+
 hipError_t layer_norm_launch(int64_t M, int64_t D, const void* x, const void* gamma, const void* beta, float eps,
                              void* out, int num_cus, hipStream_t s) {
-  const dim3 grid(persistent_grid(M, num_cus, 4)), block(kStageThreads);
+  const int64_t rows_per_block = kStageThreads / kWave;
+  const int64_t want = (M + rows_per_block - 1) / rows_per_block, cap = (int64_t)num_cus * 8;
+  const dim3 grid((unsigned)(want < cap ? want : cap)), block(kStageThreads);
   const half_t *hx = (const half_t*)x, *hg = (const half_t*)gamma, *hb = (const half_t*)beta;
   half_t* ho = (half_t*)out;
   switch (D) {
-    case 128: hipLaunchKernelGGL(layer_norm_kernel<128>, grid, block, 0, s, hx, hg, hb, eps, ho, M); break;
-    case 256: hipLaunchKernelGGL(layer_norm_kernel<256>, grid, block, 0, s, hx, hg, hb, eps, ho, M); break;
-    case 512: hipLaunchKernelGGL(layer_norm_kernel<512>, grid, block, 0, s, hx, hg, hb, eps, ho, M); break;
-    case 1024: hipLaunchKernelGGL(layer_norm_kernel<1024>, grid, block, 0, s, hx, hg, hb, eps, ho, M); break;
+    case 128: hipLaunchKernelGGL(layer_norm_rows_kernel<128>, grid, block, 0, s, hx, hg, hb, eps, ho, M); break;
+    case 256: hipLaunchKernelGGL(layer_norm_rows_kernel<256>, grid, block, 0, s, hx, hg, hb, eps, ho, M); break;
+    case 512: hipLaunchKernelGGL(layer_norm_rows_kernel<512>, grid, block, 0, s, hx, hg, hb, eps, ho, M); break;
+    case 1024: hipLaunchKernelGGL(layer_norm_rows_kernel<1024>, grid, block, 0, s, hx, hg, hb, eps, ho, M); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
