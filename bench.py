@@ -8,8 +8,13 @@ stream, the HBM traffic per launch measured with rocprofv3 counters
 (profiles/traffic.json), and the CPU oracle timed on a bounded sample on the
 host cores.
 
-  python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--workload edge|node]
+  python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--workload edge|node|edge_gather|bert]
                   [--impl fused|pipelined|pipelined_split_ln] [--no-cpu]
+
+--workload bert times the BERT-large FFN block of configs[2] instead
+(LayerNorm(GELU(x W1 + b1) W2 + b2 + x), M = 65,536, H 1024, FF 4096): a step is
+one gp_bert_ffn_out call, bound by MFMA, so its roofline is TFLOP/s against the
+dense fp16 peak.
 """
 import argparse
 import json
@@ -35,6 +40,8 @@ WORKLOADS = {
     "edge_gather": (1048576, 384, True),
 }
 GATHER_NODES = 262144
+BERT = {"M": 65536, "H": 1024, "FF": 4096, "eps": 1e-12}
+BERT_METRIC = "rows/sec + % fp16 MFMA peak, BERT-large FFN+residual+LN M=65536 (1×MI355X)"
 
 
 def algorithmic(M, K, ln, gather_nodes=0, idx_bytes=8):
@@ -79,6 +86,99 @@ def cpu_baseline(K, ln, budget_s=10.0):
     }
 
 
+def cpu_baseline_bert(budget_s=10.0):
+    """The CPU oracle's BERT FFN (oracle_bert_ffn, OpenMP over rows) on a row sample."""
+    import numpy as np
+
+    import oracle
+    from gpipes.synth import bert_params, normal_fp16
+
+    threads = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "16") or 16), 16)
+    oracle.set_num_threads(threads)
+    Ms, H, FF = 256, BERT["H"], BERT["FF"]
+    p = {k: v.float().numpy() for k, v in bert_params(H, FF, seed=0).items()}
+    x = normal_fp16(Ms, H, seed=0).float().numpy()
+    run = lambda: oracle.bert_ffn(x, p["w1"], p["b1"], p["w2"], p["b2"], p["gamma"], p["beta"],  # noqa: E731
+                                  act=oracle.ACT_GELU_TANH, eps=BERT["eps"])
+    run()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {
+        "value": Ms / med, "unit": "rows/s", "cores": threads, "kind": "port",
+        "sample": f"oracle/oracle.c BertFfn fp32 on X[{Ms},{H}] (H {H}, FF {FF}, GELU tanh), "
+                  f"{len(times)} calls in {sum(times):.1f} s, median {med * 1e3:.1f} ms/call",
+    }
+
+
+def bench_bert(args):
+    """one gp_bert_ffn_out call over M = 65,536 rows per step."""
+    import torch
+
+    import gpipes
+    from gpipes.synth import bert_params, normal_fp16
+
+    dev = torch.device("cuda:0")
+    M, H, FF, eps = BERT["M"], BERT["H"], BERT["FF"], BERT["eps"]
+    p = {k: v.to(dev) for k, v in bert_params(H, FF, seed=0, init="bert").items()}
+    x = normal_fp16(M, H, seed=0, device=dev)
+    out = torch.empty_like(x)
+
+    def step():
+        gpipes.bert_ffn_out(x, p["w1"], p["b1"], p["w2"], p["b2"], p["gamma"], p["beta"], out, eps=eps,
+                            act="gelu_tanh")
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        step()
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    call_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    avg_ms = sum(call_ms) / len(call_ms)
+    ms_per_step = wall * 1e3 / args.steps
+    flops = 2 * 2 * M * H * FF  # the two GEMMs; GELU, residual and LayerNorm are O(M H) and O(M FF)
+    tflops = flops / (avg_ms * 1e-3) / 1e12
+    bytes_ = (M * H * 2) * 2 + 2 * H * FF * 2 + (FF + 3 * H) * 2  # x in, out, weights, vectors
+    rec = {
+        "metric": BERT_METRIC,
+        "value": M / (ms_per_step * 1e-3),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (X~N(0,1), W~N(0,0.02), b=0, seed 0)",
+        "config": {"workload": "bert_large_ffn", "M": M, "H": H, "FF": FF, "act": "gelu_tanh", "eps": eps,
+                   "layers": f"{H}-{FF}-{H}+residual+LN", "accumulate": "f32", "row_chunk": 16384},
+        "roofline": {
+            "bound": "mfma", "achieved": tflops, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": tflops / MFMA_F16_PEAK_TFLOPS, "traffic": None,
+            "kernel_ms_avg": avg_ms, "kernel_ms_median": call_ms[len(call_ms) // 2],
+            "flops_per_launch": flops, "algorithmic_bytes_per_launch": bytes_,
+            "launch": "one gp_bert_ffn_out call (2 weight transposes, then per 16384-row chunk: "
+                      "GEMM1+bias+GELU, GEMM2+bias+residual, LayerNorm)",
+        },
+        "cpu_baseline": None if args.no_cpu else cpu_baseline_bert(),
+    }
+    print(json.dumps(rec), flush=True)
+
+
 def load_traffic(workload, impl):
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
@@ -93,7 +193,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="edge")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["bert"], default="edge")
     ap.add_argument("--impl", choices=["fused", "pipelined", "pipelined_split_ln"], default="fused")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-ref", action="store_true",
@@ -105,6 +205,10 @@ def main():
         print(f"bench.py measures one GPU only (the path needs no cross-GPU exchange; rows shard "
               f"trivially); --gpus {args.gpus} is not supported.", file=sys.stderr)
         sys.exit(2)
+
+    if args.workload == "bert":
+        bench_bert(args)
+        return
 
     import torch
 
