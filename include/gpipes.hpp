@@ -86,6 +86,19 @@ inline void concat_out(int64_t M, int64_t N0, int64_t N1, const void* a, const v
 // Waits for `stream` and throws if its last pipelined launch failed on the device.
 inline void pipeline_check(void* stream = nullptr) { check(gp_pipeline_check(stream)); }
 
+// bert_ffn_pl_ext.cu:24-56 (H 128, FF 512, ReLU, eps 1e-5 there, the defaults here)
+inline void bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void* w1, const void* b1,
+                         const void* w2, const void* b2, const void* ga, const void* be, void* out,
+                         float eps = 1e-5f, int act = GP_ACT_RELU, void* stream = nullptr) {
+  check(gp_bert_ffn_out(M, H, FF, x, w1, b1, w2, b2, ga, be, eps, act, out, stream));
+}
+
+// the wide GEMM stage (bert_ffn_pl.cuh:79-99, bulksync_gemm)
+inline void gemm_out(int64_t M, int64_t N, int64_t K, const void* x, const void* w, const void* b, const void* r,
+                     int act, void* out, void* stream = nullptr) {
+  check(gp_gemm_out(M, N, K, x, w, b, r, act, out, stream));
+}
+
 }  // namespace gpipes
 
 #endif  // GPIPES_HPP
