@@ -32,7 +32,8 @@ HIP_FLAGS = [
 # MLP kernels.  The wide GEMM keeps its 256 accumulators in AGPRs instead.
 VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 
-SOURCES = ["mgn_fused.hip", "mgn_pipelined.hip", "stages.hip", "gemm.hip", "capi.cpp", "ffn.cpp", "arena.cpp"]
+SOURCES = ["mgn_fused.hip", "mgn_pipelined.hip", "stages.hip", "gemm.hip", "capi.cpp", "ffn.cpp", "mlp.cpp",
+           "arena.cpp"]
 SOURCE_FLAGS = {"gemm.hip": []}
 
 

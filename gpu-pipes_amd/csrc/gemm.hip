@@ -72,14 +72,15 @@ using Wide = Cfg<4, 4, 2>;    // 256 features x 256 rows
 using Narrow = Cfg<4, 2, 1>;  // 128 features x 256 rows
 
 struct Args {
-  const half_t* a;     // [M][K]
+  const half_t* a;     // [M][lda], the first K columns used
   const half_t* bt;    // [N][K]
   const half_t* bias;  // [N] or null
-  const half_t* r;     // [M][N] residual or null
-  half_t* c;           // [M][N]
+  const half_t* r;     // [M][ldr] residual or null
+  half_t* c;           // [M][ldc], the first N columns written
   int64_t M;
   int N;
   int K;
+  int lda, ldc, ldr;   // row strides in elements
 };
 
 // Byte offset of logical 16-byte chunk c of unit row r: the chunk position is
@@ -125,8 +126,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   // lie outside the descriptor's range and read as zero.
   static_assert((RPC * NW / 2) % CPR == 0, "copies of one lane share a swizzle");
   const int vrow = RPC * wave + lane / CPR;
-  const int voff = vrow * K * 2 + (((lane % CPR) ^ ((vrow >> 1) & 7)) << 4);
-  const int jstride = RPC * NW * K * 2;
+  const int vswz = ((lane % CPR) ^ ((vrow >> 1) & 7)) << 4;
+  const int voffa = vrow * p.lda * 2 + vswz, voffb = vrow * K * 2 + vswz;
+  const int jstra = RPC * NW * p.lda * 2, jstrb = RPC * NW * K * 2;
   GP_LDS char* const lds = (GP_LDS char*)ring;
 
   struct Tile {
@@ -141,7 +143,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     T.m0 = (int64_t)tm * C::BM;
     const int64_t mrows = p.M - T.m0;
     T.rows = (int)(mrows < C::BM ? mrows : C::BM);
-    T.ra = make_rsrc(p.a + T.m0 * K, T.rows * K * 2);
+    T.ra = make_rsrc(p.a + T.m0 * p.lda, T.rows * p.lda * 2);
     T.rb = make_rsrc(p.bt + (int64_t)T.n0 * K, C::BN * K * 2);
     return T;
   };
@@ -150,10 +152,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     const int so = (u >> 1) * ROWB;
     if (u & 1) {
 #pragma unroll
-      for (int j = 0; j < C::UB; ++j) dma16_buf_so(T.rb, voff, j * jstride + so, s + (j * NW + wave) * 1024);
+      for (int j = 0; j < C::UB; ++j) dma16_buf_so(T.rb, voffb, j * jstrb + so, s + (j * NW + wave) * 1024);
     } else {
 #pragma unroll
-      for (int j = 0; j < C::UA; ++j) dma16_buf_so(T.ra, voff, j * jstride + so, s + (j * NW + wave) * 1024);
+      for (int j = 0; j < C::UA; ++j) dma16_buf_so(T.ra, voffa, j * jstra + so, s + (j * NW + wave) * 1024);
     }
   };
   auto prefetch = [&](const Tile& T) {
@@ -285,15 +287,19 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     // n0 + 32 NBW wn + 32 nb + 8 g + 4 lh + (0..3).  Output and residual go
     // through buffer descriptors limited to the tile's valid rows; the
     // residual loads of one nb are all issued before the first is used.
-    const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.c + T.m0 * p.N, T.rows * p.N * 2);
-    const __amdgpu_buffer_rsrc_t rr = make_rsrc(RESID ? p.r + T.m0 * p.N : p.c, RESID ? T.rows * p.N * 2 : 0);
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.c + T.m0 * p.ldc, T.rows * p.ldc * 2);
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(RESID ? p.r + T.m0 * p.ldr : p.c, RESID ? T.rows * p.ldr * 2 : 0);
     // Per-row byte offsets, computed here (opaque: not hoisted out of the tile
     // loop as 64 live registers); the nb / g part is an instruction offset.
-    int ebase[C::MBW];
+    int ebase[C::MBW], rbase[C::MBW];
 #pragma unroll
-    for (int mb = 0; mb < C::MBW; ++mb)
-      ebase[mb] = opaque(((arow + 32 * mb) * p.N + T.n0 + 32 * C::NBW * wn + 4 * lh) * 2);
+    for (int mb = 0; mb < C::MBW; ++mb) {
+      const int col = T.n0 + 32 * C::NBW * wn + 4 * lh;
+      ebase[mb] = opaque(((arow + 32 * mb) * p.ldc + col) * 2);
+      rbase[mb] = RESID ? opaque(((arow + 32 * mb) * p.ldr + col) * 2) : 0;
+    }
     auto eoff = [&](int nb, int g, int mb) { return ebase[mb] + (32 * nb + 8 * g) * 2; };
+    auto roff = [&](int nb, int g, int mb) { return rbase[mb] + (32 * nb + 8 * g) * 2; };
 #pragma unroll
     for (int nb = 0; nb < C::NBW; ++nb) {
       // Pin the accumulators of block nb in place until here: the blocks are
@@ -305,7 +311,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 #pragma unroll
         for (int g = 0; g < 4; ++g)
 #pragma unroll
-          for (int mb = 0; mb < C::MBW; ++mb) res[g][mb] = buf_load_h4(rr, eoff(nb, g, mb));
+          for (int mb = 0; mb < C::MBW; ++mb) res[g][mb] = buf_load_h4(rr, roff(nb, g, mb));
       }
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -330,14 +336,18 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   }
 }
 
-// out[N][K] = in[K][N] (fp16), 64 x 64 tiles through LDS; K and N multiples of 64.
-__global__ __launch_bounds__(256) void transpose_kernel(const half_t* in, half_t* out, int K, int N) {
+// out[Np][Kp] = in[K][N] transposed, zero where n >= N or k >= K (fp16),
+// 64 x 64 tiles through LDS; Kp and Np multiples of 64, K <= Kp, N <= Np.
+__global__ __launch_bounds__(256) void transpose_kernel(const half_t* in, half_t* out, int K, int N, int Kp) {
   __shared__ half_t tile[64][66];
   const int k0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int r = ty; r < 64; r += 4) tile[r][tx] = in[(int64_t)(k0 + r) * N + n0 + tx];
+  for (int r = ty; r < 64; r += 4) {
+    const int k = k0 + r, n = n0 + tx;
+    tile[r][tx] = (k < K && n < N) ? in[(int64_t)k * N + n] : (half_t)0.f;
+  }
   __syncthreads();
-  for (int r = ty; r < 64; r += 4) out[(int64_t)(n0 + r) * K + k0 + tx] = tile[tx][r];
+  for (int r = ty; r < 64; r += 4) out[(int64_t)(n0 + r) * Kp + k0 + tx] = tile[tx][r];
 }
 
 template <class C, int ACT, bool RESID>
@@ -366,16 +376,22 @@ hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t s) {
   using namespace gemm;
   if (a.M <= 0) return hipSuccess;
   if (a.N % 128 != 0 || a.K % BK != 0) return hipErrorInvalidValue;
+  const int lda = a.lda ? (int)a.lda : (int)a.K, ldc = a.ldc ? (int)a.ldc : (int)a.N;
+  const int ldr = a.ldr ? (int)a.ldr : (int)a.N;
+  if (lda < a.K || ldc < a.N || (a.r && ldr < a.N) || lda % 8 || ldc % 8 || ldr % 8) return hipErrorInvalidValue;
   const Args g{(const half_t*)a.x, (const half_t*)a.wt, (const half_t*)a.b, (const half_t*)a.r, (half_t*)a.out,
-               a.M, (int)a.N, (int)a.K};
+               a.M, (int)a.N, (int)a.K, lda, ldc, ldr};
   if (a.N % Wide::BN == 0) return dispatch<Wide>(g, a.act, num_cus, s);
   return dispatch<Narrow>(g, a.act, num_cus, s);
 }
 
-hipError_t transpose_launch(const void* in, void* out, int64_t K, int64_t N, hipStream_t s) {
-  if (K % 64 != 0 || N % 64 != 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(gemm::transpose_kernel, dim3((unsigned)(N / 64), (unsigned)(K / 64)), dim3(256), 0, s,
-                     (const half_t*)in, (half_t*)out, (int)K, (int)N);
+hipError_t transpose_launch(const void* in, void* out, int64_t K, int64_t N, hipStream_t s, int64_t Kp,
+                            int64_t Np) {
+  if (Kp == 0) Kp = K;
+  if (Np == 0) Np = N;
+  if (Kp % 64 != 0 || Np % 64 != 0 || K > Kp || N > Np) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(gemm::transpose_kernel, dim3((unsigned)(Np / 64), (unsigned)(Kp / 64)), dim3(256), 0, s,
+                     (const half_t*)in, (half_t*)out, (int)K, (int)N, (int)Kp);
   return hipGetLastError();
 }
 

@@ -54,23 +54,31 @@ hipError_t layer_norm_launch(int64_t M, int64_t D, const void* x, const void* ga
                              void* out, int num_cus, hipStream_t stream);
 hipError_t add_launch(int64_t M, int64_t N, const void* a, const void* b, void* c, int num_cus, hipStream_t stream);
 
-// Wide GEMM stage: out = act(x W + b) or x W + b + r, any N multiple of 128,
-// K multiple of 32, with W passed transposed (wt = W^T, [N, K]).
+// Wide GEMM stage: out = act(x W + b) or x W + b + r, N a multiple of 128,
+// K a multiple of 64, with W passed transposed (wt = W^T, [N, K]).  Row
+// strides (elements, multiples of 8) default to K / N / N when 0; out may be a
+// column block of a wider matrix.
 struct GemmArgs {
   int64_t M;
   int64_t N;
   int64_t K;
-  const void* x;   // [M, K]
+  const void* x;   // [M, lda]
   const void* wt;  // [N, K]
   const void* b;   // [N] or nullptr
-  const void* r;   // [M, N] residual or nullptr (then act must be ACT_NONE)
+  const void* r;   // [M, ldr] residual or nullptr (then act must be ACT_NONE)
   int act;
-  void* out;       // [M, N]
+  void* out;       // [M, ldc]
+  int64_t lda = 0, ldc = 0, ldr = 0;
 };
 hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t stream);
-// out[N, K] = in[K, N]; K and N multiples of 64.
-hipError_t transpose_launch(const void* in, void* out, int64_t K, int64_t N, hipStream_t stream);
+// out[Np, Kp] = in[K, N]^T, zero-padded (Kp, Np default to K, N); Kp and Np
+// multiples of 64.
+hipError_t transpose_launch(const void* in, void* out, int64_t K, int64_t N, hipStream_t stream, int64_t Kp = 0,
+                            int64_t Np = 0);
 hipError_t concat_launch(int64_t M, int64_t N0, int64_t N1, const void* a, const void* b, void* c, int num_cus,
                          hipStream_t stream);
+// dst[m][j] = act(src[m][j]) for j < w and 0 for w <= j < wpad (strides in elements).
+hipError_t place_launch(int64_t M, const void* src, int64_t lds, int64_t w, void* dst, int64_t ldd, int64_t wpad,
+                        int act, int num_cus, hipStream_t stream);
 
 }  // namespace gp

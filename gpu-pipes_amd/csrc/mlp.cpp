@@ -1,0 +1,285 @@
+// C ABI of the dense MLP chains: the DLRM MLPs (gp_mlp_out, gp_dlrm_botmlp_out,
+// gp_dlrm_topmlp_out) and the NeRF MLP (gp_nerf_full_out).
+//
+// The reference builds each app as one pipelined kernel of GEMM stage blocks
+// linked by queues (apps/dlrm_botmlp/pipelined/dlrm_botmlp_pl.cuh:79-137,
+// apps/dlrm_topmlp/pipelined/dlrm_topmlp_pl.cuh:105-187,
+// apps/nerf_full/pipelined/nerf_full_pl.cuh:122-274).  Their layers are 256 to
+// 1024 wide, so the weights (0.34 to 6 MB) cannot stay resident in one CU;
+// here every layer is one launch of the wide GEMM stage (gemm.hip) with its
+// bias and activation fused, over row chunks of 65,536 so that a chunk's
+// activations (at most 128 MiB) can stay in the 256 MB MALL between layers.
+// Narrow and odd widths are handled by padding, never by special kernels:
+//   * weights are transposed into the workspace with zero rows and columns up
+//     to K a multiple of 64 and N a multiple of 128, biases zero-padded to N;
+//   * an input whose width is not a multiple of 64 is copied into a padded
+//     buffer; concatenated inputs ([h | x], [bottleneck | d]) are built in
+//     place -- the GEMM writes h into the first columns of the wider buffer;
+//   * a layer narrower than 128 outputs (the DLRM click head, the NeRF density
+//     and colour heads) runs at 128 and its first columns are copied out.
+// Padded activation columns hold act(0) and meet zero weight rows, so they
+// contribute nothing.
+#include <hip/hip_runtime.h>
+
+#include <vector>
+
+#include "../../include/gpipes.h"
+#include "gp_host.hpp"
+#include "gp_kernels.hpp"
+
+namespace gp {
+namespace {
+
+constexpr int64_t kChunkRows = 65536;
+constexpr int64_t kMaxRows = (int64_t(1) << 31) - 1;  // GEMM tile indices are 32-bit
+constexpr int64_t kMaxWidth = 16384;
+
+int64_t rup(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+// Sequential carving of one workspace allocation (256-byte aligned pieces).
+struct Carve {
+  size_t off = 0;
+  size_t take(size_t bytes) {
+    const size_t o = off;
+    off += (bytes + 255) & ~size_t(255);
+    return o;
+  }
+};
+
+int act_ok(int act) {
+  return act == GP_ACT_NONE || act == GP_ACT_RELU || act == GP_ACT_GELU_TANH || act == GP_ACT_SIGMOID;
+}
+
+// One dense layer prepared for the GEMM stage.
+struct Prepared {
+  const void* wt;  // [Np][Kin], zero-padded
+  const void* b;   // [Np], zero-padded
+  int64_t Kin, Np;
+  int act;
+};
+
+// Transpose / pad one layer's weight and bias into the workspace.
+hipError_t prepare(const void* w, const void* b, int64_t K, int64_t N, int64_t Kin, int64_t Np, int act, char* wt,
+                   char* bp, int ncu, hipStream_t s, Prepared* out) {
+  hipError_t e = transpose_launch(w, wt, K, N, s, Kin, Np);
+  if (e != hipSuccess) return e;
+  // a null bias becomes Np zeros (a zero-width copy writes only the padding)
+  e = place_launch(1, b ? b : (const void*)bp, N, b ? N : 0, bp, Np, Np, GP_ACT_NONE, ncu, s);
+  *out = {wt, bp, Kin, Np, act};
+  return e;
+}
+
+hipError_t layer(const Prepared& L, int64_t rows, const void* a, int64_t lda, void* c, int64_t ldc, int ncu,
+                 hipStream_t s) {
+  GemmArgs g{rows, L.Np, L.Kin, a, L.wt, L.b, nullptr, L.act, c};
+  g.lda = lda;
+  g.ldc = ldc;
+  return gemm_launch(g, ncu, s);
+}
+
+const char* row_ptr(const void* base, int64_t row, int64_t stride) { return (const char*)base + row * stride * 2; }
+
+int common_checks(int64_t M, const void* x, const void* out) {
+  if (M < 0) return fail(GP_ERR_INVALID_ARG, "M must be >= 0 (got %lld)", (long long)M);
+  if (M > kMaxRows) return fail(GP_ERR_SHAPE, "M too large (%lld)", (long long)M);
+  if (M > 0 && (!x || !out)) return fail(GP_ERR_INVALID_ARG, "x and out must be non-NULL when M > 0");
+  return GP_OK;
+}
+
+// DlrmMlp-style chain: widths[0] -> widths[1] -> ... -> widths[nl], act[i] after layer i.
+int run_chain(int64_t M, int nl, const int64_t* widths, const void* const* w, const void* const* b, const int* acts,
+              const void* x, void* out, hipStream_t s) {
+  int dev = 0, ncu = 0;
+  int rc = current_device_info(&dev, &ncu);
+  if (rc) return rc;
+  const int64_t CH = M < kChunkRows ? M : kChunkRows;
+  std::vector<int64_t> kin(nl), np(nl);
+  int64_t maxnp = 0;
+  for (int i = 0; i < nl; ++i) {
+    kin[i] = i == 0 ? rup(widths[0], 64) : np[i - 1];
+    np[i] = rup(widths[i + 1], 128);
+    maxnp = np[i] > maxnp ? np[i] : maxnp;
+  }
+  const bool direct_in = widths[0] % 64 == 0 && aligned16(x);
+  const bool direct_out = np[nl - 1] == widths[nl] && aligned16(out);
+  Carve cv;
+  std::vector<size_t> o_wt(nl), o_b(nl);
+  for (int i = 0; i < nl; ++i) {
+    o_wt[i] = cv.take((size_t)np[i] * kin[i] * 2);
+    o_b[i] = cv.take((size_t)np[i] * 2);
+  }
+  const size_t o_x = direct_in ? 0 : cv.take((size_t)CH * kin[0] * 2);
+  const size_t o_h0 = cv.take((size_t)CH * maxnp * 2);
+  const size_t o_h1 = cv.take((size_t)CH * maxnp * 2);
+  char* ws = nullptr;
+  if ((rc = workspace_acquire(dev, s, cv.off, (void**)&ws))) return rc;
+
+  std::vector<Prepared> L(nl);
+  for (int i = 0; i < nl; ++i) {
+    hipError_t e = prepare(w[i], b[i], widths[i], widths[i + 1], kin[i], np[i], acts[i], ws + o_wt[i], ws + o_b[i],
+                           ncu, s, &L[i]);
+    if (e != hipSuccess) return fail_hip(e, "MLP weight preparation");
+  }
+  char* hb[2] = {ws + o_h0, ws + o_h1};
+  for (int64_t r0 = 0; r0 < M; r0 += CH) {
+    const int64_t rows = M - r0 < CH ? M - r0 : CH;
+    const void* a = row_ptr(x, r0, widths[0]);
+    int64_t lda = widths[0];
+    hipError_t e = hipSuccess;
+    if (!direct_in) {
+      e = place_launch(rows, a, widths[0], widths[0], ws + o_x, kin[0], kin[0], GP_ACT_NONE, ncu, s);
+      a = ws + o_x;
+      lda = kin[0];
+    }
+    for (int i = 0; i < nl && e == hipSuccess; ++i) {
+      const bool last = i == nl - 1;
+      void* c = last && direct_out ? (void*)row_ptr(out, r0, widths[nl]) : (void*)hb[i % 2];
+      e = layer(L[i], rows, a, lda, c, np[i], ncu, s);
+      a = c;
+      lda = np[i];
+    }
+    if (e == hipSuccess && !direct_out)
+      e = place_launch(rows, a, lda, widths[nl], (void*)row_ptr(out, r0, widths[nl]), widths[nl], widths[nl],
+                       GP_ACT_NONE, ncu, s);
+    if (e != hipSuccess) return fail_hip(e, "MLP layer launch");
+  }
+  return GP_OK;
+}
+
+int check_chain(int nl, const int64_t* widths, const void* const* w, const int* acts) {
+  for (int i = 0; i <= nl; ++i)
+    if (widths[i] < 1 || widths[i] > kMaxWidth)
+      return fail(GP_ERR_SHAPE, "width %d must be in [1, %lld] (got %lld)", i, (long long)kMaxWidth,
+                  (long long)widths[i]);
+  for (int i = 0; i < nl; ++i) {
+    if (!w[i]) return fail(GP_ERR_INVALID_ARG, "weight %d is NULL", i);
+    if (!act_ok(acts[i])) return fail(GP_ERR_INVALID_ARG, "unknown activation %d for layer %d", acts[i], i);
+  }
+  return GP_OK;
+}
+
+}  // namespace
+}  // namespace gp
+
+using namespace gp;
+
+extern "C" {
+
+int gp_mlp_out(int64_t M, int nlayers, const int64_t* widths, const void* const* w, const void* const* b,
+               const int* acts, const void* x, void* out, void* stream) {
+  clear_error();
+  if (nlayers < 1 || nlayers > 32) return fail(GP_ERR_INVALID_ARG, "nlayers must be in [1, 32] (got %d)", nlayers);
+  if (!widths || !w || !b || !acts) return fail(GP_ERR_INVALID_ARG, "widths, w, b and acts must be non-NULL");
+  int rc = common_checks(M, x, out);
+  if (rc) return rc;
+  if ((rc = check_chain(nlayers, widths, w, acts))) return rc;
+  if (M == 0) return GP_OK;
+  return run_chain(M, nlayers, widths, w, b, acts, x, out, (hipStream_t)stream);
+}
+
+int gp_dlrm_botmlp_out(int64_t M, int64_t K0, const void* x, const void* w1, const void* b1, const void* w2,
+                       const void* b2, const void* w3, const void* b3, void* out, void* stream) {
+  const int64_t widths[4] = {K0, 512, 256, 128};
+  const void* w[3] = {w1, w2, w3};
+  const void* b[3] = {b1, b2, b3};
+  const int acts[3] = {GP_ACT_RELU, GP_ACT_RELU, GP_ACT_RELU};
+  return gp_mlp_out(M, 3, widths, w, b, acts, x, out, stream);
+}
+
+int gp_dlrm_topmlp_out(int64_t M, int64_t K0, int64_t N5, const void* x, const void* w1, const void* b1,
+                       const void* w2, const void* b2, const void* w3, const void* b3, const void* w4,
+                       const void* b4, const void* w5, const void* b5, int act5, void* out, void* stream) {
+  const int64_t widths[6] = {K0, 1024, 1024, 512, 256, N5};
+  const void* w[5] = {w1, w2, w3, w4, w5};
+  const void* b[5] = {b1, b2, b3, b4, b5};
+  const int acts[5] = {GP_ACT_RELU, GP_ACT_RELU, GP_ACT_RELU, GP_ACT_RELU, act5};
+  return gp_mlp_out(M, 5, widths, w, b, acts, x, out, stream);
+}
+
+int gp_nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb, const void* x, const void* d,
+                     const void* const* w, const void* const* b, int rgb_act, void* out_r, void* out_rgb,
+                     void* stream) {
+  clear_error();
+  int rc = common_checks(M, x, out_r);
+  if (rc) return rc;
+  if (M > 0 && (!d || !out_rgb)) return fail(GP_ERR_INVALID_ARG, "d and out_rgb must be non-NULL when M > 0");
+  if (!w || !b) return fail(GP_ERR_INVALID_ARG, "w and b must be non-NULL");
+  if (Kx < 1 || Kx > 1024 || Kd < 1 || Kd > 1024 || Na < 1 || Na > 1024 || Nrgb < 1 || Nrgb > 1024)
+    return fail(GP_ERR_SHAPE, "Kx, Kd, Na and Nrgb must be in [1, 1024]");
+  for (int i = 0; i < 12; ++i)
+    if (!w[i]) return fail(GP_ERR_INVALID_ARG, "weight %d is NULL", i + 1);
+  if (!act_ok(rgb_act)) return fail(GP_ERR_INVALID_ARG, "unknown activation %d", rgb_act);
+  if (M == 0) return GP_OK;
+  int dev = 0, ncu = 0;
+  if ((rc = current_device_info(&dev, &ncu))) return rc;
+  hipStream_t s = (hipStream_t)stream;
+
+  // Layer shapes of apps/nerf_full/torch/model.py:5-46 with hidden 256:
+  // 1: Kx->256, 2-5: 256->256 (ReLU); 6: [h | x] -> 256, 7-8: 256->256 (ReLU);
+  // 9: 256->Na (density, linear); 10: 256->256 (bottleneck, linear);
+  // 11: [bottleneck | d] -> 128 (ReLU); 12: 128->Nrgb (colour, rgb_act).
+  const int64_t H = 256, H2 = 128;
+  const int64_t kx = rup(Kx, 64), cat1 = rup(H + Kx, 64), cat2 = rup(H + Kd, 64);
+  const int64_t np9 = rup(Na, 128), np12 = rup(Nrgb, 128);
+  struct Shape {
+    int64_t K, N, Kin, Np;
+    int act;
+  };
+  const Shape sh[12] = {
+      {Kx, H, kx, H, GP_ACT_RELU},      {H, H, H, H, GP_ACT_RELU},         {H, H, H, H, GP_ACT_RELU},
+      {H, H, H, H, GP_ACT_RELU},        {H, H, H, H, GP_ACT_RELU},         {H + Kx, H, cat1, H, GP_ACT_RELU},
+      {H, H, H, H, GP_ACT_RELU},        {H, H, H, H, GP_ACT_RELU},         {H, Na, H, np9, GP_ACT_NONE},
+      {H, H, H, H, GP_ACT_NONE},        {H + Kd, H2, cat2, H2, GP_ACT_RELU}, {H2, Nrgb, H2, np12, rgb_act},
+  };
+  const int64_t CH = M < kChunkRows ? M : kChunkRows;
+  Carve cv;
+  size_t o_wt[12], o_b[12];
+  for (int i = 0; i < 12; ++i) {
+    o_wt[i] = cv.take((size_t)sh[i].Np * sh[i].Kin * 2);
+    o_b[i] = cv.take((size_t)sh[i].Np * 2);
+  }
+  const size_t o_x = cv.take((size_t)CH * kx * 2);      // x, padded
+  const size_t o_c1 = cv.take((size_t)CH * cat1 * 2);   // [h5 | x]
+  const size_t o_c2 = cv.take((size_t)CH * cat2 * 2);   // [bottleneck | d]
+  const size_t o_h0 = cv.take((size_t)CH * H * 2);
+  const size_t o_h1 = cv.take((size_t)CH * H * 2);
+  const size_t o_hd = cv.take((size_t)CH * (np9 > np12 ? np9 : np12) * 2);  // padded head outputs
+  char* ws = nullptr;
+  if ((rc = workspace_acquire(dev, s, cv.off, (void**)&ws))) return rc;
+  Prepared L[12];
+  for (int i = 0; i < 12; ++i) {
+    hipError_t e = prepare(w[i], b[i], sh[i].K, sh[i].N, sh[i].Kin, sh[i].Np, sh[i].act, ws + o_wt[i],
+                           ws + o_b[i], ncu, s, &L[i]);
+    if (e != hipSuccess) return fail_hip(e, "NeRF weight preparation");
+  }
+  char *xb = ws + o_x, *c1 = ws + o_c1, *c2 = ws + o_c2, *h0 = ws + o_h0, *h1 = ws + o_h1, *hd = ws + o_hd;
+  for (int64_t r0 = 0; r0 < M; r0 += CH) {
+    const int64_t rows = M - r0 < CH ? M - r0 : CH;
+    hipError_t e = place_launch(rows, row_ptr(x, r0, Kx), Kx, Kx, xb, kx, kx, GP_ACT_NONE, ncu, s);
+    // the skip and view-direction inputs go into the tails of the concat buffers
+    if (e == hipSuccess) e = place_launch(rows, row_ptr(x, r0, Kx), Kx, Kx, c1 + H * 2, cat1, cat1 - H, GP_ACT_NONE,
+                                          ncu, s);
+    if (e == hipSuccess) e = place_launch(rows, row_ptr(d, r0, Kd), Kd, Kd, c2 + H * 2, cat2, cat2 - H, GP_ACT_NONE,
+                                          ncu, s);
+    if (e == hipSuccess) e = layer(L[0], rows, xb, kx, h0, H, ncu, s);
+    if (e == hipSuccess) e = layer(L[1], rows, h0, H, h1, H, ncu, s);
+    if (e == hipSuccess) e = layer(L[2], rows, h1, H, h0, H, ncu, s);
+    if (e == hipSuccess) e = layer(L[3], rows, h0, H, h1, H, ncu, s);
+    if (e == hipSuccess) e = layer(L[4], rows, h1, H, c1, cat1, ncu, s);  // h5 -> first 256 columns of [h5 | x]
+    if (e == hipSuccess) e = layer(L[5], rows, c1, cat1, h0, H, ncu, s);
+    if (e == hipSuccess) e = layer(L[6], rows, h0, H, h1, H, ncu, s);
+    if (e == hipSuccess) e = layer(L[7], rows, h1, H, h0, H, ncu, s);    // trunk output
+    if (e == hipSuccess) e = layer(L[8], rows, h0, H, hd, np9, ncu, s);  // density head
+    if (e == hipSuccess)
+      e = place_launch(rows, hd, np9, Na, (void*)row_ptr(out_r, r0, Na), Na, Na, GP_ACT_NONE, ncu, s);
+    if (e == hipSuccess) e = layer(L[9], rows, h0, H, c2, cat2, ncu, s);  // bottleneck -> [bottleneck | d]
+    if (e == hipSuccess) e = layer(L[10], rows, c2, cat2, h1, H2, ncu, s);
+    if (e == hipSuccess) e = layer(L[11], rows, h1, H2, hd, np12, ncu, s);
+    if (e == hipSuccess)
+      e = place_launch(rows, hd, np12, Nrgb, (void*)row_ptr(out_rgb, r0, Nrgb), Nrgb, Nrgb, GP_ACT_NONE, ncu, s);
+    if (e != hipSuccess) return fail_hip(e, "NeRF layer launch");
+  }
+  return GP_OK;
+}
+
+}  // extern "C"

@@ -286,6 +286,29 @@ hipError_t layer_norm_launch(int64_t M, int64_t D, const void* x, const void* ga
   return hipGetLastError();
 }
 
+// dst[m][j] = act(src[m][j]) for j < w, 0 for w <= j < wpad: moves a column
+// block between matrices with zero padding (the concat inputs, padded inputs
+// and narrow heads of the MLP chains).  Strides in elements.
+__global__ __launch_bounds__(kStageThreads) void place_kernel(const half_t* src, int64_t lds, int w, half_t* dst,
+                                                              int64_t ldd, int wpad, int act, int64_t M) {
+  const int64_t total = M * wpad;
+  for (int64_t i = (int64_t)blockIdx.x * kStageThreads + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * kStageThreads) {
+    const int64_t m = i / wpad;
+    const int j = (int)(i - m * wpad);
+    dst[m * ldd + j] = j < w ? (half_t)apply_act((float)src[m * lds + j], act) : (half_t)0.f;
+  }
+}
+
+hipError_t place_launch(int64_t M, const void* src, int64_t lds, int64_t w, void* dst, int64_t ldd, int64_t wpad,
+                        int act, int num_cus, hipStream_t s) {
+  if (M <= 0) return hipSuccess;
+  const int64_t want = (M * wpad + kStageThreads - 1) / kStageThreads, cap = (int64_t)num_cus * 16;
+  hipLaunchKernelGGL(place_kernel, dim3((unsigned)(want < cap ? want : cap)), dim3(kStageThreads), 0, s,
+                     (const half_t*)src, lds, (int)w, (half_t*)dst, ldd, (int)wpad, act, M);
+  return hipGetLastError();
+}
+
 hipError_t add_launch(int64_t M, int64_t N, const void* a, const void* b, void* c, int num_cus, hipStream_t s) {
   hipLaunchKernelGGL(add_kernel, dim3(persistent_grid(M, num_cus, 4)), dim3(kStageThreads), 0, s, (const half_t*)a,
                      (const half_t*)b, (half_t*)c, M, (int)N);

@@ -25,7 +25,8 @@ __all__ = [
     "mgn_mlp", "mgn_mlp_out", "IMPL_FUSED", "IMPL_PIPELINED", "IMPL_PIPELINED_SPLIT_LN", "GpipesError",
     "linear_out", "linear_layer_norm_out", "layer_norm_out", "add_out", "concat_out", "pipe_ident",
     "pipeline_check", "ACTS", "mgn_edge_gather", "mgn_edge_gather_out", "pipe_route", "ROUTES",
-    "gemm_out", "bert_ffn", "bert_ffn_out",
+    "gemm_out", "bert_ffn", "bert_ffn_out", "mlp_out", "dlrm_botmlp", "dlrm_botmlp_out", "dlrm_topmlp",
+    "dlrm_topmlp_out", "nerf_full", "nerf_full_out",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -76,7 +77,12 @@ def _load():
     L.gp_mgn_edge_gather_out.restype = i32
     L.gp_gemm_out.argtypes = [i64, i64, i64, vp, vp, vp, vp, i32, vp, vp]
     L.gp_bert_ffn_out.argtypes = [i64, i64, i64] + [vp] * 7 + [f32, i32, vp, vp]
-    for name in ("gp_gemm_out", "gp_bert_ffn_out", "gp_linear_out", "gp_linear_layer_norm_out", "gp_layer_norm_out", "gp_add_out",
+    L.gp_mlp_out.argtypes = [i64, i32, vp, vp, vp, vp, vp, vp, vp]
+    L.gp_dlrm_botmlp_out.argtypes = [i64, i64] + [vp] * 9
+    L.gp_dlrm_topmlp_out.argtypes = [i64, i64, i64] + [vp] * 11 + [i32, vp, vp]
+    L.gp_nerf_full_out.argtypes = [i64] * 5 + [vp] * 4 + [i32, vp, vp, vp]
+    for name in ("gp_mlp_out", "gp_dlrm_botmlp_out", "gp_dlrm_topmlp_out", "gp_nerf_full_out", "gp_gemm_out",
+                 "gp_bert_ffn_out", "gp_linear_out", "gp_linear_layer_norm_out", "gp_layer_norm_out", "gp_add_out",
                  "gp_concat_out", "gp_pipe_ident", "gp_pipeline_check"):
         getattr(L, name).restype = i32
     return L
@@ -394,3 +400,105 @@ def bert_ffn(x, w1, b1, w2, b2, ga, be, eps=1e-5, act="relu"):
     """Allocating form (bert_ffn_pl_ext.cu:59-72)."""
     out = torch.zeros_like(x)
     return bert_ffn_out(x, w1, b1, w2, b2, ga, be, out, eps=eps, act=act)
+
+
+# ---------------------------------------------------------------------------
+# Dense MLP chains: DLRM and NeRF
+# ---------------------------------------------------------------------------
+
+def _same_device(*ts):
+    devs = {t.device for t in ts if t is not None}
+    if len(devs) != 1:
+        raise RuntimeError("all tensors must be on the same device")
+
+
+def mlp_out(x, ws, bs, acts, out=None):
+    """DlrmMlp-style chain (common/mlps.py:23-34): layer i = acts[i](h @ ws[i] + bs[i]).
+    ws[i] is [in, out] (``weight.t()``); bs[i] may be None; acts are names of ACTS or ids."""
+    _check_input("x", x)
+    if x.dim() != 2:
+        raise RuntimeError("x must be 2-D [M, K]")
+    if not (len(ws) == len(bs) == len(acts)) or not ws:
+        raise RuntimeError("ws, bs and acts must have the same non-zero length")
+    M, K = x.shape
+    widths = [K]
+    for i, (w, b) in enumerate(zip(ws, bs)):
+        _check_input(f"w{i + 1}", w)
+        if w.dim() != 2 or w.shape[0] != widths[-1]:
+            raise RuntimeError(f"w{i + 1} must be [{widths[-1]}, N]")
+        widths.append(w.shape[1])
+        _opt(f"b{i + 1}", b, (w.shape[1],))
+    if out is None:
+        out = torch.empty((M, widths[-1]), dtype=torch.float16, device=x.device)
+    _check_input("out", out, (M, widths[-1]))
+    _same_device(x, out, *ws, *bs)
+    n = len(ws)
+    wa = (ctypes.c_int64 * (n + 1))(*widths)
+    wp = (ctypes.c_void_p * n)(*[w.data_ptr() for w in ws])
+    bp = (ctypes.c_void_p * n)(*[0 if b is None else b.data_ptr() for b in bs])
+    ap = (ctypes.c_int * n)(*[ACTS.get(a, a) for a in acts])
+    with torch.cuda.device(x.device):
+        _check(lib.gp_mlp_out(M, n, wa, wp, bp, ap, _ptr(x), _ptr(out), _stream(x)))
+    return out
+
+
+def dlrm_botmlp_out(x, w1, b1, w2, b2, w3, b3, out):
+    """DLRM bottom MLP K0 -> 512 -> 256 -> 128, ReLU each
+    (apps/dlrm_botmlp/pipelined/dlrm_botmlp_pl_ext.cu:24-66)."""
+    return mlp_out(x, [w1, w2, w3], [b1, b2, b3], ["relu"] * 3, out)
+
+
+def dlrm_botmlp(x, w1, b1, w2, b2, w3, b3):
+    out = torch.zeros((x.shape[0], w3.shape[1]), dtype=x.dtype, device=x.device)
+    return dlrm_botmlp_out(x, w1, b1, w2, b2, w3, b3, out)
+
+
+def dlrm_topmlp_out(x, w1, b1, w2, b2, w3, b3, w4, b4, w5, b5, out, act5="relu"):
+    """DLRM top MLP K0 -> 1024 -> 1024 -> 512 -> 256 -> N5, ReLU after the first four layers
+    and act5 after the last (apps/dlrm_topmlp/pipelined/dlrm_topmlp_pl_ext.cu:24-71; the
+    DLRM click head is N5 = 1 with act5="sigmoid")."""
+    return mlp_out(x, [w1, w2, w3, w4, w5], [b1, b2, b3, b4, b5], ["relu"] * 4 + [act5], out)
+
+
+def dlrm_topmlp(x, w1, b1, w2, b2, w3, b3, w4, b4, w5, b5, act5="relu"):
+    out = torch.zeros((x.shape[0], w5.shape[1]), dtype=x.dtype, device=x.device)
+    return dlrm_topmlp_out(x, w1, b1, w2, b2, w3, b3, w4, b4, w5, b5, out, act5=act5)
+
+
+def nerf_full_out(x, d, *wb_and_outs, rgb_act="none"):
+    """NeRF MLP (apps/nerf_full/pipelined/nerf_full_pl_ext.cu:24-97): arguments
+    x, d, w1, b1, ..., w12, b12, out_r, out_rgb; see gp_nerf_full_out for the shapes."""
+    if len(wb_and_outs) != 26:
+        raise RuntimeError("expected w1, b1, ..., w12, b12, out_r, out_rgb")
+    ws, bs = list(wb_and_outs[0:24:2]), list(wb_and_outs[1:24:2])
+    out_r, out_rgb = wb_and_outs[24], wb_and_outs[25]
+    _check_input("x", x)
+    _check_input("d", d)
+    if x.dim() != 2 or d.dim() != 2 or d.shape[0] != x.shape[0]:
+        raise RuntimeError("x and d must be 2-D with the same number of rows")
+    M, Kx = x.shape
+    Kd = d.shape[1]
+    Na, Nrgb = ws[8].shape[1], ws[11].shape[1]
+    shapes = [(Kx, 256)] + [(256, 256)] * 4 + [(256 + Kx, 256), (256, 256), (256, 256), (256, Na), (256, 256),
+                                                (256 + Kd, 128), (128, Nrgb)]
+    for i, (w, b, shp) in enumerate(zip(ws, bs, shapes)):
+        _check_input(f"w{i + 1}", w, shp)
+        _opt(f"b{i + 1}", b, (shp[1],))
+    _check_input("out_r", out_r, (M, Na))
+    _check_input("out_rgb", out_rgb, (M, Nrgb))
+    _same_device(x, d, out_r, out_rgb, *ws, *bs)
+    wp = (ctypes.c_void_p * 12)(*[w.data_ptr() for w in ws])
+    bp = (ctypes.c_void_p * 12)(*[0 if b is None else b.data_ptr() for b in bs])
+    with torch.cuda.device(x.device):
+        _check(lib.gp_nerf_full_out(M, Kx, Kd, Na, Nrgb, _ptr(x), _ptr(d), wp, bp, ACTS.get(rgb_act, rgb_act),
+                                    _ptr(out_r), _ptr(out_rgb), _stream(x)))
+    return out_r, out_rgb
+
+
+def nerf_full(x, d, *wb, rgb_act="none"):
+    """Allocating form: returns (out_r, out_rgb) (nerf_full_pl_ext.cu:99-126)."""
+    if len(wb) != 24:
+        raise RuntimeError("expected w1, b1, ..., w12, b12")
+    out_r = torch.zeros((x.shape[0], wb[16].shape[1]), dtype=x.dtype, device=x.device)
+    out_rgb = torch.zeros((x.shape[0], wb[22].shape[1]), dtype=x.dtype, device=x.device)
+    return nerf_full_out(x, d, *wb, out_r, out_rgb, rgb_act=rgb_act)

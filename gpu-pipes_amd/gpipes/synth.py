@@ -1,4 +1,4 @@
-"""Deterministic synthetic inputs for the MGN MLP and BERT FFN workloads.
+"""Deterministic synthetic inputs for the MGN MLP, BERT FFN, DLRM and NeRF workloads.
 
 Parameters follow torch.nn defaults, which is what the workload definition
 asks for: Linear weights Kaiming-uniform(a=sqrt(5)) = U(+-1/sqrt(fan_in)),
@@ -68,3 +68,79 @@ def normal_fp16(M, K, seed=0, device="cpu"):
     dev = torch.device(device)
     g = torch.Generator(device=dev).manual_seed(seed)
     return torch.randn((M, K), generator=g, device=dev, dtype=torch.float32).to(torch.float16)
+
+
+def dlrm_params(widths, seed=0, init="xavier", device="cpu"):
+    """Parameters of DlrmMlp(widths) (common/mlps.py:23-34) in kernel layout:
+    init="xavier" draws the weights Xavier-uniform (the DLRM workload), "torch"
+    keeps nn.Linear's defaults; biases keep nn.Linear's default init."""
+    with torch.random.fork_rng(devices=[]):
+        torch.manual_seed(seed)
+        lins = [torch.nn.Linear(widths[i], widths[i + 1]) for i in range(len(widths) - 1)]
+        with torch.no_grad():
+            if init == "xavier":
+                for lin in lins:
+                    torch.nn.init.xavier_uniform_(lin.weight)
+            elif init != "torch":
+                raise ValueError(f"unknown init {init!r}")
+    ws = [lin.weight.detach().t().contiguous().to(torch.float16).to(device) for lin in lins]
+    bs = [lin.bias.detach().to(torch.float16).to(device) for lin in lins]
+    return ws, bs
+
+
+def padded_uniform(M, K, Kp, seed=0, device="cpu"):
+    """U(0, 1) dense features [M, K] zero-padded to [M, Kp] (DLRM bottom input)."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.zeros((M, Kp), dtype=torch.float32)
+    x[:, :K] = torch.rand((M, K), generator=g)
+    return x.to(torch.float16).to(device)
+
+
+def padded_normal(M, K, Kp, seed=0, device="cpu"):
+    """N(0, 1) features [M, K] zero-padded to [M, Kp] (DLRM top input)."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.zeros((M, Kp), dtype=torch.float32)
+    x[:, :K] = torch.randn((M, K), generator=g)
+    return x.to(torch.float16).to(device)
+
+
+def positional_encoding(M, octaves, seed=0, device="cpu", unit=False):
+    """NeRF positional encoding: [p, sin(2^i p), cos(2^i p) for i < octaves] of
+    p ~ U(-1, 1)^3 (or random unit directions), width 3 + 6 octaves."""
+    g = torch.Generator().manual_seed(seed)
+    p = torch.rand((M, 3), generator=g, dtype=torch.float64) * 2 - 1
+    if unit:
+        p = p / p.norm(dim=1, keepdim=True).clamp_min(1e-6)
+    feats = [p]
+    for i in range(octaves):
+        feats += [torch.sin((2.0 ** i) * p), torch.cos((2.0 ** i) * p)]
+    return torch.cat(feats, dim=1).to(torch.float16).to(device)
+
+
+def nerf_inputs(M, seed=0, device="cpu", Kx=64, Kd=27):
+    """x: encoded positions (63 features, 10 octaves) zero-padded to Kx; d: encoded
+    view directions (27 features, 4 octaves) padded to Kd."""
+    x = torch.zeros((M, Kx), dtype=torch.float16)
+    x[:, :63] = positional_encoding(M, 10, seed=seed)
+    d = torch.zeros((M, Kd), dtype=torch.float16)
+    d[:, :27] = positional_encoding(M, 4, seed=seed + 1, unit=True)
+    return x.to(device), d.to(device)
+
+
+def nerf_params(Kx=64, Kd=27, Na=1, Nrgb=3, seed=0, device="cpu", zero_pad_rows=63):
+    """Parameters w1..w12 / b1..b12 of the NeRF MLP (apps/nerf_full/torch/model.py:5-46,
+    hidden 256) in kernel layout with nn.Linear's default (Kaiming-uniform) init.  The
+    weight rows of input columns at and past zero_pad_rows (the zero padding of x) are
+    set to zero in w1 and in the skip part of w6."""
+    shapes = [(Kx, 256)] + [(256, 256)] * 4 + [(256 + Kx, 256), (256, 256), (256, 256), (256, Na), (256, 256),
+                                                (256 + Kd, 128), (128, Nrgb)]
+    with torch.random.fork_rng(devices=[]):
+        torch.manual_seed(seed)
+        lins = [torch.nn.Linear(k, n) for k, n in shapes]
+    ws = [lin.weight.detach().t().contiguous() for lin in lins]
+    bs = [lin.bias.detach() for lin in lins]
+    if zero_pad_rows is not None and zero_pad_rows < Kx:
+        ws[0][zero_pad_rows:] = 0
+        ws[5][256 + zero_pad_rows:] = 0
+    h = lambda t: t.to(torch.float16).contiguous().to(device)  # noqa: E731
+    return [h(w) for w in ws], [h(b) for b in bs]

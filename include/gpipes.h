@@ -119,6 +119,57 @@ int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void*
                     const void* w2, const void* b2, const void* gamma, const void* beta, float eps, int act,
                     void* out, void* stream);
 
+/*
+ * Dense MLP chain: widths[0] -> widths[1] -> ... -> widths[nlayers], layer i
+ * out = act_i(in . w[i] + b[i]) with w[i] [widths[i], widths[i+1]] (fp16,
+ * weight.t()), b[i] [widths[i+1]] or NULL, acts[i] one of GP_ACT_*.  Any
+ * widths in [1, 16384]; x [M, widths[0]], out [M, widths[nlayers]].  This is
+ * DlrmMlp(widths, sigmoid_i) of common/mlps.py:23-34 (ReLU after every layer,
+ * sigmoid after layer sigmoid_i) with the activation of each layer given.
+ * Rows go through in chunks of 65,536 with the activations in the per-stream
+ * workspace.
+ */
+int gp_mlp_out(int64_t M, int nlayers, const int64_t* widths, const void* const* w, const void* const* b,
+               const int* acts, const void* x, void* out, void* stream);
+
+/*
+ * DLRM bottom MLP: x[M,K0] -> 512 -> 256 -> 128, ReLU after each layer.
+ * Replaces dlrm_botmlp_out(x, w1, b1, w2, b2, w3, b3, out),
+ * apps/dlrm_botmlp/pipelined/dlrm_botmlp_pl_ext.cu:24-66 (K0 = 32 there;
+ * 13 dense features padded to 16 in the DLRM workload).
+ */
+int gp_dlrm_botmlp_out(int64_t M, int64_t K0, const void* x, const void* w1, const void* b1, const void* w2,
+                       const void* b2, const void* w3, const void* b3, void* out, void* stream);
+
+/*
+ * DLRM top MLP: x[M,K0] -> 1024 -> 1024 -> 512 -> 256 (ReLU after each) -> N5
+ * with act5 after the last layer.  Replaces dlrm_topmlp_out(x, w1, b1, ...,
+ * w5, b5, out), apps/dlrm_topmlp/pipelined/dlrm_topmlp_pl_ext.cu:24-71 (K0 =
+ * 512, N5 = 64, every layer ReLU per DlrmMlp, common/mlps.py:23-34; the
+ * reference kernel drops the ReLU of layer 4, dlrm_topmlp_pl.cuh:157, which is
+ * not reproduced).  The DLRM click head is N5 = 1 with act5 = GP_ACT_SIGMOID.
+ */
+int gp_dlrm_topmlp_out(int64_t M, int64_t K0, int64_t N5, const void* x, const void* w1, const void* b1,
+                       const void* w2, const void* b2, const void* w3, const void* b3, const void* w4,
+                       const void* b4, const void* w5, const void* b5, int act5, void* out, void* stream);
+
+/*
+ * NeRF MLP, apps/nerf_full/torch/model.py:5-66 (hidden 256, skip after the
+ * fifth layer, view directions): with w[0..11] / b[0..11] the reference's
+ * w1..w12 / b1..b12 (nerf_full_pl_ext.cu:24-97),
+ *   h = ReLU chain of w1 [Kx,256], w2..w5 [256,256]; h = [h | x];
+ *   h = ReLU chain of w6 [256+Kx,256], w7, w8 [256,256];
+ *   out_r [M,Na]   = h . w9 [256,Na] + b9;
+ *   f = h . w10 [256,256] + b10;  g = ReLU([f | d] . w11 [256+Kd,128] + b11);
+ *   out_rgb [M,Nrgb] = rgb_act(g . w12 [128,Nrgb] + b12).
+ * x [M,Kx], d [M,Kd]; Kx, Kd, Na, Nrgb in [1, 1024].  The reference app has
+ * Kx 64, Kd 32, Na = Nrgb = 64 and no colour activation; the NeRF workload has
+ * Kx 64 (63 + 1 zero), Kd 27, Na 1, Nrgb 3 and a sigmoid.
+ */
+int gp_nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb, const void* x, const void* d,
+                     const void* const* w, const void* const* b, int rgb_act, void* out_r, void* out_rgb,
+                     void* stream);
+
 /* ------------------------------------------------------------------------
  * Stage-level entry points: one stage function of the library run over a
  * whole matrix (tiles of 128 rows, persistent workgroups).

@@ -111,6 +111,32 @@ def bert_ffn(x, w1, b1, w2, b2, gamma=None, beta=None, act=ACT_RELU, eps=1e-5):
     return out
 
 
+def mlp(x, ws, bs, acts):
+    """DlrmMlp(widths, sigmoid_i) forward in fp32 (common/mlps.py:23-34): every layer
+    Linear then its activation (ReLU, or Sigmoid at sigmoid_i); acts gives them per layer."""
+    h = _f32(x)
+    for w, b, a in zip(ws, bs, acts):
+        h = linear(h, w, b, a)
+    return h
+
+
+def nerf(x, d, ws, bs, rgb_act=ACT_NONE):
+    """Nerf forward in fp32 (apps/nerf_full/torch/model.py:48-66, hidden 256, skip at
+    layer 4, view directions): returns (density [M, Na], rgb [M, Nrgb])."""
+    x, d = _f32(x), _f32(d)
+    h = x
+    for i in range(5):                                 # preskip: 5 x (Linear, ReLU)
+        h = linear(h, ws[i], bs[i], ACT_RELU)
+    h = concat(h, x)                                   # resid = cat([preskip_out, x])
+    for i in range(5, 8):                              # postskip: 3 x (Linear, ReLU)
+        h = linear(h, ws[i], bs[i], ACT_RELU)
+    alpha = linear(h, ws[8], bs[8])                    # alpha: Linear
+    f = linear(h, ws[9], bs[9])                        # bottleneck: Linear
+    g = linear(concat(f, d), ws[10], bs[10], ACT_RELU)  # rgb[0], rgb[1]
+    rgb = linear(g, ws[11], bs[11], rgb_act)           # rgb[2] (+ the workload's sigmoid)
+    return alpha, rgb
+
+
 def add(a, b):
     a, b = _f32(a), _f32(b)
     c = np.empty_like(a)

@@ -18,6 +18,12 @@ ReLU, eps 1e-5, nn.Linear init) and once with the BERT-large recipe (GELU(tanh),
 eps 1e-12, N(0, 0.02) weights, zero biases) at a small width; expected outputs
 are again the torch.nn modules in float64.
 
+The DLRM fixtures are DlrmMlp (common/mlps.py:23-34) built from torch.nn
+modules in float64; the NeRF fixture follows the module structure of
+apps/nerf_full/torch/model.py:5-66.  Its 1.2 MB of weights are not stored:
+gpipes.synth.nerf_params regenerates them from the seed, and the fixture
+keeps their SHA-256 so a changed generator is detected.
+
 The LayerNorm fixture uses the literal 128-value input row that the
 reference's own LayerNorm check types in (misc_tests/layer_norm/torch_val.py:88-105,
 repeated over 128 rows there, gamma = 1, beta = 0); its expected output is
@@ -36,7 +42,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, os.path.join(ROOT, "gpu-pipes_amd"))
-from gpipes.synth import bert_params, mgn_params, normal_fp16  # noqa: E402
+from gpipes.synth import bert_params, dlrm_params, mgn_params, nerf_inputs, nerf_params, normal_fp16  # noqa: E402
 
 M_FIX = 256
 
@@ -124,6 +130,73 @@ def make_bert_fixture(name, M, H, FF, act, eps, init, seed, affine_random):
     return path
 
 
+def torch_dlrm_f64(x16, ws, bs, sigmoid_i=None):
+    """DlrmMlp(widths, sigmoid_i) (common/mlps.py:23-34) with torch.nn modules in float64."""
+    mods = []
+    for i, (w, b) in enumerate(zip(ws, bs)):
+        lin = torch.nn.Linear(w.shape[0], w.shape[1]).double()
+        with torch.no_grad():
+            lin.weight.copy_(w.double().t())
+            lin.bias.copy_(b.double())
+        mods += [lin, torch.nn.Sigmoid() if i == sigmoid_i else torch.nn.ReLU()]
+    with torch.no_grad():
+        return torch.nn.Sequential(*mods)(x16.double())
+
+
+def make_dlrm_fixture(name, M, widths, sigmoid_i, init, seed):
+    ws, bs = dlrm_params(widths, seed=seed, init=init)
+    x = normal_fp16(M, widths[0], seed=seed + 1000)
+    y = torch_dlrm_f64(x, ws, bs, sigmoid_i)
+    arrs = {"x": x.numpy(), "expected": y.numpy().astype(np.float32),
+            "sigmoid_i": np.int64(-1 if sigmoid_i is None else sigmoid_i)}
+    for i, (w, b) in enumerate(zip(ws, bs)):
+        arrs[f"w{i + 1}"], arrs[f"b{i + 1}"] = w.numpy(), b.numpy()
+    path = os.path.join(HERE, f"{name}.npz")
+    np.savez_compressed(path, **arrs)
+    return path
+
+
+def torch_nerf_f64(x16, d16, ws, bs, sigmoid):
+    """The NeRF MLP with the module structure of apps/nerf_full/torch/model.py:5-66
+    (hidden 256, skip after the fifth layer, view directions), torch.nn in float64;
+    sigmoid adds the workload's colour activation."""
+    def lin(i):
+        m = torch.nn.Linear(ws[i].shape[0], ws[i].shape[1]).double()
+        with torch.no_grad():
+            m.weight.copy_(ws[i].double().t())
+            m.bias.copy_(bs[i].double())
+        return m
+    relu = torch.nn.ReLU
+    preskip = torch.nn.Sequential(lin(0), relu(), lin(1), relu(), lin(2), relu(), lin(3), relu(), lin(4), relu())
+    postskip = torch.nn.Sequential(lin(5), relu(), lin(6), relu(), lin(7), relu())
+    alpha, bottleneck = lin(8), lin(9)
+    rgb = torch.nn.Sequential(lin(10), relu(), lin(11), *([torch.nn.Sigmoid()] if sigmoid else []))
+    with torch.no_grad():
+        x, d = x16.double(), d16.double()
+        enc = postskip(torch.cat([preskip(x), x], dim=-1))
+        return alpha(enc), rgb(torch.cat([bottleneck(enc), d], dim=-1))
+
+
+def weights_digest(ws, bs):
+    h = hashlib.sha256()
+    for t in list(ws) + list(bs):
+        h.update(t.contiguous().view(torch.int16).numpy().tobytes())
+    return h.hexdigest()
+
+
+def make_nerf_fixture(name, M, seed, Kd, Na, Nrgb, sigmoid):
+    """Inputs and expected outputs; the 1.2 MB of weights are regenerated from the
+    seed by gpipes.synth.nerf_params and checked against the stored digest."""
+    ws, bs = nerf_params(64, Kd, Na, Nrgb, seed=seed)
+    x, d = nerf_inputs(M, seed=seed + 1000, Kx=64, Kd=Kd)
+    alpha, rgb = torch_nerf_f64(x, d, ws, bs, sigmoid)
+    path = os.path.join(HERE, f"{name}.npz")
+    np.savez_compressed(path, x=x.numpy(), d=d.numpy(), alpha=alpha.numpy().astype(np.float32),
+                        rgb=rgb.numpy().astype(np.float32), seed=np.int64(seed), Kd=np.int64(Kd), Na=np.int64(Na),
+                        Nrgb=np.int64(Nrgb), sigmoid=np.int64(sigmoid), weights_sha256=np.array(weights_digest(ws, bs)))
+    return path
+
+
 def make_ln_fixture():
     row = torch.tensor(LN_ROW, dtype=torch.float16)
     x = row.repeat(128, 1)
@@ -144,6 +217,11 @@ def main():
         # the reference app's shape and defaults (H 128, FF 512, ReLU, eps 1e-5)
         make_bert_fixture("bert_ffn_relu", 256, 128, 512, "relu", 1e-5, "torch", seed=10, affine_random=False),
         # the BERT-large recipe (GELU(tanh), eps 1e-12, N(0, 0.02) weights) at a small width
+        # DlrmMlp at the reference's bottom-MLP shape, and a narrow chain with a sigmoid head
+        make_dlrm_fixture("dlrm_bot", 64, [32, 512, 256, 128], None, "torch", seed=20),
+        make_dlrm_fixture("dlrm_sigmoid_head", 64, [24, 256, 128, 1], 2, "xavier", seed=21),
+        # the NeRF MLP at the workload's shape (view dirs 27, density 1, colour 3 + sigmoid)
+        make_nerf_fixture("nerf_workload", 64, seed=22, Kd=27, Na=1, Nrgb=3, sigmoid=True),
         make_bert_fixture("bert_ffn_gelu", 128, 256, 512, "gelu_tanh", 1e-12, "bert", seed=11,
                           affine_random=True),
     ]

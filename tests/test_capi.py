@@ -143,3 +143,34 @@ def test_gemm_argument_errors(M, N, K, x, w, r, act, out, code):
     vp = ctypes.c_void_p
     P = lambda v: vp(v) if v else None  # noqa: E731
     assert gpipes.lib.gp_gemm_out(M, N, K, P(x), P(w), None, P(r), act, P(out), None) == code
+
+
+def test_mlp_chain_argument_errors():
+    vp = ctypes.c_void_p
+    L = gpipes.lib
+    widths = (ctypes.c_int64 * 3)(16, 512, 128)
+    w = (ctypes.c_void_p * 2)(16, 16)
+    b = (ctypes.c_void_p * 2)(0, 0)
+    acts = (ctypes.c_int * 2)(1, 1)
+    bad_w = (ctypes.c_int64 * 3)(16, 0, 128)
+    assert L.gp_mlp_out(16, 2, bad_w, w, b, acts, vp(16), vp(16), None) == -2
+    assert L.gp_mlp_out(16, 0, widths, w, b, acts, vp(16), vp(16), None) == -1
+    nullw = (ctypes.c_void_p * 2)(16, 0)
+    assert L.gp_mlp_out(16, 2, widths, nullw, b, acts, vp(16), vp(16), None) == -1
+    bad_act = (ctypes.c_int * 2)(1, 9)
+    assert L.gp_mlp_out(16, 2, widths, w, b, bad_act, vp(16), vp(16), None) == -1
+    assert L.gp_mlp_out(-1, 2, widths, w, b, acts, vp(16), vp(16), None) == -1
+    assert L.gp_mlp_out(0, 2, widths, w, b, acts, None, None, None) == 0
+
+
+def test_nerf_argument_errors():
+    vp = ctypes.c_void_p
+    L = gpipes.lib
+    w = (ctypes.c_void_p * 12)(*([16] * 12))
+    b = (ctypes.c_void_p * 12)(*([0] * 12))
+    assert L.gp_nerf_full_out(16, 0, 27, 1, 3, vp(16), vp(16), w, b, 3, vp(16), vp(16), None) == -2
+    assert L.gp_nerf_full_out(16, 64, 27, 1, 3, vp(16), None, w, b, 3, vp(16), vp(16), None) == -1
+    w11 = (ctypes.c_void_p * 12)(*([16] * 11 + [0]))
+    assert L.gp_nerf_full_out(16, 64, 27, 1, 3, vp(16), vp(16), w11, b, 3, vp(16), vp(16), None) == -1
+    assert L.gp_nerf_full_out(16, 64, 27, 1, 3, vp(16), vp(16), w, b, 7, vp(16), vp(16), None) == -1
+    assert L.gp_nerf_full_out(0, 64, 27, 1, 3, None, None, w, b, 3, None, None, None) == 0

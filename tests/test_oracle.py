@@ -285,3 +285,124 @@ def test_bert_ffn_closed_forms():
     pre = torch.from_numpy(x).double() @ torch.from_numpy(w1).double() + torch.from_numpy(b1).double()
     np.testing.assert_allclose(h, F.gelu(pre, approximate="tanh").numpy(), rtol=1e-5, atol=1e-6)
     assert np.abs(h - F.gelu(pre).numpy()).max() > 1e-5
+
+
+# ---------------------------------------------------------------------------- DLRM / NeRF chains
+ACT_OF = {"relu": oracle.ACT_RELU, "sigmoid": oracle.ACT_SIGMOID, "none": oracle.ACT_NONE}
+
+
+def _dlrm(z):
+    n = sum(1 for k in z if k.startswith("w"))
+    ws = [z[f"w{i + 1}"].astype(np.float32) for i in range(n)]
+    bs = [z[f"b{i + 1}"].astype(np.float32) for i in range(n)]
+    si = int(z["sigmoid_i"])
+    acts = [oracle.ACT_SIGMOID if i == si else oracle.ACT_RELU for i in range(n)]
+    return ws, bs, acts
+
+
+@pytest.mark.parametrize("name", ["dlrm_bot.npz", "dlrm_sigmoid_head.npz"])
+def test_mlp_golden(name):
+    z = load_golden(name)
+    ws, bs, acts = _dlrm(z)
+    got = oracle.mlp(z["x"], ws, bs, acts)
+    max_abs, rel = oracle.errors(got, z["expected"])
+    assert max_abs < 1e-4 and rel < 1e-5, (max_abs, rel)
+
+
+def test_mlp_golden_rejects_sigmoid_on_wrong_layer():
+    z = load_golden("dlrm_sigmoid_head.npz")
+    ws, bs, _ = _dlrm(z)
+    got = oracle.mlp(z["x"], ws, bs, [oracle.ACT_RELU] * 3)
+    max_abs, rel = oracle.errors(got, z["expected"])
+    assert max_abs > oracle.MAX_ABS_TOL or rel > oracle.REL_L2_TOL
+
+
+def _nerf_fixture():
+    import hashlib
+    import torch
+    from gpipes.synth import nerf_params
+    z = load_golden("nerf_workload.npz")
+    ws, bs = nerf_params(64, int(z["Kd"]), int(z["Na"]), int(z["Nrgb"]), seed=int(z["seed"]))
+    h = hashlib.sha256()
+    for t in ws + bs:
+        h.update(t.contiguous().view(torch.int16).numpy().tobytes())
+    assert h.hexdigest() == str(z["weights_sha256"]), "nerf_params no longer reproduces the fixture's weights"
+    f = lambda ts: [t.float().numpy() for t in ts]  # noqa: E731
+    return z, f(ws), f(bs)
+
+
+def test_nerf_golden():
+    z, ws, bs = _nerf_fixture()
+    alpha, rgb = oracle.nerf(z["x"], z["d"], ws, bs, oracle.ACT_SIGMOID)
+    for got, want in ((alpha, z["alpha"]), (rgb, z["rgb"])):
+        max_abs, rel = oracle.errors(got, want)
+        assert max_abs < 1e-4 and rel < 1e-5, (max_abs, rel)
+
+
+def _torch_nerf(x, d, ws, bs, sigmoid):
+    """The NeRF MLP built from torch.nn modules in float64 with the module structure of
+    apps/nerf_full/torch/model.py:5-66 (an implementation independent of the oracle)."""
+    import torch
+
+    def lin(i):
+        m = torch.nn.Linear(ws[i].shape[0], ws[i].shape[1]).double()
+        with torch.no_grad():
+            m.weight.copy_(torch.from_numpy(ws[i]).double().t())
+            m.bias.copy_(torch.from_numpy(bs[i]).double())
+        return m
+    relu = torch.nn.ReLU
+    pre = torch.nn.Sequential(lin(0), relu(), lin(1), relu(), lin(2), relu(), lin(3), relu(), lin(4), relu())
+    post = torch.nn.Sequential(lin(5), relu(), lin(6), relu(), lin(7), relu())
+    rgb = torch.nn.Sequential(lin(10), relu(), lin(11), *([torch.nn.Sigmoid()] if sigmoid else []))
+    with torch.no_grad():
+        xt, dt = torch.from_numpy(x).double(), torch.from_numpy(d).double()
+        enc = post(torch.cat([pre(xt), xt], dim=-1))
+        return lin(8)(enc).numpy(), rgb(torch.cat([lin(9)(enc), dt], dim=-1)).numpy()
+
+
+def _nerf_scaled():
+    """Weights 3x the default init, so every layer's signal survives to the outputs."""
+    _, ws, bs = _nerf_fixture()
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((48, 64)).astype(np.float32)
+    d = rng.standard_normal((48, 27)).astype(np.float32)
+    return x, d, [w * 3 for w in ws], [b * 3 for b in bs]
+
+
+def test_nerf_vs_torch_scaled():
+    x, d, ws, bs = _nerf_scaled()
+    for sig in (False, True):
+        a_o, r_o = oracle.nerf(x, d, ws, bs, oracle.ACT_SIGMOID if sig else oracle.ACT_NONE)
+        a_t, r_t = _torch_nerf(x, d, ws, bs, sig)
+        np.testing.assert_allclose(a_o, a_t, rtol=1e-4, atol=1e-4)
+        np.testing.assert_allclose(r_o, r_t, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("mutant", ["skip_order", "no_skip", "w9_rows_rotated", "bottleneck_relu", "d_dropped",
+                                    "no_sigmoid"])
+def test_nerf_rejects_planted_mistakes(mutant):
+    """Plausible oracle mistakes must fail against torch.nn at the parity bar."""
+    x, d, ws, bs = _nerf_scaled()
+    want_alpha, want_rgb = _torch_nerf(x, d, ws, bs, True)
+    lin = oracle.linear
+    h = x
+    for i in range(5):
+        h = lin(h, ws[i], bs[i], oracle.ACT_RELU)
+    if mutant == "skip_order":
+        h = oracle.concat(x, h)
+    elif mutant == "no_skip":
+        h = oracle.concat(h, np.zeros_like(x))
+    else:
+        h = oracle.concat(h, x)
+    for i in range(5, 8):
+        h = lin(h, ws[i], bs[i], oracle.ACT_RELU)
+    alpha = lin(h, np.roll(ws[8], 1, axis=0) if mutant == "w9_rows_rotated" else ws[8], bs[8])
+    dd = np.zeros_like(d) if mutant == "d_dropped" else d
+    f = lin(h, ws[9], bs[9], oracle.ACT_RELU if mutant == "bottleneck_relu" else oracle.ACT_NONE)
+    g = lin(oracle.concat(f, dd), ws[10], bs[10], oracle.ACT_RELU)
+    rgb = lin(g, ws[11], bs[11], oracle.ACT_NONE if mutant == "no_sigmoid" else oracle.ACT_SIGMOID)
+    fails = []
+    for got, want in ((alpha, want_alpha), (rgb, want_rgb)):
+        max_abs, rel = oracle.errors(got, want)
+        fails.append(max_abs > oracle.MAX_ABS_TOL or rel > oracle.REL_L2_TOL)
+    assert any(fails), mutant
