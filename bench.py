@@ -14,7 +14,9 @@ host cores.
 --workload bert times the BERT-large FFN block of configs[2] instead
 (LayerNorm(GELU(x W1 + b1) W2 + b2 + x), M = 65,536, H 1024, FF 4096): a step is
 one gp_bert_ffn_out call, bound by MFMA, so its roofline is TFLOP/s against the
-dense fp16 peak.
+dense fp16 peak.  --workload dlrm (configs[3]: the bottom and top MLPs over
+M = 262,144) and --workload nerf (configs[4]: the NeRF MLP over M = 1,048,576
+samples) are measured the same way.
 """
 import argparse
 import json
@@ -179,6 +181,153 @@ def bench_bert(args):
     print(json.dumps(rec), flush=True)
 
 
+DLRM_BOT = [16, 512, 256, 128]
+DLRM_TOP = [480, 1024, 1024, 512, 256, 1]
+CHAIN_METRIC = {
+    "dlrm": "rows/sec + % fp16 MFMA peak, DLRM bottom+top MLPs M=262144 (1×MI355X)",
+    "nerf": "samples/sec + % fp16 MFMA peak, NeRF full MLP M=1048576 (1×MI355X)",
+}
+
+
+def chain_flops(widths):
+    return sum(2 * widths[i] * widths[i + 1] for i in range(len(widths) - 1))
+
+
+NERF_FLOPS = 2 * (64 * 256 + 4 * 256 * 256 + 320 * 256 + 2 * 256 * 256 + 256 * 1 + 256 * 256 + 283 * 128 + 128 * 3)
+
+
+def cpu_baseline_chain(workload, budget_s=10.0):
+    """The CPU oracle (oracle.mlp / oracle.nerf over oracle/oracle.c) on a row sample."""
+    import numpy as np
+
+    import oracle
+    from gpipes.synth import dlrm_params, nerf_inputs, nerf_params, padded_normal, padded_uniform
+
+    threads = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "16") or 16), 16)
+    oracle.set_num_threads(threads)
+    f = lambda ts: [t.float().numpy() for t in ts]  # noqa: E731
+    if workload == "dlrm":
+        Ms = 2048
+        wb, bb = dlrm_params(DLRM_BOT, seed=0)
+        wt, bt = dlrm_params(DLRM_TOP, seed=1)
+        xb, xt = padded_uniform(Ms, 13, 16, seed=2).float().numpy(), padded_normal(Ms, 479, 480, seed=3).float().numpy()
+        wb, bb, wt, bt = f(wb), f(bb), f(wt), f(bt)
+        R, S = oracle.ACT_RELU, oracle.ACT_SIGMOID
+
+        def run():
+            oracle.mlp(xb, wb, bb, [R] * 3)
+            oracle.mlp(xt, wt, bt, [R] * 4 + [S])
+        what = f"oracle DlrmMlp bottom {DLRM_BOT} + top {DLRM_TOP} fp32 on {Ms} rows"
+    else:
+        Ms = 2048
+        ws, bs = nerf_params(64, 27, 1, 3, seed=0)
+        x, d = nerf_inputs(Ms, seed=0)
+        ws, bs, x, d = f(ws), f(bs), x.float().numpy(), d.float().numpy()
+
+        def run():
+            oracle.nerf(x, d, ws, bs, oracle.ACT_SIGMOID)
+        what = f"oracle Nerf fp32 on {Ms} samples"
+    run()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {"value": Ms / med, "unit": "rows/s" if workload == "dlrm" else "samples/s", "cores": threads,
+            "kind": "port", "sample": f"{what}, {len(times)} calls in {sum(times):.1f} s, median {med * 1e3:.1f} ms"}
+
+
+def bench_chain(args):
+    """configs[3] (DLRM bottom + top MLP, M = 262,144) or configs[4] (NeRF, M = 1,048,576)."""
+    import torch
+
+    import gpipes
+    from gpipes.synth import dlrm_params, nerf_inputs, nerf_params, padded_normal, padded_uniform
+
+    dev = torch.device("cuda:0")
+    if args.workload == "dlrm":
+        M = 262144
+        wb, bb = dlrm_params(DLRM_BOT, seed=0)
+        wb[0][13:] = 0
+        wt, bt = dlrm_params(DLRM_TOP, seed=1)
+        wt[0][479:] = 0
+        wb, bb, wt, bt = ([t.to(dev) for t in ts] for ts in (wb, bb, wt, bt))
+        xb, xt = padded_uniform(M, 13, 16, seed=2, device=dev), padded_normal(M, 479, 480, seed=3, device=dev)
+        ob = torch.empty((M, 128), dtype=torch.float16, device=dev)
+        ot = torch.empty((M, 1), dtype=torch.float16, device=dev)
+
+        def step():
+            gpipes.mlp_out(xb, wb, bb, ["relu"] * 3, ob)
+            gpipes.mlp_out(xt, wt, bt, ["relu"] * 4 + ["sigmoid"], ot)
+        flops = M * (chain_flops(DLRM_BOT) + chain_flops(DLRM_TOP))
+        bytes_ = M * (16 + 128 + 480 + 1) * 2
+        config = {"workload": "dlrm_bottom_top_mlp", "M": M, "bottom": "16(13)-512-256-128 ReLU",
+                  "top": "480(479)-1024-1024-512-256 ReLU, 256-1 sigmoid", "accumulate": "f32", "row_chunk": 262144}
+        data = "synthetic (dense U(0,1), top input N(0,1), Xavier-uniform weights, seed 0)"
+        unit = "rows/s"
+    else:
+        M = 1048576
+        ws, bs = nerf_params(64, 27, 1, 3, seed=0, device=dev)
+        x, d = nerf_inputs(M, seed=0, device=dev)
+        o_r = torch.empty((M, 1), dtype=torch.float16, device=dev)
+        o_rgb = torch.empty((M, 3), dtype=torch.float16, device=dev)
+        wb = [t for pair in zip(ws, bs) for t in pair]
+
+        def step():
+            gpipes.nerf_full_out(x, d, *wb, o_r, o_rgb, rgb_act="sigmoid")
+        flops = M * NERF_FLOPS
+        bytes_ = M * (64 + 27 + 1 + 3) * 2
+        config = {"workload": "nerf_full_mlp", "M": M, "x": "63 encoded + 1 pad", "d": 27,
+                  "layers": "8x256 ReLU (skip at 5), density 1, feature 256, 283-128 ReLU, 128-3 sigmoid",
+                  "accumulate": "f32", "row_chunk": 262144}
+        data = "synthetic (positional encodings of U(-1,1) points and unit directions, Kaiming-uniform, seed 0)"
+        unit = "samples/s"
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        step()
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    call_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    avg_ms = sum(call_ms) / len(call_ms)
+    ms_per_step = wall * 1e3 / args.steps
+    tflops = flops / (avg_ms * 1e-3) / 1e12
+    rec = {
+        "metric": CHAIN_METRIC[args.workload],
+        "value": M / (ms_per_step * 1e-3),
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": data,
+        "config": config,
+        "roofline": {
+            "bound": "mfma", "achieved": tflops, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": tflops / MFMA_F16_PEAK_TFLOPS, "traffic": None,
+            "kernel_ms_avg": avg_ms, "kernel_ms_median": call_ms[len(call_ms) // 2],
+            "flops_per_launch": flops, "algorithmic_bytes_per_launch": bytes_,
+            "launch": "one step: every layer a wide-GEMM launch per 262,144-row chunk (weights transposed per call)",
+        },
+        "cpu_baseline": None if args.no_cpu else cpu_baseline_chain(args.workload),
+    }
+    print(json.dumps(rec), flush=True)
+
+
 def load_traffic(workload, impl):
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
@@ -193,7 +342,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["bert"], default="edge")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["bert", "dlrm", "nerf"], default="edge")
     ap.add_argument("--impl", choices=["fused", "pipelined", "pipelined_split_ln"], default="fused")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-ref", action="store_true",
@@ -208,6 +357,9 @@ def main():
 
     if args.workload == "bert":
         bench_bert(args)
+        return
+    if args.workload in ("dlrm", "nerf"):
+        bench_chain(args)
         return
 
     import torch

@@ -7,8 +7,7 @@
 // apps/nerf_full/pipelined/nerf_full_pl.cuh:122-274).  Their layers are 256 to
 // 1024 wide, so the weights (0.34 to 6 MB) cannot stay resident in one CU;
 // here every layer is one launch of the wide GEMM stage (gemm.hip) with its
-// bias and activation fused, over row chunks of 65,536 so that a chunk's
-// activations (at most 128 MiB) can stay in the 256 MB MALL between layers.
+// bias and activation fused, over row chunks of 262,144.
 // Narrow and odd widths are handled by padding, never by special kernels:
 //   * weights are transposed into the workspace with zero rows and columns up
 //     to K a multiple of 64 and N a multiple of 128, biases zero-padded to N;
@@ -30,7 +29,10 @@
 namespace gp {
 namespace {
 
-constexpr int64_t kChunkRows = 65536;
+// Rows per chunk: 262,144 rows give a 256-wide layer 1,024 tiles (four per CU,
+// so each CU's next tile is copied while the previous one's epilogue runs)
+// and keep a 256-wide activation (128 MiB) MALL-sized.
+constexpr int64_t kChunkRows = 262144;
 constexpr int64_t kMaxRows = (int64_t(1) << 31) - 1;  // GEMM tile indices are 32-bit
 constexpr int64_t kMaxWidth = 16384;
 

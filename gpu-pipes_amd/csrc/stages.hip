@@ -288,24 +288,45 @@ hipError_t layer_norm_launch(int64_t M, int64_t D, const void* x, const void* ga
 
 // dst[m][j] = act(src[m][j]) for j < w, 0 for w <= j < wpad: moves a column
 // block between matrices with zero padding (the concat inputs, padded inputs
-// and narrow heads of the MLP chains).  Strides in elements.
+// and narrow heads of the MLP chains).  Strides in elements.  V elements per
+// thread: 8 (16-byte vectors) when every width, stride and base allows it.
+template <int V>
 __global__ __launch_bounds__(kStageThreads) void place_kernel(const half_t* src, int64_t lds, int w, half_t* dst,
                                                               int64_t ldd, int wpad, int act, int64_t M) {
-  const int64_t total = M * wpad;
+  typedef _Float16 hv __attribute__((ext_vector_type(V)));
+  const int vpr = wpad / V;  // vectors per row
+  const int64_t total = M * vpr;
   for (int64_t i = (int64_t)blockIdx.x * kStageThreads + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * kStageThreads) {
-    const int64_t m = i / wpad;
-    const int j = (int)(i - m * wpad);
-    dst[m * ldd + j] = j < w ? (half_t)apply_act((float)src[m * lds + j], act) : (half_t)0.f;
+    const int64_t m = i / vpr;
+    const int j = (int)(i - m * vpr) * V;
+    hv v;
+    if (j + V <= w) {
+      v = *(const hv*)(src + m * lds + j);
+#pragma unroll
+      for (int e = 0; e < V; ++e) v[e] = (half_t)apply_act((float)v[e], act);
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e) v[e] = j + e < w ? (half_t)apply_act((float)src[m * lds + j + e], act) : (half_t)0.f;
+    }
+    *(hv*)(dst + m * ldd + j) = v;
   }
 }
 
 hipError_t place_launch(int64_t M, const void* src, int64_t lds, int64_t w, void* dst, int64_t ldd, int64_t wpad,
                         int act, int num_cus, hipStream_t s) {
-  if (M <= 0) return hipSuccess;
-  const int64_t want = (M * wpad + kStageThreads - 1) / kStageThreads, cap = (int64_t)num_cus * 16;
-  hipLaunchKernelGGL(place_kernel, dim3((unsigned)(want < cap ? want : cap)), dim3(kStageThreads), 0, s,
-                     (const half_t*)src, lds, (int)w, (half_t*)dst, ldd, (int)wpad, act, M);
+  if (M <= 0 || wpad <= 0) return hipSuccess;
+  const bool vec = wpad % 8 == 0 && ldd % 8 == 0 && ((uintptr_t)dst & 15) == 0 &&
+                   (w == 0 || (w % 8 == 0 && lds % 8 == 0 && ((uintptr_t)src & 15) == 0));
+  const int V = vec ? 8 : 1;
+  const int64_t want = (M * (wpad / V) + kStageThreads - 1) / kStageThreads, cap = (int64_t)num_cus * 16;
+  const dim3 grid((unsigned)(want < cap ? want : cap)), block(kStageThreads);
+  if (vec)
+    hipLaunchKernelGGL(place_kernel<8>, grid, block, 0, s, (const half_t*)src, lds, (int)w, (half_t*)dst, ldd,
+                       (int)wpad, act, M);
+  else
+    hipLaunchKernelGGL(place_kernel<1>, grid, block, 0, s, (const half_t*)src, lds, (int)w, (half_t*)dst, ldd,
+                       (int)wpad, act, M);
   return hipGetLastError();
 }
 

@@ -126,7 +126,7 @@ int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void*
  * widths in [1, 16384]; x [M, widths[0]], out [M, widths[nlayers]].  This is
  * DlrmMlp(widths, sigmoid_i) of common/mlps.py:23-34 (ReLU after every layer,
  * sigmoid after layer sigmoid_i) with the activation of each layer given.
- * Rows go through in chunks of 65,536 with the activations in the per-stream
+ * Rows go through in chunks of 262,144 with the activations in the per-stream
  * workspace.
  */
 int gp_mlp_out(int64_t M, int nlayers, const int64_t* widths, const void* const* w, const void* const* b,
