@@ -281,9 +281,11 @@ def bench_chain(args):
         bytes_ = M * (64 + 27 + 1 + 3) * 2
         config = {"workload": "nerf_full_mlp", "M": M, "x": "63 encoded + 1 pad", "d": 27,
                   "layers": "8x256 ReLU (skip at 5), density 1, feature 256, 283-128 ReLU, 128-3 sigmoid",
-                  "accumulate": "f32", "row_chunk": 262144}
+                  "accumulate": "f32", "tile_rows": 256}
         data = "synthetic (positional encodings of U(-1,1) points and unit directions, Kaiming-uniform, seed 0)"
         unit = "samples/s"
+    launch = {"dlrm": "one step: every layer a wide-GEMM launch per 262,144-row chunk (weights transposed per call)",
+              "nerf": "one step: the weight-packing kernel, then the fused 12-layer kernel over 256-row tiles"}
 
     for _ in range(args.warmup):
         step()
@@ -321,7 +323,7 @@ def bench_chain(args):
             "frac": tflops / MFMA_F16_PEAK_TFLOPS, "traffic": None,
             "kernel_ms_avg": avg_ms, "kernel_ms_median": call_ms[len(call_ms) // 2],
             "flops_per_launch": flops, "algorithmic_bytes_per_launch": bytes_,
-            "launch": "one step: every layer a wide-GEMM launch per 262,144-row chunk (weights transposed per call)",
+            "launch": launch[args.workload],
         },
         "cpu_baseline": None if args.no_cpu else cpu_baseline_chain(args.workload),
     }

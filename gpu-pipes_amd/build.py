@@ -29,12 +29,13 @@ HIP_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 # MFMA accumulators in VGPRs: the AGPR file holds the resident weights of the
-# MLP kernels.  The wide GEMM keeps its 256 accumulators in AGPRs instead.
+# MLP kernels.  The wide GEMM and the fused NeRF kernel keep their 256
+# accumulators in AGPRs instead.
 VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 
-SOURCES = ["mgn_fused.hip", "mgn_pipelined.hip", "stages.hip", "gemm.hip", "capi.cpp", "ffn.cpp", "mlp.cpp",
-           "arena.cpp"]
-SOURCE_FLAGS = {"gemm.hip": []}
+SOURCES = ["mgn_fused.hip", "mgn_pipelined.hip", "stages.hip", "gemm.hip", "nerf_fused.hip", "capi.cpp", "ffn.cpp",
+           "mlp.cpp", "arena.cpp"]
+SOURCE_FLAGS = {"gemm.hip": [], "nerf_fused.hip": []}
 
 
 def _run(cmd, verbose):

@@ -81,4 +81,15 @@ hipError_t concat_launch(int64_t M, int64_t N0, int64_t N1, const void* a, const
 hipError_t place_launch(int64_t M, const void* src, int64_t lds, int64_t w, void* dst, int64_t ldd, int64_t wpad,
                         int act, int num_cus, hipStream_t stream);
 
+// The NeRF MLP (apps/nerf_full/torch/model.py:5-66, hidden 256) as one fused
+// kernel: supported for Kx, Kd, Na, Nrgb <= 64; x and d 16-byte aligned.
+// w[i], b[i]: layer i+1's [K, N] weight and [N] bias (b may be null).  The
+// workspace (nerf_fused_workspace() bytes, 16-byte aligned) receives the
+// packed weight stream.
+bool nerf_fused_supported(int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb);
+size_t nerf_fused_workspace();
+hipError_t nerf_fused_launch(int64_t M, int Kx, int Kd, int Na, int Nrgb, const void* x, const void* d,
+                             const void* const* w, const void* const* b, int rgb_act, void* out_r, void* out_rgb,
+                             void* ws, int num_cus, hipStream_t stream);
+
 }  // namespace gp

@@ -216,6 +216,28 @@ int gp_nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb
   if ((rc = current_device_info(&dev, &ncu))) return rc;
   hipStream_t s = (hipStream_t)stream;
 
+  if (nerf_fused_supported(Kx, Kd, Na, Nrgb)) {
+    // The fused kernel copies x and d rows from 16-byte aligned bases; an
+    // input that is not (a row slice of a [M, 27] tensor, say) is copied into
+    // the workspace first, so results never depend on how inputs are sliced.
+    const bool cx = !aligned16(x), cd = !aligned16(d);
+    Carve cv;
+    const size_t o_st = cv.take(nerf_fused_workspace());
+    const size_t o_x = cx ? cv.take((size_t)M * Kx * 2) : 0;
+    const size_t o_d = cd ? cv.take((size_t)M * Kd * 2) : 0;
+    char* ws = nullptr;
+    if ((rc = workspace_acquire(dev, s, cv.off, (void**)&ws))) return rc;
+    hipError_t e = hipSuccess;
+    if (cx) e = hipMemcpyAsync(ws + o_x, x, (size_t)M * Kx * 2, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess && cd) e = hipMemcpyAsync(ws + o_d, d, (size_t)M * Kd * 2, hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) return fail_hip(e, "NeRF input alignment copy");
+    e = nerf_fused_launch(M, (int)Kx, (int)Kd, (int)Na, (int)Nrgb, cx ? ws + o_x : x, cd ? ws + o_d : d, w, b,
+                          rgb_act, out_r, out_rgb, ws + o_st, ncu, s);
+    if (e != hipSuccess) return fail_hip(e, "NeRF fused kernel launch");
+    return GP_OK;
+  }
+
+  // Wider inputs or heads: one wide-GEMM launch per layer.
   // Layer shapes of apps/nerf_full/torch/model.py:5-46 with hidden 256:
   // 1: Kx->256, 2-5: 256->256 (ReLU); 6: [h | x] -> 256, 7-8: 256->256 (ReLU);
   // 9: 256->Na (density, linear); 10: 256->256 (bottleneck, linear);

@@ -166,3 +166,106 @@ def test_nerf_full_size(cuda):
     assert torch.equal(sa.view(torch.int16), a[261900:262900].view(torch.int16))  # across a chunk edge
     assert torch.equal(sr.view(torch.int16), r[261900:262900].view(torch.int16))
     assert torch.isfinite(a.float()).all() and ((r.float() >= 0) & (r.float() <= 1)).all()
+
+
+def nerf_general_inputs(M, Kx, Kd, seed, device="cpu"):
+    """Inputs of any width: the positional encodings (63 and 27 features) cut or zero-padded."""
+    x0, d0 = nerf_inputs(M, seed=seed)
+    x = torch.zeros((M, Kx), dtype=torch.float16)
+    x[:, :min(Kx, 63)] = x0[:, :min(Kx, 63)]
+    d = torch.zeros((M, Kd), dtype=torch.float16)
+    d[:, :min(Kd, 27)] = d0[:, :min(Kd, 27)]
+    return x.to(device), d.to(device)
+
+
+@pytest.mark.parametrize("Kx,Kd,Na,Nrgb", [
+    (60, 24, 1, 3),     # the reference model's defaults (in_x_ch 60, in_d_ch 24)
+    (63, 27, 4, 3),     # odd input widths (rows not 16-byte multiples)
+    (64, 32, 64, 64),   # the reference pipelined app's padded shapes
+    (8, 1, 33, 63),     # narrow inputs, heads of two feature blocks
+    (72, 27, 1, 3),     # x wider than 64: one GEMM launch per layer
+    (64, 70, 1, 3),     # d wider than 64: likewise
+    (64, 27, 65, 3),    # density head wider than 64: likewise
+])
+@pytest.mark.parametrize("M", [33, 255, 257, 4099])
+def test_nerf_widths_vs_oracle(cuda, Kx, Kd, Na, Nrgb, M):
+    """Every input / head width the C ABI accepts goes through one of the two paths
+    (the fused kernel for Kx, Kd, Na, Nrgb <= 64, the GEMM chain otherwise).  At least
+    33 rows: the relative-L2 bar over a single near-zero density value is meaningless
+    (M = 1 is covered at the workload widths above)."""
+    ws, bs = nerf_params(Kx, Kd, Na, Nrgb, seed=M + Kx, zero_pad_rows=None)
+    ws, bs = [(w.float() * 2).half() for w in ws], [(b.float() * 2).half() for b in bs]
+    x, d = nerf_general_inputs(M, Kx, Kd, seed=M)
+    a, r = nerf_call(x.to(cuda), d.to(cuda), to(ws, cuda), to(bs, cuda), "sigmoid")
+    wa, wr = oracle.nerf(f(x), f(d), [f(w) for w in ws], [f(b) for b in bs], oracle.ACT_SIGMOID)
+    assert_parity(f(a), wa, f"nerf alpha Kx={Kx} Kd={Kd} Na={Na} M={M}")
+    assert_parity(f(r), wr, f"nerf rgb Kx={Kx} Kd={Kd} Nrgb={Nrgb} M={M}")
+
+
+def test_nerf_null_biases(cuda):
+    M = 1000
+    ws, bs = nerf_params(64, 27, 1, 3, seed=5)
+    bs = [None if i % 2 else b for i, b in enumerate(bs)]
+    x, d = nerf_inputs(M, seed=5)
+    a, r = nerf_call(x.to(cuda), d.to(cuda), to(ws, cuda), to(bs, cuda), "none")
+    wa, wr = oracle.nerf(f(x), f(d), [f(w) for w in ws], [f(b) for b in bs], oracle.ACT_NONE)
+    assert_parity(f(a), wa, "nerf null biases alpha")
+    assert_parity(f(r), wr, "nerf null biases rgb")
+
+
+def test_nerf_fused_matches_layer_chain(cuda):
+    """The same network through both paths: x zero-padded from 64 to 72 columns (with zero
+    weight rows for the padding) takes the per-layer GEMM chain; both agree with each other
+    and with the oracle."""
+    M = 20000
+    ws, bs = nerf_params(64, 27, 1, 3, seed=9, device=cuda)
+    x, d = nerf_inputs(M, seed=9, device=cuda)
+    x72 = torch.zeros((M, 72), dtype=torch.float16, device=cuda)
+    x72[:, :64] = x
+    w72 = list(ws)
+    w72[0] = torch.cat([ws[0], torch.zeros((8, 256), dtype=torch.float16, device=cuda)])
+    w72[5] = torch.cat([ws[5], torch.zeros((8, 256), dtype=torch.float16, device=cuda)])
+    a1, r1 = nerf_call(x, d, ws, bs, "sigmoid")
+    a2, r2 = nerf_call(x72, d, w72, bs, "sigmoid")
+    assert_parity(f(a1), f(a2), "fused vs chain alpha")
+    assert_parity(f(r1), f(r2), "fused vs chain rgb")
+    rows = np.r_[0:100, M - 100:M]
+    wa, wr = oracle.nerf(f(x[rows]), f(d[rows]), [f(w) for w in ws], [f(b) for b in bs], oracle.ACT_SIGMOID)
+    assert_parity(f(a2)[rows], wa, "chain alpha")
+    assert_parity(f(r2)[rows], wr, "chain rgb")
+
+
+def test_nerf_unaligned_inputs_bit_exact(cuda):
+    """Row slices of [M, 27] or [M, 63] inputs start at addresses that are not 16-byte aligned;
+    they are copied into the workspace and give exactly the aligned call's results."""
+    M = 5000
+    for Kx, Kd in ((64, 27), (63, 27), (64, 32)):
+        ws, bs = nerf_params(Kx, Kd, 1, 3, seed=Kx + Kd, device=cuda, zero_pad_rows=None)
+        x, d = nerf_general_inputs(M + 7, Kx, Kd, seed=3, device=cuda)
+        a1, r1 = nerf_call(x[3:3 + M].clone(), d[3:3 + M].clone(), ws, bs, "sigmoid")
+        xs, ds = x[3:3 + M], d[3:3 + M]   # views: 3 rows into the buffers
+        a2, r2 = nerf_call(xs, ds, ws, bs, "sigmoid")
+        assert torch.equal(a1.view(torch.int16), a2.view(torch.int16)), (Kx, Kd)
+        assert torch.equal(r1.view(torch.int16), r2.view(torch.int16)), (Kx, Kd)
+
+
+def test_nerf_back_to_back_and_streams(cuda):
+    """Two calls with different weights on one stream, then one on a side stream: the packed
+    weight stream lives in the per-stream workspace and is rebuilt by every call."""
+    M = 3000
+    x, d = nerf_inputs(M, seed=11, device=cuda)
+    p1 = nerf_params(64, 27, 1, 3, seed=12, device=cuda)
+    p2 = nerf_params(64, 27, 1, 3, seed=13, device=cuda)
+    a1, r1 = nerf_call(x, d, *p1, "sigmoid")
+    a2, r2 = nerf_call(x, d, *p2, "sigmoid")
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        a3, r3 = nerf_call(x, d, *p1, "sigmoid")
+    s.synchronize()
+    torch.cuda.synchronize()
+    for (a, r), (ws, bs) in (((a1, r1), p1), ((a2, r2), p2)):
+        wa, wr = oracle.nerf(f(x), f(d), [f(w) for w in ws], [f(b) for b in bs], oracle.ACT_SIGMOID)
+        assert_parity(f(a), wa, "alpha")
+        assert_parity(f(r), wr, "rgb")
+    assert torch.equal(a1.view(torch.int16), a3.view(torch.int16))
+    assert torch.equal(r1.view(torch.int16), r3.view(torch.int16))
