@@ -144,6 +144,7 @@ __device__ __forceinline__ void dma16_buf_nt(__amdgpu_buffer_rsrc_t rsrc, int vo
 // Accesses at or beyond the descriptor's range read zero / are dropped, which
 // is how partial tiles are bounded without per-row branches.
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ h4 buf_load_h4(__amdgpu_buffer_rsrc_t rsrc, int off) {
   return __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rsrc, off, 0, 0));
 }

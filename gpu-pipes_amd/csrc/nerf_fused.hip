@@ -25,21 +25,25 @@
 //    the host packs all layers once per call into the exact order the kernel
 //    consumes them, as 1 KiB fragments (64 lanes x 16 bytes), 16 to a 16 KiB
 //    slot.  Slots are copied L2 -> LDS with buffer_load ... lds into a ring of
-//    nine (144 KiB); up to eight are in flight while one is read.  The
-//    remaining 16 KiB of LDS hold every layer's bias.
+//    nine (144 KiB); eight are in flight while one is read.
 //  * The network inputs travel through the same ring: a tile's x rows (twice:
 //    for layer 1 and for the skip input of layer 6) and its d rows occupy
 //    "pseudo-slots" of the stream whose copies read x or d instead of
-//    weights, 128 rows per slot, zero-filled past the last valid row.
-//  * Slot bookkeeping is per wave and wave-uniform: before a slot is read,
-//    each wave waits until its own copies of that slot have landed (vmcnt
-//    counts only the copies issued after it) and the workgroup passes one
-//    barrier; the barrier also certifies that every wave has finished reading
-//    the slots released at that point, which the copies then refill.
-//  * Epilogues: bias (from LDS, added in fp32), ReLU in packed fp16 after RNE
-//    rounding (max commutes with rounding), straight into the B-operand
-//    registers; the density and colour heads are stored through buffer
-//    descriptors bounded to the tile's valid rows.
+//    weights, 128 rows per slot, zero-filled past the last valid row.  Each
+//    is read into registers as soon as it is acquired.
+//  * Every slot is therefore dead once the next one is acquired, which makes
+//    the ring bookkeeping fixed: acquiring slot q waits for this wave's copies
+//    of q (the 28 copies issued after them may still be in flight) and passes
+//    one workgroup barrier, after which no wave reads slot q-1 again; slot
+//    q+8 is copied into q-1's place once slot q's first MFMAs are issued.
+//  * Bias of a hidden layer: one extra MFMA per accumulator block, the bias
+//    fragment (bias in k = 0) times a constant B operand that is 1 in k = 0,
+//    is each accumulator's first product, so the epilogue is only the fp16
+//    conversion and ReLU (in packed fp16: max commutes with RNE rounding).
+//    The wave issues at most one instruction every four cycles, so an MFMA
+//    (32 cycles) in place of 16 VALU adds is the cheaper side.
+//  * The density and colour heads add their bias in fp32 and are stored
+//    through buffer descriptors bounded to the tile's valid rows.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -53,9 +57,11 @@
 namespace gp {
 namespace nerf {
 
-constexpr int NW = 4;
+constexpr int NW = 8;              // waves per workgroup, two per SIMD
+constexpr int RB = 1;              // 32-row blocks per wave
 constexpr int NT = NW * kWave;
-constexpr int ROWS = 64 * NW;      // rows per tile
+constexpr int ROWS = 32 * RB * NW; // rows per tile
+constexpr int CPW = 16 / NW;       // 1 KiB copies per wave per slot
 constexpr int FRAG = 1024;         // one A operand: 64 lanes x 16 bytes
 constexpr int FPS = 16;            // fragments per slot
 constexpr int SLOT = FPS * FRAG;   // bytes per ring slot
@@ -65,9 +71,17 @@ constexpr int PART = 128;          // rows of x or d per pseudo-slot
 // Local slot map of one tile's stream (82 slots, 1.31 MB).
 constexpr int S_X1 = 0, S_L1 = 2, S_L2 = 4, S_X2 = 36, S_L6 = 38, S_L7 = 48, S_L9 = 64, S_L10 = 66, S_D = 74,
               S_L11 = 76, S_L12 = 81, S_TOTAL = 82;
-// Bias table (2560 values): layers 1-8 at 256 i, then 9, 10, 11, 12.
-constexpr int B_L9 = 2048, B_L10 = 2112, B_L11 = 2368, B_L12 = 2496, B_TOTAL = 2560;
-constexpr int BIAS_BYTES = B_TOTAL * 4;  // held as fp32 in LDS
+// Pseudo-slot positions as a 128-bit mask (bits 0, 1, 36, 37, 74, 75).
+constexpr uint64_t PSEUDO_LO = (1ull << S_X1) | (1ull << (S_X1 + 1)) | (1ull << S_X2) | (1ull << (S_X2 + 1));
+constexpr uint64_t PSEUDO_HI = (1ull << (S_D - 64)) | (1ull << (S_D + 1 - 64));
+
+// Bias tables (fp16 in global memory).  Hidden layers: per feature block fb a
+// 64-entry A-operand column, bias[32 fb + lane] for lanes < 32 and 0 for the
+// upper half (k = 8..15).  Heads: plain vectors of 64.
+constexpr int BF_L1 = 0, BF_L2 = 512, BF_L6 = 2560, BF_L7 = 3072, BF_L10 = 4096, BF_L11 = 4608, BF_END = 4864;
+constexpr int BH_L9 = BF_END, BH_L12 = BF_END + 64, B_TOTAL = BF_END + 128;
+// LDS: the hidden-layer table as fp16, then the head biases as fp32.
+constexpr int BIAS_BYTES = BF_END * 2 + 128 * 4;
 static_assert(NS * SLOT + BIAS_BYTES <= 160 * 1024, "LDS");
 
 struct Args {
@@ -87,26 +101,20 @@ __host__ __device__ constexpr int sigma(int p) { return p < 4 ? p : p < 8 ? p + 
 
 // Slot kinds.  A compute slot holds 16 fragments of one layer: FB feature
 // blocks per input k-block, starting at k-block KB0; the layer's first NEXT
-// k-blocks take their B operand from pseudo-slots (EXT 1: x for layer 1,
-// 2: x for layer 6, 3: d for layer 11), the rest from registers.
+// k-blocks take their B operand from a pseudo-slot input, the rest from
+// registers; HB: the layer's bias enters through the MFMA (hidden layers).
 //   1-2 layer 1, 3-10 a 256 -> 256 layer, 11-20 layer 6, 21-22 layer 9,
-//   23-27 layer 11, 28 layer 12; 0 a pseudo-slot (nothing to compute).
+//   23-27 layer 11, 28 layer 12.
 struct Kind {
-  int fb, kb0, next, ext;
+  int fb, kb0, next, hb;
 };
 __host__ __device__ constexpr Kind kind_info(int k) {
   return k <= 2    ? Kind{8, 2 * (k - 1), 4, 1}
-         : k <= 10 ? Kind{8, 2 * (k - 3), 0, 0}
-         : k <= 20 ? Kind{8, 2 * (k - 11), 4, 2}
+         : k <= 10 ? Kind{8, 2 * (k - 3), 0, 1}
+         : k <= 20 ? Kind{8, 2 * (k - 11), 4, 1}
          : k <= 22 ? Kind{2, 8 * (k - 21), 0, 0}
-         : k <= 27 ? Kind{4, 4 * (k - 23), 4, 3}
+         : k <= 27 ? Kind{4, 4 * (k - 23), 4, 1}
                    : Kind{2, 0, 0, 0};
-}
-// Returns v unchanged in a scalar register, hiding its value from the
-// optimiser so that values derived from it are not hoisted and kept live.
-__device__ __forceinline__ int opaque_s(int v) {
-  asm volatile("" : "+s"(v));
-  return v;
 }
 
 template <int... I, class F>
@@ -114,111 +122,132 @@ __device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&&
   (f(std::integral_constant<int, I>{}), ...);
 }
 
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void nerf_fused_kernel(Args p) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void nerf_fused_kernel(Args p) {
   __shared__ __attribute__((aligned(1024))) char smem[NS * SLOT + BIAS_BYTES];
   GP_LDS char* const ring = (GP_LDS char*)smem;
-  GP_LDS float* const btab = (GP_LDS float*)(smem + NS * SLOT);
+  GP_LDS half_t* const bfrag = (GP_LDS half_t*)(smem + NS * SLOT);
+  GP_LDS float* const bhead = (GP_LDS float*)(smem + NS * SLOT + BF_END * 2);
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, lr = lane & 31, lh = lane >> 5;
+  const int lane0 = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = gridDim.x;
-  const int64_t ntiles = (p.M + ROWS - 1) / ROWS;
-  const int my = (int)((ntiles - blockIdx.x + G - 1) / G);  // tiles blockIdx.x + k G, k < my
-  const int total = my * S_TOTAL;                            // slots this workgroup consumes
+  // Tile and slot counts fit in 32 bits: the host limits M to 2^31 - 1.
+  const int ntiles = (int)((p.M + ROWS - 1) / ROWS);
+  const int my = (ntiles - (int)blockIdx.x + G - 1) / G;  // tiles blockIdx.x + k G, k < my
 
-  for (int i = tid; i < B_TOTAL; i += NT) btab[i] = (float)p.bias[i];
+  for (int i = tid; i < BF_END / 8; i += NT) ((GP_LDS h8*)bfrag)[i] = ((const h8*)p.bias)[i];
+  if (tid < 128) bhead[tid] = (float)p.bias[BF_END + tid];
   __syncthreads();
 
   // ---------------------------------------------------------------- copies
-  // Global slot q (tile q / S_TOTAL, local slot q % S_TOTAL) goes to ring
-  // slot q % NS; 16-byte chunk c = 4 i + wave of the slot is this wave's copy i.
+  // Global slot q = k S_TOTAL + l (tile k, local slot l) lives in ring slot
+  // q % NS.  `cur` is the ring slot of the last acquired slot; (iss_k, iss_l)
+  // the next slot to copy, which goes to ring slot (cur + NS - 1) % NS.
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.stream, S_TOTAL * SLOT);
   auto tile_r0 = [&](int k) { return ((int64_t)blockIdx.x + (int64_t)k * G) * ROWS; };
-  auto issue = [&](int q) {
-    const int k = q / S_TOTAL, l = q - k * S_TOTAL;
-    GP_LDS char* const dst = ring + (q % NS) * SLOT;
-    __amdgpu_buffer_rsrc_t r = rw;
-    int base = l * SLOT;
-    const bool px = l == S_X1 || l == S_X1 + 1 || l == S_X2 || l == S_X2 + 1;
-    if (px || l == S_D || l == S_D + 1) {
-      const int part = l & 1;  // every pseudo-slot pair starts at an even slot
-      const int K = px ? p.Kx : p.Kd;
-      const int64_t row0 = tile_r0(k) + part * PART;
-      const int64_t left = p.M - row0;
-      const int rows = left <= 0 ? 0 : left < PART ? (int)left : PART;
-      // The range is rounded up to whole 16-byte copies; the bytes past the
-      // last valid row lie in the same 16-byte block (so the same page) and
-      // land only in rows that are never stored.
-      r = make_rsrc((px ? p.x : p.d) + row0 * K, (rows * K * 2 + 15) & ~15);
-      base = 0;
-    }
+  int cur = NS - 1, iss_k = 0, iss_l = 0;
+  // Copy the next slot into ring slot `rs`: chunk c = NW i + wave of the slot
+  // is this wave's copy i.
+  auto issue = [&](int rs) {
+    const int l = iss_l;
+    // Branch-free, so that a slot's MFMAs and its copies form one basic block
+    // the scheduler can interleave.  Past the last slot (iss_k == my) the
+    // descriptor range is 0: the copies read nothing and zero a dead slot,
+    // and every acquire still finds exactly 28 newer copies in flight.
+    const bool pseudo = l < 64 ? (PSEUDO_LO >> l) & 1 : (PSEUDO_HI >> (l - 64)) & 1;
+    const bool px = l < S_D;
+    const int K = px ? p.Kx : p.Kd;
+    const int64_t row0 = tile_r0(iss_k) + (l & 1) * PART;  // pseudo-slot pairs start at even slots
+    const int64_t left = p.M - row0;
+    const int rows = left <= 0 ? 0 : left < PART ? (int)left : PART;
+    // The range is rounded up to whole 16-byte copies; the bytes past the
+    // last valid row lie in the same 16-byte block (so the same page) and
+    // land only in rows that are never stored.
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc((px ? p.x : p.d) + row0 * K, (rows * K * 2 + 15) & ~15);
+    const __amdgpu_buffer_rsrc_t r = pseudo ? rp : iss_k < my ? rw : make_rsrc(p.stream, 0);
+    const int base = pseudo ? 0 : l * SLOT;
+    GP_LDS char* const dst = ring + rs * SLOT;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = 4 * i + wave;
-      dma16_buf_so(r, 16 * lane, base + c * FRAG, dst + c * FRAG);
+    for (int i = 0; i < CPW; ++i) {
+      const int c = NW * i + wave;
+      dma16_buf_so(r, 16 * lane0, base + c * FRAG, dst + c * FRAG);
     }
+    const bool wrap = ++iss_l == S_TOTAL;
+    iss_l = wrap ? 0 : iss_l;
+    iss_k += wrap ? 1 : 0;
   };
-  // Slots 0 .. NS-2 are copied ahead; acquiring slot q copies slot q + NS - 1
-  // into the ring slot of q - 1, which every wave has finished reading when
-  // it passes the barrier.  Until then the NS - 2 slots after q are in flight.
-  for (int q = 0; q < total && q < NS - 1; ++q) issue(q);
-  auto acquire = [&](int q) {
-    if (q + NS - 2 < total) wait_vmcnt<4 * (NS - 2)>();
-    else wait_vmcnt<0>();
+  for (int i = 0; i < NS - 1; ++i) issue(i);
+  // Acquire the next slot in stream order.  The copy that refills the ring
+  // slot of the previous one (dead from the barrier on) is issued by refill(),
+  // after the first MFMAs of the new slot, so that the scalar work of the
+  // copy does not sit between the barrier and the matrix pipe.  Every
+  // acquire is followed by exactly one refill() before the next acquire.
+  auto acquire = [&] {
+    wait_vmcnt<CPW * (NS - 2)>();
     lds_barrier();
-    if (q + NS - 1 < total) issue(q + NS - 1);
+    cur = cur == NS - 1 ? 0 : cur + 1;
   };
+  auto refill = [&] { issue(cur == 0 ? NS - 1 : cur - 1); };
 
-  f16x acc[8][2];  // [feature block][row block]
-  h8 act[16][2];   // B operands of register-fed k-blocks: [k-block][row block]
-  h8 xin[4][2];    // B operands of the x / d k-blocks: [k-block][row block]
-  h8 fa[2][4];     // A fragments of two groups in flight
+  f16x acc[8][RB];  // [feature block][row block]
+  h8 act[16][RB];   // B operands of register-fed k-blocks: [k-block][row block]
+  h8 xin[4][RB];    // B operands of the x / d k-blocks: [k-block][row block]
+  h8 fa[1][4];     // A fragments of the current group
+  // B operand that is 1 at k = 0 and 0 elsewhere: lanes 0-31 hold k = 0..7.
+  h8 ones = {};
+  ones[0] = lane0 < 32 ? (half_t)1.f : (half_t)0.f;
 
   for (int k = 0; k < my; ++k) {
-    const int qb = k * S_TOTAL;
     const int64_t r0 = tile_r0(k);
     const int vrows = p.M - r0 < ROWS ? (int)(p.M - r0) : ROWS;
-    // LDS address of local slot l, recomputed at every use (opaque) rather
-    // than hoisted: 82 live slot addresses would spill scalar registers.
-    auto slot = [&](int l) { return (GP_LDS const char*)(ring + ((opaque_s(qb) + l) % NS) * SLOT); };
 
-    // Acquire the pseudo-slot pair at local slots l0, l0+1 and read this
-    // wave's rows of it (slot l0 + wave / 2 holds them, K columns per row)
-    // into xin, zero for columns >= K.  Each half of the pair is read right
+    auto cur_slot = [&] { return (GP_LDS const char*)(ring + cur * SLOT); };
+
+    // Acquire the next two slots, a pseudo-slot pair, and read this wave's
+    // rows of it (the pair's slot wave / 2 holds them, K columns per row) into
+    // xin, zero for columns >= K.  Each half of the pair is read right
     // after it is acquired, so both are dead when the next slot is acquired.
-    auto take_input = [&](int l0, int K) {
+    auto take_input = [&](int K) {
 #pragma unroll
       for (int part = 0; part < 2; ++part) {
-        if (qb + l0 + part < total) acquire(qb + l0 + part);
-        if ((wave >> 1) == part) {
-          GP_LDS const char* const b = slot(l0 + part);
+        acquire();
+        refill();
+        if ((32 * RB * wave) / PART == part) {
+          GP_LDS const char* const b = cur_slot();
+          const int lane = opaque(lane0), lr = lane & 31, lh = lane >> 5;
+          // K as an opaque vector value: the column masks below are rebuilt
+          // here instead of being hoisted out of the tile loop (dozens of live
+          // lane masks would spill).
+          const int Kv = opaque(K);
 #pragma unroll
-          for (int rb = 0; rb < 2; ++rb) {
-            const int e0 = ((64 * wave + 32 * rb + lr) & (PART - 1)) * K + 8 * lh;
+          for (int rb = 0; rb < RB; ++rb) {
+            const int e0 = ((32 * RB * wave + 32 * rb + lr) & (PART - 1)) * Kv + 8 * lh;
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
-              const int c0 = 16 * kb + 8 * lh;
+              // valid halves of this lane's 8 columns 16 kb + 8 lh ..
+              const int n = min(max(Kv - 16 * kb - 8 * lh, 0), 8);
               h8 v;
               if ((K & 7) == 0) {
                 v = *(GP_LDS const h8*)(b + (e0 + 16 * kb) * 2);
               } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] = *(GP_LDS const half_t*)(b + (e0 + 16 * kb + e) * 2);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = c0 + e < K ? v[e] : (half_t)0.f;
               }
-              xin[kb][rb] = c0 < K ? v : h8{};
+              u32x4 w = __builtin_bit_cast(u32x4, v);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) w[i] &= n >= 2 * i + 2 ? 0xffffffffu : n == 2 * i + 1 ? 0xffffu : 0u;
+              xin[kb][rb] = __builtin_bit_cast(h8, w);
             }
           }
         }
       }
     };
 
-    // Read group g (fragments 4g .. 4g+3) of local slot l into fa[BUF].
-    auto fetch = [&](int l, auto gc, auto bufc) {
+    // Read group g (fragments 4g .. 4g+3) of the current slot into fa[BUF].
+    auto fetch = [&](auto gc, auto bufc) {
       constexpr int g = decltype(gc)::value, buf = decltype(bufc)::value;
-      GP_LDS const char* const s = slot(l) + 4 * g * FRAG + 16 * lane;
+      GP_LDS const char* const s = cur_slot() + 4 * g * FRAG + 16 * lane0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) fa[buf][i] = *(GP_LDS const h8*)(s + i * FRAG);
     };
@@ -231,36 +260,45 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         constexpr int fi = K.kb0 * K.fb + 4 * g + i;
         constexpr int kb = fi / K.fb, fb = fi % K.fb;
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
+        for (int rb = 0; rb < RB; ++rb) {
           h8 b;
           if constexpr (kb < K.next) b = xin[kb][rb];
           else b = act[kb - K.next][rb];
-          acc[fb][rb] = mfma32(fa[buf][i], b, kb == 0 ? f16x{} : acc[fb][rb]);
+          acc[fb][rb] = mfma32(fa[buf][i], b, (kb == 0 && !K.hb) ? f16x{} : acc[fb][rb]);
         }
       });
+    };
+    // Hidden-layer bias: acc[fb][rb] = bias (x) ones, the first product of
+    // every accumulator of the layer.
+    auto bias_init = [&](auto FBc, int off) {
+      constexpr int FB = decltype(FBc)::value;
+#pragma unroll
+      for (int fb = 0; fb < FB; ++fb) {
+        h8 a = {};
+        a[0] = bfrag[off + 64 * fb + lane0];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) acc[fb][rb] = mfma32(a, ones, f16x{});
+      }
     };
     using G0 = std::integral_constant<int, 0>;
     using G1 = std::integral_constant<int, 1>;
     using G2 = std::integral_constant<int, 2>;
     using G3 = std::integral_constant<int, 3>;
 
-    // Hidden-layer epilogue: act[2 fb + s][rb] = relu?(acc + bias) in fp16.
-    // Lane (row lr, half lh) holds, in element 4 g + e of block fb, feature
+    // Hidden-layer epilogue: act[2 fb + s][rb] = relu?(acc) in fp16.  Lane
+    // (row lr, half lh) holds, in element 4 g + e of block fb, feature
     // 32 fb + 8 g + 4 lh + e.
-    auto epi_hidden = [&](auto FBc, int boff, bool relu) {
+    auto epi_hidden = [&](auto FBc, bool relu) {
       constexpr int FB = decltype(FBc)::value;
 #pragma unroll
-      for (int fb = 0; fb < FB; ++fb) {
-        f4 bb[4];
+      for (int fb = 0; fb < FB; ++fb)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) bb[g] = *(GP_LDS const f4*)(btab + boff + 32 * fb + 8 * g + 4 * lh);
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
+        for (int rb = 0; rb < RB; ++rb) {
           h8 lo, hi;
 #pragma unroll
           for (int r = 0; r < 8; ++r) {
-            lo[r] = (half_t)(acc[fb][rb][r] + bb[r / 4][r % 4]);
-            hi[r] = (half_t)(acc[fb][rb][8 + r] + bb[2 + r / 4][r % 4]);
+            lo[r] = (half_t)acc[fb][rb][r];
+            hi[r] = (half_t)acc[fb][rb][8 + r];
           }
           if (relu) {
             lo = __builtin_elementwise_max(lo, h8{});
@@ -269,36 +307,40 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
           act[2 * fb][rb] = lo;
           act[2 * fb + 1][rb] = hi;
         }
-      }
     };
 
     // Head epilogue: out[row][c] = fn(acc + bias) for c < N, rows < vrows.
     auto epi_head = [&](int boff, half_t* out, int N, int fn) {
       const __amdgpu_buffer_rsrc_t ro = make_rsrc(out + r0 * N, vrows * N * 2);
       const bool vec = (N & 3) == 0 && ((uintptr_t)out & 7) == 0;
+      // Lane id and N as opaque values: the row / column indices and masks are
+      // built here, where they are used, rather than early in the tile and
+      // kept live through ten layers.
+      const int lane = opaque(lane0), lr = lane & 31, lh = lane >> 5;
+      const int Nv = opaque(N);
 #pragma unroll
       for (int fb = 0; fb < 2; ++fb)
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-          const int row = 64 * wave + 32 * rb + lr;
+        for (int rb = 0; rb < RB; ++rb) {
+          const int row = 32 * RB * wave + 32 * rb + lr;
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             const int c = 32 * fb + 8 * g + 4 * lh;
-            const f4 bb = *(GP_LDS const f4*)(btab + boff + c);
+            const f4 bb = *(GP_LDS const f4*)(bhead + boff + c);
             f4 v;
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = apply_act(acc[fb][rb][4 * g + e] + bb[e], fn);
             const h4 h = __builtin_convertvector(v, h4);
-            const int off = (row * N + c) * 2;
+            const int off = (row * Nv + c) * 2;
             if (vec) {
-              if (c < N) buf_store_h4(ro, off, h);
+              if (c < Nv) buf_store_h4(ro, off, h);
             } else {
               // 16-bit words taken out with integer shifts: the b16 store of a
               // bit-cast vector element was compiled to store element 0 each time.
               const u32x2 w2 = __builtin_bit_cast(u32x2, h);
 #pragma unroll
               for (int e = 0; e < 4; ++e)
-                if (c + e < N)
+                if (c + e < Nv)
                   __builtin_amdgcn_raw_buffer_store_b16((unsigned short)(w2[e >> 1] >> (16 * (e & 1))), ro, off + 2 * e,
                                                         0, 0);
             }
@@ -311,30 +353,30 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     // acquired and its first group read, so the barrier and the read latency
     // hide behind running MFMAs -- across layer boundaries too, where the
     // epilogue runs after the next layer's first fragments were requested.
-    // Acquire local slot l (global qb + l; l may run into the next tile) and
-    // read its first group.
-    auto advance = [&](int l) {
-      if (qb + l >= total) return;
-      acquire(qb + l);
-      fetch(l, G0{}, G0{});
+    // Acquire the next slot and read its first group.
+    auto advance = [&] {
+      acquire();
+      fetch(G0{}, G0{});
     };
-    // The slots of one layer: kinds KD0 .. KD0+N-1 at local slots l0 ...;
-    // `after` acquires what follows the layer, between the last slot's parts.
-    auto run_layer = [&](auto kd0c, auto nc, int l0, auto&& after) {
+    // The N slots of one layer, of kinds KD0 .. KD0+N-1; `after` acquires what
+    // follows the layer, between the last slot's parts.
+    auto run_layer = [&](auto kd0c, auto nc, auto&& after) {
       constexpr int KD0 = decltype(kd0c)::value, N = decltype(nc)::value;
       static_for(std::make_integer_sequence<int, N>{}, [&](auto jc) {
         constexpr int j = decltype(jc)::value;
         using KD = std::integral_constant<int, KD0 + j>;
-        const int l = l0 + j;
-        fetch(l, G1{}, G1{});
+        // One fragment buffer: the other wave on the SIMD covers the read
+        // latency while this one waits.
         mma(KD{}, G0{}, G0{});
-        fetch(l, G2{}, G0{});
-        mma(KD{}, G1{}, G1{});
-        fetch(l, G3{}, G1{});
+        refill();
+        fetch(G1{}, G0{});
+        mma(KD{}, G1{}, G0{});
+        fetch(G2{}, G0{});
         mma(KD{}, G2{}, G0{});
-        if constexpr (j + 1 < N) advance(l + 1);
+        fetch(G3{}, G0{});
+        mma(KD{}, G3{}, G0{});
+        if constexpr (j + 1 < N) advance();
         else after();
-        mma(KD{}, G3{}, G1{});
       });
     };
     using C1 = std::integral_constant<int, 1>;
@@ -352,39 +394,42 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     auto nothing = [] {};
 
     // Layer 1: x -> 256, ReLU.
-    take_input(S_X1, p.Kx);
-    advance(S_L1);
-    run_layer(C1{}, C2{}, S_L1, [&] { advance(S_L2); });
-    epi_hidden(E8{}, 0, true);
+    take_input(p.Kx);
+    advance();
+    bias_init(E8{}, BF_L1);
+    run_layer(C1{}, C2{}, [&] { advance(); });
+    epi_hidden(E8{}, true);
     // Layers 2-5, 7, 8 (ReLU) and 10 (bottleneck, linear): 256 -> 256.
     // Layer 6 ([h5 | x] -> 256) runs before 7, the density head before 10.
 #pragma nounroll
     for (int i = 0; i < 7; ++i) {
       if (i == 4) {
-        take_input(S_X2, p.Kx);
-        advance(S_L6);
-        run_layer(C11{}, C10{}, S_L6, [&] { advance(S_L7); });
-        epi_hidden(E8{}, 5 * 256, true);
+        take_input(p.Kx);
+        advance();
+        bias_init(E8{}, BF_L6);
+        run_layer(C11{}, C10{}, [&] { advance(); });
+        epi_hidden(E8{}, true);
       }
       if (i == 6) {
-        run_layer(C21{}, C2{}, S_L9, [&] { advance(S_L10); });
-        epi_head(B_L9, p.out_r, p.Na, ACT_NONE);
+        run_layer(C21{}, C2{}, [&] { advance(); });
+        epi_head(BH_L9 - BF_END, p.out_r, p.Na, ACT_NONE);
       }
-      const int l0 = i < 4 ? S_L2 + 8 * i : i < 6 ? S_L7 + 8 * (i - 4) : S_L10;
+      bias_init(E8{}, i < 4 ? BF_L2 + 512 * i : i < 6 ? BF_L7 + 512 * (i - 4) : BF_L10);
       // what follows is another 256 -> 256 layer or the density head, or a
       // pseudo-slot pair (before layers 6 and 11), taken after the epilogue
-      run_layer(C3{}, C8{}, l0, [&] {
-        if (i != 3 && i != 6) advance(l0 + 8);
+      run_layer(C3{}, C8{}, [&] {
+        if (i != 3 && i != 6) advance();
       });
-      epi_hidden(E8{}, i < 4 ? 256 * (i + 1) : i < 6 ? 256 * (i + 2) : B_L10, i != 6);
+      epi_hidden(E8{}, i != 6);
     }
     // Layer 11 ([bottleneck | d] -> 128, ReLU) and layer 12 (128 -> Nrgb).
-    take_input(S_D, p.Kd);
-    advance(S_L11);
-    run_layer(C23{}, C5{}, S_L11, [&] { advance(S_L12); });
-    epi_hidden(E4{}, B_L11, true);
-    run_layer(C28{}, C1{}, S_L12, nothing);
-    epi_head(B_L12, p.out_rgb, p.Nrgb, p.rgb_act);
+    take_input(p.Kd);
+    advance();
+    bias_init(E4{}, BF_L11);
+    run_layer(C23{}, C5{}, [&] { advance(); });
+    epi_hidden(E4{}, true);
+    run_layer(C28{}, C1{}, nothing);
+    epi_head(BH_L12 - BF_END, p.out_rgb, p.Nrgb, p.rgb_act);
   }
 }
 
@@ -392,7 +437,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 struct PackLayer {
   const half_t* w;  // [krows][n] (nn.Linear.weight.t())
   const half_t* b;  // [n] or null
-  int slot0, fb, kb, next, ext_w, ext_koff, n, f, boff;
+  int slot0, fb, kb, next, ext_w, ext_koff, n, boff, head;
 };
 struct PackArgs {
   PackLayer L[12];
@@ -437,16 +482,21 @@ __global__ __launch_bounds__(256) void nerf_pack_kernel(PackArgs a) {
 #pragma unroll
   for (int li = 0; li < 12; ++li) {
     const PackLayer& L = a.L[li];
-    if (t >= L.boff && t < L.boff + L.f) {
-      const int f = t - L.boff;
-      a.bias[t] = (L.b && f < L.n) ? L.b[f] : (half_t)0.f;
+    if (L.head) {
+      if (t >= L.boff && t < L.boff + 64) {
+        const int f = t - L.boff;
+        a.bias[t] = (L.b && f < L.n) ? L.b[f] : (half_t)0.f;
+      }
+    } else if (t >= L.boff && t < L.boff + 64 * L.fb) {
+      const int fb = (t - L.boff) / 64, ln = (t - L.boff) % 64, f = 32 * fb + ln;
+      a.bias[t] = (L.b && ln < 32 && f < L.n) ? L.b[f] : (half_t)0.f;
     }
   }
 }
 
 }  // namespace nerf
 
-size_t nerf_fused_workspace() { return (size_t)nerf::S_TOTAL * nerf::SLOT + nerf::BIAS_BYTES; }
+size_t nerf_fused_workspace() { return (size_t)nerf::S_TOTAL * nerf::SLOT + (size_t)nerf::B_TOTAL * 2; }
 
 bool nerf_fused_supported(int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb) {
   return Kx >= 1 && Kx <= 64 && Kd >= 1 && Kd <= 64 && Na >= 1 && Na <= 64 && Nrgb >= 1 && Nrgb <= 64;
@@ -457,17 +507,18 @@ hipError_t nerf_fused_launch(int64_t M, int Kx, int Kd, int Na, int Nrgb, const 
                              void* ws, int num_cus, hipStream_t s) {
   using namespace nerf;
   if (M <= 0) return hipSuccess;
+  if (M > (int64_t(1) << 31) - 1) return hipErrorInvalidValue;
   if (((uintptr_t)x & 15) || ((uintptr_t)d & 15) || ((uintptr_t)ws & 15)) return hipErrorInvalidValue;
   PackArgs pa{};
-  // slot0, fb, kb, next, ext_w, ext_koff, n, f, boff
+  // slot0, fb, kb, next, ext_w, ext_koff, n, boff, head
   const int H = 256;
   const int shape[12][9] = {
-      {S_L1, 8, 4, 4, Kx, 0, H, H, 0},           {S_L2, 8, 16, 0, 0, 0, H, H, 256},
-      {S_L2 + 8, 8, 16, 0, 0, 0, H, H, 512},     {S_L2 + 16, 8, 16, 0, 0, 0, H, H, 768},
-      {S_L2 + 24, 8, 16, 0, 0, 0, H, H, 1024},   {S_L6, 8, 20, 4, Kx, H, H, H, 1280},
-      {S_L7, 8, 16, 0, 0, 0, H, H, 1536},        {S_L7 + 8, 8, 16, 0, 0, 0, H, H, 1792},
-      {S_L9, 2, 16, 0, 0, 0, Na, 64, B_L9},      {S_L10, 8, 16, 0, 0, 0, H, H, B_L10},
-      {S_L11, 4, 20, 4, Kd, H, 128, 128, B_L11}, {S_L12, 2, 8, 0, 0, 0, Nrgb, 64, B_L12},
+      {S_L1, 8, 4, 4, Kx, 0, H, BF_L1, 0},             {S_L2, 8, 16, 0, 0, 0, H, BF_L2, 0},
+      {S_L2 + 8, 8, 16, 0, 0, 0, H, BF_L2 + 512, 0},   {S_L2 + 16, 8, 16, 0, 0, 0, H, BF_L2 + 1024, 0},
+      {S_L2 + 24, 8, 16, 0, 0, 0, H, BF_L2 + 1536, 0}, {S_L6, 8, 20, 4, Kx, H, H, BF_L6, 0},
+      {S_L7, 8, 16, 0, 0, 0, H, BF_L7, 0},             {S_L7 + 8, 8, 16, 0, 0, 0, H, BF_L7 + 512, 0},
+      {S_L9, 2, 16, 0, 0, 0, Na, BH_L9, 1},            {S_L10, 8, 16, 0, 0, 0, H, BF_L10, 0},
+      {S_L11, 4, 20, 4, Kd, H, 128, BF_L11, 0},        {S_L12, 2, 8, 0, 0, 0, Nrgb, BH_L12, 1},
   };
   for (int i = 0; i < 12; ++i) {
     const int* sh = shape[i];
