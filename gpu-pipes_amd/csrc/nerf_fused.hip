@@ -8,14 +8,14 @@
 // of one tile are a single wave's instruction stream instead.
 //
 // Design.
-//  * A workgroup of four waves (one per SIMD) owns a tile of 256 rows; wave w
-//    owns rows 64w .. 64w+63 as two 32-row blocks and computes every output
-//    feature of every layer for them, as C^T = W^T X^T with
+//  * A workgroup of eight waves (two per SIMD) owns a tile of 256 rows; wave
+//    w owns rows 32w .. 32w+31 and computes every output feature of every
+//    layer for them, as C^T = W^T X^T with
 //    v_mfma_f32_32x32x16_f16: the MFMA A operand is a 32-feature x 16-k block
 //    of the weights (a "fragment"), the B operand a 16-k x 32-row block of the
 //    layer input.
-//  * Activations stay in registers.  A 256-feature layer's accumulators fill
-//    the 256 AGPRs; converted to fp16 they fill 128 VGPRs, and in exactly the
+//  * Activations stay in registers.  A 256-feature layer's accumulators take
+//    128 registers; converted to fp16 they take 64, in exactly the
 //    register layout of the next layer's B operands, because the accumulator
 //    lane layout (4 features x 4 groups of one row) is a permutation of the B
 //    operand layout (8 consecutive k of one row).  The permutation is folded
@@ -24,24 +24,26 @@
 //  * Weights (1.2 MB) do not fit on chip, so every tile streams them from L2:
 //    the host packs all layers once per call into the exact order the kernel
 //    consumes them, as 1 KiB fragments (64 lanes x 16 bytes), 16 to a 16 KiB
-//    slot.  Slots are copied L2 -> LDS with buffer_load ... lds into a ring of
-//    nine (144 KiB); eight are in flight while one is read.
-//  * The network inputs travel through the same ring: a tile's x rows (twice:
-//    for layer 1 and for the skip input of layer 6) and its d rows occupy
-//    "pseudo-slots" of the stream whose copies read x or d instead of
-//    weights, 128 rows per slot, zero-filled past the last valid row.  Each
-//    is read into registers as soon as it is acquired.
-//  * Every slot is therefore dead once the next one is acquired, which makes
-//    the ring bookkeeping fixed: acquiring slot q waits for this wave's copies
-//    of q (the 28 copies issued after them may still be in flight) and passes
-//    one workgroup barrier, after which no wave reads slot q-1 again; slot
-//    q+8 is copied into q-1's place once slot q's first MFMAs are issued.
+//    slot.  Waves 0-3 copy slots L2 -> LDS with buffer_load ... lds into a
+//    ring of six (96 KiB); four are in flight while one is read.  Every slot
+//    is dead once the next one is acquired, so the bookkeeping is fixed:
+//    acquiring slot q waits for this wave's copies of q (the 16 copies issued
+//    after them may still be in flight) and passes one workgroup barrier,
+//    after which no wave reads slot q-1 again; slot q+5 is copied into q-1's
+//    place once slot q's first MFMAs are issued.
+//  * The network inputs come through their own LDS tiles (x 32 KiB, d 16
+//    KiB), copied by waves 4-7 a whole stretch of layers ahead: the next
+//    tile's x once layer 6 has read this tile's, its d once layer 11 has.
+//    Only waves 4-7 copy them, so their HBM latency never holds up a wait
+//    for a ring slot (vmcnt counts a wave's own loads, in order).
 //  * Bias of a hidden layer: one extra MFMA per accumulator block, the bias
 //    fragment (bias in k = 0) times a constant B operand that is 1 in k = 0,
 //    is each accumulator's first product, so the epilogue is only the fp16
 //    conversion and ReLU (in packed fp16: max commutes with RNE rounding).
-//    The wave issues at most one instruction every four cycles, so an MFMA
-//    (32 cycles) in place of 16 VALU adds is the cheaper side.
+//    A SIMD issues at most one VALU instruction every four cycles, so an MFMA
+//    (32 cycles of the matrix pipe) in place of 16 VALU adds is the cheaper
+//    side.  With two waves per SIMD, one wave's epilogue, copies and scalar
+//    work issue while the other's MFMAs run.
 //  * The density and colour heads add their bias in fp32 and are stored
 //    through buffer descriptors bounded to the tile's valid rows.
 #include <hip/hip_runtime.h>
@@ -61,33 +63,34 @@ constexpr int NW = 8;              // waves per workgroup, two per SIMD
 constexpr int RB = 1;              // 32-row blocks per wave
 constexpr int NT = NW * kWave;
 constexpr int ROWS = 32 * RB * NW; // rows per tile
-constexpr int CPW = 16 / NW;       // 1 KiB copies per wave per slot
 constexpr int FRAG = 1024;         // one A operand: 64 lanes x 16 bytes
 constexpr int FPS = 16;            // fragments per slot
 constexpr int SLOT = FPS * FRAG;   // bytes per ring slot
-constexpr int NS = 9;              // ring slots
-constexpr int PART = 128;          // rows of x or d per pseudo-slot
+constexpr int NS = 6;              // ring slots
+constexpr int RW = 4;              // waves 0 .. RW-1 copy the ring; the others copy x and d
+constexpr int CPW = FPS / RW;      // 1 KiB ring copies per copying wave per slot
+constexpr int XBUF = ROWS * 64 * 2;  // one tile of x (Kx <= 64)
+constexpr int DBUF = ROWS * 32 * 2;  // one tile of d (Kd <= 32)
+constexpr int XCPW = XBUF / FRAG / (NW - RW), DCPW = DBUF / FRAG / (NW - RW);  // input copies per wave
 
-// Local slot map of one tile's stream (82 slots, 1.31 MB).
-constexpr int S_X1 = 0, S_L1 = 2, S_L2 = 4, S_X2 = 36, S_L6 = 38, S_L7 = 48, S_L9 = 64, S_L10 = 66, S_D = 74,
-              S_L11 = 76, S_L12 = 81, S_TOTAL = 82;
-// Pseudo-slot positions as a 128-bit mask (bits 0, 1, 36, 37, 74, 75).
-constexpr uint64_t PSEUDO_LO = (1ull << S_X1) | (1ull << (S_X1 + 1)) | (1ull << S_X2) | (1ull << (S_X2 + 1));
-constexpr uint64_t PSEUDO_HI = (1ull << (S_D - 64)) | (1ull << (S_D + 1 - 64));
+// Local slot map of one tile's weight stream (76 slots, 1.25 MB).
+constexpr int S_L1 = 0, S_L2 = 2, S_L6 = 34, S_L7 = 44, S_L9 = 60, S_L10 = 62, S_L11 = 70, S_L12 = 75, S_TOTAL = 76;
 
 // Bias tables (fp16 in global memory).  Hidden layers: per feature block fb a
 // 64-entry A-operand column, bias[32 fb + lane] for lanes < 32 and 0 for the
 // upper half (k = 8..15).  Heads: plain vectors of 64.
 constexpr int BF_L1 = 0, BF_L2 = 512, BF_L6 = 2560, BF_L7 = 3072, BF_L10 = 4096, BF_L11 = 4608, BF_END = 4864;
 constexpr int BH_L9 = BF_END, BH_L12 = BF_END + 64, B_TOTAL = BF_END + 128;
-// LDS: the hidden-layer table as fp16, then the head biases as fp32.
+// LDS: ring, x tile, d tile, the hidden-layer bias table as fp16, then the
+// head biases as fp32.
 constexpr int BIAS_BYTES = BF_END * 2 + 128 * 4;
-static_assert(NS * SLOT + BIAS_BYTES <= 160 * 1024, "LDS");
+constexpr int L_X = NS * SLOT, L_D = L_X + XBUF, L_B = L_D + DBUF, LDS_BYTES = L_B + BIAS_BYTES;
+static_assert(LDS_BYTES <= 160 * 1024, "LDS");
 
 struct Args {
   const half_t* x;       // [M][Kx]
   const half_t* d;       // [M][Kd]
-  const char* stream;    // S_TOTAL slots (pseudo-slot positions unused)
+  const char* stream;    // S_TOTAL slots
   const half_t* bias;    // B_TOTAL
   half_t* out_r;         // [M][Na]
   half_t* out_rgb;       // [M][Nrgb]
@@ -99,10 +102,11 @@ struct Args {
 // feature 16 kb + sigma(p) (the accumulator layout of the layer before).
 __host__ __device__ constexpr int sigma(int p) { return p < 4 ? p : p < 8 ? p + 4 : p < 12 ? p - 4 : p; }
 
-// Slot kinds.  A compute slot holds 16 fragments of one layer: FB feature
-// blocks per input k-block, starting at k-block KB0; the layer's first NEXT
-// k-blocks take their B operand from a pseudo-slot input, the rest from
-// registers; HB: the layer's bias enters through the MFMA (hidden layers).
+// Slot kinds.  A slot holds 16 fragments of one layer, read and multiplied
+// as four groups of four: FB feature blocks per input k-block, starting at
+// k-block KB0; the layer's first NEXT k-blocks take their B operand from the
+// x or d tile, the rest from registers; HB: the layer's bias enters through
+// the MFMA (hidden layers).
 //   1-2 layer 1, 3-10 a 256 -> 256 layer, 11-20 layer 6, 21-22 layer 9,
 //   23-27 layer 11, 28 layer 12.
 struct Kind {
@@ -123,14 +127,15 @@ __device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&&
 }
 
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void nerf_fused_kernel(Args p) {
-  __shared__ __attribute__((aligned(1024))) char smem[NS * SLOT + BIAS_BYTES];
+  __shared__ __attribute__((aligned(1024))) char smem[LDS_BYTES];
   GP_LDS char* const ring = (GP_LDS char*)smem;
-  GP_LDS half_t* const bfrag = (GP_LDS half_t*)(smem + NS * SLOT);
-  GP_LDS float* const bhead = (GP_LDS float*)(smem + NS * SLOT + BF_END * 2);
+  GP_LDS half_t* const bfrag = (GP_LDS half_t*)(smem + L_B);
+  GP_LDS float* const bhead = (GP_LDS float*)(smem + L_B + BF_END * 2);
 
   const int tid = threadIdx.x;
   const int lane0 = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool ring_wave = wave < RW;
   const int G = gridDim.x;
   // Tile and slot counts fit in 32 bits: the host limits M to 2^31 - 1.
   const int ntiles = (int)((p.M + ROWS - 1) / ROWS);
@@ -140,49 +145,70 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   if (tid < 128) bhead[tid] = (float)p.bias[BF_END + tid];
   __syncthreads();
 
-  // ---------------------------------------------------------------- copies
+  auto tile_r0 = [&](int k) { return ((int64_t)blockIdx.x + (int64_t)k * G) * ROWS; };
+
+  // ---------------------------------------------------------- input tiles
+  // Waves RW .. NW-1 copy tile k's x rows (or d rows) into the x (d) buffer,
+  // chunk c = (NW - RW) i + (wave - RW) being copy i.  A tile past the last
+  // one copies nothing (range 0) and only zeroes a dead buffer, so every such
+  // wave always has the same copies in flight: x of tile k+1 is issued after
+  // layer 6 of tile k, d of tile k+1 after layer 11.
+  auto copy_input = [&](int k, bool is_x) {
+    if (ring_wave) return;
+    const int K = is_x ? p.Kx : p.Kd;
+    const int64_t row0 = tile_r0(k);
+    const int64_t left = k < my ? p.M - row0 : 0;
+    const int rows = left <= 0 ? 0 : left < ROWS ? (int)left : ROWS;
+    // The range is rounded up to whole 16-byte copies; the bytes past the last
+    // valid row lie in the same 16-byte block (so the same page) and land only
+    // in rows that are never stored.
+    const __amdgpu_buffer_rsrc_t r = make_rsrc((is_x ? p.x : p.d) + row0 * K, (rows * K * 2 + 15) & ~15);
+    GP_LDS char* const dst = (GP_LDS char*)smem + (is_x ? L_X : L_D);
+    const int n = is_x ? XCPW : DCPW;
+    for (int i = 0; i < n; ++i) {
+      const int c = (NW - RW) * i + (wave - RW);
+      dma16_buf_so(r, 16 * lane0, c * FRAG, dst + c * FRAG);
+    }
+  };
+
+  // ---------------------------------------------------------------- ring
   // Global slot q = k S_TOTAL + l (tile k, local slot l) lives in ring slot
   // q % NS.  `cur` is the ring slot of the last acquired slot; (iss_k, iss_l)
   // the next slot to copy, which goes to ring slot (cur + NS - 1) % NS.
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.stream, S_TOTAL * SLOT);
-  auto tile_r0 = [&](int k) { return ((int64_t)blockIdx.x + (int64_t)k * G) * ROWS; };
   int cur = NS - 1, iss_k = 0, iss_l = 0;
-  // Copy the next slot into ring slot `rs`: chunk c = NW i + wave of the slot
-  // is this wave's copy i.
+  // Copy the next slot into ring slot `rs` (ring waves; chunk c = RW i + wave
+  // is copy i).  Branch-free apart from the wave test, so that a slot's MFMAs
+  // and its copies form one basic block the scheduler can interleave.  Past
+  // the last slot (iss_k == my) the range is 0: the copies read nothing and
+  // zero a dead slot, and every acquire finds the same copies in flight.
   auto issue = [&](int rs) {
-    const int l = iss_l;
-    // Branch-free, so that a slot's MFMAs and its copies form one basic block
-    // the scheduler can interleave.  Past the last slot (iss_k == my) the
-    // descriptor range is 0: the copies read nothing and zero a dead slot,
-    // and every acquire still finds exactly 28 newer copies in flight.
-    const bool pseudo = l < 64 ? (PSEUDO_LO >> l) & 1 : (PSEUDO_HI >> (l - 64)) & 1;
-    const bool px = l < S_D;
-    const int K = px ? p.Kx : p.Kd;
-    const int64_t row0 = tile_r0(iss_k) + (l & 1) * PART;  // pseudo-slot pairs start at even slots
-    const int64_t left = p.M - row0;
-    const int rows = left <= 0 ? 0 : left < PART ? (int)left : PART;
-    // The range is rounded up to whole 16-byte copies; the bytes past the
-    // last valid row lie in the same 16-byte block (so the same page) and
-    // land only in rows that are never stored.
-    const __amdgpu_buffer_rsrc_t rp = make_rsrc((px ? p.x : p.d) + row0 * K, (rows * K * 2 + 15) & ~15);
-    const __amdgpu_buffer_rsrc_t r = pseudo ? rp : iss_k < my ? rw : make_rsrc(p.stream, 0);
-    const int base = pseudo ? 0 : l * SLOT;
+    const __amdgpu_buffer_rsrc_t r = iss_k < my ? rw : make_rsrc(p.stream, 0);
+    const int base = iss_l * SLOT;
     GP_LDS char* const dst = ring + rs * SLOT;
+    if (ring_wave) {
 #pragma unroll
-    for (int i = 0; i < CPW; ++i) {
-      const int c = NW * i + wave;
-      dma16_buf_so(r, 16 * lane0, base + c * FRAG, dst + c * FRAG);
+      for (int i = 0; i < CPW; ++i) {
+        const int c = RW * i + wave;
+        dma16_buf_so(r, 16 * lane0, base + c * FRAG, dst + c * FRAG);
+      }
     }
     const bool wrap = ++iss_l == S_TOTAL;
     iss_l = wrap ? 0 : iss_l;
     iss_k += wrap ? 1 : 0;
   };
+  // Order of the first copies: x and d of tile 0, then the ring.
+  copy_input(0, true);
+  copy_input(0, false);
   for (int i = 0; i < NS - 1; ++i) issue(i);
-  // Acquire the next slot in stream order.  The copy that refills the ring
-  // slot of the previous one (dead from the barrier on) is issued by refill(),
-  // after the first MFMAs of the new slot, so that the scalar work of the
-  // copy does not sit between the barrier and the matrix pipe.  Every
-  // acquire is followed by exactly one refill() before the next acquire.
+  // Acquire the next slot in stream order: a ring wave waits for its own
+  // copies of it (the CPW (NS - 2) copies issued after them may still be in
+  // flight; an input wave has at most XCPW + DCPW < that in flight, so the
+  // wait is a no-op for it), then one barrier.  The copy that refills the
+  // ring slot of the previous one (dead from the barrier on) is issued by
+  // refill(), after the first MFMAs of the new slot.  Every acquire is
+  // followed by exactly one refill() before the next acquire.
+  static_assert(XCPW + DCPW <= CPW * (NS - 2), "input copies in flight");
   auto acquire = [&] {
     wait_vmcnt<CPW * (NS - 2)>();
     lds_barrier();
@@ -204,42 +230,38 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 
     auto cur_slot = [&] { return (GP_LDS const char*)(ring + cur * SLOT); };
 
-    // Acquire the next two slots, a pseudo-slot pair, and read this wave's
-    // rows of it (the pair's slot wave / 2 holds them, K columns per row) into
-    // xin, zero for columns >= K.  Each half of the pair is read right
-    // after it is acquired, so both are dead when the next slot is acquired.
-    auto take_input = [&](int K) {
+    // Read this wave's rows of the x (d) tile, K columns per row, into xin
+    // (NKB k-blocks; zero for columns >= K and k-blocks past NKB).  Called
+    // right after an acquire whose barrier follows the input waves' wait for
+    // the tile's copies.
+    auto take_input = [&](bool is_x, int K) {
+      GP_LDS const char* const b = (GP_LDS const char*)smem + (is_x ? L_X : L_D);
+      const int nkb = is_x ? 4 : 2;
+      const int lane = opaque(lane0), lr = lane & 31, lh = lane >> 5;
+      // K as an opaque vector value: the column masks below are rebuilt here
+      // instead of being hoisted out of the tile loop (dozens of live lane
+      // masks would spill).
+      const int Kv = opaque(K);
 #pragma unroll
-      for (int part = 0; part < 2; ++part) {
-        acquire();
-        refill();
-        if ((32 * RB * wave) / PART == part) {
-          GP_LDS const char* const b = cur_slot();
-          const int lane = opaque(lane0), lr = lane & 31, lh = lane >> 5;
-          // K as an opaque vector value: the column masks below are rebuilt
-          // here instead of being hoisted out of the tile loop (dozens of live
-          // lane masks would spill).
-          const int Kv = opaque(K);
+      for (int rb = 0; rb < RB; ++rb) {
+        const int e0 = (32 * RB * wave + 32 * rb + lr) * Kv + 8 * lh;
 #pragma unroll
-          for (int rb = 0; rb < RB; ++rb) {
-            const int e0 = ((32 * RB * wave + 32 * rb + lr) & (PART - 1)) * Kv + 8 * lh;
+        for (int kb = 0; kb < 4; ++kb) {
+          // valid halves of this lane's 8 columns 16 kb + 8 lh ..
+          const int n = kb < nkb ? min(max(Kv - 16 * kb - 8 * lh, 0), 8) : 0;
+          h8 v = {};
+          if (kb < nkb) {
+            if ((K & 7) == 0) {
+              v = *(GP_LDS const h8*)(b + (e0 + 16 * kb) * 2);
+            } else {
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-              // valid halves of this lane's 8 columns 16 kb + 8 lh ..
-              const int n = min(max(Kv - 16 * kb - 8 * lh, 0), 8);
-              h8 v;
-              if ((K & 7) == 0) {
-                v = *(GP_LDS const h8*)(b + (e0 + 16 * kb) * 2);
-              } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = *(GP_LDS const half_t*)(b + (e0 + 16 * kb + e) * 2);
-              }
-              u32x4 w = __builtin_bit_cast(u32x4, v);
-#pragma unroll
-              for (int i = 0; i < 4; ++i) w[i] &= n >= 2 * i + 2 ? 0xffffffffu : n == 2 * i + 1 ? 0xffffu : 0u;
-              xin[kb][rb] = __builtin_bit_cast(h8, w);
+              for (int e = 0; e < 8; ++e) v[e] = *(GP_LDS const half_t*)(b + (e0 + 16 * kb + e) * 2);
             }
           }
+          u32x4 w = __builtin_bit_cast(u32x4, v);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) w[i] &= n >= 2 * i + 2 ? 0xffffffffu : n == 2 * i + 1 ? 0xffffu : 0u;
+          xin[kb][rb] = __builtin_bit_cast(h8, w);
         }
       }
     };
@@ -348,11 +370,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         }
     };
 
-    // Slot program.  A slot is 4 groups of 4 fragments; group g+1 is read
-    // while group g is multiplied, and before the last group the next slot is
-    // acquired and its first group read, so the barrier and the read latency
-    // hide behind running MFMAs -- across layer boundaries too, where the
-    // epilogue runs after the next layer's first fragments were requested.
+    // Slot program.  A slot is 4 groups of 4 fragments, read and multiplied
+    // in turn; the next slot is acquired and its first group read right after
+    // the last group's MFMAs are issued -- across layer boundaries too, where
+    // the epilogue runs after the next layer's first fragments were requested.
     // Acquire the next slot and read its first group.
     auto advance = [&] {
       acquire();
@@ -365,16 +386,19 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       static_for(std::make_integer_sequence<int, N>{}, [&](auto jc) {
         constexpr int j = decltype(jc)::value;
         using KD = std::integral_constant<int, KD0 + j>;
+        constexpr int NG = 4;
         // One fragment buffer: the other wave on the SIMD covers the read
         // latency while this one waits.
         mma(KD{}, G0{}, G0{});
         refill();
-        fetch(G1{}, G0{});
-        mma(KD{}, G1{}, G0{});
-        fetch(G2{}, G0{});
-        mma(KD{}, G2{}, G0{});
-        fetch(G3{}, G0{});
-        mma(KD{}, G3{}, G0{});
+        static_for(std::make_integer_sequence<int, NG - 1>{}, [&](auto gc) {
+          using G = std::integral_constant<int, decltype(gc)::value + 1>;
+          // keep each group's reads below the previous group's MFMAs: reads
+          // hoisted further ahead run out of registers and spill
+          __builtin_amdgcn_sched_barrier(0);
+          fetch(G{}, G0{});
+          mma(KD{}, G{}, G0{});
+        });
         if constexpr (j + 1 < N) advance();
         else after();
       });
@@ -393,9 +417,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     using E8 = std::integral_constant<int, 8>;
     auto nothing = [] {};
 
-    // Layer 1: x -> 256, ReLU.
-    take_input(p.Kx);
+    // Layer 1: x -> 256, ReLU.  The input waves wait for this tile's x copies
+    // (this tile's d copies, issued after them, may still be in flight); the
+    // acquire's barrier then publishes the x tile.
+    if (!ring_wave) wait_vmcnt<DCPW>();
     advance();
+    take_input(true, p.Kx);
     bias_init(E8{}, BF_L1);
     run_layer(C1{}, C2{}, [&] { advance(); });
     epi_hidden(E8{}, true);
@@ -404,30 +431,36 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #pragma nounroll
     for (int i = 0; i < 7; ++i) {
       if (i == 4) {
-        take_input(p.Kx);
-        advance();
+        take_input(true, p.Kx);
         bias_init(E8{}, BF_L6);
         run_layer(C11{}, C10{}, [&] { advance(); });
         epi_hidden(E8{}, true);
+        // every wave has read this tile's x (barriers have passed since):
+        // the next tile's x goes into the buffer now
+        copy_input(k + 1, true);
       }
       if (i == 6) {
         run_layer(C21{}, C2{}, [&] { advance(); });
         epi_head(BH_L9 - BF_END, p.out_r, p.Na, ACT_NONE);
       }
       bias_init(E8{}, i < 4 ? BF_L2 + 512 * i : i < 6 ? BF_L7 + 512 * (i - 4) : BF_L10);
-      // what follows is another 256 -> 256 layer or the density head, or a
-      // pseudo-slot pair (before layers 6 and 11), taken after the epilogue
+      // what follows is another 256 -> 256 layer, layer 6 or the density
+      // head; layer 11 is acquired after the input waves' wait below
       run_layer(C3{}, C8{}, [&] {
-        if (i != 3 && i != 6) advance();
+        if (i != 6) advance();
       });
       epi_hidden(E8{}, i != 6);
     }
-    // Layer 11 ([bottleneck | d] -> 128, ReLU) and layer 12 (128 -> Nrgb).
-    take_input(p.Kd);
+    // Layer 11 ([bottleneck | d] -> 128, ReLU): the input waves wait for this
+    // tile's d copies (the next tile's x copies may still be in flight).
+    if (!ring_wave) wait_vmcnt<XCPW>();
     advance();
+    take_input(false, p.Kd);
     bias_init(E4{}, BF_L11);
     run_layer(C23{}, C5{}, [&] { advance(); });
     epi_hidden(E4{}, true);
+    copy_input(k + 1, false);
+    // Layer 12: 128 -> Nrgb.
     run_layer(C28{}, C1{}, nothing);
     epi_head(BH_L12 - BF_END, p.out_rgb, p.Nrgb, p.rgb_act);
   }
@@ -499,7 +532,7 @@ __global__ __launch_bounds__(256) void nerf_pack_kernel(PackArgs a) {
 size_t nerf_fused_workspace() { return (size_t)nerf::S_TOTAL * nerf::SLOT + (size_t)nerf::B_TOTAL * 2; }
 
 bool nerf_fused_supported(int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb) {
-  return Kx >= 1 && Kx <= 64 && Kd >= 1 && Kd <= 64 && Na >= 1 && Na <= 64 && Nrgb >= 1 && Nrgb <= 64;
+  return Kx >= 1 && Kx <= 64 && Kd >= 1 && Kd <= 32 && Na >= 1 && Na <= 64 && Nrgb >= 1 && Nrgb <= 64;
 }
 
 hipError_t nerf_fused_launch(int64_t M, int Kx, int Kd, int Na, int Nrgb, const void* x, const void* d,
