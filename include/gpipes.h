@@ -165,6 +165,10 @@ int gp_dlrm_topmlp_out(int64_t M, int64_t K0, int64_t N5, const void* x, const v
  * x [M,Kx], d [M,Kd]; Kx, Kd, Na, Nrgb in [1, 1024].  The reference app has
  * Kx 64, Kd 32, Na = Nrgb = 64 and no colour activation; the NeRF workload has
  * Kx 64 (63 + 1 zero), Kd 27, Na 1, Nrgb 3 and a sigmoid.
+ * With Kx <= 64, Kd <= 32, Na <= 64 and Nrgb <= 64 (both of those shapes) the
+ * call is one fused kernel over 256-row tiles (x or d rows not 16-byte
+ * aligned are first copied into the workspace); other widths run as one wide
+ * GEMM launch per layer over chunks of 262,144 rows.
  */
 int gp_nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb, const void* x, const void* d,
                      const void* const* w, const void* const* b, int rgb_act, void* out_r, void* out_rgb,

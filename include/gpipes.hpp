@@ -99,6 +99,32 @@ inline void gemm_out(int64_t M, int64_t N, int64_t K, const void* x, const void*
   check(gp_gemm_out(M, N, K, x, w, b, r, act, out, stream));
 }
 
+// DlrmMlp chain (common/mlps.py:23-34): widths[0..nlayers], w/b/acts per layer.
+inline void mlp_out(int64_t M, int nlayers, const int64_t* widths, const void* const* w, const void* const* b,
+                    const int* acts, const void* x, void* out, void* stream = nullptr) {
+  check(gp_mlp_out(M, nlayers, widths, w, b, acts, x, out, stream));
+}
+
+// dlrm_botmlp_out / dlrm_topmlp_out (apps/dlrm_botmlp/pipelined/dlrm_botmlp_pl_ext.cu:24-66,
+// apps/dlrm_topmlp/pipelined/dlrm_topmlp_pl_ext.cu:24-71).
+inline void dlrm_botmlp_out(int64_t M, int64_t K0, const void* x, const void* w1, const void* b1, const void* w2,
+                            const void* b2, const void* w3, const void* b3, void* out, void* stream = nullptr) {
+  check(gp_dlrm_botmlp_out(M, K0, x, w1, b1, w2, b2, w3, b3, out, stream));
+}
+inline void dlrm_topmlp_out(int64_t M, int64_t K0, int64_t N5, const void* x, const void* w1, const void* b1,
+                            const void* w2, const void* b2, const void* w3, const void* b3, const void* w4,
+                            const void* b4, const void* w5, const void* b5, void* out, int act5 = GP_ACT_RELU,
+                            void* stream = nullptr) {
+  check(gp_dlrm_topmlp_out(M, K0, N5, x, w1, b1, w2, b2, w3, b3, w4, b4, w5, b5, act5, out, stream));
+}
+
+// nerf_full_out (apps/nerf_full/pipelined/nerf_full_pl_ext.cu:24-97); w[0..11], b[0..11] = w1..w12, b1..b12.
+inline void nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb, const void* x, const void* d,
+                          const void* const* w, const void* const* b, void* out_r, void* out_rgb,
+                          int rgb_act = GP_ACT_NONE, void* stream = nullptr) {
+  check(gp_nerf_full_out(M, Kx, Kd, Na, Nrgb, x, d, w, b, rgb_act, out_r, out_rgb, stream));
+}
+
 }  // namespace gpipes
 
 #endif  // GPIPES_HPP
