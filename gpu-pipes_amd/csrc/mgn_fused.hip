@@ -217,6 +217,22 @@ __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Stores output features [32j, 32j+32) of row l16 from the fp16 groups of a
+// 16x16 accumulator pair: hv[t] holds features 16(2j+t) + 4q4 + (0..3) in
+// lane (l16, q4).  v_permlane16_swap trades one group between lanes q4 and
+// q4^1, after which each lane holds eight consecutive features (q4 = 0: +0,
+// 1: +16, 2: +8, 3: +24), so one 16-byte store per lane writes 64
+// contiguous bytes of each of the 16 rows -- half the store instructions
+// and twice the segment length of four-feature stores.
+__device__ __forceinline__ void store_row_pair(half_t* row, const h4 (&hv)[2], int j, int q4, bool ok) {
+  const u32x2 a = __builtin_bit_cast(u32x2, hv[0]);
+  const u32x2 b = __builtin_bit_cast(u32x2, hv[1]);
+  const auto lo = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  const auto hi = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  const u32x4 w = {(unsigned)lo[0], (unsigned)hi[0], (unsigned)lo[1], (unsigned)hi[1]};
+  if (ok) *(u32x4*)((char*)row + 64 * j + (q4 & 1) * 32 + (q4 >> 1) * 16) = w;
+}
+
 template <int K, bool LN, int GATHER_IDX = 0>  // GATHER_IDX: 0 = X given; 4 / 8 = gather, index bytes
 __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void mgn_fused_kernel(Params p) {
@@ -483,7 +499,7 @@ void mgn_fused_kernel(Params p) {
       }
 
       const int64_t grow = (t0 + (int64_t)k * G) * TM + 16 * n + l16;
-      half_t* o = p.out + grow * D + 4 * q4;
+      half_t* const orow = p.out + grow * D;
       if constexpr (LN) {
         // Lanes l16, l16+16, l16+32, l16+48 hold the row's 128 features.
         float s = 0.f;
@@ -501,18 +517,26 @@ void mgn_fused_kernel(Params p) {
         const float rstd = rsqrtf(sum_lanes_16_32(v) * (1.f / D) + p.eps);
         const float nmr = -mu * rstd;
 #pragma unroll
-        for (int fb = 0; fb < 8; ++fb) {
-          const f4 gm = *(const f4*)&prm[3][16 * fb + 4 * q4];
-          const f4 bt = *(const f4*)&prm[4][16 * fb + 4 * q4];
-          f4 z;
+        for (int j = 0; j < 4; ++j) {
+          h4 hv[2];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) z[e] = __builtin_fmaf(__builtin_fmaf(y[fb][e], rstd, nmr), gm[e], bt[e]);
-          if (grow < M) *(h4*)(o + 16 * fb) = __builtin_convertvector(z, h4);
+          for (int t = 0; t < 2; ++t) {
+            const int fb = 2 * j + t;
+            const f4 gm = *(const f4*)&prm[3][16 * fb + 4 * q4];
+            const f4 bt = *(const f4*)&prm[4][16 * fb + 4 * q4];
+            f4 z;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) z[e] = __builtin_fmaf(__builtin_fmaf(y[fb][e], rstd, nmr), gm[e], bt[e]);
+            hv[t] = __builtin_convertvector(z, h4);
+          }
+          store_row_pair(orow, hv, j, q4, grow < M);
         }
       } else {
 #pragma unroll
-        for (int fb = 0; fb < 8; ++fb)
-          if (grow < M) *(h4*)(o + 16 * fb) = __builtin_convertvector(y[fb], h4);
+        for (int j = 0; j < 4; ++j) {
+          const h4 hv[2] = {__builtin_convertvector(y[2 * j], h4), __builtin_convertvector(y[2 * j + 1], h4)};
+          store_row_pair(orow, hv, j, q4, grow < M);
+        }
       }
     };
 
