@@ -80,6 +80,7 @@ struct Args {
   int64_t M;
   int N;
   int K;
+  int ka;              // columns of A read (a multiple of 8, <= K); columns [ka, K) read as zero
   int lda, ldc, ldr;   // row strides in elements
 };
 
@@ -128,6 +129,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   const int vrow = RPC * wave + lane / CPR;
   const int vswz = ((lane % CPR) ^ ((vrow >> 1) & 7)) << 4;
   const int voffa = vrow * p.lda * 2 + vswz, voffb = vrow * K * 2 + vswz;
+  // A slabs that reach past column ka: a lane whose chunk starts at or past
+  // ka reads from an offset beyond every descriptor's range, so the copy
+  // writes zeros (the weight rows it meets are zero too).
+  const int lck = (vswz >> 4) * 8;  // the lane's first column within a slab
+  constexpr int kBeyond = 0x40000000;
   const int jstra = RPC * NW * p.lda * 2, jstrb = RPC * NW * K * 2;
   GP_LDS char* const lds = (GP_LDS char*)ring;
 
@@ -154,8 +160,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 #pragma unroll
       for (int j = 0; j < C::UB; ++j) dma16_buf_so(T.rb, voffb, j * jstrb + so, s + (j * NW + wave) * 1024);
     } else {
+      const int k0 = (u >> 1) * BK;
+      const int vo = k0 + BK <= p.ka || k0 + lck < p.ka ? voffa : kBeyond;
 #pragma unroll
-      for (int j = 0; j < C::UA; ++j) dma16_buf_so(T.ra, voffa, j * jstra + so, s + (j * NW + wave) * 1024);
+      for (int j = 0; j < C::UA; ++j) dma16_buf_so(T.ra, vo, j * jstra + so, s + (j * NW + wave) * 1024);
     }
   };
   auto prefetch = [&](const Tile& T) {
@@ -350,6 +358,42 @@ __global__ __launch_bounds__(256) void transpose_kernel(const half_t* in, half_t
   for (int r = ty; r < 64; r += 4) out[(int64_t)(n0 + r) * Kp + k0 + tx] = tile[tx][r];
 }
 
+// The weight preparation of a whole chain in one launch: for every layer,
+// wt[Np][Kp] = w[K][N] transposed and zero-padded (the 64 x 64 tiles of
+// transpose_kernel), and bp[Np] = b zero-padded (zeros for a null b).  Layer i
+// owns blocks [blk0_i, blk0_{i+1}); its first block also writes the bias.
+struct PrepLayer {
+  const half_t* w;
+  half_t* wt;
+  const half_t* b;
+  half_t* bp;
+  int K, N, Kp, Np, blk0;
+};
+constexpr int kMaxPrep = 32;
+struct PrepBatch {
+  PrepLayer L[kMaxPrep];
+  int n;
+};
+
+__global__ __launch_bounds__(256) void prep_kernel(PrepBatch pb) {
+  __shared__ half_t tile[64][66];
+  int i = 0;
+  while (i + 1 < pb.n && (int)blockIdx.x >= pb.L[i + 1].blk0) ++i;
+  const PrepLayer& L = pb.L[i];
+  const int local = (int)blockIdx.x - L.blk0;
+  const int tn = L.Np / 64;
+  const int n0 = (local % tn) * 64, k0 = (local / tn) * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int r = ty; r < 64; r += 4) {
+    const int k = k0 + r, n = n0 + tx;
+    tile[r][tx] = (k < L.K && n < L.N) ? L.w[(int64_t)k * L.N + n] : (half_t)0.f;
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) L.wt[(int64_t)(n0 + r) * L.Kp + k0 + tx] = tile[tx][r];
+  if (local == 0)
+    for (int j = threadIdx.x; j < L.Np; j += 256) L.bp[j] = (L.b && j < L.N) ? L.b[j] : (half_t)0.f;
+}
+
 template <class C, int ACT, bool RESID>
 static hipError_t launch(const Args& a, int num_cus, hipStream_t s) {
   const int64_t tiles = ((a.M + C::BM - 1) / C::BM) * (a.N / C::BN);
@@ -376,13 +420,37 @@ hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t s) {
   using namespace gemm;
   if (a.M <= 0) return hipSuccess;
   if (a.N % 128 != 0 || a.K % BK != 0) return hipErrorInvalidValue;
-  const int lda = a.lda ? (int)a.lda : (int)a.K, ldc = a.ldc ? (int)a.ldc : (int)a.N;
+  const int ka = a.ka ? (int)a.ka : (int)a.K;
+  if (ka < 1 || ka > a.K || ka % 8) return hipErrorInvalidValue;
+  const int lda = a.lda ? (int)a.lda : ka, ldc = a.ldc ? (int)a.ldc : (int)a.N;
   const int ldr = a.ldr ? (int)a.ldr : (int)a.N;
-  if (lda < a.K || ldc < a.N || (a.r && ldr < a.N) || lda % 8 || ldc % 8 || ldr % 8) return hipErrorInvalidValue;
+  if (lda < ka || ldc < a.N || (a.r && ldr < a.N) || lda % 8 || ldc % 8 || ldr % 8) return hipErrorInvalidValue;
   const Args g{(const half_t*)a.x, (const half_t*)a.wt, (const half_t*)a.b, (const half_t*)a.r, (half_t*)a.out,
-               a.M, (int)a.N, (int)a.K, lda, ldc, ldr};
+               a.M, (int)a.N, (int)a.K, ka, lda, ldc, ldr};
   if (a.N % Wide::BN == 0) return dispatch<Wide>(g, a.act, num_cus, s);
   return dispatch<Narrow>(g, a.act, num_cus, s);
+}
+
+hipError_t prep_launch(const PrepSpec* L, int n, hipStream_t s) {
+  using namespace gemm;
+  for (int i0 = 0; i0 < n; i0 += kMaxPrep) {
+    PrepBatch pb{};
+    int blocks = 0;
+    pb.n = n - i0 < kMaxPrep ? n - i0 : kMaxPrep;
+    for (int i = 0; i < pb.n; ++i) {
+      const PrepSpec& q = L[i0 + i];
+      if (q.Kp % 64 != 0 || q.Np % 64 != 0 || q.K > q.Kp || q.N > q.Np || q.K < 1 || q.N < 1 || !q.w || !q.wt ||
+          !q.bp)
+        return hipErrorInvalidValue;
+      pb.L[i] = {(const half_t*)q.w, (half_t*)q.wt, (const half_t*)q.b, (half_t*)q.bp,
+                 (int)q.K, (int)q.N, (int)q.Kp, (int)q.Np, blocks};
+      blocks += (int)(q.Np / 64 * (q.Kp / 64));
+    }
+    hipLaunchKernelGGL(prep_kernel, dim3((unsigned)blocks), dim3(256), 0, s, pb);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t transpose_launch(const void* in, void* out, int64_t K, int64_t N, hipStream_t s, int64_t Kp,

@@ -69,12 +69,23 @@ struct GemmArgs {
   int act;
   void* out;       // [M, ldc]
   int64_t lda = 0, ldc = 0, ldr = 0;
+  int64_t ka = 0;  // columns of x read (a multiple of 8; 0 = K); columns [ka, K) count as zero
 };
 hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t stream);
 // out[Np, Kp] = in[K, N]^T, zero-padded (Kp, Np default to K, N); Kp and Np
 // multiples of 64.
 hipError_t transpose_launch(const void* in, void* out, int64_t K, int64_t N, hipStream_t stream, int64_t Kp = 0,
                             int64_t Np = 0);
+// One launch for the weights of a layer chain: wt[Np, Kp] = w[K, N]^T and
+// bp[Np] = b (zeros for a null b), both zero-padded; Kp and Np multiples of 64.
+struct PrepSpec {
+  const void* w;
+  void* wt;
+  const void* b;
+  void* bp;
+  int64_t K, N, Kp, Np;
+};
+hipError_t prep_launch(const PrepSpec* layers, int n, hipStream_t stream);
 hipError_t concat_launch(int64_t M, int64_t N0, int64_t N1, const void* a, const void* b, void* c, int num_cus,
                          hipStream_t stream);
 // dst[m][j] = act(src[m][j]) for j < w and 0 for w <= j < wpad (strides in elements).

@@ -11,9 +11,11 @@
 // Narrow and odd widths are handled by padding, never by special kernels:
 //   * weights are transposed into the workspace with zero rows and columns up
 //     to K a multiple of 64 and N a multiple of 128, biases zero-padded to N;
-//   * an input whose width is not a multiple of 64 is copied into a padded
-//     buffer; concatenated inputs ([h | x], [bottleneck | d]) are built in
-//     place -- the GEMM writes h into the first columns of the wider buffer;
+//   * an input whose width is not a multiple of 8 (or not 16-byte aligned) is
+//     copied into a padded buffer; other inputs are read in place, and the
+//     GEMM zero-fills the columns past their width;
+//   * concatenated inputs ([h | x], [bottleneck | d]) are built in place --
+//     the GEMM writes h into the first columns of the wider buffer;
 //   * a layer narrower than 128 outputs (the DLRM click head, the NeRF density
 //     and colour heads) runs at 128 and its first columns are copied out.
 // Padded activation columns hold act(0) and meet zero weight rows, so they
@@ -60,22 +62,14 @@ struct Prepared {
   int act;
 };
 
-// Transpose / pad one layer's weight and bias into the workspace.
-hipError_t prepare(const void* w, const void* b, int64_t K, int64_t N, int64_t Kin, int64_t Np, int act, char* wt,
-                   char* bp, int ncu, hipStream_t s, Prepared* out) {
-  hipError_t e = transpose_launch(w, wt, K, N, s, Kin, Np);
-  if (e != hipSuccess) return e;
-  // a null bias becomes Np zeros (a zero-width copy writes only the padding)
-  e = place_launch(1, b ? b : (const void*)bp, N, b ? N : 0, bp, Np, Np, GP_ACT_NONE, ncu, s);
-  *out = {wt, bp, Kin, Np, act};
-  return e;
-}
 
+// ka: columns of `a` read (a multiple of 8, <= L.Kin); the rest count as zero.
 hipError_t layer(const Prepared& L, int64_t rows, const void* a, int64_t lda, void* c, int64_t ldc, int ncu,
-                 hipStream_t s) {
+                 hipStream_t s, int64_t ka = 0) {
   GemmArgs g{rows, L.Np, L.Kin, a, L.wt, L.b, nullptr, L.act, c};
   g.lda = lda;
   g.ldc = ldc;
+  g.ka = ka;
   return gemm_launch(g, ncu, s);
 }
 
@@ -102,7 +96,9 @@ int run_chain(int64_t M, int nl, const int64_t* widths, const void* const* w, co
     np[i] = rup(widths[i + 1], 128);
     maxnp = np[i] > maxnp ? np[i] : maxnp;
   }
-  const bool direct_in = widths[0] % 64 == 0 && aligned16(x);
+  // An input whose rows are whole 16-byte chunks is read in place; the GEMM
+  // zero-fills its columns up to the padded width.
+  const bool direct_in = widths[0] % 8 == 0 && aligned16(x);
   const bool direct_out = np[nl - 1] == widths[nl] && aligned16(out);
   Carve cv;
   std::vector<size_t> o_wt(nl), o_b(nl);
@@ -116,12 +112,14 @@ int run_chain(int64_t M, int nl, const int64_t* widths, const void* const* w, co
   char* ws = nullptr;
   if ((rc = workspace_acquire(dev, s, cv.off, (void**)&ws))) return rc;
 
+  // Transpose and pad every layer's weight and bias into the workspace.
   std::vector<Prepared> L(nl);
+  std::vector<PrepSpec> ps(nl);
   for (int i = 0; i < nl; ++i) {
-    hipError_t e = prepare(w[i], b[i], widths[i], widths[i + 1], kin[i], np[i], acts[i], ws + o_wt[i], ws + o_b[i],
-                           ncu, s, &L[i]);
-    if (e != hipSuccess) return fail_hip(e, "MLP weight preparation");
+    ps[i] = {w[i], ws + o_wt[i], b[i], ws + o_b[i], widths[i], widths[i + 1], kin[i], np[i]};
+    L[i] = {ws + o_wt[i], ws + o_b[i], kin[i], np[i], acts[i]};
   }
+  if (hipError_t e = prep_launch(ps.data(), nl, s); e != hipSuccess) return fail_hip(e, "MLP weight preparation");
   char* hb[2] = {ws + o_h0, ws + o_h1};
   for (int64_t r0 = 0; r0 < M; r0 += CH) {
     const int64_t rows = M - r0 < CH ? M - r0 : CH;
@@ -136,7 +134,7 @@ int run_chain(int64_t M, int nl, const int64_t* widths, const void* const* w, co
     for (int i = 0; i < nl && e == hipSuccess; ++i) {
       const bool last = i == nl - 1;
       void* c = last && direct_out ? (void*)row_ptr(out, r0, widths[nl]) : (void*)hb[i % 2];
-      e = layer(L[i], rows, a, lda, c, np[i], ncu, s);
+      e = layer(L[i], rows, a, lda, c, np[i], ncu, s, i == 0 && direct_in ? widths[0] : 0);
       a = c;
       lda = np[i];
     }
@@ -271,11 +269,12 @@ int gp_nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb
   char* ws = nullptr;
   if ((rc = workspace_acquire(dev, s, cv.off, (void**)&ws))) return rc;
   Prepared L[12];
+  PrepSpec ps[12];
   for (int i = 0; i < 12; ++i) {
-    hipError_t e = prepare(w[i], b[i], sh[i].K, sh[i].N, sh[i].Kin, sh[i].Np, sh[i].act, ws + o_wt[i],
-                           ws + o_b[i], ncu, s, &L[i]);
-    if (e != hipSuccess) return fail_hip(e, "NeRF weight preparation");
+    ps[i] = {w[i], ws + o_wt[i], b[i], ws + o_b[i], sh[i].K, sh[i].N, sh[i].Kin, sh[i].Np};
+    L[i] = {ws + o_wt[i], ws + o_b[i], sh[i].Kin, sh[i].Np, sh[i].act};
   }
+  if (hipError_t e = prep_launch(ps, 12, s); e != hipSuccess) return fail_hip(e, "NeRF weight preparation");
   char *xb = ws + o_x, *c1 = ws + o_c1, *c2 = ws + o_c2, *h0 = ws + o_h0, *h1 = ws + o_h1, *hd = ws + o_hd;
   for (int64_t r0 = 0; r0 < M; r0 += CH) {
     const int64_t rows = M - r0 < CH ? M - r0 : CH;

@@ -68,6 +68,21 @@ def test_mlp_vs_oracle(cuda, widths, acts, M):
     assert_parity(f(y), want, f"mlp {widths} M={M}")
 
 
+def test_mlp_input_tail_reads_zero(cuda):
+    """A 200-wide input is read in place and the GEMM's k-loop runs to 256: the columns
+    past 200 must read as zeros, not as the next row's head.  Row 5 starts with +inf, so
+    row 4 would turn NaN (inf x zero weight) if its tail read row 5."""
+    widths = [200, 128, 5]
+    ws, bs = dlrm_params(widths, seed=11, init="xavier")
+    x = normal_fp16(64, 200, seed=12)
+    x[5, 0] = float("inf")
+    y = f(gpipes.mlp_out(x.to(cuda), to(ws, cuda), to(bs, cuda), ["relu", "none"]))
+    keep = np.r_[0:5, 6:64]
+    assert np.isfinite(y[keep]).all()
+    want = oracle.mlp(f(x[keep]), [f(w) for w in ws], [f(b) for b in bs], [oracle.ACT_RELU, oracle.ACT_NONE])
+    assert_parity(y[keep], want, "mlp input tail")
+
+
 def test_mlp_no_bias_and_odd_stride(cuda):
     """Null biases; an input whose row is not 16-byte aligned (width 13) takes the padded path."""
     widths = [13, 256, 40]
