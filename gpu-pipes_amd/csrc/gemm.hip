@@ -205,7 +205,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 
   // Memory operations of one epilogue: a store (and a residual load) per
   // fragment and element group.
-  constexpr int EPI_OPS = C::NBW * 4 * C::MBW * (RESID ? 2 : 1);
+  constexpr int EPI_OPS = C::NBW * C::MBW * (RESID ? 6 : 2);
   // Waits until units 0 and 1 of a tile have landed.  Issued after them: the
   // tile's units 2 .. npre-1 (A, Bt, A) and, from the second tile on, the
   // previous tile's epilogue.  The counter field holds at most 63, which still
@@ -292,9 +292,14 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 
     // Epilogue.  For fragment (nb, mb) the lane holds row arow + 32 mb of the
     // tile and, in elements 4g .. 4g+3, features
-    // n0 + 32 NBW wn + 32 nb + 8 g + 4 lh + (0..3).  Output and residual go
-    // through buffer descriptors limited to the tile's valid rows; the
-    // residual loads of one nb are all issued before the first is used.
+    // n0 + 32 NBW wn + 32 nb + 8 g + 4 lh + (0..3).  After bias, activation
+    // and residual, v_permlane32_swap trades groups g = 2q+1 of the lanes in
+    // the lower half for groups g = 2q of the upper half, so each lane holds
+    // eight consecutive features -- 32 nb + 16 q + 8 lh + (0..7) -- and one
+    // 16-byte store per lane writes 32 contiguous bytes of each of the 32
+    // rows.  Output and residual go through buffer descriptors limited to the
+    // tile's valid rows; the residual loads of one nb are all issued before
+    // the first is used.
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.c + T.m0 * p.ldc, T.rows * p.ldc * 2);
     const __amdgpu_buffer_rsrc_t rr = make_rsrc(RESID ? p.r + T.m0 * p.ldr : p.c, RESID ? T.rows * p.ldr * 2 : 0);
     // Per-row byte offsets, computed here (opaque: not hoisted out of the tile
@@ -302,11 +307,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     int ebase[C::MBW], rbase[C::MBW];
 #pragma unroll
     for (int mb = 0; mb < C::MBW; ++mb) {
-      const int col = T.n0 + 32 * C::NBW * wn + 4 * lh;
-      ebase[mb] = opaque(((arow + 32 * mb) * p.ldc + col) * 2);
-      rbase[mb] = RESID ? opaque(((arow + 32 * mb) * p.ldr + col) * 2) : 0;
+      const int col = T.n0 + 32 * C::NBW * wn;
+      ebase[mb] = opaque(((arow + 32 * mb) * p.ldc + col + 8 * lh) * 2);
+      rbase[mb] = RESID ? opaque(((arow + 32 * mb) * p.ldr + col + 4 * lh) * 2) : 0;
     }
-    auto eoff = [&](int nb, int g, int mb) { return ebase[mb] + (32 * nb + 8 * g) * 2; };
+    auto eoff = [&](int nb, int q, int mb) { return ebase[mb] + (32 * nb + 16 * q) * 2; };
     auto roff = [&](int nb, int g, int mb) { return rbase[mb] + (32 * nb + 8 * g) * 2; };
 #pragma unroll
     for (int nb = 0; nb < C::NBW; ++nb) {
@@ -322,16 +327,24 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
           for (int mb = 0; mb < C::MBW; ++mb) res[g][mb] = buf_load_h4(rr, roff(nb, g, mb));
       }
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
+      for (int mb = 0; mb < C::MBW; ++mb) {
+        u32x2 o[4];
 #pragma unroll
-        for (int mb = 0; mb < C::MBW; ++mb) {
+        for (int g = 0; g < 4; ++g) {
           f4 v;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             v[e] = apply_act(acc[nb][mb][4 * g + e] + (float)bias[nb][g][e], ACT);
             if constexpr (RESID) v[e] += (float)res[g][mb][e];
           }
-          buf_store_h4(rc, eoff(nb, g, mb), __builtin_convertvector(v, h4));
+          o[g] = __builtin_bit_cast(u32x2, __builtin_convertvector(v, h4));
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const auto lo = __builtin_amdgcn_permlane32_swap(o[2 * q][0], o[2 * q + 1][0], false, false);
+          const auto hi = __builtin_amdgcn_permlane32_swap(o[2 * q][1], o[2 * q + 1][1], false, false);
+          const u32x4 w = {(unsigned)lo[0], (unsigned)hi[0], (unsigned)lo[1], (unsigned)hi[1]};
+          buf_store_u4(rc, eoff(nb, q, mb), w);
         }
       }
 #pragma unroll

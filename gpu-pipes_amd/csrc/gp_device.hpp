@@ -151,6 +151,9 @@ __device__ __forceinline__ h4 buf_load_h4(__amdgpu_buffer_rsrc_t rsrc, int off) 
 __device__ __forceinline__ void buf_store_h4(__amdgpu_buffer_rsrc_t rsrc, int off, h4 v) {
   __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), rsrc, off, 0, 0);
 }
+__device__ __forceinline__ void buf_store_u4(__amdgpu_buffer_rsrc_t rsrc, int off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, off, 0, 0);
+}
 
 // ---------------------------------------------------------------------------
 // MFMA 32x32x16 f16 -> f32.  Operand layout (wave64):
