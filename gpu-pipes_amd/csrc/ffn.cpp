@@ -117,8 +117,8 @@ int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void*
   if ((rc = workspace_acquire(dev, s, total, (void**)&ws))) return rc;
   void *w1t = ws, *w2t = ws + o_w2t, *hbuf = ws + o_act, *ybuf = ws + o_y;
 
-  hipError_t e = transpose_launch(w1, w1t, H, FF, s);
-  if (e == hipSuccess) e = transpose_launch(w2, w2t, FF, H, s);
+  const PrepSpec ps[2] = {{w1, w1t, nullptr, nullptr, H, FF, H, FF}, {w2, w2t, nullptr, nullptr, FF, H, FF, H}};
+  hipError_t e = prep_launch(ps, 2, s);
   if (e != hipSuccess) return fail_hip(e, "transpose launch");
   for (int64_t r0 = 0; r0 < M; r0 += CH) {
     const int64_t rows = M - r0 < CH ? M - r0 : CH;

@@ -403,8 +403,38 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepBatch pb) {
   }
   __syncthreads();
   for (int r = ty; r < 64; r += 4) L.wt[(int64_t)(n0 + r) * L.Kp + k0 + tx] = tile[tx][r];
-  if (local == 0)
+  if (local == 0 && L.bp)
     for (int j = threadIdx.x; j < L.Np; j += 256) L.bp[j] = (L.b && j < L.N) ? L.b[j] : (half_t)0.f;
+}
+
+// A one-output layer, out[m] = act(a[m][0:K] . w[0:K] + b), fp32 accumulate:
+// a GEMV over rows, which a 128-wide GEMM tile would spend 128 columns of
+// MFMA and output on.  Each half of a wave takes one row and reads it as
+// 16-byte chunks (one 512-byte row per instruction at K = 256), then sums
+// its 32 partial dot products with lane exchanges.
+__global__ __launch_bounds__(256) void gemv1_kernel(const half_t* a, int lda, int64_t M, int K, const half_t* w,
+                                                    const half_t* b, int act, half_t* out) {
+  const int lane = threadIdx.x & 63, hw = lane >> 5, l32 = lane & 31;
+  const int64_t wv = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t nw = (int64_t)gridDim.x * 4;
+  const int nc = K / 8;
+  const float bias = b ? (float)b[0] : 0.f;
+  for (int64_t m0 = 2 * wv; m0 < M; m0 += 2 * nw) {
+    const int64_t m = m0 + hw;
+    float s = 0.f;
+    if (m < M) {
+      const half_t* row = a + m * lda;
+      for (int c = l32; c < nc; c += 32) {
+        const h8 x = *(const h8*)(row + 8 * c);
+        const h8 v = *(const h8*)(w + 8 * c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s = __builtin_fmaf((float)x[e], (float)v[e], s);
+      }
+    }
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 32);
+    if (l32 == 0 && m < M) out[m] = (half_t)apply_act(s + bias, act);
+  }
 }
 
 template <class C, int ACT, bool RESID>
@@ -452,8 +482,7 @@ hipError_t prep_launch(const PrepSpec* L, int n, hipStream_t s) {
     pb.n = n - i0 < kMaxPrep ? n - i0 : kMaxPrep;
     for (int i = 0; i < pb.n; ++i) {
       const PrepSpec& q = L[i0 + i];
-      if (q.Kp % 64 != 0 || q.Np % 64 != 0 || q.K > q.Kp || q.N > q.Np || q.K < 1 || q.N < 1 || !q.w || !q.wt ||
-          !q.bp)
+      if (q.Kp % 64 != 0 || q.Np % 64 != 0 || q.K > q.Kp || q.N > q.Np || q.K < 1 || q.N < 1 || !q.w || !q.wt)
         return hipErrorInvalidValue;
       pb.L[i] = {(const half_t*)q.w, (half_t*)q.wt, (const half_t*)q.b, (half_t*)q.bp,
                  (int)q.K, (int)q.N, (int)q.Kp, (int)q.Np, blocks};
@@ -464,6 +493,17 @@ hipError_t prep_launch(const PrepSpec* L, int n, hipStream_t s) {
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
+}
+
+hipError_t gemv1_launch(int64_t M, int64_t K, const void* a, int64_t lda, const void* w, const void* b, int act,
+                        void* out, int num_cus, hipStream_t s) {
+  if (M <= 0) return hipSuccess;
+  if (K < 8 || K % 8 || lda < K || lda % 8 || !a || !w || !out) return hipErrorInvalidValue;
+  const int64_t want = (M + 7) / 8;  // eight rows per block and pass
+  const int64_t grid = want < (int64_t)num_cus * 8 ? want : (int64_t)num_cus * 8;
+  hipLaunchKernelGGL(gemm::gemv1_kernel, dim3((unsigned)grid), dim3(256), 0, s, (const half_t*)a, (int)lda, M,
+                     (int)K, (const half_t*)w, (const half_t*)b, act, (half_t*)out);
+  return hipGetLastError();
 }
 
 hipError_t transpose_launch(const void* in, void* out, int64_t K, int64_t N, hipStream_t s, int64_t Kp,

@@ -100,6 +100,9 @@ int run_chain(int64_t M, int nl, const int64_t* widths, const void* const* w, co
   // zero-fills its columns up to the padded width.
   const bool direct_in = widths[0] % 8 == 0 && aligned16(x);
   const bool direct_out = np[nl - 1] == widths[nl] && aligned16(out);
+  // A one-output last layer (the DLRM click head) is a GEMV over the previous
+  // activations, written straight to out.
+  const bool gemv_head = widths[nl] == 1 && nl >= 2 && widths[nl - 1] % 8 == 0 && aligned16(w[nl - 1]);
   Carve cv;
   std::vector<size_t> o_wt(nl), o_b(nl);
   for (int i = 0; i < nl; ++i) {
@@ -133,12 +136,16 @@ int run_chain(int64_t M, int nl, const int64_t* widths, const void* const* w, co
     }
     for (int i = 0; i < nl && e == hipSuccess; ++i) {
       const bool last = i == nl - 1;
+      if (last && gemv_head) {
+        e = gemv1_launch(rows, widths[i], a, lda, w[i], b[i], acts[i], (void*)row_ptr(out, r0, 1), ncu, s);
+        break;
+      }
       void* c = last && direct_out ? (void*)row_ptr(out, r0, widths[nl]) : (void*)hb[i % 2];
       e = layer(L[i], rows, a, lda, c, np[i], ncu, s, i == 0 && direct_in ? widths[0] : 0);
       a = c;
       lda = np[i];
     }
-    if (e == hipSuccess && !direct_out)
+    if (e == hipSuccess && !direct_out && !gemv_head)
       e = place_launch(rows, a, lda, widths[nl], (void*)row_ptr(out, r0, widths[nl]), widths[nl], widths[nl],
                        GP_ACT_NONE, ncu, s);
     if (e != hipSuccess) return fail_hip(e, "MLP layer launch");

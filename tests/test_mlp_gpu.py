@@ -68,6 +68,24 @@ def test_mlp_vs_oracle(cuda, widths, acts, M):
     assert_parity(f(y), want, f"mlp {widths} M={M}")
 
 
+@pytest.mark.parametrize("widths,acts,bias", [
+    ([64, 128, 1], ["relu", "none"], False),      # one-output head as a GEMV, no bias
+    ([64, 256, 1], ["relu", "sigmoid"], True),    # ... with bias and sigmoid
+    ([64, 100, 1], ["relu", "sigmoid"], True),    # K = 100 is not a multiple of 8: GEMM head
+    ([32, 4104, 1], ["relu", "relu"], True),      # K past 4096: several chunks per lane
+])
+def test_mlp_one_output_head(cuda, widths, acts, bias):
+    ws, bs = dlrm_params(widths, seed=21, init="xavier")
+    if not bias:
+        bs = [None] * len(bs)
+    M = 1027
+    x = normal_fp16(M, widths[0], seed=22)
+    y = gpipes.mlp_out(x.to(cuda), to(ws, cuda), [None if b is None else b.to(cuda) for b in bs], acts)
+    assert y.shape == (M, 1)
+    want = oracle.mlp(f(x), [f(w) for w in ws], [None if b is None else f(b) for b in bs], [ACT[a] for a in acts])
+    assert_parity(f(y), want, f"mlp head {widths}")
+
+
 def test_mlp_input_tail_reads_zero(cuda):
     """A 200-wide input is read in place and the GEMM's k-loop runs to 256: the columns
     past 200 must read as zeros, not as the next row's head.  Row 5 starts with +inf, so
