@@ -173,7 +173,7 @@ def bench_bert(args):
             "frac": tflops / MFMA_F16_PEAK_TFLOPS, "traffic": None,
             "kernel_ms_avg": avg_ms, "kernel_ms_median": call_ms[len(call_ms) // 2],
             "flops_per_launch": flops, "algorithmic_bytes_per_launch": bytes_,
-            "launch": "one gp_bert_ffn_out call (2 weight transposes, then per 16384-row chunk: "
+            "launch": "one gp_bert_ffn_out call (one weight-transpose launch, then per 16384-row chunk: "
                       "GEMM1+bias+GELU, GEMM2+bias+residual, LayerNorm)",
         },
         "cpu_baseline": None if args.no_cpu else cpu_baseline_bert(),
@@ -284,7 +284,8 @@ def bench_chain(args):
                   "accumulate": "f32", "tile_rows": 256}
         data = "synthetic (positional encodings of U(-1,1) points and unit directions, Kaiming-uniform, seed 0)"
         unit = "samples/s"
-    launch = {"dlrm": "one step: every layer a wide-GEMM launch per 262,144-row chunk (weights transposed per call)",
+    launch = {"dlrm": "one step: per MLP one weight-preparation launch, then a wide-GEMM launch per layer "
+                      "(the one-output click head a GEMV launch)",
               "nerf": "one step: the weight-packing kernel, then the fused 12-layer kernel over 256-row tiles"}
 
     for _ in range(args.warmup):
