@@ -45,10 +45,18 @@ __device__ __forceinline__ float gelu_tanh(float v) {
   return v * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(z));
 }
 
+// Logistic sigmoid 1 / (1 + e^(-v)) with e^(-v) = 2^(-v log2(e)): one
+// multiply, v_exp_f32, one add and v_rcp_f32.  For v -> -inf the power
+// overflows to +inf and the result is 0; for v -> +inf it is 1.  Relative
+// error is a few ulp of fp32, far below the fp16 rounding of the output.
+__device__ __forceinline__ float sigmoid(float v) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(v * -1.4426950408889634f));
+}
+
 __device__ __forceinline__ float apply_act(float v, int act) {
   if (act == ACT_RELU) return v > 0.f ? v : 0.f;
   if (act == ACT_GELU_TANH) return gelu_tanh(v);
-  if (act == ACT_SIGMOID) return 1.f / (1.f + expf(-v));
+  if (act == ACT_SIGMOID) return sigmoid(v);
   return v;
 }
 
