@@ -153,17 +153,20 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     T.rb = make_rsrc(p.bt + (int64_t)T.n0 * K, C::BN * K * 2);
     return T;
   };
-  auto issue = [&](const Tile& T, int u) {
+  // Copies [j0, j1) of unit u (default: all of them).
+  auto issue = [&](const Tile& T, int u, int j0 = 0, int j1 = 64) {
     GP_LDS char* const s = lds + (u % NU) * C::UNIT;
     const int so = (u >> 1) * ROWB;
     if (u & 1) {
 #pragma unroll
-      for (int j = 0; j < C::UB; ++j) dma16_buf_so(T.rb, voffb, j * jstrb + so, s + (j * NW + wave) * 1024);
+      for (int j = 0; j < C::UB; ++j)
+        if (j >= j0 && j < j1) dma16_buf_so(T.rb, voffb, j * jstrb + so, s + (j * NW + wave) * 1024);
     } else {
       const int k0 = (u >> 1) * BK;
       const int vo = k0 + BK <= p.ka || k0 + lck < p.ka ? voffa : kBeyond;
 #pragma unroll
-      for (int j = 0; j < C::UA; ++j) dma16_buf_so(T.ra, vo, j * jstra + so, s + (j * NW + wave) * 1024);
+      for (int j = 0; j < C::UA; ++j)
+        if (j >= j0 && j < j1) dma16_buf_so(T.ra, vo, j * jstra + so, s + (j * NW + wave) * 1024);
     }
   };
   auto prefetch = [&](const Tile& T) {
@@ -239,17 +242,26 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     // Main loop.  Fragments of k-step ks live in f[ks % 2]; the reads of step
     // ks+1 are issued just before the MFMAs of step ks.  Before the last step
     // of slab kt: wait for slab kt+1 (units 2kt+2, 2kt+3; unit 2kt+4 may still
-    // be in flight), barrier, copy units 2kt+5 and 2kt+6 into the slots of
-    // slab kt, and read step 0 of slab kt+1.  The barrier certifies that every
-    // wave's copies of slab kt+1 landed and that every wave has read slab kt
-    // into registers.
+    // be in flight), barrier, and read step 0 of slab kt+1.  The barrier
+    // certifies that every wave's copies of slab kt+1 landed and that every
+    // wave has read slab kt into registers, so units 2kt+5 (pb) and 2kt+6
+    // (pa) may go into slab kt's slots: their copies are spread over the
+    // first three steps of slab kt+1 (pb over steps 0-1, then pa over steps
+    // 1-2), so that no step's MFMAs wait behind a burst of copy issues.  pa
+    // is still the last unit issued at the next wait.
+    static_assert(KS == 4, "the copies of two units are spread over three steps");
     Frags f[2];
     lds_barrier();
     load(f[0], 0, 0);
+    int pa = -1, pb = -1;
     for (int kt = 0; kt + 1 < nslab; ++kt) {
 #pragma unroll
       for (int ks = 0; ks + 1 < KS; ++ks) {
         load(f[(ks + 1) % 2], kt, ks + 1);
+        if (ks == 0 && pb >= 0) issue(T, pb, 0, C::UB / 2);
+        if (ks == 1 && pb >= 0) issue(T, pb, C::UB / 2, C::UB);
+        if (ks == 1 && pa >= 0) issue(T, pa, 0, C::UA / 2);
+        if (ks == 2 && pa >= 0) issue(T, pa, C::UA / 2, C::UA);
         mma(f[ks % 2], std::integral_constant<int, NFR>{});
       }
       if (kt + 3 <= nslab)
@@ -257,8 +269,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
       else
         wait_vmcnt<0>();
       lds_barrier();
-      if (2 * kt + 5 < nunit) issue(T, 2 * kt + 5);
-      if (2 * kt + 6 < nunit) issue(T, 2 * kt + 6);
+      pb = 2 * kt + 5 < nunit ? 2 * kt + 5 : -1;
+      pa = 2 * kt + 6 < nunit ? 2 * kt + 6 : -1;
       load(f[0], kt + 1, 0);
       mma(f[1], std::integral_constant<int, NFR>{});
     }
