@@ -38,6 +38,7 @@
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
+#include <utility>
 
 #include "../../include/gpipes.h"
 #include "gp_device.hpp"
@@ -88,6 +89,11 @@ struct Args {
 // XOR-swizzled with (r / 2) so 16 consecutive rows (two per 256-byte bank
 // window) read at one logical chunk cover 16 distinct 16-byte bank groups.
 __device__ __forceinline__ int unit_off(int r, int c) { return r * ROWB + ((c ^ ((r >> 1) & 7)) << 4); }
+
+template <typename F, int... I>
+__device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&& f) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
 
 template <class C, int ACT, bool RESID>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_kernel(Args p) {
@@ -190,21 +196,23 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     for (int mb = 0; mb < C::MBW; ++mb) f.b[mb] = *(GP_LDS const h8*)(ua + 32 * mb * ROWB);
   };
   f16x acc[C::NBW][C::MBW];
-  // MFMAs of one step; the NFR fragment reads issued just before are spread
-  // over the first MFMAs so that their latency hides behind the matrix pipe.
-  auto mma = [&](const Frags& f, auto nfr_c) {
-    constexpr int nfr = decltype(nfr_c)::value;
+  // MFMAs of one step; the nfr fragment reads and nv copies issued just
+  // before are spread one per MFMA over the first MFMAs, so that their
+  // latency hides behind the matrix pipe.
+  auto mma = [&](const Frags& f, auto nfr_c, auto nv_c) {
+    constexpr int nfr = decltype(nfr_c)::value, nv = decltype(nv_c)::value;
 #pragma unroll
     for (int nb = 0; nb < C::NBW; ++nb)
 #pragma unroll
       for (int mb = 0; mb < C::MBW; ++mb) acc[nb][mb] = mfma32(f.a[nb], f.b[mb], acc[nb][mb]);
 #pragma unroll
-    for (int i = 0; i < nfr; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    for (int i = 0; i < C::NBW * C::MBW; ++i) {
+      if (i < nfr) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i < nv) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, C::NBW * C::MBW - nfr, 0);
   };
+  using I0 = std::integral_constant<int, 0>;
 
   // Memory operations of one epilogue: a store (and a residual load) per
   // fragment and element group.
@@ -244,42 +252,50 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     // of slab kt: wait for slab kt+1 (units 2kt+2, 2kt+3; unit 2kt+4 may still
     // be in flight), barrier, and read step 0 of slab kt+1.  The barrier
     // certifies that every wave's copies of slab kt+1 landed and that every
-    // wave has read slab kt into registers, so units 2kt+5 (pb) and 2kt+6
-    // (pa) may go into slab kt's slots: their copies are spread over the
-    // first three steps of slab kt+1 (pb over steps 0-1, then pa over steps
-    // 1-2), so that no step's MFMAs wait behind a burst of copy issues.  pa
-    // is still the last unit issued at the next wait.
+    // wave has read slab kt into registers, so units 2kt+5 and 2kt+6 may go
+    // into slab kt's slots.  Their copies are issued during the first three
+    // steps of slab kt+1 (the Bt unit over steps 0-1, then the A unit over
+    // steps 1-2), one copy after each of the first MFMAs of a step, so no
+    // step's MFMAs wait behind a burst of copy issues; the A unit is still
+    // the last one issued at the next wait.  Which units a slab copies
+    // depends only on its position in the tile, so the slab body is
+    // instantiated per case and stays branch-free for the scheduler.
     static_assert(KS == 4, "the copies of two units are spread over three steps");
     Frags f[2];
     lds_barrier();
     load(f[0], 0, 0);
-    int pa = -1, pb = -1;
-    for (int kt = 0; kt + 1 < nslab; ++kt) {
-#pragma unroll
-      for (int ks = 0; ks + 1 < KS; ++ks) {
+    // One slab kt < nslab - 1; MODE: which freed units are copied during it
+    // (0 none, 1 the Bt unit 2kt+3, 2 both 2kt+3 and the A unit 2kt+4).
+    auto slab = [&](int kt, auto mode_c) {
+      constexpr int MODE = decltype(mode_c)::value;
+      const int pb = 2 * kt + 3, pa = 2 * kt + 4;
+      static_for(std::make_integer_sequence<int, KS - 1>{}, [&](auto ks_c) {
+        constexpr int ks = decltype(ks_c)::value;
         load(f[(ks + 1) % 2], kt, ks + 1);
-        if (ks == 0 && pb >= 0) issue(T, pb, 0, C::UB / 2);
-        if (ks == 1 && pb >= 0) issue(T, pb, C::UB / 2, C::UB);
-        if (ks == 1 && pa >= 0) issue(T, pa, 0, C::UA / 2);
-        if (ks == 2 && pa >= 0) issue(T, pa, C::UA / 2, C::UA);
-        mma(f[ks % 2], std::integral_constant<int, NFR>{});
-      }
+        if constexpr (MODE >= 1 && ks == 0) issue(T, pb, 0, C::UB / 2);
+        if constexpr (MODE >= 1 && ks == 1) issue(T, pb, C::UB / 2, C::UB);
+        if constexpr (MODE == 2 && ks == 1) issue(T, pa, 0, C::UA / 2);
+        if constexpr (MODE == 2 && ks == 2) issue(T, pa, C::UA / 2, C::UA);
+        constexpr int nv = (MODE >= 1 && ks < 2 ? C::UB / 2 : 0) + (MODE == 2 && ks > 0 ? C::UA / 2 : 0);
+        mma(f[ks % 2], std::integral_constant<int, NFR>{}, std::integral_constant<int, nv>{});
+      });
       if (kt + 3 <= nslab)
         wait_vmcnt<C::UA>();
       else
         wait_vmcnt<0>();
       lds_barrier();
-      pb = 2 * kt + 5 < nunit ? 2 * kt + 5 : -1;
-      pa = 2 * kt + 6 < nunit ? 2 * kt + 6 : -1;
       load(f[0], kt + 1, 0);
-      mma(f[1], std::integral_constant<int, NFR>{});
-    }
+      mma(f[1], std::integral_constant<int, NFR>{}, I0{});
+    };
+    if (nslab >= 2) slab(0, I0{});
+    for (int kt = 1; kt + 2 < nslab; ++kt) slab(kt, std::integral_constant<int, 2>{});
+    if (nslab >= 3) slab(nslab - 2, std::integral_constant<int, 1>{});
 #pragma unroll
     for (int ks = 0; ks + 1 < KS; ++ks) {
       load(f[(ks + 1) % 2], nslab - 1, ks + 1);
-      mma(f[ks % 2], std::integral_constant<int, NFR>{});
+      mma(f[ks % 2], std::integral_constant<int, NFR>{}, I0{});
     }
-    mma(f[1], std::integral_constant<int, 0>{});
+    mma(f[1], I0{}, I0{});
 
     // Bias of the features this lane holds (see the epilogue), loaded before
     // the next tile's copies so that waiting for it does not wait for them.
