@@ -8,8 +8,15 @@ stream, the HBM traffic per launch measured with rocprofv3 counters
 (profiles/traffic.json), and the CPU oracle timed on a bounded sample on the
 host cores.
 
-  python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--workload edge|node|edge_gather|bert]
+  python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--settle-ms 1000]
+                  [--workload edge|node|edge_gather|bert|dlrm|nerf]
                   [--impl fused|pipelined|pipelined_split_ln] [--no-cpu]
+
+Every line carries "spread": the per-launch HIP-event times of the timed
+region in launch order (min, median, max, and the means of the first and last
+five launches), so a clock ramp or a slow box shows in the line itself.
+--settle-ms runs untimed launches for that long between the warm-up and the
+timed region; the line states it in "settle".
 
 --workload bert times the BERT-large FFN block of configs[2] instead
 (LayerNorm(GELU(x W1 + b1) W2 + b2 + x), M = 65,536, H 1024, FF 4096): a step is
@@ -59,62 +66,146 @@ def algorithmic(M, K, ln, gather_nodes=0, idx_bytes=8):
     return bytes_, flops
 
 
-def cpu_baseline(K, ln, budget_s=10.0):
-    """The CPU oracle (oracle/oracle.c, OpenMP over rows) on the config-0 shape."""
+def host_cores():
+    """(threads to use, description): the cores of this process's affinity set,
+    capped by a cgroup CPU quota when one is set (threads beyond the quota only
+    time-slice)."""
+    n = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as fh:
+            q, period = fh.read().split()[:2]
+            if q != "max":
+                quota = max(1, int(int(q) // int(period)))
+    except (OSError, ValueError):
+        pass
+    use = min(n, quota) if quota else n
+    how = f"{n} cores in the affinity set" + (f", cgroup quota {quota} cores" if quota else ", no cgroup quota")
+    return use, how
+
+
+def _median_runs(run, budget_s, min_runs=10, warmups=3):
+    """3 warm-ups, then runs until budget_s has passed and at least min_runs
+    were timed; returns (median seconds, runs, total seconds)."""
     import numpy as np
 
+    for _ in range(warmups):
+        run()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < min_runs:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times), sum(times)
+
+
+def cpu_baseline_torch_mgn(K, ln, budget_s=8.0):
+    """MgnMlp (common/mlps.py:3-20) restated as torch.nn modules in fp32 on the
+    host cores, under inference_mode, on the config-0 shape X[16384, K]."""
+    import torch
+
+    threads, how = host_cores()
+    torch.set_num_threads(threads)
+    Ms = 16384
+    with torch.random.fork_rng(devices=[]):
+        torch.manual_seed(0)
+        layers = [torch.nn.Linear(K, 128), torch.nn.ReLU(), torch.nn.Linear(128, 128), torch.nn.ReLU(),
+                  torch.nn.Linear(128, 128)]
+        if ln:
+            layers.append(torch.nn.LayerNorm(128))
+        model = torch.nn.Sequential(*layers).eval()
+        x = torch.randn(Ms, K)
+    with torch.inference_mode():
+        med, n, tot = _median_runs(lambda: model(x), budget_s)
+    return {
+        "value": Ms / med, "unit": "rows/s", "cores": threads, "kind": "port",
+        "sample": f"torch.nn MgnMlp({K},[128,128,128]) fp32 on X[{Ms},{K}] (config-0 shape), torch "
+                  f"{torch.__version__}, {threads} threads ({how}), 3 warm-ups, median of {n} runs "
+                  f"({tot:.1f} s): {med * 1e3:.2f} ms/call",
+    }
+
+
+def cpu_baseline(K, ln, budget_s=8.0):
+    """The CPU oracle (oracle/oracle.c, OpenMP over rows) on the config-0 shape."""
     import oracle
     from gpipes.synth import mgn_params, normal_fp16
 
-    threads = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "16") or 16), 16)
+    threads, how = host_cores()
     oracle.set_num_threads(threads)
     Ms = 16384
     p = mgn_params(K, seed=0, layernorm=ln)
     f = lambda t: None if t is None else t.float().numpy()  # noqa: E731
     x = f(normal_fp16(Ms, K, seed=0))
     args = [f(p[k]) for k in ("w1", "b1", "w2", "b2", "w3", "b3", "gamma", "beta")]
-    oracle.mgn_mlp(x, *args)  # warm-up
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        oracle.mgn_mlp(x, *args)
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
+    med, n, tot = _median_runs(lambda: oracle.mgn_mlp(x, *args), budget_s)
     return {
         "value": Ms / med, "unit": "rows/s", "cores": threads, "kind": "port",
-        "sample": f"oracle/oracle.c MgnMlp fp32 on X[{Ms},{K}] (config-0 shape), "
-                  f"{len(times)} calls in {sum(times):.1f} s, median {med * 1e3:.2f} ms/call",
+        "sample": f"oracle/oracle.c MgnMlp fp32 on X[{Ms},{K}] (config-0 shape), {threads} OpenMP threads "
+                  f"({how}), 3 warm-ups, median of {n} calls ({tot:.1f} s): {med * 1e3:.2f} ms/call",
     }
 
 
 def cpu_baseline_bert(budget_s=10.0):
     """The CPU oracle's BERT FFN (oracle_bert_ffn, OpenMP over rows) on a row sample."""
-    import numpy as np
-
     import oracle
     from gpipes.synth import bert_params, normal_fp16
 
-    threads = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "16") or 16), 16)
+    threads, how = host_cores()
     oracle.set_num_threads(threads)
     Ms, H, FF = 256, BERT["H"], BERT["FF"]
     p = {k: v.float().numpy() for k, v in bert_params(H, FF, seed=0).items()}
     x = normal_fp16(Ms, H, seed=0).float().numpy()
     run = lambda: oracle.bert_ffn(x, p["w1"], p["b1"], p["w2"], p["b2"], p["gamma"], p["beta"],  # noqa: E731
                                   act=oracle.ACT_GELU_TANH, eps=BERT["eps"])
-    run()
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
+    med, n, tot = _median_runs(run, budget_s, min_runs=3, warmups=1)
     return {
         "value": Ms / med, "unit": "rows/s", "cores": threads, "kind": "port",
-        "sample": f"oracle/oracle.c BertFfn fp32 on X[{Ms},{H}] (H {H}, FF {FF}, GELU tanh), "
-                  f"{len(times)} calls in {sum(times):.1f} s, median {med * 1e3:.1f} ms/call",
+        "sample": f"oracle/oracle.c BertFfn fp32 on X[{Ms},{H}] (H {H}, FF {FF}, GELU tanh), {threads} threads "
+                  f"({how}), median of {n} calls ({tot:.1f} s): {med * 1e3:.1f} ms/call",
     }
+
+
+def spread(ms):
+    """Per-launch times (ms) in launch order -> min / median / max and the
+    means of the first and last five launches."""
+    s = sorted(ms)
+    k = min(5, len(ms))
+    return {"min": s[0], "median": s[len(s) // 2], "max": s[-1],
+            "first5_mean": sum(ms[:k]) / k, "last5_mean": sum(ms[-k:]) / k}
+
+
+def timed_steps(step, args, dev):
+    """Warm-up, optional settle, then the timed region.  step(i) enqueues step
+    i on torch's current stream (the stream every entry point launches on).
+    Each step is bracketed by HIP events recorded on that stream.  Returns
+    (per-step ms in launch order, wall ms per step, settle record)."""
+    import torch
+
+    stream = torch.cuda.current_stream(dev)
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    settle = {"ms": 0.0, "launches": 0}
+    if args.settle_ms > 0:
+        t0 = time.perf_counter()
+        n = 0
+        while (time.perf_counter() - t0) * 1e3 < args.settle_ms:
+            for _ in range(16):
+                step(args.warmup + n)
+                n += 1
+            torch.cuda.synchronize()
+        settle = {"ms": (time.perf_counter() - t0) * 1e3, "launches": n}
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        step(i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return [a.elapsed_time(b) for a, b in ev], wall * 1e3 / args.steps, settle
 
 
 def bench_bert(args):
@@ -130,26 +221,12 @@ def bench_bert(args):
     x = normal_fp16(M, H, seed=0, device=dev)
     out = torch.empty_like(x)
 
-    def step():
+    def step(i):
         gpipes.bert_ffn_out(x, p["w1"], p["b1"], p["w2"], p["b2"], p["gamma"], p["beta"], out, eps=eps,
                             act="gelu_tanh")
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        ev[i][0].record(stream)
-        step()
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    call_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    call_ms, ms_per_step, settle = timed_steps(step, args, dev)
     avg_ms = sum(call_ms) / len(call_ms)
-    ms_per_step = wall * 1e3 / args.steps
     flops = 2 * 2 * M * H * FF  # the two GEMMs; GELU, residual and LayerNorm are O(M H) and O(M FF)
     tflops = flops / (avg_ms * 1e-3) / 1e12
     bytes_ = (M * H * 2) * 2 + 2 * H * FF * 2 + (FF + 3 * H) * 2  # x in, out, weights, vectors
@@ -171,11 +248,13 @@ def bench_bert(args):
         "roofline": {
             "bound": "mfma", "achieved": tflops, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": tflops / MFMA_F16_PEAK_TFLOPS, "traffic": None,
-            "kernel_ms_avg": avg_ms, "kernel_ms_median": call_ms[len(call_ms) // 2],
+            "kernel_ms_avg": avg_ms, "kernel_ms_median": spread(call_ms)["median"],
             "flops_per_launch": flops, "algorithmic_bytes_per_launch": bytes_,
             "launch": "one gp_bert_ffn_out call (one weight-transpose launch, then per 16384-row chunk: "
                       "GEMM1+bias+GELU, GEMM2+bias+residual, LayerNorm)",
         },
+        "spread": spread(call_ms),
+        "settle": settle,
         "cpu_baseline": None if args.no_cpu else cpu_baseline_bert(),
     }
     print(json.dumps(rec), flush=True)
@@ -198,12 +277,10 @@ NERF_FLOPS = 2 * (64 * 256 + 4 * 256 * 256 + 320 * 256 + 2 * 256 * 256 + 256 * 1
 
 def cpu_baseline_chain(workload, budget_s=10.0):
     """The CPU oracle (oracle.mlp / oracle.nerf over oracle/oracle.c) on a row sample."""
-    import numpy as np
-
     import oracle
     from gpipes.synth import dlrm_params, nerf_inputs, nerf_params, padded_normal, padded_uniform
 
-    threads = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "16") or 16), 16)
+    threads, how = host_cores()
     oracle.set_num_threads(threads)
     f = lambda ts: [t.float().numpy() for t in ts]  # noqa: E731
     if workload == "dlrm":
@@ -227,16 +304,10 @@ def cpu_baseline_chain(workload, budget_s=10.0):
         def run():
             oracle.nerf(x, d, ws, bs, oracle.ACT_SIGMOID)
         what = f"oracle Nerf fp32 on {Ms} samples"
-    run()
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
+    med, n, tot = _median_runs(run, budget_s, min_runs=3, warmups=1)
     return {"value": Ms / med, "unit": "rows/s" if workload == "dlrm" else "samples/s", "cores": threads,
-            "kind": "port", "sample": f"{what}, {len(times)} calls in {sum(times):.1f} s, median {med * 1e3:.1f} ms"}
+            "kind": "port", "sample": f"{what}, {threads} threads ({how}), median of {n} calls ({tot:.1f} s): "
+                                      f"{med * 1e3:.1f} ms"}
 
 
 def bench_chain(args):
@@ -258,7 +329,7 @@ def bench_chain(args):
         ob = torch.empty((M, 128), dtype=torch.float16, device=dev)
         ot = torch.empty((M, 1), dtype=torch.float16, device=dev)
 
-        def step():
+        def step(i):
             gpipes.mlp_out(xb, wb, bb, ["relu"] * 3, ob)
             gpipes.mlp_out(xt, wt, bt, ["relu"] * 4 + ["sigmoid"], ot)
         flops = M * (chain_flops(DLRM_BOT) + chain_flops(DLRM_TOP))
@@ -275,7 +346,7 @@ def bench_chain(args):
         o_rgb = torch.empty((M, 3), dtype=torch.float16, device=dev)
         wb = [t for pair in zip(ws, bs) for t in pair]
 
-        def step():
+        def step(i):
             gpipes.nerf_full_out(x, d, *wb, o_r, o_rgb, rgb_act="sigmoid")
         flops = M * NERF_FLOPS
         bytes_ = M * (64 + 27 + 1 + 3) * 2
@@ -288,22 +359,8 @@ def bench_chain(args):
                       "(the one-output click head a GEMV launch)",
               "nerf": "one step: the weight-packing kernel, then the fused 12-layer kernel over 256-row tiles"}
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        ev[i][0].record(stream)
-        step()
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    call_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    call_ms, ms_per_step, settle = timed_steps(step, args, dev)
     avg_ms = sum(call_ms) / len(call_ms)
-    ms_per_step = wall * 1e3 / args.steps
     tflops = flops / (avg_ms * 1e-3) / 1e12
     rec = {
         "metric": CHAIN_METRIC[args.workload],
@@ -322,10 +379,12 @@ def bench_chain(args):
         "roofline": {
             "bound": "mfma", "achieved": tflops, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": tflops / MFMA_F16_PEAK_TFLOPS, "traffic": None,
-            "kernel_ms_avg": avg_ms, "kernel_ms_median": call_ms[len(call_ms) // 2],
+            "kernel_ms_avg": avg_ms, "kernel_ms_median": spread(call_ms)["median"],
             "flops_per_launch": flops, "algorithmic_bytes_per_launch": bytes_,
             "launch": launch[args.workload],
         },
+        "spread": spread(call_ms),
+        "settle": settle,
         "cpu_baseline": None if args.no_cpu else cpu_baseline_chain(args.workload),
     }
     print(json.dumps(rec), flush=True)
@@ -347,6 +406,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["bert", "dlrm", "nerf"], default="edge")
     ap.add_argument("--impl", choices=["fused", "pipelined", "pipelined_split_ln"], default="fused")
+    ap.add_argument("--settle-ms", type=float, default=1000.0,
+                    help="untimed launches for this long between the warm-up and the timed region: the "
+                         "engine clock swings for tens of ms after a burst starts (launches run fast, then "
+                         "up to 1.5x slower, then settle), so the timed region starts in the steady state")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-ref", action="store_true",
                     help="first run one plain 1 GiB device copy (a known-size reference kernel "
@@ -406,24 +469,8 @@ def main():
         torch.cuda.synchronize()
         del ref_in, ref_out
 
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-
-    stream = torch.cuda.current_stream(dev)  # the stream the kernels are launched on
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        ev[i][0].record(stream)
-        step(i)
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-
-    launch_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    launch_ms, ms_per_step, settle = timed_steps(step, args, dev)
     avg_launch_ms = sum(launch_ms) / len(launch_ms)
-    ms_per_step = wall * 1e3 / args.steps
     bytes_, flops = algorithmic(M, K, ln, GATHER_NODES if gather else 0)
     achieved_gbs = bytes_ / (avg_launch_ms * 1e-3) / 1e9
     tflops = flops / (avg_launch_ms * 1e-3) / 1e12
@@ -448,12 +495,15 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": achieved_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": load_traffic(args.workload, args.impl),
-            "kernel_ms_avg": avg_launch_ms, "kernel_ms_median": launch_ms[len(launch_ms) // 2],
+            "kernel_ms_avg": avg_launch_ms, "kernel_ms_median": spread(launch_ms)["median"],
             "algorithmic_bytes_per_launch": bytes_,
         },
         "mfma": {"achieved_tflops": tflops, "peak_tflops": MFMA_F16_PEAK_TFLOPS,
                  "frac": tflops / MFMA_F16_PEAK_TFLOPS, "flops_per_launch": flops},
-        "cpu_baseline": None if args.no_cpu else cpu_baseline(K, ln),
+        "spread": spread(launch_ms),
+        "settle": settle,
+        "cpu_baseline": None if args.no_cpu else cpu_baseline_torch_mgn(K, ln),
+        "cpu_baseline_oracle": None if args.no_cpu else cpu_baseline(K, ln),
     }
     print(json.dumps(rec), flush=True)
 

@@ -98,13 +98,4 @@ int workspace_acquire(int dev, hipStream_t stream, size_t bytes, void** base) {
   return GP_OK;
 }
 
-int arena_last(int dev, hipStream_t stream, void** base, uint32_t* epoch) {
-  std::lock_guard<std::mutex> lk(g_mu);
-  auto it = g_arenas.find({dev, stream});
-  if (it == g_arenas.end() || !it->second.base) return fail(GP_ERR_INVALID_ARG, "no pipelined launch on this stream");
-  *base = it->second.base;
-  *epoch = it->second.epoch;
-  return GP_OK;
-}
-
 }  // namespace gp

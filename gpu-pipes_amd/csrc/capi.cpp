@@ -69,14 +69,6 @@ int current_device_info(int* dev_out, int* num_cus) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-// Host view of the pipeline control block (layout of PipeCtl, pipeline.hpp):
-// 16 ticket counters and the barrier counter, 128 bytes each, then the
-// launch error word.
-struct PipeCtlView {
-  char counters[17 * 128];
-  unsigned long long err;
-};
-
 int check_mgn_args(const MgnArgs& a) {
   if (a.M < 0) return fail(GP_ERR_INVALID_ARG, "M must be >= 0 (got %lld)", (long long)a.M);
   if (a.K != 128 && a.K != 256 && a.K != 384)
@@ -107,9 +99,12 @@ int run_mgn(const MgnArgs& a, int impl, hipStream_t stream) {
   int dev = 0, ncu = 0;
   rc = current_device_info(&dev, &ncu);
   if (rc != GP_OK) return rc;
-  hipError_t e;
   if (impl == GP_IMPL_FUSED) {
-    e = mgn_fused_launch(a, ncu, stream);
+    MgnArgs f = a;
+    rc = status_acquire(dev, stream, &f.status, &f.epoch);
+    if (rc != GP_OK) return rc;
+    f.spin_limit = (int)wait_limit(0);
+    hipError_t e = mgn_fused_launch(f, ncu, stream);
     if (e != hipSuccess) return fail_hip(e, "mgn_fused launch");
     return GP_OK;
   }
@@ -239,18 +234,26 @@ int gp_pipeline_check(void* stream) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return fail_hip(e, "hipGetDevice");
-  void* base = nullptr;
+  unsigned long long* word = nullptr;
   uint32_t epoch = 0;
-  int rc = arena_last(dev, (hipStream_t)stream, &base, &epoch);
+  int rc = status_last(dev, (hipStream_t)stream, &word, &epoch);
   if (rc != GP_OK) return rc;
   e = hipStreamSynchronize((hipStream_t)stream);
   if (e != hipSuccess) return fail_hip(e, "hipStreamSynchronize");
   unsigned long long err = 0;
-  e = hipMemcpy(&err, &((PipeCtlView*)base)->err, sizeof(err), hipMemcpyDeviceToHost);
-  if (e != hipSuccess) return fail_hip(e, "hipMemcpy (pipeline status)");
+  e = hipMemcpy(&err, word, sizeof(err), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return fail_hip(e, "hipMemcpy (launch status)");
   if ((uint32_t)(err >> 32) == epoch && (uint32_t)err != 0)
-    return fail(GP_ERR_TIMEOUT, "the last pipelined launch failed: %s (error bits 0x%x)",
-                (err & 1) ? "a queue wait timed out" : "no complete pipeline fitted on one XCD", (unsigned)err);
+    return fail(GP_ERR_TIMEOUT, "the last launch on this stream failed on the device: %s (error bits 0x%x)",
+                (err & 1) ? "a wait timed out; its outputs are not valid" : "no complete pipeline fitted on one XCD",
+                (unsigned)err);
+  return GP_OK;
+}
+
+int gp_set_wait_limit(int64_t polls) {
+  clear_error();
+  if (polls < 0 || polls > (int64_t(1) << 30)) return fail(GP_ERR_INVALID_ARG, "polls must be in [0, 2^30]");
+  set_wait_limit((long long)polls);
   return GP_OK;
 }
 
@@ -292,6 +295,9 @@ int gp_mgn_edge_gather_out(int64_t E, int64_t N, const void* nf, const void* ef,
   int dev = 0, ncu = 0;
   rc = current_device_info(&dev, &ncu);
   if (rc != GP_OK) return rc;
+  rc = status_acquire(dev, (hipStream_t)stream, &a.status, &a.epoch);
+  if (rc != GP_OK) return rc;
+  a.spin_limit = (int)wait_limit(0);
   hipError_t e = mgn_fused_launch(a, ncu, (hipStream_t)stream);
   return e == hipSuccess ? GP_OK : fail_hip(e, "mgn_edge_gather launch");
 }

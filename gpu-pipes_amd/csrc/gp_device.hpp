@@ -70,10 +70,21 @@ __device__ __forceinline__ void lds_barrier() {
 // drains its own LDS traffic (lgkmcnt(0)) so that everything it wrote
 // before signalling is visible to the waves that observe the signal.
 // ---------------------------------------------------------------------------
-constexpr int kSpinLimit = 1 << 20;  // ~0.1 s: a broken protocol ends instead of hanging
+constexpr int kSpinLimit = 1 << 20;  // default poll bound (~0.1 s): a broken protocol ends instead of hanging
 
 __device__ __forceinline__ int lds_load_relaxed(GP_LDS int* c) {
   return __hip_atomic_load((int*)c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Record error `bits` for launch `epoch` in a status word: the word is lifted
+// to (epoch << 32) first (an older launch's value reads as no error), then the
+// bits are or-ed in.  Vector atomics at agent scope; one lane calls it.
+constexpr unsigned kErrTimeout = 1;
+__device__ __forceinline__ void status_fail(unsigned long long* word, uint32_t epoch, unsigned bits) {
+  __hip_atomic_fetch_max(word, (unsigned long long)epoch << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 7, 15));
+  __hip_atomic_fetch_or(word, (unsigned long long)bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 7, 15));
 }
 
 // Add 1 to an LDS counter once per wave, after this wave's LDS writes.
@@ -85,13 +96,14 @@ __device__ __forceinline__ void lds_signal(GP_LDS int* c, int lane) {
 }
 
 // Spin until an LDS counter is >= target (every lane reads the same word).
-// If the bound runs out, the sticky abort word is set and every later wait of
-// the workgroup returns at once, so the kernel always terminates.
-__device__ __forceinline__ void lds_wait_geq(GP_LDS int* c, int target, GP_LDS int* abort) {
+// If `limit` polls run out, the sticky abort word is set and every later wait
+// of the workgroup returns at once, so the kernel always terminates; the
+// kernel then skips its output stores and reports the timeout (status_fail).
+__device__ __forceinline__ void lds_wait_geq(GP_LDS int* c, int target, GP_LDS int* abort, int limit) {
   compiler_fence();
   for (int it = 0;; ++it) {
     if (lds_load_relaxed(c) >= target || lds_load_relaxed(abort) != 0) break;
-    if (it == kSpinLimit) {
+    if (it >= limit) {
       __hip_atomic_store((int*)abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       break;
     }
@@ -102,10 +114,11 @@ __device__ __forceinline__ void lds_wait_geq(GP_LDS int* c, int target, GP_LDS i
 
 // Barrier among the `nw` waves that share counter c; `gen` is this wave's
 // running target (starts at 0, advanced by nw per barrier).
-__device__ __forceinline__ void group_barrier(GP_LDS int* c, int& gen, int nw, int lane, GP_LDS int* abort) {
+__device__ __forceinline__ void group_barrier(GP_LDS int* c, int& gen, int nw, int lane, GP_LDS int* abort,
+                                              int limit) {
   gen += nw;
   lds_signal(c, lane);
-  lds_wait_geq(c, gen, abort);
+  lds_wait_geq(c, gen, abort, limit);
 }
 
 // 16-byte global->LDS copy.  Lane i of the wave writes LDS bytes

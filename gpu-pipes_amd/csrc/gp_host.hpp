@@ -27,16 +27,28 @@ int pipe_route_run(int64_t M, const void* x, void* out, void* out2, int route, i
                    hipStream_t stream);
 
 // Queue arenas, one per (device, stream), zeroed when allocated and when the
-// queue layout changes; each call returns a new launch epoch.  arena_last
-// returns the arena and epoch of the last call.
+// queue layout changes; each call returns a new launch epoch.
 constexpr uint32_t kArenaLayoutMgn = 1;    // mgn_pipelined Queues
 constexpr uint32_t kArenaLayoutRoute = 2;  // route kernels (+1 for the split layout)
 int arena_acquire(int dev, hipStream_t stream, size_t bytes, uint32_t layout, void** base, uint32_t* epoch);
-int arena_last(int dev, hipStream_t stream, void** base, uint32_t* epoch);
 
 // Scratch memory of the wide operators, one per (device, stream), grown on
 // demand (a grow synchronises the stream); contents are not preserved.
 int workspace_acquire(int dev, hipStream_t stream, size_t bytes, void** base);
+
+// Launch status (status.hip).  status_acquire gives a launch on (dev, stream)
+// its device status word and a new epoch, and records it as the stream's last
+// reporting launch; status_note records a word kept elsewhere (the pipelined
+// kernels' arena); status_last returns the stream's last record, which
+// gp_pipeline_check reads.  A word reads as a failure of the launch when its
+// high 32 bits equal the launch's epoch and its low bits are non-zero.
+int status_acquire(int dev, hipStream_t stream, unsigned long long** word, uint32_t* epoch);
+void status_note(int dev, hipStream_t stream, unsigned long long* word, uint32_t epoch);
+int status_last(int dev, hipStream_t stream, unsigned long long** word, uint32_t* epoch);
+// Poll bound of the device-side waits of later launches: the test hook
+// gp_set_wait_limit's value, or dflt when none is set.
+long long wait_limit(long long dflt);
+void set_wait_limit(long long polls);
 
 bool aligned16(const void* p);
 

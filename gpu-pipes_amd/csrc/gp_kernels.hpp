@@ -30,6 +30,11 @@ struct MgnArgs {
   const void* src = nullptr;
   const void* dst = nullptr;
   int idx_bytes = 0;  // 4 (int32) or 8 (int64)
+  // Launch status word and epoch (status_acquire) and the poll bound of the
+  // kernel's waits (0: the default).
+  unsigned long long* status = nullptr;
+  uint32_t epoch = 0;
+  int spin_limit = 0;
 };
 
 // Persistent fused kernel (all layers in one workgroup per CU).

@@ -80,6 +80,12 @@ struct Params {
   int64_t N;
   const void* src;
   const void* dst;
+  // Launch status: a wait that runs out of its `spin_limit` polls aborts the
+  // workgroup, which then skips its output stores and records the timeout in
+  // *status for this launch's epoch (gp_pipeline_check reports it).
+  unsigned long long* status;
+  uint32_t epoch;
+  int spin_limit;
 };
 
 // LDS synchronisation words (monotonic counters, one count per wave per tile).
@@ -284,6 +290,7 @@ void mgn_fused_kernel(Params p) {
   const int fq = 32 * n + 4 * lh;  // 32x32 accumulator group g covers features fq + 8g + (0..3)
   const int arow0 = lr * ACT_STRIDE, arow1 = (32 + lr) * ACT_STRIDE;
   GP_LDS int* const ab = (GP_LDS int*)&sy.abort;
+  const int lim = p.spin_limit;
   constexpr int NS1 = K / 64;
 
   if (stage_a) {
@@ -385,7 +392,7 @@ void mgn_fused_kernel(Params p) {
         index_copy(1, 1);
       }
       wait_vmcnt<0>();
-      group_barrier((GP_LDS int*)&sy.a_bar, abar0, 4, lane, ab);
+      group_barrier((GP_LDS int*)&sy.a_bar, abar0, 4, lane, ab, lim);
       gather_offsets(0);
       const __amdgpu_buffer_rsrc_t rsrc = tile_rsrc(0);
 #pragma unroll
@@ -402,7 +409,7 @@ void mgn_fused_kernel(Params p) {
       // every A wave and every A wave is done with tile k-1, whose buffer is
       // refilled with X(k+1) at once.
       wait_vmcnt<0>();
-      group_barrier((GP_LDS int*)&sy.a_bar, abar, 4, lane, ab);
+      group_barrier((GP_LDS int*)&sy.a_bar, abar, 4, lane, ab, lim);
       // Layer 1; the copies of X(k+1) into xnext are issued between its
       // MFMAs, so a busy memory pipeline stalls the copies, not the MFMAs.
       // (Gather: tile k+1's indices landed with X(k); tile k+2's are copied
@@ -423,7 +430,7 @@ void mgn_fused_kernel(Params p) {
       });
 
       // Handoff slot k%2 was last read by stage B for tile k-2.
-      if (k >= 2) lds_wait_geq((GP_LDS int*)&sy.h_free, 4 * (k - 1), ab);
+      if (k >= 2) lds_wait_geq((GP_LDS int*)&sy.h_free, 4 * (k - 1), ab, lim);
       store_relu_row(hand + arow0, fq, acc0);
       store_relu_row(hand + arow1, fq, acc1);
       lds_signal((GP_LDS int*)&sy.h_full, lane);
@@ -469,7 +476,7 @@ void mgn_fused_kernel(Params p) {
     __builtin_amdgcn_s_setprio(1);
 
     auto tile_b = [&](GP_LDS char* hand, int k) {
-      lds_wait_geq((GP_LDS int*)&sy.h_full, 4 * (k + 1), ab);
+      lds_wait_geq((GP_LDS int*)&sy.h_full, 4 * (k + 1), ab, lim);
 
       // layer 2, features [32n, 32n+32) of all 64 rows, from the handoff tile
       f16x acc0 = bias_frag(prm[1], fq), acc1 = acc0;
@@ -479,11 +486,11 @@ void mgn_fused_kernel(Params p) {
       lds_signal((GP_LDS int*)&sy.h_free, lane);  // B operands are in registers: release the slot
 
       // exchange: act2 was last read (layer 3) for tile k-1
-      if (k >= 1) lds_wait_geq((GP_LDS int*)&sy.x2_free, 4 * k, ab);
+      if (k >= 1) lds_wait_geq((GP_LDS int*)&sy.x2_free, 4 * k, ab, lim);
       store_relu_row((GP_LDS char*)act2 + arow0, fq, acc0);
       store_relu_row((GP_LDS char*)act2 + arow1, fq, acc1);
       lds_signal((GP_LDS int*)&sy.x2_full, lane);
-      lds_wait_geq((GP_LDS int*)&sy.x2_full, 4 * (k + 1), ab);
+      lds_wait_geq((GP_LDS int*)&sy.x2_full, 4 * (k + 1), ab, lim);
 
       // layer 3, all features of rows [16n, 16n+16)
       h8 bf[4];
@@ -500,6 +507,8 @@ void mgn_fused_kernel(Params p) {
 
       const int64_t grow = (t0 + (int64_t)k * G) * TM + 16 * n + l16;
       half_t* const orow = p.out + grow * D;
+      // After a timed-out wait the tile's inputs are not trustworthy: store nothing.
+      const bool st = grow < M && lds_load_relaxed(ab) == 0;
       if constexpr (LN) {
         // Lanes l16, l16+16, l16+32, l16+48 hold the row's 128 features.
         float s = 0.f;
@@ -529,13 +538,13 @@ void mgn_fused_kernel(Params p) {
             for (int e = 0; e < 4; ++e) z[e] = __builtin_fmaf(__builtin_fmaf(y[fb][e], rstd, nmr), gm[e], bt[e]);
             hv[t] = __builtin_convertvector(z, h4);
           }
-          store_row_pair(orow, hv, j, q4, grow < M);
+          store_row_pair(orow, hv, j, q4, st);
         }
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const h4 hv[2] = {__builtin_convertvector(y[2 * j], h4), __builtin_convertvector(y[2 * j + 1], h4)};
-          store_row_pair(orow, hv, j, q4, grow < M);
+          store_row_pair(orow, hv, j, q4, st);
         }
       }
     };
@@ -545,6 +554,9 @@ void mgn_fused_kernel(Params p) {
       if (k + 1 < nt) tile_b((GP_LDS char*)hand1, k + 1);
     }
   }
+  // The abort word is sticky and is set before the wave that set it gets
+  // here, so the workgroup's timeout is reported at least once.
+  if (lds_load_relaxed(ab) != 0 && lane == 0) status_fail(p.status, p.epoch, kErrTimeout);
 }
 
 }  // namespace fused
@@ -556,12 +568,14 @@ template <int K, bool LN, int GI = 0>
 static hipError_t launch_fused(const MgnArgs& a, int grid, hipStream_t stream) {
   fused::Params p{(const half_t*)a.x,  (const half_t*)a.w1, (const half_t*)a.b1, (const half_t*)a.w2,
                   (const half_t*)a.b2, (const half_t*)a.w3, (const half_t*)a.b3, (const half_t*)a.gamma,
-                  (const half_t*)a.beta, (half_t*)a.out, a.M, a.eps, (const half_t*)a.nf, a.N, a.src, a.dst};
+                  (const half_t*)a.beta, (half_t*)a.out, a.M, a.eps, (const half_t*)a.nf, a.N, a.src, a.dst,
+                  a.status, a.epoch, a.spin_limit > 0 ? a.spin_limit : kSpinLimit};
   hipLaunchKernelGGL((fused::mgn_fused_kernel<K, LN, GI>), dim3(grid), dim3(fused::NTHREADS), 0, stream, p);
   return hipGetLastError();
 }
 
 hipError_t mgn_fused_launch(const MgnArgs& a, int num_cus, hipStream_t stream) {
+  if (a.status == nullptr) return hipErrorInvalidValue;  // every launch reports to a status word
   const int64_t ntiles = (a.M + fused::TM - 1) / fused::TM;
   const int grid = (int)(ntiles < num_cus ? ntiles : num_cus);
   const bool ln = a.gamma != nullptr;

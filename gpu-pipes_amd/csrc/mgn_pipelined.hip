@@ -9,8 +9,9 @@
 // (mlp0_sm0 :83-101, mlp1_sm0 :146-160, mlp2_sm0 :162-181, ln_sm :183-203).
 //
 // MI355X: stage roles come from the XCD-aware assignment (pipeline.hpp), so
-// every queue's producer and consumer share an L2; the launch is cooperative
-// (all workgroups resident, as spin-waiting stages require); pipelines take
+// every queue's producer and consumer share an L2; the grid is sized to the
+// occupancy limit so that all workgroups are resident, as spin-waiting stages
+// require (pipeline.hpp); pipelines take
 // tiles g, g+P, ... of any M, with the partial last tile carried by the
 // queue's row count.  Stage bodies are the library's stage functions.
 #include <hip/hip_runtime.h>
@@ -107,10 +108,11 @@ static int run(const MgnArgs& m, int dev, int num_cus, hipStream_t s) {
   a.m = m;
   a.ctl = (PipeCtl*)base;
   a.queues = (Queues*)((char*)base + sizeof(PipeCtl));
-  a.ctx = QueueCtx{epoch, &a.ctl->err.v};
-  void* args[] = {&a};
-  e = hipLaunchCooperativeKernel((const void*)kern, dim3(grid), dim3(kStageThreads), args, lds, s);
-  if (e != hipSuccess) return fail_hip(e, "mgn_pipelined cooperative launch");
+  a.ctx = QueueCtx{epoch, &a.ctl->err.v, (int)wait_limit(kQueueSpinLimit)};
+  status_note(dev, s, &a.ctl->err.v, epoch);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kStageThreads), lds, s, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return fail_hip(e, "mgn_pipelined launch");
   return GP_OK;
 }
 

@@ -6,9 +6,15 @@
 // and a ring queue is only coherent through L2 when producer and consumer sit
 // on the same XCD.  So roles are not derived from blockIdx: every workgroup
 // reads its hardware XCC id, takes a ticket from its XCD's counter, and after
-// a grid-wide barrier (the launch is cooperative, so all workgroups are
-// resident) the tickets of each XCD are cut into whole pipelines of S stage
-// workgroups.  Workgroups left over on an XCD stay idle.
+// a grid-wide barrier the tickets of each XCD are cut into whole pipelines of
+// S stage workgroups.  Workgroups left over on an XCD stay idle.
+//
+// Stages spin on each other, so every workgroup of a launch must be resident
+// at once.  The launchers size the grid to the occupancy limit (workgroups
+// per CU x CUs) and launch normally: on an otherwise idle GPU the whole grid
+// is resident.  If it is not (other work holds CUs), the grid barrier's
+// bounded wait runs out, every workgroup leaves with the launch's timeout
+// bit set, and gp_pipeline_check reports it.
 #pragma once
 
 #include "pipes.hpp"
@@ -24,9 +30,6 @@ struct PipeCtl {
   QCounter arrive;        // grid barrier
   QCounter err;           // (epoch << 32) | error bits of the launch (QueueCtx::err)
 };
-
-// gp_pipeline_check (capi.cpp) reads `err` at this offset.
-static_assert(__builtin_offsetof(PipeCtl, err) == 17 * 128, "PipeCtl layout is shared with the host");
 
 struct Role {
   int pipe;    // global pipeline index, or -1 when idle
@@ -68,7 +71,7 @@ __device__ inline Role assign_role(PipeCtl* ctl, int S, const QueueCtx& ctx, int
     for (int it = 0;; ++it) {
       const unsigned long long v = __hip_atomic_load(&ctl->arrive.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (qcount(v, ctx.epoch) >= gridDim.x) break;
-      if (it == kQueueSpinLimit) {
+      if (it >= ctx.limit) {
         q_fail(ctx, kErrTimeout);
         ok = false;
         break;

@@ -48,10 +48,10 @@ struct TensorView {
 struct QueueCtx {
   uint32_t epoch;            // launch epoch (never 0)
   unsigned long long* err;   // (epoch << 32) | error bits; bits of this epoch abort all waits
+  int limit;                 // polls before a wait gives up (kQueueSpinLimit unless a test lowers it)
 };
 
-constexpr int kQueueSpinLimit = 1 << 22;  // polls of ~1 us before a wait gives up
-constexpr unsigned kErrTimeout = 1;
+constexpr int kQueueSpinLimit = 1 << 22;  // default: polls of ~1 us before a wait gives up
 constexpr unsigned kErrNoPipes = 2;  // the launch held no complete pipeline
 
 __device__ __forceinline__ bool q_aborted(const QueueCtx& c) {
@@ -59,11 +59,7 @@ __device__ __forceinline__ bool q_aborted(const QueueCtx& c) {
   return (uint32_t)(v >> 32) == c.epoch && (uint32_t)v != 0;
 }
 
-__device__ __forceinline__ void q_fail(const QueueCtx& c, unsigned bits) {
-  __hip_atomic_fetch_max(c.err, (unsigned long long)c.epoch << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __builtin_amdgcn_s_waitcnt(kWaitAll);
-  __hip_atomic_fetch_or(c.err, (unsigned long long)bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+__device__ __forceinline__ void q_fail(const QueueCtx& c, unsigned bits) { status_fail(c.err, c.epoch, bits); }
 
 struct alignas(128) QCounter {
   unsigned long long v;  // (epoch << 32) | count
@@ -98,7 +94,7 @@ __device__ __forceinline__ bool qwait(QCounter* c, uint32_t target, const QueueC
         r = 0;
         break;
       }
-      if (it == kQueueSpinLimit) {
+      if (it >= ctx.limit) {
         q_fail(ctx, kErrTimeout);
         r = 0;
         break;
@@ -167,11 +163,13 @@ struct RingQueue {
     if (threadIdx.x == 0) qcommit(&s.full, ctx.epoch);
   }
   // Wait until all NP producers of `seq` have committed; returns the payload.
+  // After an aborted wait the slot holds no tile of this launch: the view has
+  // no rows, so the consumer stores nothing for it.
   __device__ Entry* read_wait(int64_t seq, int* rows, const QueueCtx& ctx) {
     QueueSlot<Entry>& s = slot(seq);
-    qwait(&s.full, (uint32_t)(seq / N + 1) * NP, ctx);
+    const bool ok = qwait(&s.full, (uint32_t)(seq / N + 1) * NP, ctx);
     l1_invalidate();
-    *rows = *(volatile int*)&s.rows;
+    *rows = ok ? *(volatile int*)&s.rows : 0;
     return &s.data;
   }
   __device__ void read_commit(int64_t seq, const QueueCtx& ctx) {

@@ -371,11 +371,12 @@ static int route_launch(int64_t M, const void* x, void* out, void* out2, int max
   a.M = M;
   a.ctl = (PipeCtl*)base;
   a.queues = (RouteQueues*)((char*)base + sizeof(PipeCtl));
-  a.ctx = QueueCtx{epoch, &a.ctl->err.v};
+  a.ctx = QueueCtx{epoch, &a.ctl->err.v, (int)wait_limit(kQueueSpinLimit)};
+  status_note(dev, s, &a.ctl->err.v, epoch);
   a.max_pipes = max_pipes;
-  void* args[] = {&a};
-  e = hipLaunchCooperativeKernel((const void*)kern, dim3(grid), dim3(kStageThreads), args, 0, s);
-  if (e != hipSuccess) return fail_hip(e, "route_kernel cooperative launch");
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kStageThreads), 0, s, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return fail_hip(e, "route_kernel launch");
   return GP_OK;
 }
 

@@ -24,7 +24,7 @@ __all__ = [
     "lib", "mgn_fullmlp", "mgn_fullmlp_out", "mgn_linears", "mgn_linears_out",
     "mgn_mlp", "mgn_mlp_out", "IMPL_FUSED", "IMPL_PIPELINED", "IMPL_PIPELINED_SPLIT_LN", "GpipesError",
     "linear_out", "linear_layer_norm_out", "layer_norm_out", "add_out", "concat_out", "pipe_ident",
-    "pipeline_check", "ACTS", "mgn_edge_gather", "mgn_edge_gather_out", "pipe_route", "ROUTES",
+    "pipeline_check", "set_wait_limit", "ACTS", "mgn_edge_gather", "mgn_edge_gather_out", "pipe_route", "ROUTES",
     "gemm_out", "bert_ffn", "bert_ffn_out", "mlp_out", "dlrm_botmlp", "dlrm_botmlp_out", "dlrm_topmlp",
     "dlrm_topmlp_out", "nerf_full", "nerf_full_out",
 ]
@@ -73,6 +73,8 @@ def _load():
     L.gp_pipe_route.argtypes = [i64, vp, vp, vp, i32, i32, vp]
     L.gp_pipe_route.restype = i32
     L.gp_pipeline_check.argtypes = [vp]
+    L.gp_set_wait_limit.argtypes = [i64]
+    L.gp_set_wait_limit.restype = i32
     L.gp_mgn_edge_gather_out.argtypes = [i64, i64, vp, vp, vp, vp, i32] + [vp] * 8 + [f32, vp, vp]
     L.gp_mgn_edge_gather_out.restype = i32
     L.gp_gemm_out.argtypes = [i64, i64, i64, vp, vp, vp, vp, i32, vp, vp]
@@ -305,10 +307,17 @@ def pipe_route(x, route="ident", max_pipes=0):
 
 
 def pipeline_check(device=None):
-    """Wait for the current stream; raise GpipesError if its last pipelined launch timed out."""
+    """Wait for the current stream; raise GpipesError (code -5) if its last launch that
+    reports device-side failures (the MGN MLPs, the gather front end, the pipes) timed out."""
     dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
     with torch.cuda.device(dev):
         _check(lib.gp_pipeline_check(ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
+
+
+def set_wait_limit(polls):
+    """Test hook: bound the device-side waits of later launches to ``polls`` polls (0: the
+    defaults), so that a launch times out and reports it while its kernels still end."""
+    _check(lib.gp_set_wait_limit(int(polls)))
 
 
 def mgn_edge_gather_out(nf, ef, src, dst, w1, b1, w2, b2, w3, b3, gamma, beta, out, eps=1e-5):

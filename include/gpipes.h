@@ -28,9 +28,10 @@ extern "C" {
 #define GP_ERR_SHAPE (-2)       /* a dimension the kernels do not support      */
 #define GP_ERR_ALIGN (-3)       /* pointer not 16-byte aligned                 */
 #define GP_ERR_HIP (-4)         /* HIP runtime / launch failure                */
-#define GP_ERR_TIMEOUT (-5)     /* a pipelined launch failed on the device: a   */
-                                /* queue wait exceeded its spin bound, or no    */
-                                /* pipeline fitted on one XCD                   */
+#define GP_ERR_TIMEOUT (-5)     /* a launch failed on the device: a wait       */
+                                /* exceeded its poll bound (its outputs are not */
+                                /* valid), or no pipeline fitted on one XCD;    */
+                                /* reported by gp_pipeline_check                */
 #define GP_ERR_NO_DEVICE (-6)   /* no usable gfx950 device                     */
 
 /* Implementation selector for gp_mgn_mlp_out. */
@@ -258,13 +259,29 @@ int gp_pipe_ident(int64_t M, const void* x, void* out, int max_pipes, void* stre
 int gp_pipe_route(int64_t M, const void* x, void* out, void* out2, int route, int max_pipes, void* stream);
 
 /*
- * Waits for `stream`, then reports whether the last pipelined launch on it
- * (GP_IMPL_PIPELINED*, gp_pipe_ident) failed on the device (GP_ERR_TIMEOUT: a
- * queue wait timed out, or no pipeline's workgroups shared an XCD) or
- * completed (GP_OK).  The reference has no such check:
- * a stuck queue spins forever (common/mpmcq.cuh:83,104).
+ * Waits for `stream`, then reports whether the last launch on it that
+ * reports device-side failures failed (GP_ERR_TIMEOUT) or completed (GP_OK).
+ * Those are the launches of gp_mgn_fullmlp_out, gp_mgn_linears_out,
+ * gp_mgn_mlp_out (every impl), gp_mgn_edge_gather_out, gp_pipe_ident and
+ * gp_pipe_route: every wait between their workgroups or waves is bounded, and
+ * one that runs out makes the launch end early and leave its outputs invalid
+ * (the fused kernels store nothing after it).  The pipelined layouts also fail
+ * when no pipeline's workgroups shared an XCD.  GP_ERR_INVALID_ARG if no such
+ * launch was made on this stream.  The reference has no such check: a stuck
+ * queue spins forever (common/mpmcq.cuh:83,104).
  */
 int gp_pipeline_check(void* stream);
+
+/*
+ * Test hook: bounds every device-side wait of later launches (of the entry
+ * points gp_pipeline_check covers) to `polls` polls; 0 restores the defaults
+ * (2^20 polls of about 0.1 us for the waits inside a fused kernel's
+ * workgroup, 2^22 polls of about 1 us for the queue waits between
+ * workgroups).  A tiny bound makes those launches time out, so that a caller
+ * can check its handling of GP_ERR_TIMEOUT with kernels that still end
+ * normally.  Process-wide.  No counterpart in the reference.
+ */
+int gp_set_wait_limit(int64_t polls);
 
 #ifdef __cplusplus
 }
