@@ -112,5 +112,8 @@ size_t nerf_fused_workspace();
 hipError_t nerf_fused_launch(int64_t M, int Kx, int Kd, int Na, int Nrgb, const void* x, const void* d,
                              const void* const* w, const void* const* b, int rgb_act, void* out_r, void* out_rgb,
                              void* ws, int num_cus, hipStream_t stream);
+// Device address and size of the NeRF kernel's static scratch on device `dev`
+// (the current device), for the allocation-free entry point.
+int nerf_static_scratch(int dev, void** ptr, size_t* bytes);
 
 }  // namespace gp

@@ -203,10 +203,9 @@ int gp_dlrm_topmlp_out(int64_t M, int64_t K0, int64_t N5, const void* x, const v
   return gp_mlp_out(M, 5, widths, w, b, acts, x, out, stream);
 }
 
-int gp_nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb, const void* x, const void* d,
-                     const void* const* w, const void* const* b, int rgb_act, void* out_r, void* out_rgb,
-                     void* stream) {
-  clear_error();
+// Argument checks shared by both NeRF entry points.
+static int nerf_checks(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb, const void* x, const void* d,
+                       const void* const* w, const void* const* b, int rgb_act, void* out_r, void* out_rgb) {
   int rc = common_checks(M, x, out_r);
   if (rc) return rc;
   if (M > 0 && (!d || !out_rgb)) return fail(GP_ERR_INVALID_ARG, "d and out_rgb must be non-NULL when M > 0");
@@ -216,6 +215,15 @@ int gp_nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb
   for (int i = 0; i < 12; ++i)
     if (!w[i]) return fail(GP_ERR_INVALID_ARG, "weight %d is NULL", i + 1);
   if (!act_ok(rgb_act)) return fail(GP_ERR_INVALID_ARG, "unknown activation %d", rgb_act);
+  return GP_OK;
+}
+
+int gp_nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb, const void* x, const void* d,
+                     const void* const* w, const void* const* b, int rgb_act, void* out_r, void* out_rgb,
+                     void* stream) {
+  clear_error();
+  int rc = nerf_checks(M, Kx, Kd, Na, Nrgb, x, d, w, b, rgb_act, out_r, out_rgb);
+  if (rc) return rc;
   if (M == 0) return GP_OK;
   int dev = 0, ncu = 0;
   if ((rc = current_device_info(&dev, &ncu))) return rc;
@@ -309,6 +317,35 @@ int gp_nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb
       e = place_launch(rows, hd, np12, Nrgb, (void*)row_ptr(out_rgb, r0, Nrgb), Nrgb, Nrgb, GP_ACT_NONE, ncu, s);
     if (e != hipSuccess) return fail_hip(e, "NeRF layer launch");
   }
+  return GP_OK;
+}
+
+int gp_nerf_full_out_noalloc(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb, const void* x,
+                             const void* d, const void* const* w, const void* const* b, int rgb_act, void* out_r,
+                             void* out_rgb, void* stream) {
+  clear_error();
+  int rc = nerf_checks(M, Kx, Kd, Na, Nrgb, x, d, w, b, rgb_act, out_r, out_rgb);
+  if (rc) return rc;
+  if (!nerf_fused_supported(Kx, Kd, Na, Nrgb))
+    return fail(GP_ERR_SHAPE,
+                "the allocation-free NeRF call runs the fused kernel only, whose scratch is fixed: Kx <= 64, "
+                "Kd <= 32, Na <= 64, Nrgb <= 64 (got %lld, %lld, %lld, %lld); use gp_nerf_full_out",
+                (long long)Kx, (long long)Kd, (long long)Na, (long long)Nrgb);
+  if (M == 0) return GP_OK;
+  if (M > (int64_t(1) << 31) - 1) return fail(GP_ERR_SHAPE, "M must be < 2^31 (got %lld)", (long long)M);
+  if (!aligned16(x) || !aligned16(d))
+    return fail(GP_ERR_ALIGN, "x and d must be 16-byte aligned (the allocation-free call cannot copy them)");
+  int dev = 0, ncu = 0;
+  if ((rc = current_device_info(&dev, &ncu))) return rc;
+  void* ws = nullptr;
+  size_t bytes = 0;
+  if ((rc = nerf_static_scratch(dev, &ws, &bytes))) return rc;
+  if (bytes < nerf_fused_workspace())
+    return fail(GP_ERR_SHAPE, "static scratch of %zu bytes is below the %zu the kernel needs", bytes,
+                nerf_fused_workspace());
+  hipError_t e = nerf_fused_launch(M, (int)Kx, (int)Kd, (int)Na, (int)Nrgb, x, d, w, b, rgb_act, out_r, out_rgb, ws,
+                                   ncu, (hipStream_t)stream);
+  if (e != hipSuccess) return fail_hip(e, "NeRF fused kernel launch");
   return GP_OK;
 }
 

@@ -52,7 +52,11 @@
 #include <utility>
 
 #include "../../include/gpipes.h"
+#include <mutex>
+
+#include "../../include/gpipes.h"
 #include "gp_device.hpp"
+#include "gp_host.hpp"
 #include "gp_kernels.hpp"
 #include "stages.hpp"
 
@@ -530,6 +534,35 @@ __global__ __launch_bounds__(256) void nerf_pack_kernel(PackArgs a) {
 }  // namespace nerf
 
 size_t nerf_fused_workspace() { return (size_t)nerf::S_TOTAL * nerf::SLOT + (size_t)nerf::B_TOTAL * 2; }
+
+// Scratch of the allocation-free entry point (gp_nerf_full_out_noalloc): the
+// packed weight stream and bias tables, in a file-scope device array instead
+// of the per-stream workspace.  Every GPU the library runs on holds its own
+// copy until the process ends.  The packing kernel rewrites every byte the
+// fused kernel reads on each call, so nothing has to start at zero; calls that
+// overlap on one GPU share the array and race.
+constexpr size_t kNerfScratchBytes =
+    ((size_t)nerf::S_TOTAL * nerf::SLOT + (size_t)nerf::B_TOTAL * 2 + 255) & ~size_t(255);
+static __device__ __align__(256) char scratch[kNerfScratchBytes];
+
+int nerf_static_scratch(int dev, void** ptr, size_t* bytes) {
+  // In host code `scratch` names a host-side stand-in, never the device
+  // memory: its device address is looked up once per device (with that device
+  // current) and only that address is handed to kernels.
+  static std::mutex mu;
+  static void* dev_ptr[64];
+  if (dev < 0 || dev >= 64) return fail(GP_ERR_NO_DEVICE, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lk(mu);
+  if (dev_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return fail_hip(e, "hipGetSymbolAddress (NeRF static scratch)");
+    dev_ptr[dev] = p;
+  }
+  *ptr = dev_ptr[dev];
+  *bytes = kNerfScratchBytes;
+  return GP_OK;
+}
 
 bool nerf_fused_supported(int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb) {
   return Kx >= 1 && Kx <= 64 && Kd >= 1 && Kd <= 32 && Na >= 1 && Na <= 64 && Nrgb >= 1 && Nrgb <= 64;

@@ -26,7 +26,7 @@ __all__ = [
     "linear_out", "linear_layer_norm_out", "layer_norm_out", "add_out", "concat_out", "pipe_ident",
     "pipeline_check", "set_wait_limit", "ACTS", "mgn_edge_gather", "mgn_edge_gather_out", "pipe_route", "ROUTES",
     "gemm_out", "bert_ffn", "bert_ffn_out", "mlp_out", "dlrm_botmlp", "dlrm_botmlp_out", "dlrm_topmlp",
-    "dlrm_topmlp_out", "nerf_full", "nerf_full_out",
+    "dlrm_topmlp_out", "nerf_full", "nerf_full_out", "nerf_full_out_noalloc",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -83,6 +83,8 @@ def _load():
     L.gp_dlrm_botmlp_out.argtypes = [i64, i64] + [vp] * 9
     L.gp_dlrm_topmlp_out.argtypes = [i64, i64, i64] + [vp] * 11 + [i32, vp, vp]
     L.gp_nerf_full_out.argtypes = [i64] * 5 + [vp] * 4 + [i32, vp, vp, vp]
+    L.gp_nerf_full_out_noalloc.argtypes = [i64] * 5 + [vp] * 4 + [i32, vp, vp, vp]
+    L.gp_nerf_full_out_noalloc.restype = i32
     for name in ("gp_mlp_out", "gp_dlrm_botmlp_out", "gp_dlrm_topmlp_out", "gp_nerf_full_out", "gp_gemm_out",
                  "gp_bert_ffn_out", "gp_linear_out", "gp_linear_layer_norm_out", "gp_layer_norm_out", "gp_add_out",
                  "gp_concat_out", "gp_pipe_ident", "gp_pipeline_check"):
@@ -501,6 +503,26 @@ def nerf_full_out(x, d, *wb_and_outs, rgb_act="none"):
     with torch.cuda.device(x.device):
         _check(lib.gp_nerf_full_out(M, Kx, Kd, Na, Nrgb, _ptr(x), _ptr(d), wp, bp, ACTS.get(rgb_act, rgb_act),
                                     _ptr(out_r), _ptr(out_rgb), _stream(x)))
+    return out_r, out_rgb
+
+
+def nerf_full_out_noalloc(x, d, *wb_and_outs, rgb_act="none"):
+    """nerf_full_out through the allocation-free entry point (gp_nerf_full_out_noalloc): the
+    fused kernel's shapes only (Kx <= 64, Kd <= 32, Na <= 64, Nrgb <= 64), x and d 16-byte
+    aligned; its scratch is a static per-GPU array, so calls that overlap on one GPU race."""
+    if len(wb_and_outs) != 26:
+        raise RuntimeError("expected w1, b1, ..., w12, b12, out_r, out_rgb")
+    ws, bs = list(wb_and_outs[0:24:2]), list(wb_and_outs[1:24:2])
+    out_r, out_rgb = wb_and_outs[24], wb_and_outs[25]
+    for name, t in (("x", x), ("d", d), ("out_r", out_r), ("out_rgb", out_rgb)):
+        _check_input(name, t)
+    M, Kx = x.shape
+    _same_device(x, d, out_r, out_rgb, *ws, *bs)
+    wp = (ctypes.c_void_p * 12)(*[w.data_ptr() for w in ws])
+    bp = (ctypes.c_void_p * 12)(*[0 if b is None else b.data_ptr() for b in bs])
+    with torch.cuda.device(x.device):
+        _check(lib.gp_nerf_full_out_noalloc(M, Kx, d.shape[1], out_r.shape[1], out_rgb.shape[1], _ptr(x), _ptr(d), wp,
+                                            bp, ACTS.get(rgb_act, rgb_act), _ptr(out_r), _ptr(out_rgb), _stream(x)))
     return out_r, out_rgb
 
 

@@ -175,6 +175,22 @@ int gp_nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb
                      const void* const* w, const void* const* b, int rgb_act, void* out_r, void* out_rgb,
                      void* stream);
 
+/*
+ * gp_nerf_full_out without any allocation: no reference counterpart.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments and
+ * results as gp_nerf_full_out (bit-identical: the same kernels), limited to
+ * the fused kernel's shapes (Kx <= 64, Kd <= 32, Na <= 64, Nrgb <= 64) and to
+ * 16-byte aligned x and d; other shapes are rejected with GP_ERR_SHAPE /
+ * GP_ERR_ALIGN.  Its scratch (the packed weight stream, 1,255,168 bytes) is a
+ * static device array that every GPU the library runs on holds until the
+ * process ends; every call on a GPU shares it, so calls that overlap on one
+ * GPU race.  Calls no hipMalloc, hipFree or allocating library routine.
+ */
+int gp_nerf_full_out_noalloc(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb, const void* x,
+                             const void* d, const void* const* w, const void* const* b, int rgb_act, void* out_r,
+                             void* out_rgb, void* stream);
+
 /* ------------------------------------------------------------------------
  * Stage-level entry points: one stage function of the library run over a
  * whole matrix (tiles of 128 rows, persistent workgroups).
