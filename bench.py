@@ -265,7 +265,13 @@ DLRM_TOP = [480, 1024, 1024, 512, 256, 1]
 CHAIN_METRIC = {
     "dlrm": "rows/sec + % fp16 MFMA peak, DLRM bottom+top MLPs M=262144 (1×MI355X)",
     "nerf": "samples/sec + % fp16 MFMA peak, NeRF full MLP M=1048576 (1×MI355X)",
+    "bert_addln": "rows/sec + % fp16 MFMA peak, bert_addln_ffn H=128 FF=512 M=32768 (1×MI355X)",
+    "nerf_a": "samples/sec + % fp16 MFMA peak, NerfA trunk M=65536 (1×MI355X)",
 }
+# The reference apps' own batches: apps/bert_addln_ffn/pipelined/perf.py (64 x 512 rows)
+# and apps/nerf_a/pipelined/val.py (65,536 samples).
+ADDLN = {"M": 64 * 512, "H": 128, "FF": 512}
+NERF_A = {"M": 65536, "Kx": 64}
 
 
 def chain_flops(widths):
@@ -278,7 +284,8 @@ NERF_FLOPS = 2 * (64 * 256 + 4 * 256 * 256 + 320 * 256 + 2 * 256 * 256 + 256 * 1
 def cpu_baseline_chain(workload, budget_s=10.0):
     """The CPU oracle (oracle.mlp / oracle.nerf over oracle/oracle.c) on a row sample."""
     import oracle
-    from gpipes.synth import dlrm_params, nerf_inputs, nerf_params, padded_normal, padded_uniform
+    from gpipes.synth import (bert_addln_params, dlrm_params, nerf_a_params, nerf_inputs, nerf_params, normal_fp16,
+                              padded_normal, padded_uniform)
 
     threads, how = host_cores()
     oracle.set_num_threads(threads)
@@ -295,7 +302,7 @@ def cpu_baseline_chain(workload, budget_s=10.0):
             oracle.mlp(xb, wb, bb, [R] * 3)
             oracle.mlp(xt, wt, bt, [R] * 4 + [S])
         what = f"oracle DlrmMlp bottom {DLRM_BOT} + top {DLRM_TOP} fp32 on {Ms} rows"
-    else:
+    elif workload == "nerf":
         Ms = 2048
         ws, bs = nerf_params(64, 27, 1, 3, seed=0)
         x, d = nerf_inputs(Ms, seed=0)
@@ -304,18 +311,38 @@ def cpu_baseline_chain(workload, budget_s=10.0):
         def run():
             oracle.nerf(x, d, ws, bs, oracle.ACT_SIGMOID)
         what = f"oracle Nerf fp32 on {Ms} samples"
+    elif workload == "bert_addln":
+        Ms = 4096
+        p = {k: v.float().numpy() for k, v in bert_addln_params(seed=0).items()}
+        attn, x = (normal_fp16(Ms, 128, seed=i).float().numpy() for i in (0, 1))
+        keys = ("w0", "b0", "w1", "b1", "w2", "b2", "ga0", "be0", "ga2", "be2")
+
+        def run():
+            oracle.bert_addln_ffn(attn, x, *(p[k] for k in keys))
+        what = f"oracle bert_addln_ffn fp32 on {Ms} rows"
+    else:
+        Ms = 2048
+        ws, bs = nerf_a_params(64, seed=0)
+        ws, bs = f(ws), f(bs)
+        x = normal_fp16(Ms, 64, seed=0).float().numpy()
+
+        def run():
+            oracle.nerf_a(x, ws, bs)
+        what = f"oracle NerfA fp32 on {Ms} samples"
     med, n, tot = _median_runs(run, budget_s, min_runs=3, warmups=1)
-    return {"value": Ms / med, "unit": "rows/s" if workload == "dlrm" else "samples/s", "cores": threads,
+    return {"value": Ms / med, "unit": "samples/s" if workload.startswith("nerf") else "rows/s", "cores": threads,
             "kind": "port", "sample": f"{what}, {threads} threads ({how}), median of {n} calls ({tot:.1f} s): "
                                       f"{med * 1e3:.1f} ms"}
 
 
 def bench_chain(args):
-    """configs[3] (DLRM bottom + top MLP, M = 262,144) or configs[4] (NeRF, M = 1,048,576)."""
+    """configs[3] (DLRM bottom + top MLP, M = 262,144), configs[4] (NeRF, M = 1,048,576), or the
+    bert_addln_ffn / nerf_a apps at their reference batches."""
     import torch
 
     import gpipes
-    from gpipes.synth import dlrm_params, nerf_inputs, nerf_params, padded_normal, padded_uniform
+    from gpipes.synth import (bert_addln_params, dlrm_params, nerf_a_params, nerf_inputs, nerf_params, normal_fp16,
+                              padded_normal, padded_uniform)
 
     dev = torch.device("cuda:0")
     if args.workload == "dlrm":
@@ -338,6 +365,38 @@ def bench_chain(args):
                   "top": "480(479)-1024-1024-512-256 ReLU, 256-1 sigmoid", "accumulate": "f32", "row_chunk": 262144}
         data = "synthetic (dense U(0,1), top input N(0,1), Xavier-uniform weights, seed 0)"
         unit = "rows/s"
+    elif args.workload == "bert_addln":
+        M, H, FF = ADDLN["M"], ADDLN["H"], ADDLN["FF"]
+        p = {k: v.to(dev) for k, v in bert_addln_params(H, FF, seed=0).items()}
+        attn, x = normal_fp16(M, H, seed=0, device=dev), normal_fp16(M, H, seed=1, device=dev)
+        out = torch.empty_like(x)
+        keys = ("w0", "b0", "w1", "b1", "w2", "b2", "ga0", "be0", "ga2", "be2")
+        impl = "pipelined" if args.impl == "pipelined" else "fused"
+
+        def step(i):
+            gpipes.bert_addln_ffn_out(attn, x, *(p[k] for k in keys), out, impl=impl)
+        flops = 2 * M * (H * H + H * FF + FF * H)
+        bytes_ = M * H * 2 * 3
+        config = {"workload": "bert_addln_ffn", "M": M, "H": H, "FF": FF, "act": "relu", "eps": 1e-5,
+                  "impl": impl, "accumulate": "f32"}
+        data = "synthetic (attn_out, x ~ N(0,1), nn.Linear default init, seed 0)"
+        unit = "rows/s"
+    elif args.workload == "nerf_a":
+        M, Kx = NERF_A["M"], NERF_A["Kx"]
+        ws, bs = nerf_a_params(Kx, seed=0, device=dev)
+        x = normal_fp16(M, Kx, seed=0, device=dev)
+        out = torch.empty((M, 256), dtype=torch.float16, device=dev)
+        wb = [t for pair in zip(ws, bs) for t in pair]
+        impl = "pipelined" if args.impl == "pipelined" else "fused"
+
+        def step(i):
+            gpipes.nerf_a_out(x, *wb, out, impl=impl)
+        flops = 2 * M * (Kx * 256 + 4 * 256 * 256 + (256 + Kx) * 256 + 2 * 256 * 256)
+        bytes_ = M * (Kx + 256) * 2
+        config = {"workload": "nerf_a", "M": M, "Kx": Kx, "layers": "5x256 ReLU, skip concat, 3x256 ReLU",
+                  "impl": impl, "accumulate": "f32"}
+        data = "synthetic (x ~ N(0,1), nn.Linear default init, seed 0)"
+        unit = "samples/s"
     else:
         M = 1048576
         ws, bs = nerf_params(64, 27, 1, 3, seed=0, device=dev)
@@ -357,7 +416,11 @@ def bench_chain(args):
         unit = "samples/s"
     launch = {"dlrm": "one step: per MLP one weight-preparation launch, then a wide-GEMM launch per layer "
                       "(the one-output click head a GEMV launch)",
-              "nerf": "one step: the weight-packing kernel, then the fused 12-layer kernel over 256-row tiles"}
+              "nerf": "one step: the weight-packing kernel, then the fused 12-layer kernel over 256-row tiles",
+              "bert_addln": "one step: one gp_bert_addln_ffn_out call (fused: weight transposes, then GEMM0 + b0 + x, "
+                            "LN0, GEMM1 + act, GEMM2 + b2 + h0, LN2; pipelined: one queue-chained kernel)",
+              "nerf_a": "one step: one gp_nerf_a_out call (fused: weight preparation, input placement and eight "
+                        "GEMM launches; pipelined: one queue-chained kernel)"}
 
     call_ms, ms_per_step, settle = timed_steps(step, args, dev)
     avg_ms = sum(call_ms) / len(call_ms)
@@ -404,7 +467,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["bert", "dlrm", "nerf"], default="edge")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["bert", "dlrm", "nerf", "bert_addln", "nerf_a"],
+                    default="edge")
     ap.add_argument("--impl", choices=["fused", "pipelined", "pipelined_split_ln"], default="fused")
     ap.add_argument("--settle-ms", type=float, default=1000.0,
                     help="untimed launches for this long between the warm-up and the timed region: the "
@@ -424,7 +488,7 @@ def main():
     if args.workload == "bert":
         bench_bert(args)
         return
-    if args.workload in ("dlrm", "nerf"):
+    if args.workload in ("dlrm", "nerf", "bert_addln", "nerf_a"):
         bench_chain(args)
         return
 

@@ -1,5 +1,6 @@
-// C ABI of the wide operators: the GEMM stage with any N / K (gp_gemm_out)
-// and the BERT feed-forward block (gp_bert_ffn_out).
+// C ABI of the wide operators: the GEMM stage with any N / K (gp_gemm_out),
+// the BERT feed-forward block (gp_bert_ffn_out) and the add + LayerNorm + FFN
+// block of the bert_addln_ffn app (gp_bert_addln_ffn_out).
 //
 // The reference's pipelined BERT FFN (apps/bert_ffn/pipelined/bert_ffn_pl.cuh:
 // 79-162) chains GEMM + bias + ReLU -> GEMM + bias with the residual as
@@ -129,6 +130,66 @@ int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void*
     if (e != hipSuccess) return fail_hip(e, "FFN GEMM2 launch");
     e = layer_norm_launch(rows, H, ybuf, gamma, beta, eps, (char*)out + r0 * H * 2, ncu, s);
     if (e != hipSuccess) return fail_hip(e, "FFN LayerNorm launch");
+  }
+  return GP_OK;
+}
+
+int gp_bert_addln_ffn_out(int64_t M, int64_t H, int64_t FF, const void* attn, const void* x, const void* w0,
+                          const void* b0, const void* w1, const void* b1, const void* w2, const void* b2,
+                          const void* ga0, const void* be0, const void* ga2, const void* be2, float eps, int act,
+                          void* out, int impl, void* stream) {
+  clear_error();
+  int rc;
+  if (M < 0) return fail(GP_ERR_INVALID_ARG, "M must be >= 0 (got %lld)", (long long)M);
+  if (H != 128 && H != 256 && H != 512 && H != 1024)
+    return fail(GP_ERR_SHAPE, "H must be 128, 256, 512 or 1024 (got %lld)", (long long)H);
+  if (FF < 128 || FF > kMaxDim || FF % 128)
+    return fail(GP_ERR_SHAPE, "FF must be a multiple of 128 in [128, %lld] (got %lld)", (long long)kMaxDim,
+                (long long)FF);
+  if (M > kMaxRows) return fail(GP_ERR_SHAPE, "M too large (%lld)", (long long)M);
+  if ((rc = check_act(act))) return rc;
+  if (impl != GP_IMPL_FUSED && impl != GP_IMPL_PIPELINED) return fail(GP_ERR_INVALID_ARG, "unknown impl %d", impl);
+  if (!(eps >= 0.f)) return fail(GP_ERR_INVALID_ARG, "eps must be >= 0");
+  if ((rc = need16(w0, "w0")) || (rc = need16(w1, "w1")) || (rc = need16(w2, "w2")) || (rc = opt16(b0, "b0")) ||
+      (rc = opt16(b1, "b1")) || (rc = opt16(b2, "b2")) || (rc = opt16(ga0, "ga0")) || (rc = opt16(be0, "be0")) ||
+      (rc = opt16(ga2, "ga2")) || (rc = opt16(be2, "be2")))
+    return rc;
+  if (M == 0) return GP_OK;
+  if ((rc = need16(attn, "attn_out")) || (rc = need16(x, "x")) || (rc = need16(out, "out"))) return rc;
+  int dev = 0, ncu = 0;
+  if ((rc = current_device_info(&dev, &ncu))) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  if (impl == GP_IMPL_PIPELINED) {
+    const BertAddlnArgs a{M, H, FF, attn, x, w0, b0, w1, b1, w2, b2, ga0, be0, ga2, be2, eps, act, out};
+    return bert_addln_pipelined_run(a, dev, ncu, s);
+  }
+
+  // Chain: per row chunk, GEMM0 (+ b0 + x), LN0, GEMM1 (+ b1, act), GEMM2 (+ b2 + h0), LN2.
+  // Workspace: w0^T [H][H], w1^T [FF][H], w2^T [H][FF], then for one chunk the
+  // pre-LayerNorm rows y [CH][H], h0 [CH][H] and the activations [CH][FF].
+  const int64_t CH = M < kFfnChunkRows ? M : kFfnChunkRows;
+  const size_t o_w1t = round_up((size_t)H * H * 2);
+  const size_t o_w2t = o_w1t + round_up((size_t)FF * H * 2);
+  const size_t o_y = o_w2t + round_up((size_t)FF * H * 2);
+  const size_t o_h0 = o_y + round_up((size_t)CH * H * 2);
+  const size_t o_act = o_h0 + round_up((size_t)CH * H * 2);
+  const size_t total = o_act + round_up((size_t)CH * FF * 2);
+  char* ws = nullptr;
+  if ((rc = workspace_acquire(dev, s, total, (void**)&ws))) return rc;
+  void *w0t = ws, *w1t = ws + o_w1t, *w2t = ws + o_w2t, *ybuf = ws + o_y, *h0 = ws + o_h0, *abuf = ws + o_act;
+  const PrepSpec ps[3] = {{w0, w0t, nullptr, nullptr, H, H, H, H},
+                          {w1, w1t, nullptr, nullptr, H, FF, H, FF},
+                          {w2, w2t, nullptr, nullptr, FF, H, FF, H}};
+  hipError_t e = prep_launch(ps, 3, s);
+  if (e != hipSuccess) return fail_hip(e, "transpose launch");
+  for (int64_t r0 = 0; r0 < M; r0 += CH) {
+    const int64_t rows = M - r0 < CH ? M - r0 : CH;
+    e = gemm_launch({rows, H, H, at_row(attn, r0, H), w0t, b0, at_row(x, r0, H), GP_ACT_NONE, ybuf}, ncu, s);
+    if (e == hipSuccess) e = layer_norm_launch(rows, H, ybuf, ga0, be0, eps, h0, ncu, s);
+    if (e == hipSuccess) e = gemm_launch({rows, FF, H, h0, w1t, b1, nullptr, act, abuf}, ncu, s);
+    if (e == hipSuccess) e = gemm_launch({rows, H, FF, abuf, w2t, b2, h0, GP_ACT_NONE, ybuf}, ncu, s);
+    if (e == hipSuccess) e = layer_norm_launch(rows, H, ybuf, ga2, be2, eps, (char*)out + r0 * H * 2, ncu, s);
+    if (e != hipSuccess) return fail_hip(e, "bert_addln_ffn launch");
   }
   return GP_OK;
 }

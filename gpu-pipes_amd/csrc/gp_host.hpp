@@ -22,6 +22,12 @@ int check_mgn_args(const MgnArgs& a);
 // split_ln: the reference's layout with separate LayerNorm workers.
 int mgn_pipelined_run(const MgnArgs& a, bool split_ln, int dev, int num_cus, hipStream_t stream);
 
+// The reference's queue-chained layouts of the bert_addln_ffn and nerf_a apps
+// (stage workgroups linked by L2 ring queues; pipe_add / pipe_concat stages
+// fed from queues).  H 128 / FF 512 and Kx a multiple of 8 up to 128 only.
+int bert_addln_pipelined_run(const BertAddlnArgs& a, int dev, int num_cus, hipStream_t stream);
+int nerf_a_pipelined_run(const NerfAArgs& a, int dev, int num_cus, hipStream_t stream);
+
 // Identity pipelines through ring queues (tests the queue protocol).
 int pipe_route_run(int64_t M, const void* x, void* out, void* out2, int route, int max_pipes, int dev, int num_cus,
                    hipStream_t stream);
@@ -30,6 +36,8 @@ int pipe_route_run(int64_t M, const void* x, void* out, void* out2, int route, i
 // queue layout changes; each call returns a new launch epoch.
 constexpr uint32_t kArenaLayoutMgn = 1;    // mgn_pipelined Queues
 constexpr uint32_t kArenaLayoutRoute = 2;  // route kernels (+1 for the split layout)
+constexpr uint32_t kArenaLayoutBertAddln = 4;
+constexpr uint32_t kArenaLayoutNerfA = 5;
 int arena_acquire(int dev, hipStream_t stream, size_t bytes, uint32_t layout, void** base, uint32_t* epoch);
 
 // Scratch memory of the wide operators, one per (device, stream), grown on

@@ -40,6 +40,31 @@ struct MgnArgs {
 // Persistent fused kernel (all layers in one workgroup per CU).
 hipError_t mgn_fused_launch(const MgnArgs& a, int num_cus, hipStream_t stream);
 
+// The add + LayerNorm + FFN block of apps/bert_addln_ffn (attn, x [M,H] ->
+// out [M,H]): h0 = LN0(attn w0 + b0 + x), out = LN2(act(h0 w1 + b1) w2 + b2 + h0).
+// w0 [H,H], w1 [H,FF], w2 [FF,H] (weight.t()); biases and affines may be null.
+struct BertAddlnArgs {
+  int64_t M, H, FF;
+  const void* attn;
+  const void* x;
+  const void *w0, *b0, *w1, *b1, *w2, *b2;
+  const void *ga0, *be0, *ga2, *be2;
+  float eps;
+  int act;  // GP_ACT_*
+  void* out;
+};
+
+// NerfA of apps/nerf_a (x [M,Kx] -> out [M,256]): five Linear + ReLU layers,
+// the skip concatenation [h | x], three more Linear + ReLU layers.  w[0] is
+// [Kx,256], w[5] [256+Kx,256], the rest [256,256]; biases may be null.
+struct NerfAArgs {
+  int64_t M, Kx;
+  const void* x;
+  const void* w[8];
+  const void* b[8];
+  void* out;
+};
+
 // One GEMM stage over M rows: out = act(x W + b [+ acc]) or LayerNorm(x W + b).
 struct LinearArgs {
   int64_t M;

@@ -1,5 +1,6 @@
 // C ABI of the dense MLP chains: the DLRM MLPs (gp_mlp_out, gp_dlrm_botmlp_out,
-// gp_dlrm_topmlp_out) and the NeRF MLP (gp_nerf_full_out).
+// gp_dlrm_topmlp_out), the NeRF MLP (gp_nerf_full_out and its allocation-free
+// form) and the NerfA trunk (gp_nerf_a_out).
 //
 // The reference builds each app as one pipelined kernel of GEMM stage blocks
 // linked by queues (apps/dlrm_botmlp/pipelined/dlrm_botmlp_pl.cuh:79-137,
@@ -316,6 +317,77 @@ int gp_nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb
     if (e == hipSuccess)
       e = place_launch(rows, hd, np12, Nrgb, (void*)row_ptr(out_rgb, r0, Nrgb), Nrgb, Nrgb, GP_ACT_NONE, ncu, s);
     if (e != hipSuccess) return fail_hip(e, "NeRF layer launch");
+  }
+  return GP_OK;
+}
+
+int gp_nerf_a_out(int64_t M, int64_t Kx, const void* x, const void* const* w, const void* const* b, void* out, int impl,
+                  void* stream) {
+  clear_error();
+  int rc = common_checks(M, x, out);
+  if (rc) return rc;
+  if (!w || !b) return fail(GP_ERR_INVALID_ARG, "w and b must be non-NULL");
+  if (Kx < 1 || Kx > 1024) return fail(GP_ERR_SHAPE, "Kx must be in [1, 1024] (got %lld)", (long long)Kx);
+  for (int i = 0; i < 8; ++i)
+    if (!w[i]) return fail(GP_ERR_INVALID_ARG, "weight %d is NULL", i + 1);
+  if (impl != GP_IMPL_FUSED && impl != GP_IMPL_PIPELINED) return fail(GP_ERR_INVALID_ARG, "unknown impl %d", impl);
+  if (M == 0) return GP_OK;
+  int dev = 0, ncu = 0;
+  if ((rc = current_device_info(&dev, &ncu))) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  if (impl == GP_IMPL_PIPELINED) {
+    if (!aligned16(x) || !aligned16(out)) return fail(GP_ERR_ALIGN, "x and out must be 16-byte aligned");
+    for (int i = 0; i < 8; ++i)
+      if (!aligned16(w[i])) return fail(GP_ERR_ALIGN, "weight %d must be 16-byte aligned", i + 1);
+    NerfAArgs a{M, Kx, x, {}, {}, out};
+    for (int i = 0; i < 8; ++i) {
+      a.w[i] = w[i];
+      a.b[i] = b[i];
+    }
+    return nerf_a_pipelined_run(a, dev, ncu, s);
+  }
+
+  // Chain: one wide-GEMM launch per layer (apps/nerf_a/torch/model.py:5-38):
+  // 1: Kx -> 256, 2-5: 256 -> 256; 6: [h5 | x] -> 256; 7-8: 256 -> 256; ReLU after each.
+  const int64_t H = 256;
+  const int64_t kx = rup(Kx, 64), cat1 = rup(H + Kx, 64);
+  const int64_t kin[8] = {kx, H, H, H, H, cat1, H, H};
+  const int64_t kreal[8] = {Kx, H, H, H, H, H + Kx, H, H};
+  const int64_t CH = M < kChunkRows ? M : kChunkRows;
+  Carve cv;
+  size_t o_wt[8], o_b[8];
+  for (int i = 0; i < 8; ++i) {
+    o_wt[i] = cv.take((size_t)H * kin[i] * 2);
+    o_b[i] = cv.take((size_t)H * 2);
+  }
+  const size_t o_x = cv.take((size_t)CH * kx * 2);     // x, padded
+  const size_t o_c1 = cv.take((size_t)CH * cat1 * 2);  // [h5 | x]
+  const size_t o_h0 = cv.take((size_t)CH * H * 2);
+  const size_t o_h1 = cv.take((size_t)CH * H * 2);
+  char* ws = nullptr;
+  if ((rc = workspace_acquire(dev, s, cv.off, (void**)&ws))) return rc;
+  Prepared L[8];
+  PrepSpec ps[8];
+  for (int i = 0; i < 8; ++i) {
+    ps[i] = {w[i], ws + o_wt[i], b[i], ws + o_b[i], kreal[i], H, kin[i], H};
+    L[i] = {ws + o_wt[i], ws + o_b[i], kin[i], H, GP_ACT_RELU};
+  }
+  if (hipError_t e = prep_launch(ps, 8, s); e != hipSuccess) return fail_hip(e, "NerfA weight preparation");
+  char *xb = ws + o_x, *c1 = ws + o_c1, *h0 = ws + o_h0, *h1 = ws + o_h1;
+  for (int64_t r0 = 0; r0 < M; r0 += CH) {
+    const int64_t rows = M - r0 < CH ? M - r0 : CH;
+    hipError_t e = place_launch(rows, row_ptr(x, r0, Kx), Kx, Kx, xb, kx, kx, GP_ACT_NONE, ncu, s);
+    if (e == hipSuccess) e = place_launch(rows, row_ptr(x, r0, Kx), Kx, Kx, c1 + H * 2, cat1, cat1 - H, GP_ACT_NONE,
+                                          ncu, s);
+    if (e == hipSuccess) e = layer(L[0], rows, xb, kx, h0, H, ncu, s);
+    if (e == hipSuccess) e = layer(L[1], rows, h0, H, h1, H, ncu, s);
+    if (e == hipSuccess) e = layer(L[2], rows, h1, H, h0, H, ncu, s);
+    if (e == hipSuccess) e = layer(L[3], rows, h0, H, h1, H, ncu, s);
+    if (e == hipSuccess) e = layer(L[4], rows, h1, H, c1, cat1, ncu, s);  // h5 -> first 256 columns of [h5 | x]
+    if (e == hipSuccess) e = layer(L[5], rows, c1, cat1, h0, H, ncu, s);
+    if (e == hipSuccess) e = layer(L[6], rows, h0, H, h1, H, ncu, s);
+    if (e == hipSuccess) e = layer(L[7], rows, h1, H, (void*)row_ptr(out, r0, H), H, ncu, s);
+    if (e != hipSuccess) return fail_hip(e, "NerfA layer launch");
   }
   return GP_OK;
 }

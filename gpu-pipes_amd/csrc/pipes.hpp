@@ -303,7 +303,9 @@ struct MemoryWriter {
 };
 
 // pipes.cuh:74-84 (the reference resets the queue in the constructor, :80;
-// epoch-tagged counters make that unnecessary).
+// epoch-tagged counters make that unnecessary).  `col0` offsets the view by
+// that many columns: with NP > 1 producers, producer j writes its own column
+// block of every entry (a layer wider than one GEMM stage, split by columns).
 template <typename QT>
 struct QueueWriter {
   using Queue = QT;
@@ -311,11 +313,14 @@ struct QueueWriter {
   const QueueCtx* ctx;
   int64_t seq_n = 0;
   int rows = 0;
+  int col0 = 0;
 
-  __device__ QueueWriter(Queue* q_, const QueueCtx* ctx_) : q(q_), ctx(ctx_) {}
+  __device__ QueueWriter(Queue* q_, const QueueCtx* ctx_, int col0_ = 0) : q(q_), ctx(ctx_), col0(col0_) {}
   __device__ TensorView write_acquire(int rows_) {
     rows = rows_;
-    return q->write_wait(seq_n, *ctx)->as_view(rows_);
+    TensorView v = q->write_wait(seq_n, *ctx)->as_view(rows_);
+    v.data += col0;
+    return v;
   }
   __device__ void write_release() {
     q->write_commit(seq_n, rows, *ctx);

@@ -73,14 +73,22 @@ template <int MBLK, int K>
 constexpr int gemm_stage_lds() {
   return MBLK * K * 2 > 128 * kSlabStride ? MBLK * K * 2 : 128 * kSlabStride;
 }
-constexpr int kGemmParamLds = 3 * 128 * 4 + 128 * 4 * 8;  // bias/gamma/beta + LN partials (MBLK <= 128)
+// bias/gamma/beta + the LayerNorm partials of MBLK rows
+template <int MBLK>
+constexpr int gemm_param_lds() {
+  return 3 * 128 * 4 + MBLK * 4 * 8;
+}
+constexpr int kGemmParamLds = gemm_param_lds<128>();
 
 // Copy rows [0, MBLK) x K halves of a tile view into LDS.  LDS row r holds
 // 16-byte chunk c at chunk position (c & ~15) | ((c ^ r) & 15), so the 16
 // rows read by one ds_read_b128 phase hit 16 different bank groups.  Rows at
-// or past v.rows lie outside the buffer descriptor and arrive as zeros.
+// or past v.rows lie outside the buffer descriptor and arrive as zeros, and so
+// do columns at or past kv (a multiple of 8): a narrower input (a 64-wide
+// NeRF encoding, a 320-wide concatenation) runs as a K-wide tile whose extra
+// columns are zero, never the next row's data.
 template <int MBLK, int K>
-__device__ __forceinline__ void load_tile_swz(const TensorView& v, GP_LDS char* dst) {
+__device__ __forceinline__ void load_tile_swz(const TensorView& v, GP_LDS char* dst, int kv = K) {
   static_assert(K % 128 == 0, "K must be a multiple of 128");
   constexpr int CPR = K / 8;
   constexpr int NI = MBLK * K * 2 / 1024;
@@ -94,13 +102,14 @@ __device__ __forceinline__ void load_tile_swz(const TensorView& v, GP_LDS char* 
     const int q = i * kWave + lane;
     const int r = q / CPR;
     const int c = (q - r * CPR) ^ (r & 15);
-    dma16_buf(rsrc, r * v.stride * 2 + c * 16, dst + i * 1024);
+    dma16_buf(rsrc, c * 8 < kv ? r * v.stride * 2 + c * 16 : (int)0x7FFFFFF0, dst + i * 1024);
   }
 }
 
 // Load a weight matrix W [K][128] (row stride w.stride elements) into MFMA A
 // fragments: wf[s] of wave w, lane l holds W[16s + 8(l/32) + e][32w + l%32].
 // 64-k slabs are transposed through LDS scratch (>= 128 * kSlabStride bytes).
+// Rows at or past w.rows (the valid K of a padded layer) load as zeros.
 template <int K>
 __device__ __forceinline__ void load_weight_frags(const TensorView& w, GP_LDS char* scratch, h8 (&wf)[K / 16]) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -110,7 +119,9 @@ __device__ __forceinline__ void load_weight_frags(const TensorView& w, GP_LDS ch
     // 64 rows x 16 feature octets: wave w copies octets w, w+4, w+8, w+12
     h8 v[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = *(const h8*)(w.data + (int64_t)(64 * j + lane) * w.stride + 8 * (wave + 4 * i));
+    for (int i = 0; i < 4; ++i)
+      v[i] = 64 * j + lane < w.rows ? *(const h8*)(w.data + (int64_t)(64 * j + lane) * w.stride + 8 * (wave + 4 * i))
+                                    : h8{};
     __syncthreads();  // previous slab fully read
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -138,6 +149,9 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
   static_assert(MBLK % 32 == 0 && MBLK <= 128, "MBLK must be 32, 64, 96 or 128");
   GP_LDS char* xs = dyn_lds();
   GP_LDS float* prm = (GP_LDS float*)(xs + gemm_stage_lds<MBLK, K>());
+  // The weight view's row count is the layer's real K: input columns past it
+  // are zero-filled (their weight rows are zero too).
+  const int kv = weight.rows < K ? weight.rows : K;
   GP_LDS f2* lnpart = (GP_LDS f2*)(prm + 3 * N);  // [MBLK][4]
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -156,7 +170,7 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
   const int xa = lh ^ (lr & 15);
   for (int it = 0; it < num_iters; ++it) {
     const TensorView in = ir.read_acquire();
-    load_tile_swz<MBLK, K>(in, xs);
+    load_tile_swz<MBLK, K>(in, xs, kv);
     __builtin_amdgcn_s_waitcnt(kWaitAll);
     __syncthreads();
     ir.read_release();  // the tile is in LDS: hand the input slot back at once

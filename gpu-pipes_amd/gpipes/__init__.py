@@ -26,7 +26,8 @@ __all__ = [
     "linear_out", "linear_layer_norm_out", "layer_norm_out", "add_out", "concat_out", "pipe_ident",
     "pipeline_check", "set_wait_limit", "ACTS", "mgn_edge_gather", "mgn_edge_gather_out", "pipe_route", "ROUTES",
     "gemm_out", "bert_ffn", "bert_ffn_out", "mlp_out", "dlrm_botmlp", "dlrm_botmlp_out", "dlrm_topmlp",
-    "dlrm_topmlp_out", "nerf_full", "nerf_full_out", "nerf_full_out_noalloc",
+    "dlrm_topmlp_out", "nerf_full", "nerf_full_out", "nerf_full_out_noalloc", "bert_addln_ffn",
+    "bert_addln_ffn_out", "nerf_a", "nerf_a_out",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -84,6 +85,10 @@ def _load():
     L.gp_dlrm_topmlp_out.argtypes = [i64, i64, i64] + [vp] * 11 + [i32, vp, vp]
     L.gp_nerf_full_out.argtypes = [i64] * 5 + [vp] * 4 + [i32, vp, vp, vp]
     L.gp_nerf_full_out_noalloc.argtypes = [i64] * 5 + [vp] * 4 + [i32, vp, vp, vp]
+    L.gp_bert_addln_ffn_out.argtypes = [i64, i64, i64] + [vp] * 12 + [f32, i32, vp, i32, vp]
+    L.gp_bert_addln_ffn_out.restype = i32
+    L.gp_nerf_a_out.argtypes = [i64, i64, vp, vp, vp, vp, i32, vp]
+    L.gp_nerf_a_out.restype = i32
     L.gp_nerf_full_out_noalloc.restype = i32
     for name in ("gp_mlp_out", "gp_dlrm_botmlp_out", "gp_dlrm_topmlp_out", "gp_nerf_full_out", "gp_gemm_out",
                  "gp_bert_ffn_out", "gp_linear_out", "gp_linear_layer_norm_out", "gp_layer_norm_out", "gp_add_out",
@@ -504,6 +509,81 @@ def nerf_full_out(x, d, *wb_and_outs, rgb_act="none"):
         _check(lib.gp_nerf_full_out(M, Kx, Kd, Na, Nrgb, _ptr(x), _ptr(d), wp, bp, ACTS.get(rgb_act, rgb_act),
                                     _ptr(out_r), _ptr(out_rgb), _stream(x)))
     return out_r, out_rgb
+
+
+def bert_addln_ffn_out(attn_out, x, w0, b0, w1, b1, w2, b2, ga0, be0, ga2, be2, out, eps=1e-5, act="relu",
+                       impl="fused"):
+    """ln2(ffn(h0) + h0) with h0 = ln0(attn_out @ w0 + b0 + x), into ``out`` -- bert_addln_ffn_out of
+    apps/bert_addln_ffn/pipelined/bert_addln_ffn_pl_ext.cu:17-58 (H 128, FF 512, ReLU, eps 1e-5
+    there), for H in {128, 256, 512, 1024} and FF a multiple of 128.  Weights [in, out] =
+    ``weight.t().contiguous()``; biases and LayerNorm affines may be None.  impl "fused" (one
+    GEMM launch per layer with fused epilogues) or "pipelined" (the reference's queue-chained
+    layout, H 128 / FF 512 only)."""
+    _check_input("attn_out", attn_out)
+    if attn_out.dim() != 2:
+        raise RuntimeError("attn_out must be 2-D [M, H]")
+    M, H = attn_out.shape
+    _check_input("x", x, (M, H))
+    _check_input("w0", w0, (H, H))
+    _check_input("w1", w1)
+    if w1.dim() != 2 or w1.shape[0] != H:
+        raise RuntimeError(f"w1 must be [{H}, FF]")
+    FF = w1.shape[1]
+    _check_input("w2", w2, (FF, H))
+    for name, t, n in (("b0", b0, H), ("b1", b1, FF), ("b2", b2, H), ("ga0", ga0, H), ("be0", be0, H),
+                       ("ga2", ga2, H), ("be2", be2, H)):
+        _opt(name, t, (n,))
+    _check_input("out", out, (M, H))
+    _same_device(attn_out, x, w0, b0, w1, b1, w2, b2, ga0, be0, ga2, be2, out)
+    impl_id = _IMPLS.get(impl, impl)
+    with torch.cuda.device(x.device):
+        _check(lib.gp_bert_addln_ffn_out(M, H, FF, _ptr(attn_out), _ptr(x), _ptr(w0), _ptr(b0), _ptr(w1), _ptr(b1),
+                                         _ptr(w2), _ptr(b2), _ptr(ga0), _ptr(be0), _ptr(ga2), _ptr(be2), float(eps),
+                                         ACTS.get(act, act), _ptr(out), int(impl_id), _stream(x)))
+    return out
+
+
+def bert_addln_ffn(attn_out, x, w0, b0, w1, b1, w2, b2, ga0, be0, ga2, be2, eps=1e-5, act="relu", impl="fused"):
+    """Allocating form (bert_addln_ffn_pl_ext.cu:61-76, which passes be0 for be2 -- not
+    reproduced: ga2 / be2 are used as given)."""
+    out = torch.zeros_like(x)
+    return bert_addln_ffn_out(attn_out, x, w0, b0, w1, b1, w2, b2, ga0, be0, ga2, be2, out, eps=eps, act=act,
+                              impl=impl)
+
+
+def nerf_a_out(x, *wb_and_out, impl="fused"):
+    """NerfA (apps/nerf_a/torch/model.py:5-38) into ``out``: arguments x, w1, b1, ..., w8, b8, out,
+    the order of nerf_a_out (apps/nerf_a/pipelined/nerf_a_pl_ext.cu:24-76).  w1 [Kx, 256],
+    w6 [256 + Kx, 256], the others [256, 256]; biases may be None; out [M, 256].  impl "fused"
+    (one GEMM launch per layer) or "pipelined" (the reference's queue-chained layout, Kx a
+    multiple of 8 up to 128)."""
+    if len(wb_and_out) != 17:
+        raise RuntimeError("expected w1, b1, ..., w8, b8, out")
+    ws, bs, out = list(wb_and_out[0:16:2]), list(wb_and_out[1:16:2]), wb_and_out[16]
+    _check_input("x", x)
+    if x.dim() != 2:
+        raise RuntimeError("x must be 2-D [M, Kx]")
+    M, Kx = x.shape
+    shapes = [(Kx, 256)] + [(256, 256)] * 4 + [(256 + Kx, 256), (256, 256), (256, 256)]
+    for i, (w, b, shp) in enumerate(zip(ws, bs, shapes)):
+        _check_input(f"w{i + 1}", w, shp)
+        _opt(f"b{i + 1}", b, (256,))
+    _check_input("out", out, (M, 256))
+    _same_device(x, out, *ws, *bs)
+    wp = (ctypes.c_void_p * 8)(*[w.data_ptr() for w in ws])
+    bp = (ctypes.c_void_p * 8)(*[0 if b is None else b.data_ptr() for b in bs])
+    impl_id = _IMPLS.get(impl, impl)
+    with torch.cuda.device(x.device):
+        _check(lib.gp_nerf_a_out(M, Kx, _ptr(x), wp, bp, _ptr(out), int(impl_id), _stream(x)))
+    return out
+
+
+def nerf_a(x, *wb, impl="fused"):
+    """Allocating form: returns a new [M, 256] tensor (nerf_a_pl_ext.cu:79-110)."""
+    if len(wb) != 16:
+        raise RuntimeError("expected w1, b1, ..., w8, b8")
+    out = torch.zeros((x.shape[0], 256), dtype=x.dtype, device=x.device)
+    return nerf_a_out(x, *wb, out, impl=impl)
 
 
 def nerf_full_out_noalloc(x, d, *wb_and_outs, rgb_act="none"):

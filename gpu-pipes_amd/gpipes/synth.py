@@ -144,3 +144,55 @@ def nerf_params(Kx=64, Kd=27, Na=1, Nrgb=3, seed=0, device="cpu", zero_pad_rows=
         ws[5][256 + zero_pad_rows:] = 0
     h = lambda t: t.to(torch.float16).contiguous().to(device)  # noqa: E731
     return [h(w) for w in ws], [h(b) for b in bs]
+
+
+def bert_addln_params(H=128, FF=512, seed=0, init="torch", device="cpu", affine_random=False):
+    """Parameters of the add + LayerNorm + FFN block of apps/bert_addln_ffn/torch/model.py:3-20
+    (y0w0 = Linear(H, H), ln0 = LayerNorm(H), ffn = Linear(H, FF) -> act -> Linear(FF, H),
+    ln2 = LayerNorm(H), created in that order) in kernel layout: w0 [H, H], w1 [H, FF],
+    w2 [FF, H] (weight.t()), biases, ga0 / be0, ga2 / be2.  init="torch" keeps nn.Linear's
+    defaults (the reference app's val.py); "bert" draws weights ~ N(0, 0.02) with zero
+    biases.  affine_random draws the LayerNorm affines so that ga0/be0 and ga2/be2 differ."""
+    with torch.random.fork_rng(devices=[]):
+        torch.manual_seed(seed)
+        y0w0 = torch.nn.Linear(H, H)
+        ln0 = torch.nn.LayerNorm(H)
+        f1 = torch.nn.Linear(H, FF)
+        f2 = torch.nn.Linear(FF, H)
+        ln2 = torch.nn.LayerNorm(H)
+        with torch.no_grad():
+            if init == "bert":
+                for lin in (y0w0, f1, f2):
+                    lin.weight.normal_(0.0, 0.02)
+                    lin.bias.zero_()
+            elif init != "torch":
+                raise ValueError(f"unknown init {init!r}")
+            if affine_random:
+                for ln in (ln0, ln2):
+                    ln.weight.uniform_(0.5, 1.5)
+                    ln.bias.uniform_(-0.5, 0.5)
+
+    def h(t):
+        return t.detach().to(torch.float16).contiguous().to(device)
+
+    return {"w0": h(y0w0.weight.t()), "b0": h(y0w0.bias), "w1": h(f1.weight.t()), "b1": h(f1.bias),
+            "w2": h(f2.weight.t()), "b2": h(f2.bias), "ga0": h(ln0.weight), "be0": h(ln0.bias),
+            "ga2": h(ln2.weight), "be2": h(ln2.bias)}
+
+
+def nerf_a_params(Kx=64, seed=0, device="cpu", zero_pad_rows=None):
+    """Parameters w1..w8 / b1..b8 of NerfA (apps/nerf_a/torch/model.py:5-38, hidden 256,
+    skip after the fifth layer) in kernel layout with nn.Linear's default init: w1 [Kx, 256],
+    w2..w5 [256, 256], w6 [256 + Kx, 256], w7, w8 [256, 256].  zero_pad_rows zeroes the weight
+    rows of input columns at and past it (the zero padding of x) in w1 and the skip part of w6."""
+    shapes = [(Kx, 256)] + [(256, 256)] * 4 + [(256 + Kx, 256), (256, 256), (256, 256)]
+    with torch.random.fork_rng(devices=[]):
+        torch.manual_seed(seed)
+        lins = [torch.nn.Linear(k, n) for k, n in shapes]
+    ws = [lin.weight.detach().t().contiguous() for lin in lins]
+    bs = [lin.bias.detach() for lin in lins]
+    if zero_pad_rows is not None and zero_pad_rows < Kx:
+        ws[0][zero_pad_rows:] = 0
+        ws[5][256 + zero_pad_rows:] = 0
+    h = lambda t: t.to(torch.float16).contiguous().to(device)  # noqa: E731
+    return [h(w) for w in ws], [h(b) for b in bs]

@@ -121,6 +121,48 @@ int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void*
                     void* out, void* stream);
 
 /*
+ * The add + LayerNorm + FFN block of the bert_addln_ffn app,
+ * apps/bert_addln_ffn/torch/model.py:3-20:
+ *   h0  = LayerNorm(attn . w0 + b0 + x) * ga0 + be0
+ *   out = LayerNorm(act(h0 . w1 + b1) . w2 + b2 + h0) * ga2 + be2
+ * attn, x [M,H]; w0 [H,H], w1 [H,FF], w2 [FF,H] (weight.t()); biases [N] and
+ * the affines [H] may be NULL (0, or 1 / 0); act GP_ACT_RELU (the app) or
+ * GP_ACT_GELU_TANH; eps as given (the app's is 1e-5).  H in {128, 256, 512,
+ * 1024}, FF a multiple of 128, at most 16384; any M >= 0.
+ * Replaces bert_addln_ffn_out(attn_out, x, w0, b0, w1, b1, w2, b2, ga0, be0,
+ * ga2, be2, out), apps/bert_addln_ffn/pipelined/bert_addln_ffn_pl_ext.cu:17-58
+ * (H 128, FF 512, ReLU, M a multiple of 128).  impl GP_IMPL_FUSED (0, the
+ * default) runs one GEMM launch per linear layer with bias, activation and
+ * residual fused into its epilogue, plus two LayerNorm launches, over row
+ * chunks in the per-stream workspace; GP_IMPL_PIPELINED runs the reference's
+ * queue-chained layout (bert_addln_ffn_pl.cuh:92-176: stage workgroups linked
+ * by ring queues, both adds fed from queues) for H = 128, FF = 512 and ReLU or
+ * GELU(tanh), with failures reported by gp_pipeline_check.  The reference's
+ * defects are not reproduced: its ln0 never runs and its extension passes be0
+ * for be2 (bert_addln_ffn_pl.cuh:227, _ext.cu:71).
+ */
+int gp_bert_addln_ffn_out(int64_t M, int64_t H, int64_t FF, const void* attn, const void* x, const void* w0,
+                          const void* b0, const void* w1, const void* b1, const void* w2, const void* b2,
+                          const void* ga0, const void* be0, const void* ga2, const void* be2, float eps, int act,
+                          void* out, int impl, void* stream);
+
+/*
+ * NerfA, apps/nerf_a/torch/model.py:5-38 (hidden 256, skip after the fifth
+ * layer): with w[0..7] / b[0..7] the reference's w1..w8 / b1..b8
+ * (apps/nerf_a/pipelined/nerf_a_pl_ext.cu:24-76),
+ *   h = ReLU chain of w1 [Kx,256], w2..w5 [256,256];  h = [h | x];
+ *   out [M,256] = ReLU chain of w6 [256+Kx,256], w7, w8 [256,256].
+ * x [M,Kx], Kx in [1, 1024] (the app's is 64); biases may be NULL.  impl
+ * GP_IMPL_FUSED (0, the default) runs one wide-GEMM launch per layer over row
+ * chunks; GP_IMPL_PIPELINED runs the reference's queue-chained layout
+ * (nerf_a_pl.cuh:97-179: stage workgroups linked by ring queues, the skip
+ * concatenation a pipe_concat stage fed from a queue) for Kx a multiple of 8
+ * up to 128, with failures reported by gp_pipeline_check.
+ */
+int gp_nerf_a_out(int64_t M, int64_t Kx, const void* x, const void* const* w, const void* const* b, void* out,
+                  int impl, void* stream);
+
+/*
  * Dense MLP chain: widths[0] -> widths[1] -> ... -> widths[nlayers], layer i
  * out = act_i(in . w[i] + b[i]) with w[i] [widths[i], widths[i+1]] (fp16,
  * weight.t()), b[i] [widths[i+1]] or NULL, acts[i] one of GP_ACT_*.  Any
@@ -278,8 +320,9 @@ int gp_pipe_route(int64_t M, const void* x, void* out, void* out2, int route, in
  * Waits for `stream`, then reports whether the last launch on it that
  * reports device-side failures failed (GP_ERR_TIMEOUT) or completed (GP_OK).
  * Those are the launches of gp_mgn_fullmlp_out, gp_mgn_linears_out,
- * gp_mgn_mlp_out (every impl), gp_mgn_edge_gather_out, gp_pipe_ident and
- * gp_pipe_route: every wait between their workgroups or waves is bounded, and
+ * gp_mgn_mlp_out (every impl), gp_mgn_edge_gather_out, gp_pipe_ident,
+ * gp_pipe_route, and gp_bert_addln_ffn_out / gp_nerf_a_out with
+ * GP_IMPL_PIPELINED: every wait between their workgroups or waves is bounded, and
  * one that runs out makes the launch end early and leave its outputs invalid
  * (the fused kernels store nothing after it).  The pipelined layouts also fail
  * when no pipeline's workgroups shared an XCD.  GP_ERR_INVALID_ARG if no such

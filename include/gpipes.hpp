@@ -83,7 +83,8 @@ inline void concat_out(int64_t M, int64_t N0, int64_t N1, const void* a, const v
   check(gp_concat_out(M, N0, N1, a, b, c, stream));
 }
 
-// Waits for `stream` and throws if its last pipelined launch failed on the device.
+// Waits for `stream` and throws if its last launch that reports device-side
+// failures (gp_pipeline_check) timed out.
 inline void pipeline_check(void* stream = nullptr) { check(gp_pipeline_check(stream)); }
 
 // bert_ffn_pl_ext.cu:24-56 (H 128, FF 512, ReLU, eps 1e-5 there, the defaults here)
@@ -123,6 +124,23 @@ inline void nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t
                           const void* const* w, const void* const* b, void* out_r, void* out_rgb,
                           int rgb_act = GP_ACT_NONE, void* stream = nullptr) {
   check(gp_nerf_full_out(M, Kx, Kd, Na, Nrgb, x, d, w, b, rgb_act, out_r, out_rgb, stream));
+}
+
+// bert_addln_ffn_out (apps/bert_addln_ffn/pipelined/bert_addln_ffn_pl_ext.cu:17-58; H 128, FF 512,
+// ReLU, eps 1e-5 there, the defaults here).
+inline void bert_addln_ffn_out(int64_t M, int64_t H, int64_t FF, const void* attn_out, const void* x, const void* w0,
+                               const void* b0, const void* w1, const void* b1, const void* w2, const void* b2,
+                               const void* ga0, const void* be0, const void* ga2, const void* be2, void* out,
+                               float eps = 1e-5f, int act = GP_ACT_RELU, int impl = GP_IMPL_FUSED,
+                               void* stream = nullptr) {
+  check(gp_bert_addln_ffn_out(M, H, FF, attn_out, x, w0, b0, w1, b1, w2, b2, ga0, be0, ga2, be2, eps, act, out, impl,
+                              stream));
+}
+
+// nerf_a_out (apps/nerf_a/pipelined/nerf_a_pl_ext.cu:24-76); w[0..7], b[0..7] = w1..w8, b1..b8.
+inline void nerf_a_out(int64_t M, int64_t Kx, const void* x, const void* const* w, const void* const* b, void* out,
+                       int impl = GP_IMPL_FUSED, void* stream = nullptr) {
+  check(gp_nerf_a_out(M, Kx, x, w, b, out, impl, stream));
 }
 
 }  // namespace gpipes

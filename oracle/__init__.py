@@ -137,6 +137,28 @@ def nerf(x, d, ws, bs, rgb_act=ACT_NONE):
     return alpha, rgb
 
 
+def bert_addln_ffn(attn, x, w0, b0, w1, b1, w2, b2, ga0=None, be0=None, ga2=None, be2=None, act=ACT_RELU, eps=1e-5):
+    """The add + LayerNorm + FFN block in fp32 (apps/bert_addln_ffn/torch/model.py:3-20):
+    h0 = ln0(y0w0(attn) + x);  out = ln2(ffn(h0) + h0), ffn = Linear -> act -> Linear.
+    Weights stored [in, out]; None LayerNorm affines mean 1 / 0."""
+    h0 = layer_norm(add(linear(attn, w0, b0), x), ga0, be0, eps)
+    f = linear(linear(h0, w1, b1, act), w2, b2)
+    return layer_norm(add(f, h0), ga2, be2, eps)
+
+
+def nerf_a(x, ws, bs):
+    """NerfA forward in fp32 (apps/nerf_a/torch/model.py:33-38): five Linear + ReLU layers,
+    the skip concatenation [h | x], three more Linear + ReLU layers; returns [M, 256]."""
+    x = _f32(x)
+    h = x
+    for i in range(5):
+        h = linear(h, ws[i], bs[i], ACT_RELU)
+    h = concat(h, x)
+    for i in range(5, 8):
+        h = linear(h, ws[i], bs[i], ACT_RELU)
+    return h
+
+
 def add(a, b):
     a, b = _f32(a), _f32(b)
     c = np.empty_like(a)

@@ -29,7 +29,11 @@ reference's own LayerNorm check types in (misc_tests/layer_norm/torch_val.py:88-
 repeated over 128 rows there, gamma = 1, beta = 0); its expected output is
 F.layer_norm in float64.
 
-Usage: python tests/golden/gen_fixtures.py
+The bert_addln_ffn fixtures follow apps/bert_addln_ffn/torch/model.py:3-20 and the
+nerf_a fixture apps/nerf_a/torch/model.py:5-38, each evaluated with torch.nn modules in
+float64 (the nerf_a weights are regenerated from the seed, as for NeRF).
+
+Usage: python tests/golden/gen_fixtures.py [fixture names...]   (default: all)
 """
 import hashlib
 import json
@@ -42,7 +46,8 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, os.path.join(ROOT, "gpu-pipes_amd"))
-from gpipes.synth import bert_params, dlrm_params, mgn_params, nerf_inputs, nerf_params, normal_fp16  # noqa: E402
+from gpipes.synth import (bert_addln_params, bert_params, dlrm_params, mgn_params, nerf_a_params,  # noqa: E402
+                          nerf_inputs, nerf_params, normal_fp16)
 
 M_FIX = 256
 
@@ -197,6 +202,75 @@ def make_nerf_fixture(name, M, seed, Kd, Na, Nrgb, sigmoid):
     return path
 
 
+def torch_bert_addln_f64(attn16, x16, p, act, eps):
+    """The add + LayerNorm + FFN block with the module structure of
+    apps/bert_addln_ffn/torch/model.py:3-20 (y0w0, ln0, ffn, ln2; forward
+    ln2(ffn(h) + h) with h = ln0(y0w0(attn) + x)), torch.nn in float64."""
+    H, FF = p["w1"].shape
+    a = torch.nn.ReLU() if act == "relu" else torch.nn.GELU(approximate="tanh")
+    y0w0 = torch.nn.Linear(H, H).double()
+    ln0 = torch.nn.LayerNorm(H, eps=eps).double()
+    ffn = torch.nn.Sequential(torch.nn.Linear(H, FF), a, torch.nn.Linear(FF, H)).double()
+    ln2 = torch.nn.LayerNorm(H, eps=eps).double()
+    with torch.no_grad():
+        y0w0.weight.copy_(p["w0"].double().t())
+        y0w0.bias.copy_(p["b0"].double())
+        ffn[0].weight.copy_(p["w1"].double().t())
+        ffn[0].bias.copy_(p["b1"].double())
+        ffn[2].weight.copy_(p["w2"].double().t())
+        ffn[2].bias.copy_(p["b2"].double())
+        ln0.weight.copy_(p["ga0"].double())
+        ln0.bias.copy_(p["be0"].double())
+        ln2.weight.copy_(p["ga2"].double())
+        ln2.bias.copy_(p["be2"].double())
+        h = ln0(y0w0(attn16.double()) + x16.double())
+        return ln2(ffn(h) + h)
+
+
+def make_bert_addln_fixture(name, M, H, FF, act, eps, init, seed):
+    p = bert_addln_params(H, FF, seed=seed, init=init, affine_random=True)
+    attn = normal_fp16(M, H, seed=seed + 1000)
+    x = normal_fp16(M, H, seed=seed + 2000)
+    y = torch_bert_addln_f64(attn, x, p, act, eps)
+    arrs = {"attn": attn.numpy(), "x": x.numpy(), "expected": y.numpy().astype(np.float32), "eps": np.float64(eps),
+            "act": np.array(act)}
+    for k, v in p.items():
+        arrs[k] = v.numpy()
+    path = os.path.join(HERE, f"{name}.npz")
+    np.savez_compressed(path, **arrs)
+    return path
+
+
+def torch_nerf_a_f64(x16, ws, bs):
+    """NerfA with the module structure of apps/nerf_a/torch/model.py:5-38 (preskip:
+    five Linear + ReLU; resid = cat([preskip(x), x]); postskip: three Linear + ReLU),
+    torch.nn in float64."""
+    def lin(i):
+        m = torch.nn.Linear(ws[i].shape[0], ws[i].shape[1]).double()
+        with torch.no_grad():
+            m.weight.copy_(ws[i].double().t())
+            m.bias.copy_(bs[i].double())
+        return m
+    relu = torch.nn.ReLU
+    preskip = torch.nn.Sequential(*[m for i in range(5) for m in (lin(i), relu())])
+    postskip = torch.nn.Sequential(*[m for i in range(5, 8) for m in (lin(i), relu())])
+    with torch.no_grad():
+        x = x16.double()
+        return postskip(torch.cat([preskip(x), x], dim=-1))
+
+
+def make_nerf_a_fixture(name, M, seed, Kx):
+    """Inputs and expected outputs; the weights are regenerated from the seed by
+    gpipes.synth.nerf_a_params and checked against the stored digest."""
+    ws, bs = nerf_a_params(Kx, seed=seed)
+    x = normal_fp16(M, Kx, seed=seed + 1000)
+    y = torch_nerf_a_f64(x, ws, bs)
+    path = os.path.join(HERE, f"{name}.npz")
+    np.savez_compressed(path, x=x.numpy(), expected=y.numpy().astype(np.float32), seed=np.int64(seed),
+                        Kx=np.int64(Kx), weights_sha256=np.array(weights_digest(ws, bs)))
+    return path
+
+
 def make_ln_fixture():
     row = torch.tensor(LN_ROW, dtype=torch.float16)
     x = row.repeat(128, 1)
@@ -207,25 +281,42 @@ def make_ln_fixture():
     return path
 
 
+FIXTURES = {
+    "mgn_edge_ln": lambda: make_mgn_fixture("mgn_edge_ln", 384, True, seed=0, affine_random=False),
+    "mgn_edge_ln_affine": lambda: make_mgn_fixture("mgn_edge_ln_affine", 384, True, seed=1, affine_random=True),
+    "mgn_edge_linears": lambda: make_mgn_fixture("mgn_edge_linears", 384, False, seed=2, affine_random=False),
+    "mgn_node_ln": lambda: make_mgn_fixture("mgn_node_ln", 256, True, seed=3, affine_random=True),
+    "layer_norm_row": make_ln_fixture,
+    # the reference app's shape and defaults (H 128, FF 512, ReLU, eps 1e-5)
+    "bert_ffn_relu": lambda: make_bert_fixture("bert_ffn_relu", 256, 128, 512, "relu", 1e-5, "torch", seed=10,
+                                               affine_random=False),
+    # DlrmMlp at the reference's bottom-MLP shape, and a narrow chain with a sigmoid head
+    "dlrm_bot": lambda: make_dlrm_fixture("dlrm_bot", 64, [32, 512, 256, 128], None, "torch", seed=20),
+    "dlrm_sigmoid_head": lambda: make_dlrm_fixture("dlrm_sigmoid_head", 64, [24, 256, 128, 1], 2, "xavier", seed=21),
+    # the NeRF MLP at the workload's shape (view dirs 27, density 1, colour 3 + sigmoid)
+    "nerf_workload": lambda: make_nerf_fixture("nerf_workload", 64, seed=22, Kd=27, Na=1, Nrgb=3, sigmoid=True),
+    # the BERT-large recipe (GELU(tanh), eps 1e-12, N(0, 0.02) weights) at a small width
+    "bert_ffn_gelu": lambda: make_bert_fixture("bert_ffn_gelu", 128, 256, 512, "gelu_tanh", 1e-12, "bert", seed=11,
+                                               affine_random=True),
+    # the reference app bert_addln_ffn at its shape (H 128, FF 512, ReLU, eps 1e-5, nn.Linear
+    # init), with distinct LayerNorm affines, and the BERT-large recipe at a small width
+    "bert_addln_ffn": lambda: make_bert_addln_fixture("bert_addln_ffn", 256, 128, 512, "relu", 1e-5, "torch",
+                                                      seed=30),
+    "bert_addln_ffn_gelu": lambda: make_bert_addln_fixture("bert_addln_ffn_gelu", 128, 256, 512, "gelu_tanh", 1e-12,
+                                                           "bert", seed=31),
+    # NerfA at the reference app's input width (64)
+    "nerf_a": lambda: make_nerf_a_fixture("nerf_a", 256, seed=32, Kx=64),
+}
+
+
 def main():
-    paths = [
-        make_mgn_fixture("mgn_edge_ln", 384, True, seed=0, affine_random=False),
-        make_mgn_fixture("mgn_edge_ln_affine", 384, True, seed=1, affine_random=True),
-        make_mgn_fixture("mgn_edge_linears", 384, False, seed=2, affine_random=False),
-        make_mgn_fixture("mgn_node_ln", 256, True, seed=3, affine_random=True),
-        make_ln_fixture(),
-        # the reference app's shape and defaults (H 128, FF 512, ReLU, eps 1e-5)
-        make_bert_fixture("bert_ffn_relu", 256, 128, 512, "relu", 1e-5, "torch", seed=10, affine_random=False),
-        # the BERT-large recipe (GELU(tanh), eps 1e-12, N(0, 0.02) weights) at a small width
-        # DlrmMlp at the reference's bottom-MLP shape, and a narrow chain with a sigmoid head
-        make_dlrm_fixture("dlrm_bot", 64, [32, 512, 256, 128], None, "torch", seed=20),
-        make_dlrm_fixture("dlrm_sigmoid_head", 64, [24, 256, 128, 1], 2, "xavier", seed=21),
-        # the NeRF MLP at the workload's shape (view dirs 27, density 1, colour 3 + sigmoid)
-        make_nerf_fixture("nerf_workload", 64, seed=22, Kd=27, Na=1, Nrgb=3, sigmoid=True),
-        make_bert_fixture("bert_ffn_gelu", 128, 256, 512, "gelu_tanh", 1e-12, "bert", seed=11,
-                          affine_random=True),
-    ]
-    manifest = {}
+    """Regenerate the fixtures named on the command line (default: all) and
+    update their entries of MANIFEST.json."""
+    names = sys.argv[1:] or list(FIXTURES)
+    paths = [FIXTURES[n]() for n in names]
+    mpath = os.path.join(HERE, "MANIFEST.json")
+    with open(mpath) as f:
+        manifest = json.load(f)
     for pth in paths:
         with open(pth, "rb") as f:
             manifest[os.path.basename(pth)] = hashlib.sha256(f.read()).hexdigest()

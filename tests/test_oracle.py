@@ -17,6 +17,17 @@ its own formula:
                           told apart from erf GELU), planted mistakes (no residual,
                           residual after LN, transposed w2, ReLU for GELU, wrong
                           eps) that must fail
+  * bert_addln_ffn     -- golden fixtures made by torch.nn modules in float64 with the
+                          structure of apps/bert_addln_ffn/torch/model.py:3-20 (ReLU /
+                          eps 1e-5 at the reference app's shape, GELU(tanh) / eps 1e-12 at
+                          H 256), the zero-FFN closed form, planted mistakes (be0 passed
+                          for be2 and ln0 skipped -- the reference extension's defects --,
+                          the second residual taken from x, no first residual, swapped
+                          LayerNorm affines, transposed w0) that must fail
+  * nerf_a             -- golden fixture made by torch.nn modules in float64 with the
+                          structure of apps/nerf_a/torch/model.py:5-38, planted mistakes
+                          (skip order, no skip, skip one layer early, no final ReLU,
+                          rotated skip rows of w6) that must fail
   * add / concat       -- numpy
 """
 import numpy as np
@@ -406,3 +417,123 @@ def test_nerf_rejects_planted_mistakes(mutant):
         max_abs, rel = oracle.errors(got, want)
         fails.append(max_abs > oracle.MAX_ABS_TOL or rel > oracle.REL_L2_TOL)
     assert any(fails), mutant
+
+
+# ---------------------------------------------------------------------------- bert_addln_ffn / nerf_a
+ADDLN_FIXTURES = ["bert_addln_ffn.npz", "bert_addln_ffn_gelu.npz"]
+ADDLN_KEYS = ("attn", "x", "w0", "b0", "w1", "b1", "w2", "b2", "ga0", "be0", "ga2", "be2")
+
+
+def _addln_args(z):
+    p = {k: z[k].astype(np.float32) for k in ADDLN_KEYS}
+    act = oracle.ACT_RELU if str(z["act"]) == "relu" else oracle.ACT_GELU_TANH
+    return p, act, float(z["eps"])
+
+
+@pytest.mark.parametrize("name", ADDLN_FIXTURES)
+def test_bert_addln_ffn_golden(name):
+    z = load_golden(name)
+    p, act, eps = _addln_args(z)
+    got = oracle.bert_addln_ffn(*(p[k] for k in ADDLN_KEYS), act=act, eps=eps)
+    max_abs, rel = oracle.errors(got, z["expected"])
+    assert max_abs < 2e-4 and rel < 1e-5, (max_abs, rel)
+
+
+@pytest.mark.parametrize("mutant", ["be0_for_be2", "ln0_skipped", "residual_x_not_h0", "no_attn_residual",
+                                    "ln2_affine_swapped", "w0_transposed"])
+def test_bert_addln_ffn_rejects_planted_mistakes(mutant):
+    """Plausible mistakes (among them the reference extension's, SURVEY App. B item 6:
+    be0 passed for be2, ln0 never run) must fail the fixture at the parity bar."""
+    z = load_golden("bert_addln_ffn.npz")
+    p, act, eps = _addln_args(z)
+    a = dict(p)
+    if mutant == "be0_for_be2":
+        a["be2"] = p["be0"]
+    elif mutant == "ln2_affine_swapped":
+        a["ga2"], a["ga0"] = p["ga0"], p["ga2"]
+    elif mutant == "w0_transposed":
+        a["w0"] = p["w0"].T.copy()
+    if mutant == "ln0_skipped":
+        h0 = oracle.add(oracle.linear(p["attn"], p["w0"], p["b0"]), p["x"])
+        f = oracle.linear(oracle.linear(h0, p["w1"], p["b1"], act), p["w2"], p["b2"])
+        got = oracle.layer_norm(oracle.add(f, h0), p["ga2"], p["be2"], eps)
+    elif mutant == "residual_x_not_h0":
+        h0 = oracle.layer_norm(oracle.add(oracle.linear(p["attn"], p["w0"], p["b0"]), p["x"]), p["ga0"], p["be0"], eps)
+        f = oracle.linear(oracle.linear(h0, p["w1"], p["b1"], act), p["w2"], p["b2"])
+        got = oracle.layer_norm(oracle.add(f, p["x"]), p["ga2"], p["be2"], eps)
+    elif mutant == "no_attn_residual":
+        h0 = oracle.layer_norm(oracle.linear(p["attn"], p["w0"], p["b0"]), p["ga0"], p["be0"], eps)
+        f = oracle.linear(oracle.linear(h0, p["w1"], p["b1"], act), p["w2"], p["b2"])
+        got = oracle.layer_norm(oracle.add(f, h0), p["ga2"], p["be2"], eps)
+    else:
+        got = oracle.bert_addln_ffn(*(a[k] for k in ADDLN_KEYS), act=act, eps=eps)
+    max_abs, rel = oracle.errors(got, z["expected"])
+    assert max_abs > oracle.MAX_ABS_TOL or rel > oracle.REL_L2_TOL, (mutant, max_abs, rel)
+
+
+def test_bert_addln_ffn_closed_forms():
+    """w1 = w2 = 0 and b1 = b2 = 0: the FFN adds nothing, so out = LN(LN(attn W0 + b0 + x))
+    with unit affines, and LayerNorm of an already normalised row is that row (up to eps):
+    out = F.layer_norm(attn W0 + b0 + x)."""
+    M, H, FF = 16, 128, 256
+    attn = RNG.standard_normal((M, H)).astype(np.float32)
+    x = RNG.standard_normal((M, H)).astype(np.float32)
+    w0 = RNG.standard_normal((H, H)).astype(np.float32) * 0.1
+    b0 = RNG.standard_normal(H).astype(np.float32)
+    zw1, zb1 = np.zeros((H, FF), np.float32), np.zeros(FF, np.float32)
+    zw2, zb2 = np.zeros((FF, H), np.float32), np.zeros(H, np.float32)
+    got = oracle.bert_addln_ffn(attn, x, w0, b0, zw1, zb1, zw2, zb2, eps=1e-12)
+    pre = torch.from_numpy(attn).double() @ torch.from_numpy(w0).double() + torch.from_numpy(b0).double() \
+        + torch.from_numpy(x).double()
+    ref = F.layer_norm(pre, [H], eps=1e-12).numpy()
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4)
+
+
+def _nerf_a_fixture():
+    import hashlib
+    from gpipes.synth import nerf_a_params
+    z = load_golden("nerf_a.npz")
+    ws, bs = nerf_a_params(int(z["Kx"]), seed=int(z["seed"]))
+    h = hashlib.sha256()
+    for t in ws + bs:
+        h.update(t.contiguous().view(torch.int16).numpy().tobytes())
+    assert h.hexdigest() == str(z["weights_sha256"]), "nerf_a_params no longer reproduces the fixture's weights"
+    f = lambda ts: [t.float().numpy() for t in ts]  # noqa: E731
+    return z, f(ws), f(bs)
+
+
+def test_nerf_a_golden():
+    z, ws, bs = _nerf_a_fixture()
+    got = oracle.nerf_a(z["x"], ws, bs)
+    max_abs, rel = oracle.errors(got, z["expected"])
+    assert max_abs < 1e-4 and rel < 1e-5, (max_abs, rel)
+
+
+@pytest.mark.parametrize("mutant", ["skip_order", "no_skip", "skip_one_layer_early", "last_layer_no_relu",
+                                    "w6_skip_rows_rotated"])
+def test_nerf_a_rejects_planted_mistakes(mutant):
+    """Plausible mistakes must fail the fixture at the parity bar."""
+    z, ws, bs = _nerf_a_fixture()
+    x = z["x"].astype(np.float32)
+    lin = oracle.linear
+    h = x
+    nskip = 4 if mutant == "skip_one_layer_early" else 5
+    for i in range(nskip):
+        h = lin(h, ws[i], bs[i], oracle.ACT_RELU)
+    if mutant == "skip_order":
+        h = oracle.concat(x, h)
+    elif mutant == "no_skip":
+        h = oracle.concat(h, np.zeros_like(x))
+    else:
+        h = oracle.concat(h, x)
+    if mutant == "skip_one_layer_early":
+        h = lin(h, ws[5], bs[5], oracle.ACT_RELU)  # layer 5 never runs
+    else:
+        w6 = ws[5].copy()
+        if mutant == "w6_skip_rows_rotated":
+            w6[256:] = np.roll(w6[256:], 1, axis=0)
+        h = lin(h, w6, bs[5], oracle.ACT_RELU)
+    h = lin(h, ws[6], bs[6], oracle.ACT_RELU)
+    h = lin(h, ws[7], bs[7], oracle.ACT_NONE if mutant == "last_layer_no_relu" else oracle.ACT_RELU)
+    max_abs, rel = oracle.errors(h, z["expected"])
+    assert max_abs > oracle.MAX_ABS_TOL or rel > oracle.REL_L2_TOL, (mutant, max_abs, rel)
