@@ -3,10 +3,21 @@
 //
 // Reference: apps/mgn_fullmlp/pipelined/mgn_fullmlp_pl.cuh:23-273 and
 // apps/mgn_linears/pipelined/mgn_linears_pl.cuh:22-212.  Per pipeline:
-//   X -> [Linear K->128 + ReLU] -q12-> [Linear + ReLU] -q23-> [Linear (+ LN)] -> out
-// with, in the split layout, the reference's LayerNorm workers:
-//   ... -q23-> [Linear] -lnq-> 5 x [LayerNorm] (round-robin split queue) -> out
+//   X -> 3 x [Linear K->128 + ReLU] -q12-> [Linear + ReLU] -q23-> [Linear (+ LN)] -> out
+// Layer 1 carries K/128 times the work of layers 2 and 3 (60% of the FLOPs at
+// K = 384), which sets the reference's pipeline pace (one block per stage,
+// mgn_fullmlp_pl.cuh:83-101; its K-split fix is disabled, :103-144).  Here two
+// layer-1 workers (for K > 128) take the pipeline's tiles round robin and
+// write q12 through a split queue writer, so no partial sums pass through fp16
+// queues.  A stage's time per tile is mostly fixed cost (queue hand-offs, the
+// tile copy, store completion), so more workers per pipeline mean fewer
+// pipelines: at K = 384 two workers measured 0.88 ms, one 0.92 ms and three
+// 1.16 ms per call.  The split layout keeps the reference's shape, one
+// layer-1 block and five LayerNorm workers:
+//   X -> [Linear K->128 + ReLU] -q12-> [Linear] -q23-> [Linear] -lnq-> 5 x [LayerNorm] -> out
 // (mlp0_sm0 :83-101, mlp1_sm0 :146-160, mlp2_sm0 :162-181, ln_sm :183-203).
+// X tiles are copied with the non-temporal policy (stream-once input), so they
+// do not evict the queues' lines from L2.
 //
 // MI355X: stage roles come from the XCD-aware assignment (pipeline.hpp), so
 // every queue's producer and consumer share an L2; the grid is sized to the
@@ -29,14 +40,21 @@ constexpr int D = 128;
 constexpr int NLN = 5;  // LayerNorm workers per pipeline in the split layout (mgn_fullmlp_pl.cuh:28)
 
 using QEntry = QueueEntry2D<MBLK, D>;
-using Queue = RingQueue<QEntry, 2>;              // q12, q23 (qlen = 2, mgn_fullmlp_pl.cuh:32)
+using Queue = RingQueue<QEntry, 2>;              // q23 (qlen = 2, mgn_fullmlp_pl.cuh:32); q12 with one writer
+using Queue1 = RingQueue<QEntry, 4>;             // q12 written round robin by up to three layer-1 workers
 using LnQueue = RingQueue<QEntry, NLN + 1>;      // lnq (ln_qlen = n_ln_cols + 1, :33)
 
 struct Queues {
-  Queue q12;
+  Queue1 q12;
   Queue q23;
   LnQueue lnq;
 };
+
+// Layer-1 workers per pipeline: 2 for K > 128 (1 in the reference's split layout).
+template <int K, bool SPLIT>
+constexpr int layer1_workers() {
+  return SPLIT ? 1 : (K > 128 ? 2 : 1);
+}
 
 struct Args {
   MgnArgs m;
@@ -47,7 +65,8 @@ struct Args {
 
 template <int K, bool LN, bool SPLIT>
 __global__ __launch_bounds__(kStageThreads) void mgn_pipelined_kernel(Args a) {
-  constexpr int S = SPLIT ? 3 + NLN : 3;
+  constexpr int W1 = layer1_workers<K, SPLIT>();
+  constexpr int S = W1 + (SPLIT ? 2 + NLN : 2);
   const Role r = assign_role(a.ctl, S, a.ctx);
   if (r.pipe < 0) return;
   const MgnArgs& m = a.m;
@@ -58,15 +77,21 @@ __global__ __launch_bounds__(kStageThreads) void mgn_pipelined_kernel(Args a) {
   const TensorView gamma{(half_t*)m.gamma, 1, 1}, beta{(half_t*)m.beta, 1, 1};
   NullReader ar;
 
-  if (r.stage == 0) {
-    MemoryReader ir((half_t*)m.x + g * MBLK * K, NP * MBLK * K, K, MBLK, m.M - g * MBLK, NP * MBLK);
-    QueueWriter<Queue> ow(&qs->q12, &a.ctx);
-    pipe_gemm_bias_relu<MBLK, K>({(half_t*)m.w1, D, K}, {(half_t*)m.b1, 1, 1}, ir, ar, ow, nt);
-  } else if (r.stage == 1) {
-    QueueReader<Queue> ir(&qs->q12, &a.ctx);
+  if (r.stage < W1) {
+    // layer-1 worker w takes the pipeline's tiles w, w + W1, ... (global tiles
+    // g + (w + i W1) NP) and writes them to q12 in sequence order
+    const int w = r.stage;
+    const int cnt = nt > w ? (nt - w + W1 - 1) / W1 : 0;
+    const int64_t first = g + (int64_t)w * NP;
+    MemoryReader ir((half_t*)m.x + first * MBLK * K, W1 * NP * MBLK * K, K, MBLK, m.M - first * MBLK,
+                    W1 * NP * MBLK);
+    SplitQueueWriter<Queue1> ow(&qs->q12, &a.ctx, w, W1);
+    pipe_gemm_bias_relu<MBLK, K>({(half_t*)m.w1, D, K}, {(half_t*)m.b1, 1, 1}, ir, ar, ow, cnt);
+  } else if (r.stage == W1) {
+    QueueReader<Queue1> ir(&qs->q12, &a.ctx);
     QueueWriter<Queue> ow(&qs->q23, &a.ctx);
     pipe_gemm_bias_relu<MBLK, D>({(half_t*)m.w2, D, D}, {(half_t*)m.b2, 1, 1}, ir, ar, ow, nt);
-  } else if (r.stage == 2) {
+  } else if (r.stage == W1 + 1) {
     QueueReader<Queue> ir(&qs->q23, &a.ctx);
     const TensorView w3{(half_t*)m.w3, D, D}, b3{(half_t*)m.b3, 1, 1};
     if constexpr (SPLIT) {
@@ -79,7 +104,7 @@ __global__ __launch_bounds__(kStageThreads) void mgn_pipelined_kernel(Args a) {
     }
   } else if constexpr (SPLIT) {
     // LayerNorm worker w takes queue sequence numbers w, w + NLN, ...
-    const int w = r.stage - 3;
+    const int w = r.stage - W1 - 2;
     const int cnt = nt > w ? (nt - w + NLN - 1) / NLN : 0;
     SplitQueueReader<LnQueue> ir(&qs->lnq, &a.ctx, w, NLN);
     MemoryWriter ow(out + (g + (int64_t)w * NP) * MBLK * D, (int64_t)NLN * NP * MBLK * D, D);
@@ -89,7 +114,7 @@ __global__ __launch_bounds__(kStageThreads) void mgn_pipelined_kernel(Args a) {
 
 template <int K, bool LN, bool SPLIT>
 static int run(const MgnArgs& m, int dev, int num_cus, hipStream_t s) {
-  constexpr int S = SPLIT ? 3 + NLN : 3;
+  constexpr int S = layer1_workers<K, SPLIT>() + (SPLIT ? 2 + NLN : 2);
   constexpr int lds = gemm_stage_lds<MBLK, K>() + kGemmParamLds;
   auto kern = mgn_pipelined_kernel<K, LN, SPLIT>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);

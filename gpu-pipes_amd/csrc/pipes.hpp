@@ -72,13 +72,17 @@ __device__ __forceinline__ uint32_t qcount(unsigned long long v, uint32_t epoch)
 
 // Count one commit on `c` in this epoch (thread-level; called by one thread).
 // The max lifts a counter left by an older launch to (epoch << 32) | 0; it
-// must be complete before the add, so the wave waits for it in between.
-__device__ __forceinline__ void qcommit(QCounter* c, uint32_t epoch) {
+// must be complete before the add, so the wave waits for it in between.  Only
+// a slot's first round of the launch needs it (first = seq < N): the protocol
+// orders every later commit of that counter after the first one.  The add is
+// not waited for: nothing this workgroup does next depends on its completion.
+__device__ __forceinline__ void qcommit(QCounter* c, uint32_t epoch, bool first = true) {
   const unsigned long long base = (unsigned long long)epoch << 32;
-  __hip_atomic_fetch_max(&c->v, base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __builtin_amdgcn_s_waitcnt(kWaitAll);
+  if (first) {
+    __hip_atomic_fetch_max(&c->v, base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(kWaitAll);
+  }
   __hip_atomic_fetch_add(&c->v, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __builtin_amdgcn_s_waitcnt(kWaitAll);
 }
 
 // Workgroup-collective: wait until count(c) >= target.  Returns false if the
@@ -160,7 +164,7 @@ struct RingQueue {
     QueueSlot<Entry>& s = slot(seq);
     if (threadIdx.x == 0) s.rows = rows;
     stores_complete();
-    if (threadIdx.x == 0) qcommit(&s.full, ctx.epoch);
+    if (threadIdx.x == 0) qcommit(&s.full, ctx.epoch, seq < N);
   }
   // Wait until all NP producers of `seq` have committed; returns the payload.
   // After an aborted wait the slot holds no tile of this launch: the view has
@@ -174,7 +178,7 @@ struct RingQueue {
   }
   __device__ void read_commit(int64_t seq, const QueueCtx& ctx) {
     stores_complete();  // this workgroup's loads of the payload have returned
-    if (threadIdx.x == 0) qcommit(&slot(seq).empty, ctx.epoch);
+    if (threadIdx.x == 0) qcommit(&slot(seq).empty, ctx.epoch, seq < N);
   }
 };
 

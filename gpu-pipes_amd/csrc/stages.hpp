@@ -87,7 +87,9 @@ constexpr int kGemmParamLds = gemm_param_lds<128>();
 // do columns at or past kv (a multiple of 8): a narrower input (a 64-wide
 // NeRF encoding, a 320-wide concatenation) runs as a K-wide tile whose extra
 // columns are zero, never the next row's data.
-template <int MBLK, int K>
+// NT: copy with the non-temporal cache policy -- for an input streamed from
+// memory once, so that it does not evict the L2 lines of the ring queues.
+template <int MBLK, int K, bool NT = false>
 __device__ __forceinline__ void load_tile_swz(const TensorView& v, GP_LDS char* dst, int kv = K) {
   static_assert(K % 128 == 0, "K must be a multiple of 128");
   constexpr int CPR = K / 8;
@@ -102,7 +104,11 @@ __device__ __forceinline__ void load_tile_swz(const TensorView& v, GP_LDS char* 
     const int q = i * kWave + lane;
     const int r = q / CPR;
     const int c = (q - r * CPR) ^ (r & 15);
-    dma16_buf(rsrc, c * 8 < kv ? r * v.stride * 2 + c * 16 : (int)0x7FFFFFF0, dst + i * 1024);
+    const int off = c * 8 < kv ? r * v.stride * 2 + c * 16 : (int)0x7FFFFFF0;
+    if constexpr (NT)
+      dma16_buf_nt(rsrc, off, dst + i * 1024);
+    else
+      dma16_buf(rsrc, off, dst + i * 1024);
   }
 }
 
@@ -170,7 +176,7 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
   const int xa = lh ^ (lr & 15);
   for (int it = 0; it < num_iters; ++it) {
     const TensorView in = ir.read_acquire();
-    load_tile_swz<MBLK, K>(in, xs, kv);
+    load_tile_swz<MBLK, K, !IR::kFromQueue>(in, xs, kv);
     __builtin_amdgcn_s_waitcnt(kWaitAll);
     __syncthreads();
     ir.read_release();  // the tile is in LDS: hand the input slot back at once
