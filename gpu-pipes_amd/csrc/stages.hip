@@ -95,11 +95,17 @@ __global__ __launch_bounds__(kStageThreads) void concat_kernel(const half_t* a, 
 // Copy pipelines over the queue topologies of the reference's apps.  Every
 // stage copies 128-row tiles; pipeline g of P moves tiles g, g+P, ...
 //  * ROUTE_IDENT (2 stages): x -> q -> out
-//    (misc_tests/pipeval/pipe_val_ext.cu:65-149).
+//    (misc_tests/pipeval/pipe_val_ext.cu:65-149).  Pipeline g moves one
+//    contiguous chunk of ceil(T / P) tiles, read with read_striped_input
+//    (common/pipes.cuh:21-25), the reference apps' input striping.
 //  * ROUTE_BROADCAST (3 stages): x -> q (one producer, two consumers) -> out
 //    and -> out2, the MpmcRingQueue<E, N, 1, 2> of
 //    apps/bert_addln_ffn/pipelined/bert_addln_ffn_pl.cuh:55 and
 //    apps/nerf_a/pipelined/nerf_a_pl.cuh:55.
+//  * ROUTE_DRAIN (3 stages): the broadcast with its second consumer writing
+//    to a NullWriter (common/pipes.cuh:104-108) -- the reference's
+//    dummy_consumer (bert_addln_ffn_pl.cuh:178-187), which keeps a
+//    two-consumer queue draining; out2 is not written.
 //  * ROUTE_SPLIT (5 stages): x -> q0 -> 3 workers (SplitQueueReader, round
 //    robin) -> q1 (SplitQueueWriter, round robin) -> one reader in sequence
 //    order -> out, the split write of bert_addln_ffn_pl.cuh:121.
@@ -131,9 +137,13 @@ struct RouteArgs {
   int max_pipes;
 };
 
+constexpr int route_stages(int route) {
+  return route == GP_ROUTE_IDENT ? 2 : (route == GP_ROUTE_SPLIT ? 2 + kSplitWorkers : 3);
+}
+
 template <int ROUTE>
 __global__ __launch_bounds__(kStageThreads) void route_kernel(RouteArgs a) {
-  constexpr int S = ROUTE == GP_ROUTE_IDENT ? 2 : (ROUTE == GP_ROUTE_BROADCAST ? 3 : 2 + kSplitWorkers);
+  constexpr int S = route_stages(ROUTE);
   const Role r = assign_role(a.ctl, S, a.ctx, a.max_pipes);
   if (r.pipe < 0) return;
   const int64_t T = (a.M + MBLK - 1) / MBLK, P = r.npipes, g = r.pipe;
@@ -143,19 +153,26 @@ __global__ __launch_bounds__(kStageThreads) void route_kernel(RouteArgs a) {
   auto input = [&]() { return MemoryReader((half_t*)a.x + g * tile, P * tile, 128, MBLK, a.M - g * MBLK, P * MBLK); };
   auto output = [&](half_t* base) { return MemoryWriter(base + g * tile, P * tile, 128); };
   if constexpr (ROUTE == GP_ROUTE_IDENT) {
+    // contiguous chunks: pipeline g moves tiles [g C, g C + C) of C = ceil(T / P)
+    const int64_t C = (T + P - 1) / P;
+    const int nc = g * C < T ? (int)(T - g * C < C ? T - g * C : C) : 0;
     if (r.stage == 0) {
-      MemoryReader ir = input();
+      MemoryReader ir = read_striped_input((half_t*)a.x, (int)g, (int)C, MBLK, 128, a.M);
       QueueWriter<IdentQueue> ow(&q->ident, &a.ctx);
-      pipe_copy_n(ir, ow, nt, 128);
+      pipe_copy_n(ir, ow, nc, 128);
     } else {
       QueueReader<IdentQueue> ir(&q->ident, &a.ctx);
-      MemoryWriter ow = output(a.out);
-      pipe_copy_n(ir, ow, nt, 128);
+      MemoryWriter ow((half_t*)a.out + g * C * tile, tile, 128);
+      pipe_copy_n(ir, ow, nc, 128);
     }
-  } else if constexpr (ROUTE == GP_ROUTE_BROADCAST) {
+  } else if constexpr (ROUTE == GP_ROUTE_BROADCAST || ROUTE == GP_ROUTE_DRAIN) {
     if (r.stage == 0) {
       MemoryReader ir = input();
       QueueWriter<BcastQueue> ow(&q->bcast, &a.ctx);
+      pipe_copy_n(ir, ow, nt, 128);
+    } else if (ROUTE == GP_ROUTE_DRAIN && r.stage == 2) {
+      QueueReader<BcastQueue> ir(&q->bcast, &a.ctx);
+      NullWriter ow;
       pipe_copy_n(ir, ow, nt, 128);
     } else {
       QueueReader<BcastQueue> ir(&q->bcast, &a.ctx);
@@ -346,7 +363,7 @@ hipError_t concat_launch(int64_t M, int64_t N0, int64_t N1, const void* a, const
 template <int ROUTE>
 static int route_launch(int64_t M, const void* x, void* out, void* out2, int max_pipes, int dev, int num_cus,
                         hipStream_t s) {
-  constexpr int S = ROUTE == GP_ROUTE_IDENT ? 2 : (ROUTE == GP_ROUTE_BROADCAST ? 3 : 2 + kSplitWorkers);
+  constexpr int S = route_stages(ROUTE);
   auto kern = route_kernel<ROUTE>;
   int per_cu = 0;
   hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kStageThreads, 0);
@@ -386,6 +403,7 @@ int pipe_route_run(int64_t M, const void* x, void* out, void* out2, int route, i
     case GP_ROUTE_IDENT: return route_launch<GP_ROUTE_IDENT>(M, x, out, out2, max_pipes, dev, num_cus, s);
     case GP_ROUTE_BROADCAST: return route_launch<GP_ROUTE_BROADCAST>(M, x, out, out2, max_pipes, dev, num_cus, s);
     case GP_ROUTE_SPLIT: return route_launch<GP_ROUTE_SPLIT>(M, x, out, out2, max_pipes, dev, num_cus, s);
+    case GP_ROUTE_DRAIN: return route_launch<GP_ROUTE_DRAIN>(M, x, out, out2, max_pipes, dev, num_cus, s);
     default: return fail(GP_ERR_INVALID_ARG, "unknown route %d", route);
   }
 }

@@ -326,9 +326,10 @@ __device__ void pipe_layer_norm(TensorView gamma, TensorView beta, IR& ir, OW& o
   for (int it = 0; it < num_iters; ++it) {
     const TensorView in = ir.read_acquire();
     const TensorView ot = ow.write_acquire(in.rows);
+    const int nrows = in.rows < ot.rows ? in.rows : ot.rows;  // a NullWriter takes no rows
     for (int r0 = 0; r0 < MBLK; r0 += kStageThreads / 16) {
       const int r = r0 + rsub;
-      const bool valid = r < in.rows;
+      const bool valid = r < nrows;
       float x[NV][8];
       float s = 0.f;
 #pragma unroll
@@ -383,7 +384,8 @@ __device__ void pipe_add_n(IR0& ir0, IR1& ir1, OW& ow, int num_iters, int n) {
     const TensorView b = ir1.read_acquire();
     const int rows = a.rows < b.rows ? a.rows : b.rows;
     const TensorView c = ow.write_acquire(rows);
-    for (int i = threadIdx.x; i < rows * vpr; i += kStageThreads) {
+    const int n = rows < c.rows ? rows : c.rows;  // a NullWriter takes no rows
+    for (int i = threadIdx.x; i < n * vpr; i += kStageThreads) {
       const int r = i / vpr, v = i - r * vpr;
       const h8 x = *(const h8*)(a.data + (int64_t)r * a.stride + 8 * v);
       const h8 y = *(const h8*)(b.data + (int64_t)r * b.stride + 8 * v);
@@ -413,7 +415,8 @@ __device__ void pipe_concat_n(IR0& ir0, IR1& ir1, OW& ow, int num_iters, int n0,
     const TensorView b = ir1.read_acquire();
     const int rows = a.rows < b.rows ? a.rows : b.rows;
     const TensorView c = ow.write_acquire(rows);
-    for (int i = threadIdx.x; i < rows * vo; i += kStageThreads) {
+    const int n = rows < c.rows ? rows : c.rows;  // a NullWriter takes no rows
+    for (int i = threadIdx.x; i < n * vo; i += kStageThreads) {
       const int r = i / vo, v = i - r * vo;
       const h8 x = v < v0 ? *(const h8*)(a.data + (int64_t)r * a.stride + 8 * v)
                           : *(const h8*)(b.data + (int64_t)r * b.stride + 8 * (v - v0));
@@ -439,7 +442,8 @@ __device__ void pipe_copy_n(IR& ir, OW& ow, int num_iters, int n) {
   for (int it = 0; it < num_iters; ++it) {
     const TensorView a = ir.read_acquire();
     const TensorView c = ow.write_acquire(a.rows);
-    for (int i = threadIdx.x; i < a.rows * vpr; i += kStageThreads) {
+    const int n = a.rows < c.rows ? a.rows : c.rows;  // a NullWriter takes no rows
+    for (int i = threadIdx.x; i < n * vpr; i += kStageThreads) {
       const int r = i / vpr, v = i - r * vpr;
       *(h8*)(c.data + (int64_t)r * c.stride + 8 * v) = *(const h8*)(a.data + (int64_t)r * a.stride + 8 * v);
     }

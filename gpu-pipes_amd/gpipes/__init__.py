@@ -39,7 +39,7 @@ IMPL_PIPELINED = 1
 IMPL_PIPELINED_SPLIT_LN = 2
 _IMPLS = {"fused": IMPL_FUSED, "pipelined": IMPL_PIPELINED, "pipelined_split_ln": IMPL_PIPELINED_SPLIT_LN}
 ACTS = {"none": 0, "relu": 1, "gelu_tanh": 2, "sigmoid": 3}
-ROUTES = {"ident": 0, "broadcast": 1, "split": 2}
+ROUTES = {"ident": 0, "broadcast": 1, "split": 2, "drain": 3}
 
 
 class GpipesError(RuntimeError):
@@ -299,8 +299,9 @@ def pipe_ident(x, max_pipes=0, out=None):
 
 
 def pipe_route(x, route="ident", max_pipes=0):
-    """Copy x[M,128] through a queue topology (ident / broadcast / split); returns
-    (out, out2) -- out2 is None except for the two-consumer broadcast."""
+    """Copy x[M,128] through a queue topology (ident / broadcast / split / drain); returns
+    (out, out2) -- out2 is None except for the two-consumer broadcast (the drain's second
+    consumer discards its tiles)."""
     _check_input("x", x)
     M, D = x.shape
     if D != 128:

@@ -308,11 +308,16 @@ int gp_pipe_ident(int64_t M, const void* x, void* out, int max_pipes, void* stre
 #define GP_ROUTE_SPLIT 2     /* x -> queue -> 3 workers round robin (SplitQueueReader) ->    */
                              /* queue written round robin (SplitQueueWriter,                 */
                              /* bert_addln_ffn_pl.cuh:121) -> out in sequence order          */
+#define GP_ROUTE_DRAIN 3     /* the broadcast with the second consumer discarding its tiles  */
+                             /* (NullWriter; dummy_consumer, bert_addln_ffn_pl.cuh:178-187);  */
+                             /* out2 is not written                                          */
 
 /*
  * Copy pipelines over the queue topologies the reference's apps use; out
  * (and out2 for GP_ROUTE_BROADCAST) must equal x bit for bit.  The exercise
- * of the queue library's multi-consumer and split reader / writer paths.
+ * of the queue library's multi-consumer and split reader / writer paths,
+ * the striped input reader (GP_ROUTE_IDENT) and the null writer
+ * (GP_ROUTE_DRAIN; out2 may then be NULL).
  */
 int gp_pipe_route(int64_t M, const void* x, void* out, void* out2, int route, int max_pipes, void* stream);
 
