@@ -6,12 +6,22 @@
 //   mgn_mlp_cc [NI=1000] [edge|node|linears] [fused|pipelined|pipelined_split_ln] [M]
 //
 // Inputs are deterministic (not random) fp16 values; the driver measures
-// speed only -- parity is the job of the test suite.
+// speed only.
+//
+//   mgn_mlp_cc check DIR
+//
+// runs one call through the C++ wrappers of include/gpipes.hpp on inputs read
+// from DIR (raw fp16 files x, w1, b1, w2, b2, w3, b3 [, gamma, beta] and a
+// text file `shape` holding "M K ln impl") and writes the result to DIR/out:
+// mgn_fullmlp_out / mgn_linears_out for K = 384 with the fused impl (the
+// reference's operator names), mgn_mlp_out otherwise.  It then checks that a
+// misaligned x makes the wrapper throw gpipes::Error with GP_ERR_ALIGN.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <string>
 #include <vector>
 
 #include "../../include/gpipes.hpp"
@@ -50,7 +60,74 @@ static std::vector<uint16_t> fill(size_t n, float scale, uint32_t seed) {
   return v;
 }
 
+static std::vector<uint16_t> read_file(const std::string& path, size_t n) {
+  std::vector<uint16_t> v(n);
+  FILE* f = std::fopen(path.c_str(), "rb");
+  if (!f || std::fread(v.data(), 2, n, f) != n) {
+    std::fprintf(stderr, "cannot read %zu halves from %s\n", n, path.c_str());
+    std::exit(1);
+  }
+  std::fclose(f);
+  return v;
+}
+
+static int check_mode(const std::string& dir) {
+  long long M = 0, K = 0;
+  int ln = 0, impl = GP_IMPL_FUSED;
+  FILE* f = std::fopen((dir + "/shape").c_str(), "r");
+  if (!f || std::fscanf(f, "%lld %lld %d %d", &M, &K, &ln, &impl) != 4) {
+    std::fprintf(stderr, "cannot read %s/shape\n", dir.c_str());
+    return 1;
+  }
+  std::fclose(f);
+  void* x = upload(read_file(dir + "/x", (size_t)M * K));
+  void* w1 = upload(read_file(dir + "/w1", (size_t)K * 128));
+  void* b1 = upload(read_file(dir + "/b1", 128));
+  void* w2 = upload(read_file(dir + "/w2", 128 * 128));
+  void* b2 = upload(read_file(dir + "/b2", 128));
+  void* w3 = upload(read_file(dir + "/w3", 128 * 128));
+  void* b3 = upload(read_file(dir + "/b3", 128));
+  void* gamma = ln ? upload(read_file(dir + "/gamma", 128)) : nullptr;
+  void* beta = ln ? upload(read_file(dir + "/beta", 128)) : nullptr;
+  void* out = nullptr;
+  HIP_OK(hipMalloc(&out, (size_t)M * 128 * 2 + 16));
+  hipStream_t s;
+  HIP_OK(hipStreamCreate(&s));
+  try {
+    if (K == 384 && impl == GP_IMPL_FUSED && ln) {
+      gpipes::mgn_fullmlp_out(M, x, w1, b1, w2, b2, w3, b3, gamma, beta, out, s);
+      std::printf("called mgn_fullmlp_out\n");
+    } else if (K == 384 && impl == GP_IMPL_FUSED) {
+      gpipes::mgn_linears_out(M, x, w1, b1, w2, b2, w3, b3, out, s);
+      std::printf("called mgn_linears_out\n");
+    } else {
+      gpipes::mgn_mlp_out(M, K, x, w1, b1, w2, b2, w3, b3, gamma, beta, out, 1e-5f, impl, s);
+      std::printf("called mgn_mlp_out impl %d\n", impl);
+    }
+    gpipes::pipeline_check(s);
+  } catch (const gpipes::Error& e) {
+    std::fprintf(stderr, "unexpected: %s\n", e.what());
+    return 1;
+  }
+  std::vector<uint16_t> y((size_t)M * 128);
+  HIP_OK(hipMemcpy(y.data(), out, y.size() * 2, hipMemcpyDeviceToHost));
+  FILE* o = std::fopen((dir + "/out").c_str(), "wb");
+  if (!o || std::fwrite(y.data(), 2, y.size(), o) != y.size()) return 1;
+  std::fclose(o);
+  // A misaligned input must throw, not abort or launch.
+  int code = 0;
+  try {
+    gpipes::mgn_mlp_out(M, K, (char*)x + 2, w1, b1, w2, b2, w3, b3, gamma, beta, out, 1e-5f, impl, s);
+  } catch (const gpipes::Error& e) {
+    code = e.code();
+  }
+  std::printf("misaligned x: error code %d\n", code);
+  HIP_OK(hipStreamSynchronize(s));
+  return code == GP_ERR_ALIGN ? 0 : 1;
+}
+
 int main(int argc, char** argv) {
+  if (argc > 2 && !std::strcmp(argv[1], "check")) return check_mode(argv[2]);
   const int ni = argc > 1 ? std::atoi(argv[1]) : 1000;
   const char* which = argc > 2 ? argv[2] : "edge";
   const char* impl_s = argc > 3 ? argv[3] : "fused";
