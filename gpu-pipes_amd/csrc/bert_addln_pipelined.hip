@@ -92,7 +92,9 @@ __global__ __launch_bounds__(kStageThreads) void bert_addln_pipelined_kernel(Arg
   if (st == 0) {  // y0 = attn W0 + b0   (lin_attn_out, bert_addln_ffn_pl.cuh:92-101)
     MemoryReader ir = tiles_of(m.attn);
     QueueWriter<Q0> ow(&qs->q0, &a.ctx);
-    pipe_gemm_bias<MBLK, H>({(half_t*)m.w0, H, H}, vec(m.b0), ir, nr, ow, nt);
+    // four 64-row part buffers (within the W2 stage's LDS): the next tile's
+    // copies run under this tile's MFMAs
+    pipe_gemm_bias<MBLK, H, 4>({(half_t*)m.w0, H, H}, vec(m.b0), ir, nr, ow, nt);
     return;
   }
   if (st == 1) {  // y0 + x   (add0, :103-111)
@@ -143,6 +145,7 @@ __global__ __launch_bounds__(kStageThreads) void bert_addln_pipelined_kernel(Arg
 
 template <int ACT>
 static int run(const BertAddlnArgs& m, int dev, int num_cus, hipStream_t s) {
+  static_assert(gemm_stage_lds<MBLK, H, 4>() <= gemm_stage_lds<MBLK, FF>(), "W0's part buffers fit the W2 stage's LDS");
   constexpr int lds = gemm_stage_lds<MBLK, FF>() + gemm_param_lds<MBLK>();
   auto kern = bert_addln_pipelined_kernel<ACT>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);

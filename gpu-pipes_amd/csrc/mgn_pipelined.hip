@@ -50,6 +50,10 @@ struct Queues {
   LnQueue lnq;
 };
 
+// Layer-1 workers read X through three 64-row part buffers, so the copies of
+// the next tile (from HBM) run under the MFMAs of the current one.
+constexpr int kL1Bufs = 3;
+
 // Layer-1 workers per pipeline: 2 for K > 128 (1 in the reference's split layout).
 template <int K, bool SPLIT>
 constexpr int layer1_workers() {
@@ -86,7 +90,7 @@ __global__ __launch_bounds__(kStageThreads) void mgn_pipelined_kernel(Args a) {
     MemoryReader ir((half_t*)m.x + first * MBLK * K, W1 * NP * MBLK * K, K, MBLK, m.M - first * MBLK,
                     W1 * NP * MBLK);
     SplitQueueWriter<Queue1> ow(&qs->q12, &a.ctx, w, W1);
-    pipe_gemm_bias_relu<MBLK, K>({(half_t*)m.w1, D, K}, {(half_t*)m.b1, 1, 1}, ir, ar, ow, cnt);
+    pipe_gemm_bias_relu<MBLK, K, kL1Bufs>({(half_t*)m.w1, D, K}, {(half_t*)m.b1, 1, 1}, ir, ar, ow, cnt);
   } else if (r.stage == W1) {
     QueueReader<Queue1> ir(&qs->q12, &a.ctx);
     QueueWriter<Queue> ow(&qs->q23, &a.ctx);
@@ -115,7 +119,7 @@ __global__ __launch_bounds__(kStageThreads) void mgn_pipelined_kernel(Args a) {
 template <int K, bool LN, bool SPLIT>
 static int run(const MgnArgs& m, int dev, int num_cus, hipStream_t s) {
   constexpr int S = layer1_workers<K, SPLIT>() + (SPLIT ? 2 + NLN : 2);
-  constexpr int lds = gemm_stage_lds<MBLK, K>() + kGemmParamLds;
+  constexpr int lds = gemm_stage_lds<MBLK, K, kL1Bufs>() + kGemmParamLds;
   auto kern = mgn_pipelined_kernel<K, LN, SPLIT>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (e != hipSuccess) return fail_hip(e, "hipFuncSetAttribute");

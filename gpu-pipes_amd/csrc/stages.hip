@@ -56,6 +56,10 @@ struct OptionalReader : MemoryReader {
   }
 };
 
+// The whole-matrix linear reads its input from memory: three 64-row part
+// buffers let the next tile's copies run under this tile's MFMAs.
+constexpr int kLinearBufs = 3;
+
 template <int K, int ACT, bool LN>
 __global__ __launch_bounds__(kStageThreads) void linear_kernel(LinearArgs a) {
   const TileWalk tw = tile_walk(a.M);
@@ -67,9 +71,9 @@ __global__ __launch_bounds__(kStageThreads) void linear_kernel(LinearArgs a) {
   const TensorView w{(half_t*)a.w, 128, K}, b{(half_t*)a.b, 1, 1};
   if constexpr (LN) {
     const TensorView g{(half_t*)a.gamma, 1, 1}, be{(half_t*)a.beta, 1, 1};
-    pipe_gemm_bias_layer_norm<MBLK, K>(w, b, g, be, a.eps, ir, ar, ow, tw.nt);
+    pipe_gemm_bias_layer_norm<MBLK, K, kLinearBufs>(w, b, g, be, a.eps, ir, ar, ow, tw.nt);
   } else {
-    pipe_gemm_bias_act<MBLK, K, ACT>(w, b, ir, ar, ow, tw.nt);
+    pipe_gemm_bias_act<MBLK, K, ACT, kLinearBufs>(w, b, ir, ar, ow, tw.nt);
   }
 }
 
@@ -209,7 +213,7 @@ static int persistent_grid(int64_t M, int num_cus, int per_cu) {
 
 template <int K, int ACT, bool LN>
 static hipError_t launch_linear(const LinearArgs& a, int num_cus, hipStream_t s) {
-  constexpr int lds = gemm_stage_lds<MBLK, K>() + kGemmParamLds;
+  constexpr int lds = gemm_stage_lds<MBLK, K, kLinearBufs>() + kGemmParamLds;
   auto kern = linear_kernel<K, ACT, LN>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (e != hipSuccess) return e;

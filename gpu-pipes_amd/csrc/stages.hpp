@@ -69,9 +69,13 @@ constexpr int kStageThreads = 256;
 constexpr int kSlabStride = 64 * 2 + 16;  // padded LDS row of a transposed 64-k weight slab
 
 // LDS bytes of a GEMM stage with an MBLK x K input tile and N = 128 outputs.
-template <int MBLK, int K>
+// NB > 0: the input is staged through NB buffers of 64 rows (at least
+// MBLK / 64 of them), so the next tile's copies overlap this tile's MFMAs.
+template <int MBLK, int K, int NB = 0>
 constexpr int gemm_stage_lds() {
-  return MBLK * K * 2 > 128 * kSlabStride ? MBLK * K * 2 : 128 * kSlabStride;
+  constexpr int rows = (NB > MBLK / 64 ? NB : MBLK / 64) * 64;
+  constexpr int tile = (NB > 0 ? rows : MBLK) * K * 2;
+  return tile > 128 * kSlabStride ? tile : 128 * kSlabStride;
 }
 // bias/gamma/beta + the LayerNorm partials of MBLK rows
 template <int MBLK>
@@ -147,14 +151,33 @@ __device__ __forceinline__ void load_param(const TensorView& p, GP_LDS float* ds
   for (int i = threadIdx.x; i < n; i += kStageThreads) dst[i] = p.data ? (float)p.data[p.stride ? i : 0] : 0.f;
 }
 
-template <int MBLK, int K, int ACT, bool LN, typename IR, typename AR, typename OW>
+// One GEMM stage over num_iters tiles: out = act(in . W + b [+ acc]) or
+// LayerNorm(in . W + b).
+//
+// NB > 0 with an input read from memory (whose next tile is always there):
+// the tile is copied in 64-row parts through NB part buffers (at least
+// MBLK / 64), and the copies of tile i+1 are issued while tile i is
+// multiplied -- parts whose buffers are free at once before the MFMAs, the
+// others as each part of tile i is done.  The input of a memory-fed first
+// stage streams from HBM, so this takes its copy latency off the pipeline's
+// pace.  Queue inputs (and NB = 0) take one tile at a time: acquire, copy,
+// release, multiply, so a stage never waits for a next tile before its
+// current one is out.
+template <int MBLK, int K, int ACT, bool LN, int NB, typename IR, typename AR, typename OW>
 __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView gamma, TensorView beta, float eps,
                                 IR& ir, AR& ar, OW& ow, int num_iters) {
   constexpr int N = 128;
   constexpr int RB = MBLK / 32;
   static_assert(MBLK % 32 == 0 && MBLK <= 128, "MBLK must be 32, 64, 96 or 128");
+  constexpr bool PF = NB > 0 && !IR::kFromQueue;
+  static_assert(NB == 0 || MBLK % 64 == 0, "prefetching works in 64-row parts");
+  constexpr int H = PF ? MBLK / 64 : 1;             // parts per tile
+  constexpr int NBUF = PF ? (NB > H ? NB : H) : 1;  // part buffers
+  constexpr int PROWS = PF ? 64 : MBLK;             // rows per part
+  constexpr int PB = PROWS * K * 2;                 // bytes per part buffer
+  constexpr int RBP = PROWS / 32;                   // 32-row blocks per part
   GP_LDS char* xs = dyn_lds();
-  GP_LDS float* prm = (GP_LDS float*)(xs + gemm_stage_lds<MBLK, K>());
+  GP_LDS float* prm = (GP_LDS float*)(xs + gemm_stage_lds<MBLK, K, NB>());
   // The weight view's row count is the layer's real K: input columns past it
   // are zero-filled (their weight rows are zero too).
   const int kv = weight.rows < K ? weight.rows : K;
@@ -173,13 +196,44 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
   }
   __syncthreads();
 
+  // Part h of a tile view: rows [PROWS h, PROWS h + PROWS) into buffer `buf`.
+  auto copy_part = [&](const TensorView& v, int h, int buf) {
+    const int r0 = PROWS * h;
+    const TensorView pv{v.rows > r0 ? v.data + (int64_t)r0 * v.stride : v.data, v.stride, v.rows - r0};
+    load_tile_swz<PROWS, K, !IR::kFromQueue>(pv, xs + buf * PB, kv);
+  };
+
   const int xa = lh ^ (lr & 15);
+  TensorView cur{};
+  int pb = 0;  // buffer of part 0 of the current tile (PF)
+  if constexpr (PF) {
+    if (num_iters > 0) {
+      cur = ir.read_acquire();
+      ir.read_release();
+#pragma unroll
+      for (int h = 0; h < H; ++h) copy_part(cur, h, h);
+    }
+  }
   for (int it = 0; it < num_iters; ++it) {
-    const TensorView in = ir.read_acquire();
-    load_tile_swz<MBLK, K, !IR::kFromQueue>(in, xs, kv);
-    __builtin_amdgcn_s_waitcnt(kWaitAll);
-    __syncthreads();
-    ir.read_release();  // the tile is in LDS: hand the input slot back at once
+    const bool more = it + 1 < num_iters;
+    TensorView nxt{};
+    const int npb = (pb + H) % NBUF;
+    if constexpr (PF) {
+      __builtin_amdgcn_s_waitcnt(kWaitAll);
+      __syncthreads();  // every part of the tile is in LDS
+      if (more) {
+        nxt = ir.read_acquire();
+        ir.read_release();
+#pragma unroll
+        for (int h = 0; h < NBUF - H && h < H; ++h) copy_part(nxt, h, (npb + h) % NBUF);
+      }
+    } else {
+      cur = ir.read_acquire();
+      copy_part(cur, 0, 0);
+      __builtin_amdgcn_s_waitcnt(kWaitAll);
+      __syncthreads();
+      ir.read_release();  // the tile is in LDS: hand the input slot back at once
+    }
 
     // accumulators start at bias (+ the accumulator tile, pipe_gemm.cuh:128-146)
     f16x acc[RB];
@@ -205,12 +259,25 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
     ar.read_release();
 
 #pragma unroll
-    for (int s = 0; s < K / 16; ++s) {
-      const int off = ((2 * s) & ~15) * 16 + (((2 * s) ^ xa) & 15) * 16;
+    for (int h = 0; h < H; ++h) {
+      const GP_LDS char* xp = xs + ((pb + h) % NBUF) * PB;
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        const h8 b = *(const GP_LDS h8*)(xs + (32 * rb + lr) * (K * 2) + off);
-        acc[rb] = mfma32(wf[s], b, acc[rb]);
+      for (int s = 0; s < K / 16; ++s) {
+        const int off = ((2 * s) & ~15) * 16 + (((2 * s) ^ xa) & 15) * 16;
+#pragma unroll
+        for (int rp = 0; rp < RBP; ++rp) {
+          const h8 b = *(const GP_LDS h8*)(xp + (32 * rp + lr) * (K * 2) + off);
+          acc[RBP * h + rp] = mfma32(wf[s], b, acc[RBP * h + rp]);
+        }
+      }
+      if constexpr (PF) {
+        // part h's buffer is free once every wave is past its MFMAs: part
+        // h + NBUF - H of the next tile goes there
+        const int hn = h + NBUF - H;
+        if (hn < H && more) {
+          __syncthreads();
+          copy_part(nxt, hn, (pb + h) % NBUF);
+        }
       }
     }
 
@@ -251,54 +318,68 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
       }
     }
 
-    const TensorView ot = ow.write_acquire(in.rows);
+    // Stores: v_permlane32_swap trades groups g = 2q+1 of the lower wave half
+    // for groups g = 2q of the upper half, so each lane holds the eight
+    // consecutive features 32 wave + 16 q + 8 lh + (0..7) of its row and
+    // writes them with one 16-byte store.
+    const TensorView ot = ow.write_acquire(cur.rows);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       const int r = 32 * rb + lr;
-      if (r < ot.rows) {
+      u32x2 o[4];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          f4 v;
+      for (int g = 0; g < 4; ++g) {
+        f4 v;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = LN ? acc[rb][4 * g + e] : apply_act(acc[rb][4 * g + e], ACT);
-          *(h4*)(ot.data + (int64_t)r * ot.stride + fq + 8 * g) = __builtin_convertvector(v, h4);
-        }
+        for (int e = 0; e < 4; ++e) v[e] = LN ? acc[rb][4 * g + e] : apply_act(acc[rb][4 * g + e], ACT);
+        o[g] = __builtin_bit_cast(u32x2, __builtin_convertvector(v, h4));
+      }
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const auto lo = __builtin_amdgcn_permlane32_swap(o[2 * q][0], o[2 * q + 1][0], false, false);
+        const auto hi = __builtin_amdgcn_permlane32_swap(o[2 * q][1], o[2 * q + 1][1], false, false);
+        const u32x4 w = {(unsigned)lo[0], (unsigned)hi[0], (unsigned)lo[1], (unsigned)hi[1]};
+        if (r < ot.rows) *(u32x4*)(ot.data + (int64_t)r * ot.stride + 32 * wave + 16 * q + 8 * lh) = w;
       }
     }
     ow.write_release();
     __syncthreads();  // LDS tile / LN partials are reused by the next iteration
+    if constexpr (PF) {
+      pb = npb;
+      cur = nxt;
+    }
   }
 }
 
 // pipe_gemm_bias_relu.cuh:85-192: out = relu(in . W + b).
-template <int MBLK, int K, typename IR, typename AR, typename OW>
+template <int MBLK, int K, int NB = 0, typename IR, typename AR, typename OW>
 __device__ void pipe_gemm_bias_relu(TensorView weight, TensorView bias, IR& ir, AR& ar, OW& ow, int num_iters) {
-  gemm_stage_impl<MBLK, K, ACT_RELU, false>(weight, bias, {}, {}, 0.f, ir, ar, ow, num_iters);
+  gemm_stage_impl<MBLK, K, ACT_RELU, false, NB>(weight, bias, {}, {}, 0.f, ir, ar, ow, num_iters);
 }
 
 // pipe_gemm_bias.cuh:85-191: out = in . W + b.
-template <int MBLK, int K, typename IR, typename AR, typename OW>
+template <int MBLK, int K, int NB = 0, typename IR, typename AR, typename OW>
 __device__ void pipe_gemm_bias(TensorView weight, TensorView bias, IR& ir, AR& ar, OW& ow, int num_iters) {
-  gemm_stage_impl<MBLK, K, ACT_NONE, false>(weight, bias, {}, {}, 0.f, ir, ar, ow, num_iters);
+  gemm_stage_impl<MBLK, K, ACT_NONE, false, NB>(weight, bias, {}, {}, 0.f, ir, ar, ow, num_iters);
 }
 
 // pipe_gemm.cuh:78-183: out = in . W (+ accumulator tile from ar).
-template <int MBLK, int K, typename IR, typename AR, typename OW>
+template <int MBLK, int K, int NB = 0, typename IR, typename AR, typename OW>
 __device__ void pipe_gemm(TensorView weight, IR& ir, AR& ar, OW& ow, int num_iters) {
-  gemm_stage_impl<MBLK, K, ACT_NONE, false>(weight, {}, {}, {}, 0.f, ir, ar, ow, num_iters);
+  gemm_stage_impl<MBLK, K, ACT_NONE, false, NB>(weight, {}, {}, {}, 0.f, ir, ar, ow, num_iters);
 }
 
 // Generic activation epilogue (GELU / sigmoid heads of the later apps).
-template <int MBLK, int K, int ACT, typename IR, typename AR, typename OW>
+template <int MBLK, int K, int ACT, int NB = 0, typename IR, typename AR, typename OW>
 __device__ void pipe_gemm_bias_act(TensorView weight, TensorView bias, IR& ir, AR& ar, OW& ow, int num_iters) {
-  gemm_stage_impl<MBLK, K, ACT, false>(weight, bias, {}, {}, 0.f, ir, ar, ow, num_iters);
+  gemm_stage_impl<MBLK, K, ACT, false, NB>(weight, bias, {}, {}, 0.f, ir, ar, ow, num_iters);
 }
 
 // pipe_gemm_bias_layer_norm.cuh:100-249: out = LayerNorm(in . W + b) * gamma + beta.
-template <int MBLK, int K, typename IR, typename AR, typename OW>
+template <int MBLK, int K, int NB = 0, typename IR, typename AR, typename OW>
 __device__ void pipe_gemm_bias_layer_norm(TensorView weight, TensorView bias, TensorView gamma, TensorView beta,
                                           float eps, IR& ir, AR& ar, OW& ow, int num_iters) {
-  gemm_stage_impl<MBLK, K, ACT_NONE, true>(weight, bias, gamma, beta, eps, ir, ar, ow, num_iters);
+  gemm_stage_impl<MBLK, K, ACT_NONE, true, NB>(weight, bias, gamma, beta, eps, ir, ar, ow, num_iters);
 }
 
 // ---------------------------------------------------------------------------
