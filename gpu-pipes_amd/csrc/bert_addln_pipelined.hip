@@ -116,8 +116,9 @@ __global__ __launch_bounds__(kStageThreads) void bert_addln_pipelined_kernel(Arg
   if (st < NF1) {  // act(h0 W1 + b1), output columns [128 st, 128 st + 128)   (y1w1_relu, :128-137)
     QueueReader<Q2> ir(&qs->q2, &a.ctx);
     QueueWriter<Q3> ow(&qs->q3, &a.ctx, 128 * st);
-    pipe_gemm_bias_act<MBLK, H, ACT>({(half_t*)m.w1 + 128 * st, FF, H}, vec(m.b1 ? (const half_t*)m.b1 + 128 * st : nullptr),
-                                      ir, nr, ow, nt);
+    // two tile buffers: a tile already in the queue is copied under the MFMAs
+    pipe_gemm_bias_act<MBLK, H, ACT, 4>({(half_t*)m.w1 + 128 * st, FF, H},
+                                         vec(m.b1 ? (const half_t*)m.b1 + 128 * st : nullptr), ir, nr, ow, nt);
     return;
   }
   st -= NF1;

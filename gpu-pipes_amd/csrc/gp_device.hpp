@@ -185,10 +185,13 @@ __device__ __forceinline__ constexpr int c_row(int v, int lh) {
 
 __device__ __forceinline__ float relu(float v) { return v > 0.f ? v : 0.f; }
 
-template <typename T>
-__device__ __forceinline__ T xor_lane32(T v) {
-  // exchange with the lane 32 positions away (the other half of the wave)
-  return __shfl_xor(v, 32, 64);
+// x + (x of the lane 32 positions away), in every lane: one
+// v_permlane32_swap (a VALU exchange of the two wave halves) instead of an
+// LDS permute.
+__device__ __forceinline__ float sum_lane_halves(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (unsigned)p[0]) + __builtin_bit_cast(float, (unsigned)p[1]);
 }
 
 }  // namespace gp

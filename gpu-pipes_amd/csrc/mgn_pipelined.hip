@@ -53,6 +53,9 @@ struct Queues {
 // Layer-1 workers read X through three 64-row part buffers, so the copies of
 // the next tile (from HBM) run under the MFMAs of the current one.
 constexpr int kL1Bufs = 3;
+// Layers 2 and 3 keep two 128-row tile buffers: a tile that is already in
+// the queue is copied under the MFMAs of the one before it.
+constexpr int kQBufs = 4;
 
 // Layer-1 workers per pipeline: 2 for K > 128 (1 in the reference's split layout).
 template <int K, bool SPLIT>
@@ -94,17 +97,17 @@ __global__ __launch_bounds__(kStageThreads) void mgn_pipelined_kernel(Args a) {
   } else if (r.stage == W1) {
     QueueReader<Queue1> ir(&qs->q12, &a.ctx);
     QueueWriter<Queue> ow(&qs->q23, &a.ctx);
-    pipe_gemm_bias_relu<MBLK, D>({(half_t*)m.w2, D, D}, {(half_t*)m.b2, 1, 1}, ir, ar, ow, nt);
+    pipe_gemm_bias_relu<MBLK, D, kQBufs>({(half_t*)m.w2, D, D}, {(half_t*)m.b2, 1, 1}, ir, ar, ow, nt);
   } else if (r.stage == W1 + 1) {
     QueueReader<Queue> ir(&qs->q23, &a.ctx);
     const TensorView w3{(half_t*)m.w3, D, D}, b3{(half_t*)m.b3, 1, 1};
     if constexpr (SPLIT) {
       QueueWriter<LnQueue> ow(&qs->lnq, &a.ctx);
-      pipe_gemm_bias<MBLK, D>(w3, b3, ir, ar, ow, nt);
+      pipe_gemm_bias<MBLK, D, kQBufs>(w3, b3, ir, ar, ow, nt);
     } else {
       MemoryWriter ow(out + g * MBLK * D, NP * MBLK * D, D);
-      if constexpr (LN) pipe_gemm_bias_layer_norm<MBLK, D>(w3, b3, gamma, beta, m.eps, ir, ar, ow, nt);
-      else pipe_gemm_bias<MBLK, D>(w3, b3, ir, ar, ow, nt);
+      if constexpr (LN) pipe_gemm_bias_layer_norm<MBLK, D, kQBufs>(w3, b3, gamma, beta, m.eps, ir, ar, ow, nt);
+      else pipe_gemm_bias<MBLK, D, kQBufs>(w3, b3, ir, ar, ow, nt);
     }
   } else if constexpr (SPLIT) {
     // LayerNorm worker w takes queue sequence numbers w, w + NLN, ...
@@ -119,7 +122,8 @@ __global__ __launch_bounds__(kStageThreads) void mgn_pipelined_kernel(Args a) {
 template <int K, bool LN, bool SPLIT>
 static int run(const MgnArgs& m, int dev, int num_cus, hipStream_t s) {
   constexpr int S = layer1_workers<K, SPLIT>() + (SPLIT ? 2 + NLN : 2);
-  constexpr int lds = gemm_stage_lds<MBLK, K, kL1Bufs>() + kGemmParamLds;
+  constexpr int l1 = gemm_stage_lds<MBLK, K, kL1Bufs>(), l23 = gemm_stage_lds<MBLK, D, kQBufs>();
+  constexpr int lds = (l1 > l23 ? l1 : l23) + kGemmParamLds;
   auto kern = mgn_pipelined_kernel<K, LN, SPLIT>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (e != hipSuccess) return fail_hip(e, "hipFuncSetAttribute");

@@ -65,7 +65,8 @@ __device__ __forceinline__ void half_layer(const NerfAArgs& m, int li, int j, in
   NullReader nr;
   const TensorView w{(half_t*)m.w[li] + 128 * j, W, kvalid};
   const TensorView b{m.b[li] ? (half_t*)m.b[li] + 128 * j : nullptr, 1, 1};
-  pipe_gemm_bias_relu<MBLK, K>(w, b, ir, nr, ow, nt);
+  // fragment prefetch depth 2: keeps the stage within three workgroups per CU
+  pipe_gemm_bias_relu<MBLK, K, 0, 2>(w, b, ir, nr, ow, nt);
 }
 
 __global__ __launch_bounds__(kStageThreads) void nerf_a_pipelined_kernel(Args a) {

@@ -186,6 +186,13 @@ struct RingQueue {
     stores_complete();  // this workgroup's loads of the payload have returned
     if (threadIdx.x == 0) qcommit(&slot(seq).empty, ctx.epoch, seq < N);
   }
+  // Thread-level, no wait: have all NP producers of `seq` committed?  A
+  // consumer that sees true may load the payload after l1_invalidate().
+  __device__ bool full_peek(int64_t seq, const QueueCtx& ctx) {
+    const unsigned long long v = __hip_atomic_load(&slot(seq).full.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return qcount(v, ctx.epoch) >= (uint32_t)(seq / N + 1) * NP;
+  }
+  __device__ int rows_of(int64_t seq) { return *(volatile int*)&slot(seq).rows; }
 };
 
 // ---------------------------------------------------------------------------
@@ -261,6 +268,13 @@ struct QueueReader {
     ++seq_n;
   }
   __device__ void reset() { seq_n = 0; }
+  // Early look at the next tile (for a stage that copies it while working
+  // on the current one).  peek_next: thread-level, no wait, before the
+  // current tile's read_release.  After that release the peeked tile is the
+  // current one: view(rows) is its payload; rows() (thread-level) its rows.
+  __device__ bool peek_next() { return q->full_peek(seq_n + 1, *ctx); }
+  __device__ int rows() { return q->rows_of(seq_n); }
+  __device__ TensorView view(int rows_) { return q->slot(seq_n).data.as_view(rows_); }
 };
 
 // pipes.cuh:45-58: worker `seq_off` of `seq_stride` takes sequence numbers
@@ -287,6 +301,10 @@ struct SplitQueueReader {
     seq_n += seq_stride;
   }
   __device__ void reset() { seq_n = seq_off; }
+  // As QueueReader's: the next tile of this worker is seq_n + seq_stride.
+  __device__ bool peek_next() { return q->full_peek(seq_n + seq_stride, *ctx); }
+  __device__ int rows() { return q->rows_of(seq_n); }
+  __device__ TensorView view(int rows_) { return q->slot(seq_n).data.as_view(rows_); }
 };
 
 // ---------------------------------------------------------------------------

@@ -151,6 +151,34 @@ __device__ __forceinline__ void load_param(const TensorView& p, GP_LDS float* ds
   for (int i = threadIdx.x; i < n; i += kStageThreads) dst[i] = p.data ? (float)p.data[p.stride ? i : 0] : 0.f;
 }
 
+// The k-loop of a tile part: RBP 32-row blocks share the A operand (weight
+// fragments wf[0..KS)); B fragments come from LDS through ld(rp, s), read PF
+// k-steps ahead.  The scheduling barriers pin the issue order (PF * RBP
+// reads, then per k-step RBP MFMAs followed by the reads of step s + PF), so
+// LDS reads stay in flight behind the MFMAs; left to itself the scheduler
+// reads each step's fragments just before their MFMAs and waits for them.
+template <int KS, int RBP, int PF, typename LD>
+__device__ __forceinline__ void stage_mfma_loop(const h8* wf, LD ld, f16x* acc) {
+  static_assert(PF >= 1 && PF <= KS, "prefetch depth");
+  h8 q[PF][RBP];
+#pragma unroll
+  for (int p = 0; p < PF; ++p)
+#pragma unroll
+    for (int rp = 0; rp < RBP; ++rp) q[p][rp] = ld(rp, p);
+  __builtin_amdgcn_sched_group_barrier(0x100, PF * RBP, 0);
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+#pragma unroll
+    for (int rp = 0; rp < RBP; ++rp) acc[rp] = mfma32(wf[s], q[s % PF][rp], acc[rp]);
+    __builtin_amdgcn_sched_group_barrier(0x008, RBP, 0);
+    if (s + PF < KS) {
+#pragma unroll
+      for (int rp = 0; rp < RBP; ++rp) q[s % PF][rp] = ld(rp, s + PF);
+      __builtin_amdgcn_sched_group_barrier(0x100, RBP, 0);
+    }
+  }
+}
+
 // One GEMM stage over num_iters tiles: out = act(in . W + b [+ acc]) or
 // LayerNorm(in . W + b).
 //
@@ -161,19 +189,25 @@ __device__ __forceinline__ void load_param(const TensorView& p, GP_LDS float* ds
 // others as each part of tile i is done.  The input of a memory-fed first
 // stage streams from HBM, so this takes its copy latency off the pipeline's
 // pace.  Queue inputs (and NB = 0) take one tile at a time: acquire, copy,
-// release, multiply, so a stage never waits for a next tile before its
-// current one is out.
-template <int MBLK, int K, int ACT, bool LN, int NB, typename IR, typename AR, typename OW>
+// release, multiply.  With NB >= 2 MBLK / 64 a queue-fed stage keeps two
+// tile buffers: while it waits for the current tile's copy it also looks
+// (without waiting) at the next tile's counter, and if that tile is ready it
+// is copied into the other buffer under this tile's MFMAs and epilogue.  A
+// stage never waits for a next tile before its current one is out.  LPF is
+// the depth (k-steps) of the LDS fragment prefetch of the MFMA loop; 0 picks
+// 2 for four row blocks per part, else 4.
+template <int MBLK, int K, int ACT, bool LN, int NB, int LPF, typename IR, typename AR, typename OW>
 __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView gamma, TensorView beta, float eps,
                                 IR& ir, AR& ar, OW& ow, int num_iters) {
   constexpr int N = 128;
   constexpr int RB = MBLK / 32;
   static_assert(MBLK % 32 == 0 && MBLK <= 128, "MBLK must be 32, 64, 96 or 128");
   constexpr bool PF = NB > 0 && !IR::kFromQueue;
+  constexpr bool QPF = IR::kFromQueue && NB >= 2 * (MBLK / 64);  // queue input, two tile buffers
   static_assert(NB == 0 || MBLK % 64 == 0, "prefetching works in 64-row parts");
-  constexpr int H = PF ? MBLK / 64 : 1;             // parts per tile
-  constexpr int NBUF = PF ? (NB > H ? NB : H) : 1;  // part buffers
-  constexpr int PROWS = PF ? 64 : MBLK;             // rows per part
+  constexpr int H = PF ? MBLK / 64 : 1;                      // parts per tile
+  constexpr int NBUF = PF ? (NB > H ? NB : H) : (QPF ? 2 : 1);  // part buffers
+  constexpr int PROWS = PF ? 64 : MBLK;                      // rows per part
   constexpr int PB = PROWS * K * 2;                 // bytes per part buffer
   constexpr int RBP = PROWS / 32;                   // 32-row blocks per part
   GP_LDS char* xs = dyn_lds();
@@ -195,6 +229,29 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
     load_param(beta, prm + 2 * N, N);
   }
   __syncthreads();
+  // This lane's 16 features' bias (and LayerNorm gamma, beta) are kept in
+  // registers for all tiles -- except in 64-row stages, which are built to
+  // run three workgroups per CU and have no registers to spare; they read
+  // them from LDS for every tile.
+  constexpr bool RP = MBLK >= 128;
+  float bias_r[RP ? 16 : 1], gm_r[RP && LN ? 16 : 1], bt_r[RP && LN ? 16 : 1];
+  if constexpr (RP) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bias_r[4 * g + e] = prm[fq + 8 * g + e];
+        if constexpr (LN) {
+          gm_r[4 * g + e] = prm[N + fq + 8 * g + e];
+          bt_r[4 * g + e] = prm[2 * N + fq + 8 * g + e];
+        }
+      }
+  }
+  // parameter j (0 bias, 1 gamma, 2 beta) of this lane's feature i (0..15)
+  auto param = [&](int j, int i) -> float {
+    if constexpr (RP) return j == 0 ? bias_r[i] : (j == 1 ? gm_r[LN ? i : 0] : bt_r[LN ? i : 0]);
+    else return prm[j * N + fq + 8 * (i / 4) + i % 4];
+  };
 
   // Part h of a tile view: rows [PROWS h, PROWS h + PROWS) into buffer `buf`.
   auto copy_part = [&](const TensorView& v, int h, int buf) {
@@ -205,7 +262,9 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
 
   const int xa = lh ^ (lr & 15);
   TensorView cur{};
-  int pb = 0;  // buffer of part 0 of the current tile (PF)
+  int pb = 0;        // buffer of part 0 of the current tile (PF); tile buffer (QPF)
+  bool pre = false;  // QPF: the current tile was copied during the previous one
+  __shared__ int qflag[2];
   if constexpr (PF) {
     if (num_iters > 0) {
       cur = ir.read_acquire();
@@ -217,6 +276,7 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
   for (int it = 0; it < num_iters; ++it) {
     const bool more = it + 1 < num_iters;
     TensorView nxt{};
+    bool qnext = false;  // QPF: the next tile is being copied
     const int npb = (pb + H) % NBUF;
     if constexpr (PF) {
       __builtin_amdgcn_s_waitcnt(kWaitAll);
@@ -226,6 +286,29 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
         ir.read_release();
 #pragma unroll
         for (int h = 0; h < NBUF - H && h < H; ++h) copy_part(nxt, h, (npb + h) % NBUF);
+      }
+    } else if constexpr (QPF) {
+      if (!pre) {
+        cur = ir.read_acquire();
+        copy_part(cur, 0, pb);
+      }
+      if (threadIdx.x == 0) {
+        // both loads are in flight with the tile copy
+        const bool pk = more && ir.peek_next();
+        const int rw = pre ? ir.rows() : 0;
+        qflag[0] = pk;
+        qflag[1] = rw;
+      }
+      __builtin_amdgcn_s_waitcnt(kWaitAll);
+      __syncthreads();
+      if (pre) cur = ir.view(qflag[1]);
+      qnext = qflag[0] != 0;
+      ir.read_release();  // the tile is in LDS: hand the input slot back at once
+      if (qnext) {
+        // the peeked tile is now the reader's current one; copy all MBLK rows
+        // (rows past its count are never stored)
+        l1_invalidate();
+        copy_part(ir.view(MBLK), 0, pb ^ 1);
       }
     } else {
       cur = ir.read_acquire();
@@ -241,9 +324,7 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[rb][4 * g + e] = prm[fq + 8 * g + e];
+      for (int i = 0; i < 16; ++i) acc[rb][i] = param(0, i);
       if (at.data != nullptr) {
         const int r = 32 * rb + lr;
         if (r < at.rows) {
@@ -260,16 +341,11 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
 
 #pragma unroll
     for (int h = 0; h < H; ++h) {
-      const GP_LDS char* xp = xs + ((pb + h) % NBUF) * PB;
-#pragma unroll
-      for (int s = 0; s < K / 16; ++s) {
+      const GP_LDS char* xp = xs + ((pb + h) % NBUF) * PB + lr * (K * 2);
+      stage_mfma_loop<K / 16, RBP, LPF ? LPF : (RBP >= 4 ? 2 : 4)>(wf, [&](int rp, int s) {
         const int off = ((2 * s) & ~15) * 16 + (((2 * s) ^ xa) & 15) * 16;
-#pragma unroll
-        for (int rp = 0; rp < RBP; ++rp) {
-          const h8 b = *(const GP_LDS h8*)(xp + (32 * rp + lr) * (K * 2) + off);
-          acc[RBP * h + rp] = mfma32(wf[s], b, acc[RBP * h + rp]);
-        }
-      }
+        return *(const GP_LDS h8*)(xp + rp * (32 * K * 2) + off);
+      }, acc + RBP * h);
       if constexpr (PF) {
         // part h's buffer is free once every wave is past its MFMAs: part
         // h + NBUF - H of the next tile goes there
@@ -288,7 +364,7 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
         float s0 = 0.f;
 #pragma unroll
         for (int v = 0; v < 16; ++v) s0 += acc[rb][v];
-        s0 += xor_lane32(s0);
+        s0 = sum_lane_halves(s0);
         const float m0 = s0 * (1.f / 32.f);
         float q0 = 0.f;
 #pragma unroll
@@ -296,7 +372,7 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
           const float d = acc[rb][v] - m0;
           q0 = __builtin_fmaf(d, d, q0);
         }
-        q0 += xor_lane32(q0);
+        q0 = sum_lane_halves(q0);
         if (lh == 0) lnpart[(32 * rb + lr) * 4 + wave] = f2{m0, q0};
       }
       __syncthreads();
@@ -308,13 +384,10 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
         const float d0 = p0[0] - mu, d1 = p1[0] - mu, d2 = p2[0] - mu, d3 = p3[0] - mu;
         const float m2 = (p0[1] + p1[1]) + (p2[1] + p3[1]) + 32.f * (d0 * d0 + d1 * d1 + d2 * d2 + d3 * d3);
         const float rstd = rsqrtf(m2 * (1.f / N) + eps);
+        const float nmr = -mu * rstd;
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int f = fq + 8 * g + e;
-            acc[rb][4 * g + e] = (acc[rb][4 * g + e] - mu) * rstd * prm[N + f] + prm[2 * N + f];
-          }
+        for (int i = 0; i < 16; ++i)
+          acc[rb][i] = __builtin_fmaf(__builtin_fmaf(acc[rb][i], rstd, nmr), param(1, i), param(2, i));
       }
     }
 
@@ -347,39 +420,42 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
     if constexpr (PF) {
       pb = npb;
       cur = nxt;
+    } else if constexpr (QPF) {
+      pre = qnext;
+      if (pre) pb ^= 1;
     }
   }
 }
 
 // pipe_gemm_bias_relu.cuh:85-192: out = relu(in . W + b).
-template <int MBLK, int K, int NB = 0, typename IR, typename AR, typename OW>
+template <int MBLK, int K, int NB = 0, int LPF = 0, typename IR, typename AR, typename OW>
 __device__ void pipe_gemm_bias_relu(TensorView weight, TensorView bias, IR& ir, AR& ar, OW& ow, int num_iters) {
-  gemm_stage_impl<MBLK, K, ACT_RELU, false, NB>(weight, bias, {}, {}, 0.f, ir, ar, ow, num_iters);
+  gemm_stage_impl<MBLK, K, ACT_RELU, false, NB, LPF>(weight, bias, {}, {}, 0.f, ir, ar, ow, num_iters);
 }
 
 // pipe_gemm_bias.cuh:85-191: out = in . W + b.
-template <int MBLK, int K, int NB = 0, typename IR, typename AR, typename OW>
+template <int MBLK, int K, int NB = 0, int LPF = 0, typename IR, typename AR, typename OW>
 __device__ void pipe_gemm_bias(TensorView weight, TensorView bias, IR& ir, AR& ar, OW& ow, int num_iters) {
-  gemm_stage_impl<MBLK, K, ACT_NONE, false, NB>(weight, bias, {}, {}, 0.f, ir, ar, ow, num_iters);
+  gemm_stage_impl<MBLK, K, ACT_NONE, false, NB, LPF>(weight, bias, {}, {}, 0.f, ir, ar, ow, num_iters);
 }
 
 // pipe_gemm.cuh:78-183: out = in . W (+ accumulator tile from ar).
-template <int MBLK, int K, int NB = 0, typename IR, typename AR, typename OW>
+template <int MBLK, int K, int NB = 0, int LPF = 0, typename IR, typename AR, typename OW>
 __device__ void pipe_gemm(TensorView weight, IR& ir, AR& ar, OW& ow, int num_iters) {
-  gemm_stage_impl<MBLK, K, ACT_NONE, false, NB>(weight, {}, {}, {}, 0.f, ir, ar, ow, num_iters);
+  gemm_stage_impl<MBLK, K, ACT_NONE, false, NB, LPF>(weight, {}, {}, {}, 0.f, ir, ar, ow, num_iters);
 }
 
 // Generic activation epilogue (GELU / sigmoid heads of the later apps).
-template <int MBLK, int K, int ACT, int NB = 0, typename IR, typename AR, typename OW>
+template <int MBLK, int K, int ACT, int NB = 0, int LPF = 0, typename IR, typename AR, typename OW>
 __device__ void pipe_gemm_bias_act(TensorView weight, TensorView bias, IR& ir, AR& ar, OW& ow, int num_iters) {
-  gemm_stage_impl<MBLK, K, ACT, false, NB>(weight, bias, {}, {}, 0.f, ir, ar, ow, num_iters);
+  gemm_stage_impl<MBLK, K, ACT, false, NB, LPF>(weight, bias, {}, {}, 0.f, ir, ar, ow, num_iters);
 }
 
 // pipe_gemm_bias_layer_norm.cuh:100-249: out = LayerNorm(in . W + b) * gamma + beta.
-template <int MBLK, int K, int NB = 0, typename IR, typename AR, typename OW>
+template <int MBLK, int K, int NB = 0, int LPF = 0, typename IR, typename AR, typename OW>
 __device__ void pipe_gemm_bias_layer_norm(TensorView weight, TensorView bias, TensorView gamma, TensorView beta,
                                           float eps, IR& ir, AR& ar, OW& ow, int num_iters) {
-  gemm_stage_impl<MBLK, K, ACT_NONE, true, NB>(weight, bias, gamma, beta, eps, ir, ar, ow, num_iters);
+  gemm_stage_impl<MBLK, K, ACT_NONE, true, NB, LPF>(weight, bias, gamma, beta, eps, ir, ar, ow, num_iters);
 }
 
 // ---------------------------------------------------------------------------
