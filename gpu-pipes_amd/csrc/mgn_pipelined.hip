@@ -41,7 +41,10 @@ constexpr int NLN = 5;  // LayerNorm workers per pipeline in the split layout (m
 
 using QEntry = QueueEntry2D<MBLK, D>;
 using Queue = RingQueue<QEntry, 2>;              // q23 (qlen = 2, mgn_fullmlp_pl.cuh:32); q12 with one writer
-using Queue1 = RingQueue<QEntry, 4>;             // q12 written round robin by up to three layer-1 workers
+// q12, written round robin by the layer-1 workers.  Two slots: a deeper q12
+// was no faster and kept more queue lines in L2, so more of them were written
+// back to HBM (WRITE_SIZE 575 MiB per call with four slots, 440 with two).
+using Queue1 = RingQueue<QEntry, 2>;
 using LnQueue = RingQueue<QEntry, NLN + 1>;      // lnq (ln_qlen = n_ln_cols + 1, :33)
 
 struct Queues {
