@@ -11,8 +11,8 @@
 // write q12 through a split queue writer, so no partial sums pass through fp16
 // queues.  A stage's time per tile is mostly fixed cost (queue hand-offs, the
 // tile copy, store completion), so more workers per pipeline mean fewer
-// pipelines: at K = 384 two workers measured 0.88 ms, one 0.92 ms and three
-// 1.16 ms per call.  The split layout keeps the reference's shape, one
+// pipelines: at K = 384 two workers measured 0.41 ms, one 0.54 ms and three
+// 0.53 ms per call.  The split layout keeps the reference's shape, one
 // layer-1 block and five LayerNorm workers:
 //   X -> [Linear K->128 + ReLU] -q12-> [Linear] -q23-> [Linear] -lnq-> 5 x [LayerNorm] -> out
 // (mlp0_sm0 :83-101, mlp1_sm0 :146-160, mlp2_sm0 :162-181, ln_sm :183-203).
