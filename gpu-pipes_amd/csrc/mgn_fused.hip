@@ -169,9 +169,11 @@ __device__ __forceinline__ void store_relu_row(GP_LDS char* act_row, int fq, con
 // j < K/64 holds W1 rows [64j, 64j+64), then two slabs of W2 and two of W3.
 // All eight waves copy every slab (wave w copies feature octets w and w+8 of
 // the 64 rows); take(j, buf) then reads whatever fragments the caller needs.
-template <int K, typename Take>
+// pre() runs once the first slab's loads are issued (the bias / LayerNorm
+// parameter loads then share their latency).
+template <int K, typename Take, typename Pre>
 __device__ __forceinline__ void stage_weights(const Params& p, GP_LDS char* buf0, GP_LDS char* buf1, int wave,
-                                              int lane, Take take) {
+                                              int lane, Take take, Pre pre) {
   constexpr int NS1 = K / 64;
   constexpr int NS = NS1 + 4;
   auto slab_src = [&](int j) -> const half_t* {
@@ -191,6 +193,7 @@ __device__ __forceinline__ void stage_weights(const Params& p, GP_LDS char* buf0
         *(GP_LDS half_t*)(buf + (8 * (wave + 8 * i) + e) * SLAB_STRIDE + lane * 2) = v[i][e];
   };
   load_slab(0, va);
+  pre();
 #pragma unroll
   for (int j = 0; j < NS; ++j) {
     GP_LDS char* buf = (j & 1) ? buf1 : buf0;
@@ -276,15 +279,18 @@ void mgn_fused_kernel(Params p) {
   if (t0 >= ntiles) return;
   const int nt = (int)((ntiles - 1 - t0) / G + 1);  // tiles of this workgroup
 
-  if (tid < D) {
-    prm[0][tid] = (float)p.b1[tid];
-    prm[1][tid] = (float)p.b2[tid];
-    prm[2][tid] = (float)p.b3[tid];
-    if (LN) {
-      prm[3][tid] = (float)p.gamma[tid];
-      prm[4][tid] = (float)p.beta[tid];
+  // bias / LayerNorm parameters, loaded while the first weight slab is in flight
+  auto load_prm = [&]() {
+    if (tid < D) {
+      prm[0][tid] = (float)p.b1[tid];
+      prm[1][tid] = (float)p.b2[tid];
+      prm[2][tid] = (float)p.b3[tid];
+      if (LN) {
+        prm[3][tid] = (float)p.gamma[tid];
+        prm[4][tid] = (float)p.beta[tid];
+      }
     }
-  }
+  };
   if (tid == 0) sy = Sync{0, 0, 0, 0, 0, 0};
 
   const int fq = 32 * n + 4 * lh;  // 32x32 accumulator group g covers features fq + 8g + (0..3)
@@ -301,7 +307,7 @@ void mgn_fused_kernel(Params p) {
       if (j < NS1)
 #pragma unroll
         for (int sl = 0; sl < 4; ++sl) w1f[4 * j + sl] = slab_frag(buf, 32 * n + lr, 16 * sl + 8 * lh);
-    });
+    }, load_prm);
 #pragma unroll
     for (int s = 0; s < C::KS1; ++s) asm volatile("" : "+a"(w1f[s]));
 
@@ -460,7 +466,7 @@ void mgn_fused_kernel(Params p) {
 #pragma unroll
           for (int kl = 0; kl < 2; ++kl) w3f[fb][2 * half + kl] = slab_frag(buf, 16 * fb + l16, 32 * kl + 8 * q4);
       }
-    });
+    }, load_prm);
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) asm volatile("" : "+v"(w2f[s]));
 #pragma unroll
