@@ -474,6 +474,8 @@ def main():
                     help="untimed launches for this long between the warm-up and the timed region: the "
                          "engine clock swings for tens of ms after a burst starts (launches run fast, then "
                          "up to 1.5x slower, then settle), so the timed region starts in the steady state")
+    ap.add_argument("--dtype", choices=["f16", "bf16"], default="f16",
+                    help="element type of the MGN workloads (bf16: fused kernel, not the headline line)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-ref", action="store_true",
                     help="first run one plain 1 GiB device copy (a known-size reference kernel "
@@ -499,7 +501,11 @@ def main():
 
     dev = torch.device("cuda:0")
     M, K, ln = WORKLOADS[args.workload]
-    p = {k: (None if v is None else v.to(dev)) for k, v in mgn_params(K, seed=0, layernorm=ln).items()}
+    et = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    if et == torch.bfloat16 and (args.impl != "fused" or args.workload == "edge_gather"):
+        print("bf16 runs on the fused kernel (edge / node workloads) only", file=sys.stderr)
+        sys.exit(2)
+    p = {k: (None if v is None else v.to(dev)) for k, v in mgn_params(K, seed=0, layernorm=ln, dtype=et).items()}
     # Inputs resident in HBM.  The node batch (201 MB) would fit the 256 MB
     # MALL, so two input/output buffer pairs are rotated to keep it honest.
     nbuf = 2 if args.workload == "node" else 1
@@ -514,8 +520,8 @@ def main():
         src = torch.randint(0, GATHER_NODES, (M,), generator=g).to(dev)
         dst = torch.randint(0, GATHER_NODES, (M,), generator=g).to(dev)
     else:
-        xs = [normal_fp16(M, K, seed=i, device=dev) for i in range(nbuf)]
-    outs = [torch.empty((M, 128), dtype=torch.float16, device=dev) for _ in range(nbuf)]
+        xs = [normal_fp16(M, K, seed=i, device=dev, dtype=et) for i in range(nbuf)]
+    outs = [torch.empty((M, 128), dtype=et, device=dev) for _ in range(nbuf)]
 
     def step(i):
         b = i % nbuf
@@ -550,7 +556,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": args.dtype,
         "data": "synthetic (X~N(0,1), nn.Linear default init, seed 0)",
         "config": {"workload": f"mgn_{args.workload}_mlp", "M": M, "K": K,
                    **({"nodes": GATHER_NODES, "index": "int64"} if gather else {}),
@@ -562,12 +568,13 @@ def main():
             "kernel_ms_avg": avg_launch_ms, "kernel_ms_median": spread(launch_ms)["median"],
             "algorithmic_bytes_per_launch": bytes_,
         },
+        # the dense bf16 MFMA peak equals the fp16 one (2.5 PFLOP/s)
         "mfma": {"achieved_tflops": tflops, "peak_tflops": MFMA_F16_PEAK_TFLOPS,
                  "frac": tflops / MFMA_F16_PEAK_TFLOPS, "flops_per_launch": flops},
         "spread": spread(launch_ms),
         "settle": settle,
-        "cpu_baseline": None if args.no_cpu else cpu_baseline_torch_mgn(K, ln),
-        "cpu_baseline_oracle": None if args.no_cpu else cpu_baseline(K, ln),
+        "cpu_baseline": None if args.no_cpu or args.dtype != "f16" else cpu_baseline_torch_mgn(K, ln),
+        "cpu_baseline_oracle": None if args.no_cpu or args.dtype != "f16" else cpu_baseline(K, ln),
     }
     print(json.dumps(rec), flush=True)
 

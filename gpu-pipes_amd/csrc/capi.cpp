@@ -95,6 +95,9 @@ int run_mgn(const MgnArgs& a, int impl, hipStream_t stream) {
   if (rc != GP_OK) return rc;
   if (impl != GP_IMPL_FUSED && impl != GP_IMPL_PIPELINED && impl != GP_IMPL_PIPELINED_SPLIT_LN)
     return fail(GP_ERR_INVALID_ARG, "unknown impl %d", impl);
+  if (a.dtype != GP_DTYPE_F16 && a.dtype != GP_DTYPE_BF16) return fail(GP_ERR_INVALID_ARG, "unknown dtype %d", a.dtype);
+  if (a.dtype == GP_DTYPE_BF16 && impl != GP_IMPL_FUSED)
+    return fail(GP_ERR_INVALID_ARG, "bf16 runs on the fused kernel (impl %d) only", GP_IMPL_FUSED);
   if (a.M == 0) return GP_OK;
   int dev = 0, ncu = 0;
   rc = current_device_info(&dev, &ncu);
@@ -141,6 +144,14 @@ int gp_mgn_mlp_out(int64_t M, int64_t K, const void* x, const void* w1, const vo
                    const void* b2, const void* w3, const void* b3, const void* gamma, const void* beta,
                    float eps, void* out, int impl, void* stream) {
   MgnArgs a{M, K, x, w1, b1, w2, b2, w3, b3, gamma, beta, eps, out};
+  return run_mgn(a, impl, (hipStream_t)stream);
+}
+
+int gp_mgn_mlp_dtype_out(int64_t M, int64_t K, const void* x, const void* w1, const void* b1, const void* w2,
+                         const void* b2, const void* w3, const void* b3, const void* gamma, const void* beta,
+                         float eps, void* out, int impl, int dtype, void* stream) {
+  MgnArgs a{M, K, x, w1, b1, w2, b2, w3, b3, gamma, beta, eps, out};
+  a.dtype = dtype;
   return run_mgn(a, impl, (hipStream_t)stream);
 }
 

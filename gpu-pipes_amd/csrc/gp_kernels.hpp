@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/gpipes.h"
+
 namespace gp {
 
 // One MGN-shaped MLP call: x[M,K] -> Linear(K,128)+ReLU -> Linear(128,128)+ReLU
@@ -35,6 +37,7 @@ struct MgnArgs {
   unsigned long long* status = nullptr;
   uint32_t epoch = 0;
   int spin_limit = 0;
+  int dtype = GP_DTYPE_F16;  // element type of x, the weights and out (GP_DTYPE_BF16: fused kernel only)
 };
 
 // Persistent fused kernel (all layers in one workgroup per CU).

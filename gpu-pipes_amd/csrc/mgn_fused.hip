@@ -98,6 +98,34 @@ struct Sync {
   int abort;    // set when a wait exceeds its spin bound
 };
 
+// Element types.  Tiles, fragments and LDS hold raw 16-bit values (typed h8 /
+// h4 throughout); only the MFMAs, the fp32 -> 16-bit conversions and the
+// parameter loads depend on the type.
+struct ElemF16 {
+  __device__ static f16x mma32(h8 a, h8 b, f16x c) { return mfma32(a, b, c); }
+  __device__ static f4 mma16(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+  __device__ static h4 cvt4(f4 v) { return __builtin_convertvector(v, h4); }
+  // relu(round(x)) == round(relu(x)): the ReLU runs on the packed fp16 values
+  __device__ static h4 relu_cvt4(f4 v) { return __builtin_elementwise_max(cvt4(v), (h4){0, 0, 0, 0}); }
+  __device__ static float load(const half_t* p, int i) { return (float)p[i]; }
+};
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
+struct ElemBF16 {
+  __device__ static f16x mma32(h8 a, h8 b, f16x c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf8, a), __builtin_bit_cast(bf8, b), c, 0, 0, 0);
+  }
+  __device__ static f4 mma16(h8 a, h8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8, a), __builtin_bit_cast(bf8, b), c, 0, 0, 0);
+  }
+  // v_cvt_pk_bf16_f32: round to nearest even
+  __device__ static h4 cvt4(f4 v) { return __builtin_bit_cast(h4, __builtin_convertvector(v, bf4)); }
+  __device__ static h4 relu_cvt4(f4 v) { return cvt4(__builtin_elementwise_max(v, (f4){0.f, 0.f, 0.f, 0.f})); }
+  __device__ static float load(const half_t* p, int i) {
+    return __builtin_bit_cast(float, (unsigned)__builtin_bit_cast(unsigned short, p[i]) << 16);
+  }
+};
+
 // Accumulator initialised with the bias: C element 4g+e of a lane holds the
 // bias of feature fq + 8g + e (every row of the block shares it).
 __device__ __forceinline__ f16x bias_frag(const float* bias, int fq) {
@@ -118,7 +146,7 @@ __device__ __forceinline__ f16x bias_frag(const float* bias, int fq) {
 // flight behind every MFMA instead of the one or two the default schedule
 // leaves.  NPRE counts LDS reads the caller issues just before (the bias
 // fragments), which the scheduler places in the first group.
-template <int KS, int PF, int NPRE, int NHOOK, typename LD, typename HOOK>
+template <typename E, int KS, int PF, int NPRE, int NHOOK, typename LD, typename HOOK>
 __device__ __forceinline__ void gemm_2blk(const h8* wf, LD ld, f16x& acc0, f16x& acc1, HOOK hook) {
   static_assert(PF >= 1 && PF <= KS && NHOOK <= KS, "prefetch depth / hook steps");
   h8 q0[PF], q1[PF];
@@ -130,8 +158,8 @@ __device__ __forceinline__ void gemm_2blk(const h8* wf, LD ld, f16x& acc0, f16x&
   __builtin_amdgcn_sched_group_barrier(0x100, 2 * PF + NPRE, 0);
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    acc0 = mfma32(wf[s], q0[s % PF], acc0);
-    acc1 = mfma32(wf[s], q1[s % PF], acc1);
+    acc0 = E::mma32(wf[s], q0[s % PF], acc0);
+    acc1 = E::mma32(wf[s], q1[s % PF], acc1);
     __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     if (s + PF < KS) {
       q0[s % PF] = ld(0, s + PF);
@@ -145,22 +173,18 @@ __device__ __forceinline__ void gemm_2blk(const h8* wf, LD ld, f16x& acc0, f16x&
   }
 }
 
-template <int KS, int PF, int NPRE, typename LD>
+template <typename E, int KS, int PF, int NPRE, typename LD>
 __device__ __forceinline__ void gemm_2blk(const h8* wf, LD ld, f16x& acc0, f16x& acc1) {
-  gemm_2blk<KS, PF, NPRE, 0>(wf, ld, acc0, acc1, [](int) {});
+  gemm_2blk<E, KS, PF, NPRE, 0>(wf, ld, acc0, acc1, [](int) {});
 }
 
-// ReLU + fp16 rounding of an accumulator into this lane's row of an LDS
-// activation tile.  relu(round(x)) == round(relu(x)), so ReLU runs on the
-// packed fp16 values.
+// ReLU + 16-bit rounding of an accumulator into this lane's row of an LDS
+// activation tile.
+template <typename E>
 __device__ __forceinline__ void store_relu_row(GP_LDS char* act_row, int fq, const f16x& a) {
-  const h4 zero = {0, 0, 0, 0};
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const h4 o = __builtin_elementwise_max(
-        __builtin_convertvector((f4){a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]}, h4), zero);
-    *(GP_LDS h4*)(act_row + (fq + 8 * g) * 2) = o;
-  }
+  for (int g = 0; g < 4; ++g)
+    *(GP_LDS h4*)(act_row + (fq + 8 * g) * 2) = E::relu_cvt4((f4){a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]});
 }
 
 // Prologue shared by both stages: weights are row-major [K][128]; 64-k slabs
@@ -222,10 +246,6 @@ __device__ __forceinline__ float sum_lanes_16_32(float x) {
   return __builtin_bit_cast(float, (unsigned)b[0]) + __builtin_bit_cast(float, (unsigned)b[1]);
 }
 
-__device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
 // Stores output features [32j, 32j+32) of row l16 from the fp16 groups of a
 // 16x16 accumulator pair: hv[t] holds features 16(2j+t) + 4q4 + (0..3) in
 // lane (l16, q4).  v_permlane16_swap trades one group between lanes q4 and
@@ -242,7 +262,8 @@ __device__ __forceinline__ void store_row_pair(half_t* row, const h4 (&hv)[2], i
   if (ok) *(u32x4*)((char*)row + 64 * j + (q4 & 1) * 32 + (q4 >> 1) * 16) = w;
 }
 
-template <int K, bool LN, int GATHER_IDX = 0>  // GATHER_IDX: 0 = X given; 4 / 8 = gather, index bytes
+// GATHER_IDX: 0 = X given; 4 / 8 = gather, index bytes.  E: ElemF16 / ElemBF16.
+template <int K, bool LN, int GATHER_IDX = 0, typename E = ElemF16>
 __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void mgn_fused_kernel(Params p) {
   using C = Cfg<K>;
@@ -282,12 +303,12 @@ void mgn_fused_kernel(Params p) {
   // bias / LayerNorm parameters, loaded while the first weight slab is in flight
   auto load_prm = [&]() {
     if (tid < D) {
-      prm[0][tid] = (float)p.b1[tid];
-      prm[1][tid] = (float)p.b2[tid];
-      prm[2][tid] = (float)p.b3[tid];
+      prm[0][tid] = E::load(p.b1, tid);
+      prm[1][tid] = E::load(p.b2, tid);
+      prm[2][tid] = E::load(p.b3, tid);
       if (LN) {
-        prm[3][tid] = (float)p.gamma[tid];
-        prm[4][tid] = (float)p.beta[tid];
+        prm[3][tid] = E::load(p.gamma, tid);
+        prm[4][tid] = E::load(p.beta, tid);
       }
     }
   };
@@ -423,7 +444,7 @@ void mgn_fused_kernel(Params p) {
       gather_offsets(k + 1);
       const __amdgpu_buffer_rsrc_t nrsrc = tile_rsrc(k + 1);
       f16x acc0 = bias_frag(prm[0], fq), acc1 = acc0;
-      gemm_2blk<C::KS1, PF_L1, 4, C::DMA_PER_WAVE>(w1f, [&](int rb, int s) {
+      gemm_2blk<E, C::KS1, PF_L1, 4, C::DMA_PER_WAVE>(w1f, [&](int rb, int s) {
         const int off = (s >> 3) * XSEG + (((2 * s) ^ xa) & 15) * 16;
         return *(const GP_LDS h8*)(xs + xrow + rb * (32 * XROW) + off);
       }, acc0, acc1, [&](int ii) {
@@ -437,8 +458,8 @@ void mgn_fused_kernel(Params p) {
 
       // Handoff slot k%2 was last read by stage B for tile k-2.
       if (k >= 2) lds_wait_geq((GP_LDS int*)&sy.h_free, 4 * (k - 1), ab, lim);
-      store_relu_row(hand + arow0, fq, acc0);
-      store_relu_row(hand + arow1, fq, acc1);
+      store_relu_row<E>(hand + arow0, fq, acc0);
+      store_relu_row<E>(hand + arow1, fq, acc1);
       lds_signal((GP_LDS int*)&sy.h_full, lane);
     };
 
@@ -486,15 +507,15 @@ void mgn_fused_kernel(Params p) {
 
       // layer 2, features [32n, 32n+32) of all 64 rows, from the handoff tile
       f16x acc0 = bias_frag(prm[1], fq), acc1 = acc0;
-      gemm_2blk<D / 16, PF_L2, 4>(w2f, [&](int rb, int s) {
+      gemm_2blk<E, D / 16, PF_L2, 4>(w2f, [&](int rb, int s) {
         return *(const GP_LDS h8*)(hand + (rb ? arow1 : arow0) + (2 * s + lh) * 16);
       }, acc0, acc1);
       lds_signal((GP_LDS int*)&sy.h_free, lane);  // B operands are in registers: release the slot
 
       // exchange: act2 was last read (layer 3) for tile k-1
       if (k >= 1) lds_wait_geq((GP_LDS int*)&sy.x2_free, 4 * k, ab, lim);
-      store_relu_row((GP_LDS char*)act2 + arow0, fq, acc0);
-      store_relu_row((GP_LDS char*)act2 + arow1, fq, acc1);
+      store_relu_row<E>((GP_LDS char*)act2 + arow0, fq, acc0);
+      store_relu_row<E>((GP_LDS char*)act2 + arow1, fq, acc1);
       lds_signal((GP_LDS int*)&sy.x2_full, lane);
       lds_wait_geq((GP_LDS int*)&sy.x2_full, 4 * (k + 1), ab, lim);
 
@@ -508,7 +529,7 @@ void mgn_fused_kernel(Params p) {
       for (int fb = 0; fb < 8; ++fb) {
         y[fb] = *(const f4*)&prm[2][16 * fb + 4 * q4];  // bias of features 16fb + 4q4 + (0..3)
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) y[fb] = mfma16(w3f[fb][ks], bf[ks], y[fb]);
+        for (int ks = 0; ks < 4; ++ks) y[fb] = E::mma16(w3f[fb][ks], bf[ks], y[fb]);
       }
 
       const int64_t grow = (t0 + (int64_t)k * G) * TM + 16 * n + l16;
@@ -542,14 +563,14 @@ void mgn_fused_kernel(Params p) {
             f4 z;
 #pragma unroll
             for (int e = 0; e < 4; ++e) z[e] = __builtin_fmaf(__builtin_fmaf(y[fb][e], rstd, nmr), gm[e], bt[e]);
-            hv[t] = __builtin_convertvector(z, h4);
+            hv[t] = E::cvt4(z);
           }
           store_row_pair(orow, hv, j, q4, st);
         }
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const h4 hv[2] = {__builtin_convertvector(y[2 * j], h4), __builtin_convertvector(y[2 * j + 1], h4)};
+          const h4 hv[2] = {E::cvt4(y[2 * j]), E::cvt4(y[2 * j + 1])};
           store_row_pair(orow, hv, j, q4, st);
         }
       }
@@ -570,13 +591,13 @@ void mgn_fused_kernel(Params p) {
 // ---------------------------------------------------------------------------
 // Host launcher
 // ---------------------------------------------------------------------------
-template <int K, bool LN, int GI = 0>
+template <int K, bool LN, int GI = 0, typename E = fused::ElemF16>
 static hipError_t launch_fused(const MgnArgs& a, int grid, hipStream_t stream) {
   fused::Params p{(const half_t*)a.x,  (const half_t*)a.w1, (const half_t*)a.b1, (const half_t*)a.w2,
                   (const half_t*)a.b2, (const half_t*)a.w3, (const half_t*)a.b3, (const half_t*)a.gamma,
                   (const half_t*)a.beta, (half_t*)a.out, a.M, a.eps, (const half_t*)a.nf, a.N, a.src, a.dst,
                   a.status, a.epoch, a.spin_limit > 0 ? a.spin_limit : kSpinLimit};
-  hipLaunchKernelGGL((fused::mgn_fused_kernel<K, LN, GI>), dim3(grid), dim3(fused::NTHREADS), 0, stream, p);
+  hipLaunchKernelGGL((fused::mgn_fused_kernel<K, LN, GI, E>), dim3(grid), dim3(fused::NTHREADS), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -585,14 +606,24 @@ hipError_t mgn_fused_launch(const MgnArgs& a, int num_cus, hipStream_t stream) {
   const int64_t ntiles = (a.M + fused::TM - 1) / fused::TM;
   const int grid = (int)(ntiles < num_cus ? ntiles : num_cus);
   const bool ln = a.gamma != nullptr;
-  if (a.nf != nullptr) {  // gather front end (K = 384 = 3 x 128)
-    if (a.K != 384) return hipErrorInvalidValue;
+  if (a.nf != nullptr) {  // gather front end (K = 384 = 3 x 128), fp16
+    if (a.K != 384 || a.dtype != GP_DTYPE_F16) return hipErrorInvalidValue;
     if (a.idx_bytes == 4)
       return ln ? launch_fused<384, true, 4>(a, grid, stream) : launch_fused<384, false, 4>(a, grid, stream);
     if (a.idx_bytes == 8)
       return ln ? launch_fused<384, true, 8>(a, grid, stream) : launch_fused<384, false, 8>(a, grid, stream);
     return hipErrorInvalidValue;
   }
+  using B = fused::ElemBF16;
+  if (a.dtype == GP_DTYPE_BF16) {
+    switch (a.K) {
+      case 384: return ln ? launch_fused<384, true, 0, B>(a, grid, stream) : launch_fused<384, false, 0, B>(a, grid, stream);
+      case 256: return ln ? launch_fused<256, true, 0, B>(a, grid, stream) : launch_fused<256, false, 0, B>(a, grid, stream);
+      case 128: return ln ? launch_fused<128, true, 0, B>(a, grid, stream) : launch_fused<128, false, 0, B>(a, grid, stream);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  if (a.dtype != GP_DTYPE_F16) return hipErrorInvalidValue;
   switch (a.K) {
     case 384: return ln ? launch_fused<384, true>(a, grid, stream) : launch_fused<384, false>(a, grid, stream);
     case 256: return ln ? launch_fused<256, true>(a, grid, stream) : launch_fused<256, false>(a, grid, stream);

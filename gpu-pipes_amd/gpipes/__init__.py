@@ -65,6 +65,8 @@ def _load():
     L.gp_mgn_linears_out.restype = i32
     L.gp_mgn_mlp_out.argtypes = [i64, i64] + [vp] * 9 + [f32, vp, i32, vp]
     L.gp_mgn_mlp_out.restype = i32
+    L.gp_mgn_mlp_dtype_out.argtypes = [i64, i64] + [vp] * 9 + [f32, vp, i32, i32, vp]
+    L.gp_mgn_mlp_dtype_out.restype = i32
     L.gp_linear_out.argtypes = [i64, i64, vp, vp, vp, vp, i32, vp, vp]
     L.gp_linear_layer_norm_out.argtypes = [i64, i64] + [vp] * 5 + [f32, vp, vp]
     L.gp_layer_norm_out.argtypes = [i64, i64, vp, vp, vp, f32, vp, vp]
@@ -109,7 +111,7 @@ def _stream_ptr(t):
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
-def _check_input(name, t, shape=None):
+def _check_input(name, t, shape=None, dtype=torch.float16):
     # CHECK_CUDA / CHECK_CONTIGUOUS of mgn_fullmlp_pl_ext.cu:14-16, plus dtype/shape
     if not isinstance(t, torch.Tensor):
         raise RuntimeError(f"{name} must be a torch.Tensor")
@@ -117,8 +119,8 @@ def _check_input(name, t, shape=None):
         raise RuntimeError(f"{name} must be a CUDA tensor")
     if not t.is_contiguous():
         raise RuntimeError(f"{name} must be contiguous")
-    if t.dtype != torch.float16:
-        raise RuntimeError(f"{name} must be float16 (got {t.dtype})")
+    if t.dtype != dtype:
+        raise RuntimeError(f"{name} must be {str(dtype).replace('torch.', '')} (got {t.dtype})")
     if shape is not None and tuple(t.shape) != tuple(shape):
         raise RuntimeError(f"{name} must have shape {tuple(shape)} (got {tuple(t.shape)})")
 
@@ -127,35 +129,44 @@ def _ptr(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+_DTYPES = {torch.float16: 0, torch.bfloat16: 1}  # GP_DTYPE_F16, GP_DTYPE_BF16
+
+
 def mgn_mlp_out(x, w1, b1, w2, b2, w3, b3, gamma, beta, out, eps=1e-5, impl="fused"):
     """MgnMlp(K, [128,128,128], layernorm=gamma is not None) into ``out``.
 
     K = x.shape[1] in {128, 256, 384}; gamma/beta None -> no LayerNorm.
+    Every tensor is float16, or every tensor is bfloat16 (fused impl only:
+    gp_mgn_mlp_dtype_out).
     """
-    if x.dim() != 2:
-        raise RuntimeError("x must be 2-D [M, K]")
+    if not isinstance(x, torch.Tensor) or x.dim() != 2:
+        raise RuntimeError("x must be a 2-D tensor [M, K]")
     M, K = x.shape
-    _check_input("x", x)
-    _check_input("w1", w1, (K, 128))
-    _check_input("b1", b1, (128,))
-    _check_input("w2", w2, (128, 128))
-    _check_input("b2", b2, (128,))
-    _check_input("w3", w3, (128, 128))
-    _check_input("b3", b3, (128,))
+    dt = x.dtype if x.dtype in _DTYPES else torch.float16
+    _check_input("x", x, dtype=dt)
+    _check_input("w1", w1, (K, 128), dt)
+    _check_input("b1", b1, (128,), dt)
+    _check_input("w2", w2, (128, 128), dt)
+    _check_input("b2", b2, (128,), dt)
+    _check_input("w3", w3, (128, 128), dt)
+    _check_input("b3", b3, (128,), dt)
     if (gamma is None) != (beta is None):
         raise RuntimeError("gamma and beta must both be given or both be None")
     if gamma is not None:
-        _check_input("gamma", gamma, (128,))
-        _check_input("beta", beta, (128,))
-    _check_input("out", out, (M, 128))
+        _check_input("gamma", gamma, (128,), dt)
+        _check_input("beta", beta, (128,), dt)
+    _check_input("out", out, (M, 128), dt)
     devs = {t.device for t in (x, w1, b1, w2, b2, w3, b3, out) if t is not None}
     if len(devs) != 1:
         raise RuntimeError("all tensors must be on the same device")
     impl_id = _IMPLS.get(impl, impl)
     with torch.cuda.device(x.device):
-        rc = lib.gp_mgn_mlp_out(M, K, _ptr(x), _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2), _ptr(w3),
-                                _ptr(b3), _ptr(gamma), _ptr(beta), float(eps), _ptr(out), int(impl_id),
-                                ctypes.c_void_p(_stream_ptr(x)))
+        args = (M, K, _ptr(x), _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2), _ptr(w3), _ptr(b3), _ptr(gamma),
+                _ptr(beta), float(eps), _ptr(out), int(impl_id))
+        if dt == torch.float16:
+            rc = lib.gp_mgn_mlp_out(*args, ctypes.c_void_p(_stream_ptr(x)))
+        else:
+            rc = lib.gp_mgn_mlp_dtype_out(*args, _DTYPES[dt], ctypes.c_void_p(_stream_ptr(x)))
     _check(rc)
     return out
 

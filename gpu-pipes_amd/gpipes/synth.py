@@ -9,8 +9,9 @@ all fp16, as apps/mgn_fullmlp/pipelined/val.py:15-21 feeds them.
 import torch
 
 
-def mgn_params(K, seed=0, layernorm=True, device="cpu", affine_random=False):
-    """Parameters of MgnMlp(K, [128, 128, 128], layernorm) in kernel layout."""
+def mgn_params(K, seed=0, layernorm=True, device="cpu", affine_random=False, dtype=torch.float16):
+    """Parameters of MgnMlp(K, [128, 128, 128], layernorm) in kernel layout,
+    rounded to `dtype` (float16 or bfloat16)."""
     with torch.random.fork_rng(devices=[]):
         torch.manual_seed(seed)
         l1 = torch.nn.Linear(K, 128)
@@ -23,7 +24,7 @@ def mgn_params(K, seed=0, layernorm=True, device="cpu", affine_random=False):
                 lnm.bias.uniform_(-0.5, 0.5)
 
     def h(t):
-        return t.detach().to(torch.float16).contiguous().to(device)
+        return t.detach().to(dtype).contiguous().to(device)
 
     p = {
         "w1": h(l1.weight.t()), "b1": h(l1.bias),
@@ -63,11 +64,11 @@ def bert_params(H, FF, seed=0, init="bert", device="cpu", affine_random=False):
             "gamma": h(lnm.weight), "beta": h(lnm.bias)}
 
 
-def normal_fp16(M, K, seed=0, device="cpu"):
-    """X ~ N(0, 1) rounded to fp16, generated on `device` with a seeded generator."""
+def normal_fp16(M, K, seed=0, device="cpu", dtype=torch.float16):
+    """X ~ N(0, 1) rounded to fp16 (or `dtype`), generated on `device` with a seeded generator."""
     dev = torch.device(device)
     g = torch.Generator(device=dev).manual_seed(seed)
-    return torch.randn((M, K), generator=g, device=dev, dtype=torch.float32).to(torch.float16)
+    return torch.randn((M, K), generator=g, device=dev, dtype=torch.float32).to(dtype)
 
 
 def dlrm_params(widths, seed=0, init="xavier", device="cpu"):

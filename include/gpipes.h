@@ -41,6 +41,10 @@ extern "C" {
 #define GP_IMPL_PIPELINED_SPLIT_LN 2 /* the reference's layout: layer 3 feeds five         */
                                      /* LayerNorm workers through a round-robin split queue */
 
+/* Element types of gp_mgn_mlp_dtype_out (16-bit storage, fp32 accumulation). */
+#define GP_DTYPE_F16 0  /* IEEE binary16 */
+#define GP_DTYPE_BF16 1 /* bfloat16      */
+
 /* Activations of gp_linear_out. */
 #define GP_ACT_NONE 0
 #define GP_ACT_RELU 1
@@ -85,6 +89,22 @@ int gp_mgn_mlp_out(int64_t M, int64_t K, const void* x, const void* w1, const vo
                    const void* w2, const void* b2, const void* w3, const void* b3,
                    const void* gamma, const void* beta, float eps, void* out, int impl,
                    void* stream);
+
+/*
+ * gp_mgn_mlp_out with the element type of x, every weight / bias / gamma /
+ * beta and out given by `dtype`: GP_DTYPE_F16 (the same call as
+ * gp_mgn_mlp_out) or GP_DTYPE_BF16, which runs bf16 MFMAs with fp32
+ * accumulation and rounds the two hidden activations and the output to bf16
+ * (round to nearest even).  bf16 runs on the fused kernel only (impl
+ * GP_IMPL_FUSED; other impls return GP_ERR_INVALID_ARG).  No counterpart in
+ * the reference, whose extensions take fp16 tensors only; it is the bf16
+ * form of the same MgnMlp (common/mlps.py:3-20) for callers that keep their
+ * activations in bf16.
+ */
+int gp_mgn_mlp_dtype_out(int64_t M, int64_t K, const void* x, const void* w1, const void* b1,
+                         const void* w2, const void* b2, const void* w3, const void* b3,
+                         const void* gamma, const void* beta, float eps, void* out, int impl,
+                         int dtype, void* stream);
 
 /*
  * MeshGraphNet edge update with the gather front end fused in:

@@ -54,6 +54,15 @@ inline void mgn_mlp_out(int64_t M, int64_t K, const void* x, const void* w1, con
   check(gp_mgn_mlp_out(M, K, x, w1, b1, w2, b2, w3, b3, gamma, beta, eps, out, impl, stream));
 }
 
+// gp_mgn_mlp_dtype_out: the same MLP with every tensor in `dtype`
+// (GP_DTYPE_F16 or GP_DTYPE_BF16; bf16 on the fused kernel only).
+inline void mgn_mlp_dtype_out(int64_t M, int64_t K, const void* x, const void* w1, const void* b1, const void* w2,
+                              const void* b2, const void* w3, const void* b3, const void* gamma, const void* beta,
+                              void* out, int dtype, float eps = 1e-5f, int impl = GP_IMPL_FUSED,
+                              void* stream = nullptr) {
+  check(gp_mgn_mlp_dtype_out(M, K, x, w1, b1, w2, b2, w3, b3, gamma, beta, eps, out, impl, dtype, stream));
+}
+
 // common/pipe_gemm_bias_relu.cuh:85-192, pipe_gemm_bias.cuh:85-191, pipe_gemm.cuh:78-183
 inline void linear_out(int64_t M, int64_t K, const void* x, const void* w, const void* b, const void* acc, int act,
                        void* out, void* stream = nullptr) {

@@ -197,3 +197,7 @@ def errors(actual, expected):
 # Parity bar for fp16 I/O against the fp32 oracle (workload definition).
 MAX_ABS_TOL = 2e-2
 REL_L2_TOL = 5e-3
+# bf16 I/O: the same bar scaled by the ratio of the unit roundoffs,
+# 2^-8 (bfloat16, 8 significand bits) / 2^-11 (binary16) = 8.
+BF16_MAX_ABS_TOL = 8 * MAX_ABS_TOL
+BF16_REL_L2_TOL = 8 * REL_L2_TOL

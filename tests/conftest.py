@@ -23,6 +23,12 @@ def cuda():
     return torch.device("cuda:0")
 
 
+def bf16_to_f32(bits):
+    """uint16 bfloat16 bit patterns -> float32 values (exact: the upper half of the float)."""
+    import numpy as np
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
 def load_golden(name):
     import numpy as np
     with np.load(os.path.join(GOLDEN, name), allow_pickle=False) as z:

@@ -29,6 +29,9 @@ reference's own LayerNorm check types in (misc_tests/layer_norm/torch_val.py:88-
 repeated over 128 rows there, gamma = 1, beta = 0); its expected output is
 F.layer_norm in float64.
 
+The bf16 MGN fixtures are the same MgnMlp with inputs and parameters rounded to
+bfloat16 (stored as uint16 bit patterns), expected again from torch.nn in float64.
+
 The bert_addln_ffn fixtures follow apps/bert_addln_ffn/torch/model.py:3-20 and the
 nerf_a fixture apps/nerf_a/torch/model.py:5-38, each evaluated with torch.nn modules in
 float64 (the nerf_a weights are regenerated from the seed, as for NeRF).
@@ -98,6 +101,27 @@ def make_mgn_fixture(name, K, layernorm, seed, affine_random, eps=1e-5):
     for k, v in p.items():
         if v is not None:
             arrs[k] = v.numpy()
+    path = os.path.join(HERE, f"{name}.npz")
+    np.savez_compressed(path, **arrs)
+    return path
+
+
+def bf16_bits(t):
+    """bfloat16 tensor -> its uint16 bit patterns (numpy has no bfloat16)."""
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def make_mgn_bf16_fixture(name, K, seed, eps=1e-5):
+    """MgnMlp with bf16 inputs and parameters (stored as uint16 bit patterns,
+    key `dtype` = "bf16"); expected = torch.nn modules in float64 on the
+    bf16 values."""
+    p = mgn_params(K, seed=seed, layernorm=True, affine_random=True, dtype=torch.bfloat16)
+    x = normal_fp16(M_FIX, K, seed=seed + 1000, dtype=torch.bfloat16)
+    y = torch_mgn_f64(x, p, eps)
+    arrs = {"x": bf16_bits(x), "expected": y.numpy().astype(np.float64), "eps": np.float64(eps),
+            "dtype": np.array("bf16")}
+    for k, v in p.items():
+        arrs[k] = bf16_bits(v)
     path = os.path.join(HERE, f"{name}.npz")
     np.savez_compressed(path, **arrs)
     return path
@@ -306,6 +330,9 @@ FIXTURES = {
                                                            "bert", seed=31),
     # NerfA at the reference app's input width (64)
     "nerf_a": lambda: make_nerf_a_fixture("nerf_a", 256, seed=32, Kx=64),
+    # MgnMlp in bfloat16 (edge and node widths)
+    "mgn_edge_ln_bf16": lambda: make_mgn_bf16_fixture("mgn_edge_ln_bf16", 384, seed=40),
+    "mgn_node_ln_bf16": lambda: make_mgn_bf16_fixture("mgn_node_ln_bf16", 256, seed=41),
 }
 
 

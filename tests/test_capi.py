@@ -62,6 +62,25 @@ def test_empty_batch_is_a_noop():
     assert gpipes.lib.gp_last_error().decode() == ""
 
 
+def _call_dtype(dtype, impl=0, M=16, K=384):
+    vp = ctypes.c_void_p
+    return gpipes.lib.gp_mgn_mlp_dtype_out(M, K, vp(16), vp(16), vp(16), vp(16), vp(16), vp(16), vp(16), vp(16),
+                                           vp(16), 1e-5, vp(16), impl, dtype, None)
+
+
+@pytest.mark.parametrize("dtype,impl,code", [(2, 0, -1), (-1, 0, -1), (1, 1, -1), (1, 2, -1)])
+def test_dtype_errors(dtype, impl, code):
+    """Unknown dtypes, and bf16 on a queue-chained impl, fail before any device call."""
+    assert _call_dtype(dtype, impl) == code
+    assert gpipes.lib.gp_last_error().decode() != ""
+
+
+def test_dtype_entry_validates_like_the_fp16_call():
+    assert _call_dtype(1, K=100) == -2
+    assert _call_dtype(0, M=-1) == -1
+    assert _call_dtype(1, M=0) == 0
+
+
 def test_fullmlp_requires_affine():
     vp = ctypes.c_void_p
     rc = gpipes.lib.gp_mgn_fullmlp_out(16, vp(16), vp(16), vp(16), vp(16), vp(16), vp(16), vp(16), None,

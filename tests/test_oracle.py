@@ -36,7 +36,7 @@ import torch
 import torch.nn.functional as F
 
 import oracle
-from conftest import load_golden
+from conftest import bf16_to_f32, load_golden
 
 RNG = np.random.default_rng(1234)
 
@@ -147,6 +147,25 @@ def test_mgn_mlp_golden(name):
     z = load_golden(name)
     got = _run_fixture(z)
     np.testing.assert_allclose(got, z["expected"], rtol=1e-4, atol=1e-4)
+    max_abs, rel = oracle.errors(got, z["expected"])
+    assert max_abs < 1e-4 and rel < 1e-5
+
+
+def test_bf16_decode_matches_torch():
+    """The tests' bf16 decoder against torch.bfloat16 over all 65,536 bit patterns."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = bf16_to_f32(bits)
+    want = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).float().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", ["mgn_edge_ln_bf16.npz", "mgn_node_ln_bf16.npz"])
+def test_mgn_mlp_golden_bf16(name):
+    """The oracle on bf16 inputs (exact in fp32) against torch.nn in float64."""
+    z = load_golden(name)
+    assert str(z["dtype"]) == "bf16"
+    zf = {k: (bf16_to_f32(v) if v.dtype == np.uint16 else v) for k, v in z.items()}
+    got = _run_fixture(zf)
     max_abs, rel = oracle.errors(got, z["expected"])
     assert max_abs < 1e-4 and rel < 1e-5
 
