@@ -186,6 +186,11 @@ struct RingQueue {
     stores_complete();  // this workgroup's loads of the payload have returned
     if (threadIdx.x == 0) qcommit(&slot(seq).empty, ctx.epoch, seq < N);
   }
+  // read_commit for a caller whose every wave has already waited for its
+  // loads of the payload (vmcnt(0)) and passed a barrier since.
+  __device__ void read_commit_landed(int64_t seq, const QueueCtx& ctx) {
+    if (threadIdx.x == 0) qcommit(&slot(seq).empty, ctx.epoch, seq < N);
+  }
   // Thread-level, no wait: have all NP producers of `seq` committed?  A
   // consumer that sees true may load the payload after l1_invalidate().
   __device__ bool full_peek(int64_t seq, const QueueCtx& ctx) {
@@ -205,6 +210,7 @@ struct RingQueue {
 // base + i * stride elements; `rows_left` bounds the valid rows.
 struct MemoryReader {
   static constexpr bool kFromQueue = false;
+  __device__ void read_release_landed() { read_release(); }
   half_t* base;
   int64_t stride;
   int tile_stride;
@@ -243,6 +249,7 @@ __device__ inline MemoryReader read_striped_input(half_t* base, int row, int num
 // pipes.cuh:27-31
 struct NullReader {
   static constexpr bool kFromQueue = false;
+  __device__ void read_release_landed() {}
   __device__ TensorView read_acquire() { return {nullptr, 0, 0}; }
   __device__ void read_release() {}
   __device__ void reset() {}
@@ -265,6 +272,12 @@ struct QueueReader {
   }
   __device__ void read_release() {
     q->read_commit(seq_n, *ctx);
+    ++seq_n;
+  }
+  // read_release once every wave's loads of the tile have landed (vmcnt(0),
+  // then a barrier): the commit needs no second wait.
+  __device__ void read_release_landed() {
+    q->read_commit_landed(seq_n, *ctx);
     ++seq_n;
   }
   __device__ void reset() { seq_n = 0; }
@@ -300,6 +313,10 @@ struct SplitQueueReader {
     q->read_commit(seq_n, *ctx);
     seq_n += seq_stride;
   }
+  __device__ void read_release_landed() {
+    q->read_commit_landed(seq_n, *ctx);
+    seq_n += seq_stride;
+  }
   __device__ void reset() { seq_n = seq_off; }
   // As QueueReader's: the next tile of this worker is seq_n + seq_stride.
   __device__ bool peek_next() { return q->full_peek(seq_n + seq_stride, *ctx); }
@@ -314,6 +331,7 @@ struct SplitQueueReader {
 
 // pipes.cuh:60-72
 struct MemoryWriter {
+  static constexpr bool kReleaseBarrier = false;  // write_release passes no workgroup barrier
   half_t* base;
   int64_t stride;
   int tile_stride;
@@ -336,6 +354,7 @@ struct MemoryWriter {
 // block of every entry (a layer wider than one GEMM stage, split by columns).
 template <typename QT>
 struct QueueWriter {
+  static constexpr bool kReleaseBarrier = true;  // write_release: every wave's stores complete, then a barrier
   using Queue = QT;
   Queue* q;
   const QueueCtx* ctx;
@@ -360,6 +379,7 @@ struct QueueWriter {
 // pipes.cuh:86-102
 template <typename QT>
 struct SplitQueueWriter {
+  static constexpr bool kReleaseBarrier = true;
   using Queue = QT;
   Queue* q;
   const QueueCtx* ctx;
@@ -383,6 +403,7 @@ struct SplitQueueWriter {
 
 // pipes.cuh:104-108
 struct NullWriter {
+  static constexpr bool kReleaseBarrier = false;
   __device__ TensorView write_acquire(int) { return {nullptr, 0, 0}; }
   __device__ void write_release() {}
   __device__ void reset() {}

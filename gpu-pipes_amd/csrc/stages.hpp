@@ -303,7 +303,7 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
       __syncthreads();
       if (pre) cur = ir.view(qflag[1]);
       qnext = qflag[0] != 0;
-      ir.read_release();  // the tile is in LDS: hand the input slot back at once
+      ir.read_release_landed();  // the tile is in LDS: hand the input slot back at once
       if (qnext) {
         // the peeked tile is now the reader's current one; copy all MBLK rows
         // (rows past its count are never stored)
@@ -315,7 +315,7 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
       copy_part(cur, 0, 0);
       __builtin_amdgcn_s_waitcnt(kWaitAll);
       __syncthreads();
-      ir.read_release();  // the tile is in LDS: hand the input slot back at once
+      ir.read_release_landed();  // the tile is in LDS: hand the input slot back at once
     }
 
     // accumulators start at bias (+ the accumulator tile, pipe_gemm.cuh:128-146)
@@ -416,7 +416,9 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
       }
     }
     ow.write_release();
-    __syncthreads();  // LDS tile / LN partials are reused by the next iteration
+    // LDS tile / LN partials are reused by the next iteration; a queue
+    // writer's release already ends with a barrier after every wave's stores
+    if constexpr (!OW::kReleaseBarrier) __syncthreads();
     if constexpr (PF) {
       pb = npb;
       cur = nxt;

@@ -82,6 +82,26 @@ def test_linear(cuda, K, act, M):
 
 
 @pytest.mark.parametrize("K", [128, 384])
+@pytest.mark.parametrize("M", [63, 64, 65, 127, 129, 191, 192, 193, 100003])
+def test_linear_tile_edges(cuda, K, M):
+    """The memory-fed stage copies tiles in 64-row parts through a ring of three
+    part buffers, the next tile's parts under this tile's MFMAs: tiles whose
+    second part is partial or empty, and (M = 100,003) several tiles per
+    workgroup, with nothing written past the output rows."""
+    x = h((M, K), seed=K + 3 * M)
+    w = h((K, 128), 1.0 / np.sqrt(K), seed=17)
+    b = h((128,), 0.5, seed=18)
+    big = torch.full((M + 64, 128), 7.0, dtype=torch.float16, device=cuda)
+    y = gpipes.linear_out(x.to(cuda), w.to(cuda), b.to(cuda), act="relu", out=big[:M])
+    torch.cuda.synchronize()
+    assert torch.all(big[M:] == 7.0)
+    rows = np.unique(np.concatenate([np.arange(min(M, 300)), np.arange(max(0, M - 300), M),
+                                     np.random.default_rng(M).integers(0, M, 2000)]))
+    assert_parity(f(y)[rows], oracle.linear(f(x)[rows], f(w), f(b), gpipes.ACTS["relu"]),
+                  f"linear edges K={K} M={M}")
+
+
+@pytest.mark.parametrize("K", [128, 384])
 def test_linear_accumulator_input(cuda, K):
     """pipe_gemm: no bias, an accumulator tile added (the K-split chaining form)."""
     M = 777
