@@ -223,6 +223,10 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
 
   h8 wf[K / 16];
   load_weight_frags<K>(weight, xs, wf);
+  // The weight fragments live in AGPRs (MFMA A operands are read from there
+  // directly), which leaves the VGPRs to the accumulators and the epilogue.
+#pragma unroll
+  for (int i = 0; i < K / 16; ++i) asm volatile("" : "+a"(wf[i]));
   load_param(bias, prm, N);
   if (LN) {
     load_param(gamma, prm + N, N);
