@@ -208,6 +208,37 @@ def timed_steps(step, args, dev):
     return [a.elapsed_time(b) for a, b in ev], wall * 1e3 / args.steps, settle
 
 
+def graph_steps(step, args, dev):
+    """The timed steps submitted as one HIP graph: args.steps calls of step(i)
+    captured once (torch.cuda.CUDAGraph on torch's capture stream, which every
+    entry point launches on), replayed untimed for --settle-ms, then one timed
+    replay between synchronisations.  Only entry points that allocate nothing
+    can be captured (the fused MGN kernels).  Returns (wall ms per step,
+    settle record)."""
+    import torch
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(args.steps):
+            step(i)
+    torch.cuda.synchronize()
+    settle = {"ms": 0.0, "replays": 0}
+    if args.settle_ms > 0:
+        t0 = time.perf_counter()
+        n = 0
+        while (time.perf_counter() - t0) * 1e3 < args.settle_ms:
+            g.replay()
+            torch.cuda.synchronize()
+            n += 1
+        settle = {"ms": (time.perf_counter() - t0) * 1e3, "replays": n}
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g.replay()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall * 1e3 / args.steps, settle
+
+
 def bench_bert(args):
     """one gp_bert_ffn_out call over M = 65,536 rows per step."""
     import torch
@@ -476,6 +507,10 @@ def main():
                          "up to 1.5x slower, then settle), so the timed region starts in the steady state")
     ap.add_argument("--dtype", choices=["f16", "bf16"], default="f16",
                     help="element type of the MGN workloads (bf16: fused kernel, not the headline line)")
+    ap.add_argument("--eager", action="store_true",
+                    help="MGN fused workloads: time the steps as eager calls only (by default `value` comes "
+                         "from the same steps submitted as one HIP graph; the per-launch roofline times "
+                         "are eager in both cases)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-ref", action="store_true",
                     help="first run one plain 1 GiB device copy (a known-size reference kernel "
@@ -539,8 +574,15 @@ def main():
         torch.cuda.synchronize()
         del ref_in, ref_out
 
-    launch_ms, ms_per_step, settle = timed_steps(step, args, dev)
+    launch_ms, eager_ms_per_step, settle = timed_steps(step, args, dev)
     avg_launch_ms = sum(launch_ms) / len(launch_ms)
+    # The fused kernels allocate nothing, so the same steps can be submitted
+    # as one HIP graph, which removes the host's per-call launch gaps.
+    use_graph = args.impl == "fused" and not args.eager
+    graph_settle = None
+    ms_per_step = eager_ms_per_step
+    if use_graph:
+        ms_per_step, graph_settle = graph_steps(step, args, dev)
     bytes_, flops = algorithmic(M, K, ln, GATHER_NODES if gather else 0)
     achieved_gbs = bytes_ / (avg_launch_ms * 1e-3) / 1e9
     tflops = flops / (avg_launch_ms * 1e-3) / 1e12
@@ -561,7 +603,10 @@ def main():
         "config": {"workload": f"mgn_{args.workload}_mlp", "M": M, "K": K,
                    **({"nodes": GATHER_NODES, "index": "int64"} if gather else {}),
                    "layers": f"{K}-128-128-128" + ("+LN" if ln else ""), "impl": args.impl,
-                   "accumulate": "f32"},
+                   "accumulate": "f32",
+                   "submission": (f"one HIP graph of the {args.steps} timed calls" if use_graph
+                                  else "eager calls from Python")},
+        "eager_ms_per_step": eager_ms_per_step,
         "roofline": {
             "bound": "hbm", "achieved": achieved_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": load_traffic(args.workload, args.impl),
@@ -573,6 +618,7 @@ def main():
                  "frac": tflops / MFMA_F16_PEAK_TFLOPS, "flops_per_launch": flops},
         "spread": spread(launch_ms),
         "settle": settle,
+        "graph_settle": graph_settle,
         "cpu_baseline": None if args.no_cpu or args.dtype != "f16" else cpu_baseline_torch_mgn(K, ln),
         "cpu_baseline_oracle": None if args.no_cpu or args.dtype != "f16" else cpu_baseline(K, ln),
     }

@@ -26,6 +26,21 @@
 namespace gp {
 
 namespace {
+// True when work enqueued on `stream` is being captured into a graph.
+bool capturing(hipStream_t stream) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+}  // namespace
+
+int refuse_capture(hipStream_t stream) {
+  if (capturing(stream))
+    return fail(GP_ERR_INVALID_ARG,
+                "queue-chained launches cannot be captured into a graph (each launch takes a new queue epoch)");
+  return GP_OK;
+}
+
+namespace {
 struct ArenaRec {
   void* base = nullptr;
   size_t bytes = 0;
@@ -37,6 +52,9 @@ std::map<std::pair<int, hipStream_t>, ArenaRec> g_arenas;
 }  // namespace
 
 int arena_acquire(int dev, hipStream_t stream, size_t bytes, uint32_t layout, void** base, uint32_t* epoch) {
+  // A graph would replay the captured epoch, and counters left by the
+  // previous replay would then satisfy the next replay's waits.
+  if (int rc = refuse_capture(stream)) return rc;
   std::lock_guard<std::mutex> lk(g_mu);
   ArenaRec& a = g_arenas[{dev, stream}];
   if (a.bytes >= bytes && a.layout != layout) {
@@ -79,6 +97,12 @@ std::map<std::pair<int, hipStream_t>, WorkRec> g_work;
 }  // namespace
 
 int workspace_acquire(int dev, hipStream_t stream, size_t bytes, void** base) {
+  // A captured graph would keep the workspace address, which a later, larger
+  // call on the stream frees.
+  if (capturing(stream))
+    return fail(GP_ERR_INVALID_ARG,
+                "calls that use the per-stream workspace cannot be captured into a graph "
+                "(the allocation-free entry points can)");
   std::lock_guard<std::mutex> lk(g_mu);
   WorkRec& w = g_work[{dev, stream}];
   if (w.bytes < bytes) {

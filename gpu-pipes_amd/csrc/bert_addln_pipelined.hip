@@ -146,6 +146,7 @@ __global__ __launch_bounds__(kStageThreads) void bert_addln_pipelined_kernel(Arg
 
 template <int ACT>
 static int run(const BertAddlnArgs& m, int dev, int num_cus, hipStream_t s) {
+  if (int rc = refuse_capture(s)) return rc;
   static_assert(gemm_stage_lds<MBLK, H, 4>() <= gemm_stage_lds<MBLK, FF>(), "W0's part buffers fit the W2 stage's LDS");
   constexpr int lds = gemm_stage_lds<MBLK, FF>() + gemm_param_lds<MBLK>();
   auto kern = bert_addln_pipelined_kernel<ACT>;

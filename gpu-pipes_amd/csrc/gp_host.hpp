@@ -38,6 +38,10 @@ constexpr uint32_t kArenaLayoutMgn = 1;    // mgn_pipelined Queues
 constexpr uint32_t kArenaLayoutRoute = 2;  // route kernels (+1 for the split layout)
 constexpr uint32_t kArenaLayoutBertAddln = 4;
 constexpr uint32_t kArenaLayoutNerfA = 5;
+// GP_ERR_INVALID_ARG if `stream` is capturing into a graph: the queue-chained
+// launches call it before any other HIP call (a replay would reuse the
+// captured queue epoch).
+int refuse_capture(hipStream_t stream);
 int arena_acquire(int dev, hipStream_t stream, size_t bytes, uint32_t layout, void** base, uint32_t* epoch);
 
 // Scratch memory of the wide operators, one per (device, stream), grown on

@@ -124,6 +124,7 @@ __global__ __launch_bounds__(kStageThreads) void mgn_pipelined_kernel(Args a) {
 
 template <int K, bool LN, bool SPLIT>
 static int run(const MgnArgs& m, int dev, int num_cus, hipStream_t s) {
+  if (int rc = refuse_capture(s)) return rc;
   constexpr int S = layer1_workers<K, SPLIT>() + (SPLIT ? 2 + NLN : 2);
   constexpr int l1 = gemm_stage_lds<MBLK, K, kL1Bufs>(), l23 = gemm_stage_lds<MBLK, D, kQBufs>();
   constexpr int lds = (l1 > l23 ? l1 : l23) + kGemmParamLds;

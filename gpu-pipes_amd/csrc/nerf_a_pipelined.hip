@@ -124,6 +124,7 @@ __global__ __launch_bounds__(kStageThreads) void nerf_a_pipelined_kernel(Args a)
 
 int nerf_a_pipelined_run(const NerfAArgs& m, int dev, int num_cus, hipStream_t s) {
   using namespace nerfa;
+  if (int rc = refuse_capture(s)) return rc;
   if (m.Kx < 8 || m.Kx > 128 || m.Kx % 8)
     return fail(GP_ERR_SHAPE, "the pipelined layout takes Kx a multiple of 8 in [8, 128] (got %lld)",
                 (long long)m.Kx);

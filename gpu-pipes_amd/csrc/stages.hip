@@ -14,6 +14,8 @@
 // Stage workgroups are persistent: workgroup b of G handles tiles b, b+G, ...
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include "../../include/gpipes.h"
 #include "gp_host.hpp"
 #include "pipeline.hpp"
@@ -215,8 +217,18 @@ template <int K, int ACT, bool LN>
 static hipError_t launch_linear(const LinearArgs& a, int num_cus, hipStream_t s) {
   constexpr int lds = gemm_stage_lds<MBLK, K, kLinearBufs>() + kGemmParamLds;
   auto kern = linear_kernel<K, ACT, LN>;
-  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  // The LDS limit is set once per device (not per launch, so that a launch
+  // under graph capture makes no other runtime call).
+  static std::atomic<bool> lds_set[64];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  if (!lds_set[dev].load(std::memory_order_acquire)) {
+    e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return e;
+    lds_set[dev].store(true, std::memory_order_release);
+  }
   hipLaunchKernelGGL(kern, dim3(persistent_grid(a.M, num_cus, 1)), dim3(kStageThreads), lds, s, a);
   return hipGetLastError();
 }
@@ -367,6 +379,7 @@ hipError_t concat_launch(int64_t M, int64_t N0, int64_t N1, const void* a, const
 template <int ROUTE>
 static int route_launch(int64_t M, const void* x, void* out, void* out2, int max_pipes, int dev, int num_cus,
                         hipStream_t s) {
+  if (int rc = refuse_capture(s)) return rc;
   constexpr int S = route_stages(ROUTE);
   auto kern = route_kernel<ROUTE>;
   int per_cu = 0;
