@@ -178,24 +178,13 @@ __device__ __forceinline__ void gemm_2blk(const h8* wf, LD ld, f16x& acc0, f16x&
   gemm_2blk<E, KS, PF, NPRE, 0>(wf, ld, acc0, acc1, [](int) {});
 }
 
-// ReLU + 16-bit rounding of an accumulator block into this lane's row of an
-// LDS activation tile.  A lane of wave half lh holds features
-// 32n + 8g + 4lh + (0..3) of its row (g = 0..3); v_permlane32_swap trades
-// the odd groups of the lower half for the even groups of the upper half, so
-// a lane holds the whole 16-byte chunk 4n + 2j + lh and writes it with one
-// store.  act = the row's chunk 4n + lh.  Each 16-lane group of such a store
-// then writes one chunk of 16 consecutive rows, which the padded row stride
-// spreads over all banks.
+// ReLU + 16-bit rounding of an accumulator into this lane's row of an LDS
+// activation tile.
 template <typename E>
-__device__ __forceinline__ void store_relu_row(GP_LDS char* act, const f16x& a) {
+__device__ __forceinline__ void store_relu_row(GP_LDS char* act_row, int fq, const f16x& a) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const u32x2 ev = __builtin_bit_cast(u32x2, E::relu_cvt4((f4){a[8 * j], a[8 * j + 1], a[8 * j + 2], a[8 * j + 3]}));
-    const u32x2 od = __builtin_bit_cast(u32x2, E::relu_cvt4((f4){a[8 * j + 4], a[8 * j + 5], a[8 * j + 6], a[8 * j + 7]}));
-    const auto lo = __builtin_amdgcn_permlane32_swap(ev[0], od[0], false, false);
-    const auto hi = __builtin_amdgcn_permlane32_swap(ev[1], od[1], false, false);
-    *(GP_LDS u32x4*)(act + 32 * j) = (u32x4){(unsigned)lo[0], (unsigned)hi[0], (unsigned)lo[1], (unsigned)hi[1]};
-  }
+  for (int g = 0; g < 4; ++g)
+    *(GP_LDS h4*)(act_row + (fq + 8 * g) * 2) = E::relu_cvt4((f4){a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]});
 }
 
 // Prologue shared by both stages: weights are row-major [K][128]; 64-k slabs
@@ -326,9 +315,7 @@ void mgn_fused_kernel(Params p) {
   if (tid == 0) sy = Sync{0, 0, 0, 0, 0, 0};
 
   const int fq = 32 * n + 4 * lh;  // 32x32 accumulator group g covers features fq + 8g + (0..3)
-  // This lane's chunk lh of rows lr and lr + 32 of an activation tile: layer
-  // 2 reads chunks 2s + lh there, store_relu_row writes from chunk 4n + lh.
-  const int arow0 = lr * ACT_STRIDE + 16 * lh, arow1 = (32 + lr) * ACT_STRIDE + 16 * lh;
+  const int arow0 = lr * ACT_STRIDE, arow1 = (32 + lr) * ACT_STRIDE;
   GP_LDS int* const ab = (GP_LDS int*)&sy.abort;
   const int lim = p.spin_limit;
   constexpr int NS1 = K / 64;
@@ -471,8 +458,8 @@ void mgn_fused_kernel(Params p) {
 
       // Handoff slot k%2 was last read by stage B for tile k-2.
       if (k >= 2) lds_wait_geq((GP_LDS int*)&sy.h_free, 4 * (k - 1), ab, lim);
-      store_relu_row<E>(hand + arow0 + 64 * n, acc0);
-      store_relu_row<E>(hand + arow1 + 64 * n, acc1);
+      store_relu_row<E>(hand + arow0, fq, acc0);
+      store_relu_row<E>(hand + arow1, fq, acc1);
       lds_signal((GP_LDS int*)&sy.h_full, lane);
     };
 
@@ -521,14 +508,14 @@ void mgn_fused_kernel(Params p) {
       // layer 2, features [32n, 32n+32) of all 64 rows, from the handoff tile
       f16x acc0 = bias_frag(prm[1], fq), acc1 = acc0;
       gemm_2blk<E, D / 16, PF_L2, 4>(w2f, [&](int rb, int s) {
-        return *(const GP_LDS h8*)(hand + (rb ? arow1 : arow0) + 32 * s);
+        return *(const GP_LDS h8*)(hand + (rb ? arow1 : arow0) + (2 * s + lh) * 16);
       }, acc0, acc1);
       lds_signal((GP_LDS int*)&sy.h_free, lane);  // B operands are in registers: release the slot
 
       // exchange: act2 was last read (layer 3) for tile k-1
       if (k >= 1) lds_wait_geq((GP_LDS int*)&sy.x2_free, 4 * k, ab, lim);
-      store_relu_row<E>((GP_LDS char*)act2 + arow0 + 64 * n, acc0);
-      store_relu_row<E>((GP_LDS char*)act2 + arow1 + 64 * n, acc1);
+      store_relu_row<E>((GP_LDS char*)act2 + arow0, fq, acc0);
+      store_relu_row<E>((GP_LDS char*)act2 + arow1, fq, acc1);
       lds_signal((GP_LDS int*)&sy.x2_full, lane);
       lds_wait_geq((GP_LDS int*)&sy.x2_full, 4 * (k + 1), ab, lim);
 
