@@ -34,6 +34,11 @@
 //    s_barrier is used only in the prologue.
 //  * All chains are computed transposed, Y^T = W^T X^T, with
 //    v_mfma_f32_32x32x16_f16; the bias is the accumulator's initial value.
+//  * Prologue: the weights are copied HBM->LDS in their own row-major shape
+//    (whole 1 KiB copies into the X buffers and hand-off slots) and every
+//    wave reads its MFMA A fragments -- columns of W -- with the transposing
+//    LDS read ds_read_b64_tr_b16; W3 follows into the X buffers once W1 is
+//    read.  Two copy latencies and no transposing LDS writes.
 #include "gp_device.hpp"
 #include "gp_kernels.hpp"
 
@@ -45,7 +50,6 @@ constexpr int D = 128;          // hidden width of every MGN layer
 constexpr int NWAVES = 8;       // 4 layer-1 waves + 4 layer-2/3/LN waves
 constexpr int NTHREADS = NWAVES * kWave;
 constexpr int ACT_STRIDE = D * 2 + 16;   // padded LDS row (bytes) of a 128-wide fp16 tile
-constexpr int SLAB_STRIDE = 64 * 2 + 16; // padded LDS row (bytes) of a transposed 64-k weight slab
 constexpr int PF_L1 = 4;                 // layer-1 B-fragment prefetch depth (k-steps)
 constexpr int PF_L2 = 2;                 // layer-2 B-fragment prefetch depth (k-steps)
 
@@ -55,7 +59,7 @@ struct Cfg {
   static constexpr int KS1 = K / 16;                 // MFMA k-steps of layer 1
   static constexpr int CPR = K / 8;                  // 16-byte chunks per X row
   static constexpr int XTILE = TM * K * 2;           // bytes per X tile
-  static constexpr int XBUF = XTILE > D * SLAB_STRIDE ? XTILE : D * SLAB_STRIDE;  // also weight-slab scratch
+  static constexpr int XBUF = XTILE;                  // also W1 / W3 staging in the prologue
   static constexpr int DMA_INSTR = XTILE / 1024;     // wave-wide 1 KiB copies per tile
   static constexpr int DMA_PER_WAVE = DMA_INSTR / 4; // issued by the four A waves
   static_assert(DMA_INSTR % 4 == 0, "tile must split evenly over the A waves");
@@ -187,51 +191,71 @@ __device__ __forceinline__ void store_relu_row(GP_LDS char* act_row, int fq, con
     *(GP_LDS h4*)(act_row + (fq + 8 * g) * 2) = E::relu_cvt4((f4){a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]});
 }
 
-// Prologue shared by both stages: weights are row-major [K][128]; 64-k slabs
-// are transposed through two LDS scratch tiles ([feature][k], SLAB_STRIDE
-// bytes per feature) so every MFMA fragment is one 16-byte read.  Slab
-// j < K/64 holds W1 rows [64j, 64j+64), then two slabs of W2 and two of W3.
-// All eight waves copy every slab (wave w copies feature octets w and w+8 of
-// the 64 rows); take(j, buf) then reads whatever fragments the caller needs.
-// pre() runs once the first slab's loads are issued (the bias / LayerNorm
-// parameter loads then share their latency).
-template <int K, typename Take, typename Pre>
-__device__ __forceinline__ void stage_weights(const Params& p, GP_LDS char* buf0, GP_LDS char* buf1, int wave,
-                                              int lane, Take take, Pre pre) {
-  constexpr int NS1 = K / 64;
-  constexpr int NS = NS1 + 4;
-  auto slab_src = [&](int j) -> const half_t* {
-    return j < NS1 ? p.w1 + (64 * j) * D : (j < NS1 + 2 ? p.w2 + 64 * (j - NS1) * D : p.w3 + 64 * (j - NS1 - 2) * D);
-  };
-  h8 va[2], vb[2];
-  auto load_slab = [&](int j, h8(&v)[2]) {
-    const half_t* W = slab_src(j);
+// Weight staging for the prologue: a weight matrix W (R rows of 128 features,
+// row-major, as the caller passes it) is copied HBM->LDS unchanged in shape,
+// 256 bytes per row, with 16-byte chunk c of row k at chunk position
+// c ^ 4 (k % 4).  Copy j moves rows 4j .. 4j+3 (1 KiB; lane l fetches row
+// 4j + l/16, chunk (l % 16) ^ 4 (l / 16)); the eight waves take copies
+// wave, wave + 8, ...
+// The staged copies land in LDS buffers that are otherwise the X tiles and
+// the hand-off slots: copy j goes to the first buffer while it lasts (n
+// copies), then to the second.  (Separate buffers, not one array, so that the
+// compiler keeps them apart in the main loop.)
+struct WSpan {
+  GP_LDS char* a;
+  int n;
+  GP_LDS char* b;
+  __device__ GP_LDS char* block(int j) const { return j < n ? a + j * 1024 : b + (j - n) * 1024; }
+};
+template <int R>
+__device__ __forceinline__ void weight_dma(const half_t* W, WSpan dst, int wave, int lane) {
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(W, R * D * 2);
+  const int k4 = lane >> 4;
+  const int voff = (k4 * D + 8 * ((lane & 15) ^ (4 * k4))) * 2;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) v[i] = *(const h8*)(W + lane * D + 8 * (wave + 8 * i));
-  };
-  auto put_slab = [&](GP_LDS char* buf, const h8(&v)[2]) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        *(GP_LDS half_t*)(buf + (8 * (wave + 8 * i) + e) * SLAB_STRIDE + lane * 2) = v[i][e];
-  };
-  load_slab(0, va);
-  pre();
-#pragma unroll
-  for (int j = 0; j < NS; ++j) {
-    GP_LDS char* buf = (j & 1) ? buf1 : buf0;
-    if (j + 1 < NS) load_slab(j + 1, (j & 1) ? va : vb);
-    put_slab(buf, (j & 1) ? vb : va);
-    lds_barrier();
-    take(j, buf);
-  }
-  lds_barrier();  // the scratch tiles are reused afterwards
+  for (int j = wave; j < R / 4; j += NWAVES) dma16_buf_so(rs, voff, j * (4 * D * 2), dst.block(j));
 }
 
-// 16-byte fragment of a transposed slab: feature f, slab-local k offset kk.
-__device__ __forceinline__ h8 slab_frag(GP_LDS char* buf, int f, int kk) {
-  return *(const GP_LDS h8*)(buf + f * SLAB_STRIDE + kk * 2);
+// MFMA A fragments are columns of W (eight consecutive k of one feature).
+// ds_read_b64_tr_b16 transposes within each group of 16 lanes: when lane m
+// of the group points at the four 16-bit values S[m][0..3], lane j receives
+// S[4e + j/4][j % 4], e = 0..3.  Pointing lane m at row kb + m/4, features
+// fb + 4 (m % 4) .. +3 therefore gives lane j the values W[kb + e][fb + j].
+// In the staged layout the 16 rows x 64 bytes one 32-lane half reads fall in
+// four different chunk groups per row, so the reads are conflict free.
+typedef short s4 __attribute__((ext_vector_type(4)));
+// (kb is a multiple of 4: the four rows are one staged copy.)
+__device__ __forceinline__ s4 w_col4(const WSpan& w, int kb, int fb, int m) {
+  const int k = kb + (m >> 2), f = fb + 4 * (m & 3);
+  const GP_LDS char* a = w.block(kb >> 2) + (k & 3) * (D * 2) + (((f >> 3) ^ (4 * (k & 3))) * 16) + (f & 7) * 2;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((GP_LDS s4*)a);
+}
+// Lane j of each 16-lane group receives W[kb + e][fb + j], e = 0..7.
+__device__ __forceinline__ h8 w_col8(const WSpan& w, int kb, int fb, int m) {
+  const s4 a = w_col4(w, kb, fb, m), b = w_col4(w, kb + 4, fb, m);
+  return __builtin_bit_cast(h8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// Prologue shared by both stages: W1 (into the X buffers) and W2 (into the
+// hand-off slots) are copied at once; take12(w1, w2) then reads the caller's
+// fragments; W3 follows into the X buffers once every wave has its W1 / W2
+// fragments, and take3(w3) reads it.  pre() runs while the first copies are
+// in flight.
+template <int K, typename Pre, typename T12, typename T3>
+__device__ __forceinline__ void stage_weights_dma(const Params& p, WSpan xsp, WSpan hsp, int wave, int lane, Pre pre,
+                                                  T12 take12, T3 take3) {
+  weight_dma<K>(p.w1, xsp, wave, lane);
+  weight_dma<D>(p.w2, hsp, wave, lane);
+  pre();
+  wait_vmcnt<0>();
+  __syncthreads();
+  take12(xsp, hsp);
+  __syncthreads();  // W1 read by every wave
+  weight_dma<D>(p.w3, xsp, wave, lane);
+  wait_vmcnt<0>();
+  __syncthreads();
+  take3(xsp);
+  __syncthreads();  // the buffers return to their tiles
 }
 
 // Sum of a value over the four lanes l, l^16, l^32, l^48 (the lanes that
@@ -318,17 +342,19 @@ void mgn_fused_kernel(Params p) {
   const int arow0 = lr * ACT_STRIDE, arow1 = (32 + lr) * ACT_STRIDE;
   GP_LDS int* const ab = (GP_LDS int*)&sy.abort;
   const int lim = p.spin_limit;
-  constexpr int NS1 = K / 64;
+  // prologue weight staging: W1 / W3 in the X buffers, W2 in the hand-off slots
+  static_assert(2 * C::XBUF >= K * D * 2 && 2 * TM * ACT_STRIDE >= D * D * 2, "staged weights must fit");
+  const WSpan xspan{(GP_LDS char*)xs0, C::XBUF / 1024, (GP_LDS char*)xs1};
+  const WSpan hspan{(GP_LDS char*)hand0, TM * ACT_STRIDE / 1024, (GP_LDS char*)hand1};
 
   if (stage_a) {
     // ------------------------------------------------------------- stage A
     // W1 fragment for k-step s: lane holds W1[16s + 8*lh + e][32n + lr].
     h8 w1f[C::KS1];
-    stage_weights<K>(p, (GP_LDS char*)xs0, (GP_LDS char*)xs1, wave, lane, [&](int j, GP_LDS char* buf) {
-      if (j < NS1)
+    stage_weights_dma<K>(p, xspan, hspan, wave, lane, load_prm, [&](const WSpan& w1, const WSpan&) {
 #pragma unroll
-        for (int sl = 0; sl < 4; ++sl) w1f[4 * j + sl] = slab_frag(buf, 32 * n + lr, 16 * sl + 8 * lh);
-    }, load_prm);
+      for (int s = 0; s < C::KS1; ++s) w1f[s] = w_col8(w1, 16 * s + 8 * lh, 32 * n + 16 * ((lane >> 4) & 1), lane & 15);
+    }, [](const WSpan&) {});
 #pragma unroll
     for (int s = 0; s < C::KS1; ++s) asm volatile("" : "+a"(w1f[s]));
 
@@ -476,18 +502,15 @@ void mgn_fused_kernel(Params p) {
     const int l16 = lane & 15, q4 = lane >> 4;
     h8 w2f[D / 16];
     h8 w3f[8][4];
-    stage_weights<K>(p, (GP_LDS char*)xs0, (GP_LDS char*)xs1, wave, lane, [&](int j, GP_LDS char* buf) {
-      if (j >= NS1 && j < NS1 + 2) {
+    stage_weights_dma<K>(p, xspan, hspan, wave, lane, load_prm, [&](const WSpan&, const WSpan& w2) {
 #pragma unroll
-        for (int sl = 0; sl < 4; ++sl) w2f[4 * (j - NS1) + sl] = slab_frag(buf, 32 * n + lr, 16 * sl + 8 * lh);
-      } else if (j >= NS1 + 2) {
-        const int half = j - NS1 - 2;  // k in [64 half, 64 half + 64)
+      for (int s = 0; s < D / 16; ++s) w2f[s] = w_col8(w2, 16 * s + 8 * lh, 32 * n + 16 * ((lane >> 4) & 1), lane & 15);
+    }, [&](const WSpan& w3) {
 #pragma unroll
-        for (int fb = 0; fb < 8; ++fb)
+      for (int fb = 0; fb < 8; ++fb)
 #pragma unroll
-          for (int kl = 0; kl < 2; ++kl) w3f[fb][2 * half + kl] = slab_frag(buf, 16 * fb + l16, 32 * kl + 8 * q4);
-      }
-    }, load_prm);
+        for (int ks = 0; ks < 4; ++ks) w3f[fb][ks] = w_col8(w3, 32 * ks + 8 * q4, 16 * fb, l16);
+    });
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) asm volatile("" : "+v"(w2f[s]));
 #pragma unroll
