@@ -194,4 +194,37 @@ __device__ __forceinline__ float sum_lane_halves(float x) {
   return __builtin_bit_cast(float, (unsigned)p[0]) + __builtin_bit_cast(float, (unsigned)p[1]);
 }
 
+// ---------------------------------------------------------------------------
+// Weight rows staged in LDS.  A weight matrix W (rows of 128 16-bit values)
+// is copied HBM->LDS in its own row-major shape, 256 bytes per row, four rows
+// per 1 KiB copy, with 16-byte chunk c of row r at chunk position
+// c ^ 4 (r % 4).  Lane l of a copy fetches row l/16 of the copy's four,
+// chunk (l % 16) ^ 4 (l / 16): wrow_voff is that byte offset for a row
+// stride of `stride` bytes.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int wrow_voff(int lane, int stride) {
+  const int r = lane >> 4;
+  return r * stride + ((lane & 15) ^ (4 * r)) * 16;
+}
+
+// MFMA A fragments are columns of W (consecutive k of one feature).
+// ds_read_b64_tr_b16 transposes within each group of 16 lanes: when lane m of
+// the group points at the four 16-bit values S[m][0..3], lane j receives
+// S[4e + j/4][j % 4], e = 0..3.  With lane m pointing at row kb + m/4,
+// features fb + 4 (m % 4) .. +3 (kb a multiple of 4, fb of 16), lane j
+// receives W[kb + e][fb + j].  blk is the LDS address of row kb.  The 32
+// lanes of a wave half read four rows x 64 bytes that the swizzle puts in
+// four different chunk groups, so the read is conflict free.
+typedef short s4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ s4 wrows_col4(const GP_LDS char* blk, int fb, int m) {
+  const int r = m >> 2, f = fb + 4 * (m & 3);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((GP_LDS s4*)(blk + r * 256 + (((f >> 3) ^ (4 * r)) * 16) + (f & 7) * 2));
+}
+// Eight consecutive k: lane j receives W[kb + e][fb + j], e = 0..7, from the
+// four-row blocks at blk0 (rows kb..kb+3) and blk1 (rows kb+4..kb+7).
+__device__ __forceinline__ h8 wrows_col8(const GP_LDS char* blk0, const GP_LDS char* blk1, int fb, int m) {
+  const s4 a = wrows_col4(blk0, fb, m), b = wrows_col4(blk1, fb, m);
+  return __builtin_bit_cast(h8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 }  // namespace gp

@@ -191,15 +191,12 @@ __device__ __forceinline__ void store_relu_row(GP_LDS char* act_row, int fq, con
     *(GP_LDS h4*)(act_row + (fq + 8 * g) * 2) = E::relu_cvt4((f4){a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]});
 }
 
-// Weight staging for the prologue: a weight matrix W (R rows of 128 features,
-// row-major, as the caller passes it) is copied HBM->LDS unchanged in shape,
-// 256 bytes per row, with 16-byte chunk c of row k at chunk position
-// c ^ 4 (k % 4).  Copy j moves rows 4j .. 4j+3 (1 KiB; lane l fetches row
-// 4j + l/16, chunk (l % 16) ^ 4 (l / 16)); the eight waves take copies
-// wave, wave + 8, ...
-// The staged copies land in LDS buffers that are otherwise the X tiles and
-// the hand-off slots: copy j goes to the first buffer while it lasts (n
-// copies), then to the second.  (Separate buffers, not one array, so that the
+// Weight staging for the prologue: the weight matrices are copied HBM->LDS
+// in their own shape (the staged-rows layout of gp_device.hpp), copy j
+// holding rows 4j .. 4j+3; the eight waves take copies wave, wave + 8, ...
+// The copies land in LDS buffers that are otherwise the X tiles and the
+// hand-off slots: copy j goes to the first buffer while it lasts (n copies),
+// then to the second.  (Separate buffers, not one array, so that the
 // compiler keeps them apart in the main loop.)
 struct WSpan {
   GP_LDS char* a;
@@ -210,30 +207,14 @@ struct WSpan {
 template <int R>
 __device__ __forceinline__ void weight_dma(const half_t* W, WSpan dst, int wave, int lane) {
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(W, R * D * 2);
-  const int k4 = lane >> 4;
-  const int voff = (k4 * D + 8 * ((lane & 15) ^ (4 * k4))) * 2;
+  const int voff = wrow_voff(lane, D * 2);
 #pragma unroll
   for (int j = wave; j < R / 4; j += NWAVES) dma16_buf_so(rs, voff, j * (4 * D * 2), dst.block(j));
 }
-
-// MFMA A fragments are columns of W (eight consecutive k of one feature).
-// ds_read_b64_tr_b16 transposes within each group of 16 lanes: when lane m
-// of the group points at the four 16-bit values S[m][0..3], lane j receives
-// S[4e + j/4][j % 4], e = 0..3.  Pointing lane m at row kb + m/4, features
-// fb + 4 (m % 4) .. +3 therefore gives lane j the values W[kb + e][fb + j].
-// In the staged layout the 16 rows x 64 bytes one 32-lane half reads fall in
-// four different chunk groups per row, so the reads are conflict free.
-typedef short s4 __attribute__((ext_vector_type(4)));
-// (kb is a multiple of 4: the four rows are one staged copy.)
-__device__ __forceinline__ s4 w_col4(const WSpan& w, int kb, int fb, int m) {
-  const int k = kb + (m >> 2), f = fb + 4 * (m & 3);
-  const GP_LDS char* a = w.block(kb >> 2) + (k & 3) * (D * 2) + (((f >> 3) ^ (4 * (k & 3))) * 16) + (f & 7) * 2;
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((GP_LDS s4*)a);
-}
-// Lane j of each 16-lane group receives W[kb + e][fb + j], e = 0..7.
+// Lane j of each 16-lane group receives W[kb + e][fb + j], e = 0..7 (kb a
+// multiple of 8, fb of 16).
 __device__ __forceinline__ h8 w_col8(const WSpan& w, int kb, int fb, int m) {
-  const s4 a = w_col4(w, kb, fb, m), b = w_col4(w, kb + 4, fb, m);
-  return __builtin_bit_cast(h8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+  return wrows_col8(w.block(kb >> 2), w.block((kb >> 2) + 1), fb, m);
 }
 
 // Prologue shared by both stages: W1 (into the X buffers) and W2 (into the

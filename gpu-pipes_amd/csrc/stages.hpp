@@ -66,7 +66,6 @@ __device__ __forceinline__ GP_LDS char* dyn_lds() {
 }
 
 constexpr int kStageThreads = 256;
-constexpr int kSlabStride = 64 * 2 + 16;  // padded LDS row of a transposed 64-k weight slab
 
 // LDS bytes of a GEMM stage with an MBLK x K input tile and N = 128 outputs.
 // NB > 0: the input is staged through NB buffers of 64 rows (at least
@@ -75,7 +74,7 @@ template <int MBLK, int K, int NB = 0>
 constexpr int gemm_stage_lds() {
   constexpr int rows = (NB > MBLK / 64 ? NB : MBLK / 64) * 64;
   constexpr int tile = (NB > 0 ? rows : MBLK) * K * 2;
-  return tile > 128 * kSlabStride ? tile : 128 * kSlabStride;
+  return tile > 64 * 256 ? tile : 64 * 256;  // at least one 64-row pass of weight staging
 }
 // bias/gamma/beta + the LayerNorm partials of MBLK rows
 template <int MBLK>
@@ -118,30 +117,35 @@ __device__ __forceinline__ void load_tile_swz(const TensorView& v, GP_LDS char* 
 
 // Load a weight matrix W [K][128] (row stride w.stride elements) into MFMA A
 // fragments: wf[s] of wave w, lane l holds W[16s + 8(l/32) + e][32w + l%32].
-// 64-k slabs are transposed through LDS scratch (>= 128 * kSlabStride bytes).
-// Rows at or past w.rows (the valid K of a padded layer) load as zeros.
-template <int K>
+// W is copied into the LDS scratch (SCR bytes) in its own row-major shape --
+// whole 1 KiB copies, the staged-rows layout of gp_device.hpp -- as many
+// 64-row groups at a time as fit, and the fragments, columns of W, are read
+// with the transposing ds_read_b64_tr_b16.  Rows at or past w.rows (the valid
+// K of a padded layer) lie outside the copies' buffer descriptor and arrive
+// as zeros.
+template <int K, int SCR>
 __device__ __forceinline__ void load_weight_frags(const TensorView& w, GP_LDS char* scratch, h8 (&wf)[K / 16]) {
+  constexpr int RP0 = SCR / 256 / 64 * 64;
+  constexpr int RP = RP0 < K ? RP0 : K;  // rows per pass
+  static_assert(RP >= 64, "the scratch must hold 64 weight rows");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int lr = lane & 31, lh = lane >> 5;
+  const int lh = lane >> 5;
+  const int sb = w.stride * 2;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(w.data, w.rows * sb);
+  const int voff = wrow_voff(lane, sb);
+  const int fb = 32 * wave + 16 * ((lane >> 4) & 1);
 #pragma unroll
-  for (int j = 0; j < K / 64; ++j) {
-    // 64 rows x 16 feature octets: wave w copies octets w, w+4, w+8, w+12
-    h8 v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      v[i] = 64 * j + lane < w.rows ? *(const h8*)(w.data + (int64_t)(64 * j + lane) * w.stride + 8 * (wave + 4 * i))
-                                    : h8{};
-    __syncthreads();  // previous slab fully read
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        *(GP_LDS half_t*)(scratch + (8 * (wave + 4 * i) + e) * kSlabStride + lane * 2) = v[i][e];
+  for (int p0 = 0; p0 < K; p0 += RP) {
+    const int rows = K - p0 < RP ? K - p0 : RP;
+    if (p0 > 0) __syncthreads();  // the previous pass's rows are read
+    for (int j = wave; j < rows / 4; j += kStageThreads / kWave) dma16_buf_so(rs, voff, (p0 + 4 * j) * sb, scratch + j * 1024);
+    wait_vmcnt<0>();
     __syncthreads();
 #pragma unroll
-    for (int sl = 0; sl < 4; ++sl)
-      wf[4 * j + sl] = *(const GP_LDS h8*)(scratch + (32 * wave + lr) * kSlabStride + (16 * sl + 8 * lh) * 2);
+    for (int s = p0 / 16; s < (p0 + rows) / 16; ++s) {
+      const GP_LDS char* blk = scratch + (16 * s + 8 * lh - p0) * 256;
+      wf[s] = wrows_col8(blk, blk + 4 * 256, fb, lane & 15);
+    }
   }
   __syncthreads();
 }
@@ -222,7 +226,7 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
   const int fq = 32 * wave + 4 * lh;  // accumulator group g covers features fq + 8g + (0..3)
 
   h8 wf[K / 16];
-  load_weight_frags<K>(weight, xs, wf);
+  load_weight_frags<K, gemm_stage_lds<MBLK, K, NB>()>(weight, xs, wf);
   // The weight fragments live in AGPRs (MFMA A operands are read from there
   // directly), which leaves the VGPRs to the accumulators and the epilogue.
 #pragma unroll
