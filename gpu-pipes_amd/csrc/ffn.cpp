@@ -76,6 +76,10 @@ int gp_gemm_out(int64_t M, int64_t N, int64_t K, const void* x, const void* w, c
   int dev = 0, ncu = 0;
   if ((rc = current_device_info(&dev, &ncu))) return rc;
   hipStream_t s = (hipStream_t)stream;
+  if (weights_in_place(2.0 * M * N * K)) {
+    const hipError_t e = gemm_launch(gemm_w(M, N, K, x, w, b, r, act, out), ncu, s);
+    return e == hipSuccess ? GP_OK : fail_hip(e, "gemm launch");
+  }
   void* ws = nullptr;
   if ((rc = workspace_acquire(dev, s, (size_t)N * K * 2, &ws))) return rc;
   hipError_t e = transpose_launch(w, ws, K, N, s);
@@ -107,26 +111,36 @@ int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void*
   if ((rc = current_device_info(&dev, &ncu))) return rc;
   hipStream_t s = (hipStream_t)stream;
 
-  // Workspace: w1^T [FF][H], w2^T [H][FF], then one chunk of activations
-  // [CH][FF] and of pre-LayerNorm rows [CH][H].
+  // Workspace: w1^T [FF][H], w2^T [H][FF] (unless the GEMMs read w1 and w2
+  // in place), then one chunk of activations [CH][FF] and of pre-LayerNorm
+  // rows [CH][H].
+  const bool inplace = weights_in_place(4.0 * M * H * FF);
   const int64_t CH = M < kFfnChunkRows ? M : kFfnChunkRows;
-  const size_t o_w2t = round_up((size_t)FF * H * 2);
-  const size_t o_act = o_w2t + round_up((size_t)FF * H * 2);
+  const size_t o_w2t = inplace ? 0 : round_up((size_t)FF * H * 2);
+  const size_t o_act = o_w2t + (inplace ? 0 : round_up((size_t)FF * H * 2));
   const size_t o_y = o_act + round_up((size_t)CH * FF * 2);
   const size_t total = o_y + round_up((size_t)CH * H * 2);
   char* ws = nullptr;
   if ((rc = workspace_acquire(dev, s, total, (void**)&ws))) return rc;
   void *w1t = ws, *w2t = ws + o_w2t, *hbuf = ws + o_act, *ybuf = ws + o_y;
 
-  const PrepSpec ps[2] = {{w1, w1t, nullptr, nullptr, H, FF, H, FF}, {w2, w2t, nullptr, nullptr, FF, H, FF, H}};
-  hipError_t e = prep_launch(ps, 2, s);
-  if (e != hipSuccess) return fail_hip(e, "transpose launch");
+  hipError_t e = hipSuccess;
+  if (!inplace) {
+    const PrepSpec ps[2] = {{w1, w1t, nullptr, nullptr, H, FF, H, FF}, {w2, w2t, nullptr, nullptr, FF, H, FF, H}};
+    e = prep_launch(ps, 2, s);
+    if (e != hipSuccess) return fail_hip(e, "transpose launch");
+  }
+  // layer GEMM arguments: the weights in place or their transposed copies
+  auto g = [&](int64_t rows, int64_t N, int64_t K, const void* a, const void* w, const void* wt, const void* b,
+               const void* r, int ac, void* c) {
+    return inplace ? gemm_w(rows, N, K, a, w, b, r, ac, c) : GemmArgs{rows, N, K, a, wt, b, r, ac, c};
+  };
   for (int64_t r0 = 0; r0 < M; r0 += CH) {
     const int64_t rows = M - r0 < CH ? M - r0 : CH;
     const void* xc = at_row(x, r0, H);
-    e = gemm_launch({rows, FF, H, xc, w1t, b1, nullptr, act, hbuf}, ncu, s);
+    e = gemm_launch(g(rows, FF, H, xc, w1, w1t, b1, nullptr, act, hbuf), ncu, s);
     if (e != hipSuccess) return fail_hip(e, "FFN GEMM1 launch");
-    e = gemm_launch({rows, H, FF, hbuf, w2t, b2, xc, GP_ACT_NONE, ybuf}, ncu, s);
+    e = gemm_launch(g(rows, H, FF, hbuf, w2, w2t, b2, xc, GP_ACT_NONE, ybuf), ncu, s);
     if (e != hipSuccess) return fail_hip(e, "FFN GEMM2 launch");
     e = layer_norm_launch(rows, H, ybuf, gamma, beta, eps, (char*)out + r0 * H * 2, ncu, s);
     if (e != hipSuccess) return fail_hip(e, "FFN LayerNorm launch");
@@ -165,29 +179,38 @@ int gp_bert_addln_ffn_out(int64_t M, int64_t H, int64_t FF, const void* attn, co
   }
 
   // Chain: per row chunk, GEMM0 (+ b0 + x), LN0, GEMM1 (+ b1, act), GEMM2 (+ b2 + h0), LN2.
-  // Workspace: w0^T [H][H], w1^T [FF][H], w2^T [H][FF], then for one chunk the
-  // pre-LayerNorm rows y [CH][H], h0 [CH][H] and the activations [CH][FF].
+  // Workspace: w0^T [H][H], w1^T [FF][H], w2^T [H][FF] (unless the GEMMs
+  // read the weights in place), then for one chunk the pre-LayerNorm rows
+  // y [CH][H], h0 [CH][H] and the activations [CH][FF].
+  const bool inplace = weights_in_place(2.0 * M * H * (H + 2.0 * FF));
   const int64_t CH = M < kFfnChunkRows ? M : kFfnChunkRows;
-  const size_t o_w1t = round_up((size_t)H * H * 2);
-  const size_t o_w2t = o_w1t + round_up((size_t)FF * H * 2);
-  const size_t o_y = o_w2t + round_up((size_t)FF * H * 2);
+  const size_t o_w1t = inplace ? 0 : round_up((size_t)H * H * 2);
+  const size_t o_w2t = o_w1t + (inplace ? 0 : round_up((size_t)FF * H * 2));
+  const size_t o_y = o_w2t + (inplace ? 0 : round_up((size_t)FF * H * 2));
   const size_t o_h0 = o_y + round_up((size_t)CH * H * 2);
   const size_t o_act = o_h0 + round_up((size_t)CH * H * 2);
   const size_t total = o_act + round_up((size_t)CH * FF * 2);
   char* ws = nullptr;
   if ((rc = workspace_acquire(dev, s, total, (void**)&ws))) return rc;
   void *w0t = ws, *w1t = ws + o_w1t, *w2t = ws + o_w2t, *ybuf = ws + o_y, *h0 = ws + o_h0, *abuf = ws + o_act;
-  const PrepSpec ps[3] = {{w0, w0t, nullptr, nullptr, H, H, H, H},
-                          {w1, w1t, nullptr, nullptr, H, FF, H, FF},
-                          {w2, w2t, nullptr, nullptr, FF, H, FF, H}};
-  hipError_t e = prep_launch(ps, 3, s);
-  if (e != hipSuccess) return fail_hip(e, "transpose launch");
+  hipError_t e = hipSuccess;
+  if (!inplace) {
+    const PrepSpec ps[3] = {{w0, w0t, nullptr, nullptr, H, H, H, H},
+                            {w1, w1t, nullptr, nullptr, H, FF, H, FF},
+                            {w2, w2t, nullptr, nullptr, FF, H, FF, H}};
+    e = prep_launch(ps, 3, s);
+    if (e != hipSuccess) return fail_hip(e, "transpose launch");
+  }
+  auto g = [&](int64_t rows, int64_t N, int64_t K, const void* a, const void* w, const void* wt, const void* b,
+               const void* r, int ac, void* c) {
+    return inplace ? gemm_w(rows, N, K, a, w, b, r, ac, c) : GemmArgs{rows, N, K, a, wt, b, r, ac, c};
+  };
   for (int64_t r0 = 0; r0 < M; r0 += CH) {
     const int64_t rows = M - r0 < CH ? M - r0 : CH;
-    e = gemm_launch({rows, H, H, at_row(attn, r0, H), w0t, b0, at_row(x, r0, H), GP_ACT_NONE, ybuf}, ncu, s);
+    e = gemm_launch(g(rows, H, H, at_row(attn, r0, H), w0, w0t, b0, at_row(x, r0, H), GP_ACT_NONE, ybuf), ncu, s);
     if (e == hipSuccess) e = layer_norm_launch(rows, H, ybuf, ga0, be0, eps, h0, ncu, s);
-    if (e == hipSuccess) e = gemm_launch({rows, FF, H, h0, w1t, b1, nullptr, act, abuf}, ncu, s);
-    if (e == hipSuccess) e = gemm_launch({rows, H, FF, abuf, w2t, b2, h0, GP_ACT_NONE, ybuf}, ncu, s);
+    if (e == hipSuccess) e = gemm_launch(g(rows, FF, H, h0, w1, w1t, b1, nullptr, act, abuf), ncu, s);
+    if (e == hipSuccess) e = gemm_launch(g(rows, H, FF, abuf, w2, w2t, b2, h0, GP_ACT_NONE, ybuf), ncu, s);
     if (e == hipSuccess) e = layer_norm_launch(rows, H, ybuf, ga2, be2, eps, (char*)out + r0 * H * 2, ncu, s);
     if (e != hipSuccess) return fail_hip(e, "bert_addln_ffn launch");
   }

@@ -11,8 +11,11 @@
 // one streaming kernel over output tiles with its epilogue fused.
 //
 // Kernel design.
-//  * B is consumed transposed (Bt[N][K], from transpose_kernel), so both MFMA
-//    operands are rows of consecutive k.  The product is computed transposed,
+//  * B is consumed transposed (Bt[N][K], from transpose_kernel / prep_kernel),
+//    so both MFMA operands are rows of consecutive k -- or, for calls small
+//    enough that the transpose launch would cost more than it saves, in its
+//    own [K][N] layout, its fragments read with the transposing LDS read
+//    (the BROW kernels).  The product is computed transposed,
 //    C^T = Bt A^T, with v_mfma_f32_32x32x16_f16: the MFMA A operand is a
 //    32-feature block of Bt, the MFMA B operand a 32-row block of A, and each
 //    accumulator lane ends up holding 4 consecutive features of one row.
@@ -74,7 +77,9 @@ using Narrow = Cfg<4, 2, 1>;  // 128 features x 256 rows
 
 struct Args {
   const half_t* a;     // [M][lda], the first K columns used
-  const half_t* bt;    // [N][K]
+  const half_t* bt;    // [N][K] (transposed weights), or
+  const half_t* w;     // [kw][ldw] (the weights in their own layout, BROW kernels)
+  int ldw, kw;         // row stride and rows of w; rows [kw, K) read as zero
   const half_t* bias;  // [N] or null
   const half_t* r;     // [M][ldr] residual or null
   half_t* c;           // [M][ldc], the first N columns written
@@ -95,7 +100,13 @@ __device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&&
   (f(std::integral_constant<int, I>{}), ...);
 }
 
-template <class C, int ACT, bool RESID>
+// BROW: the weights are read in their own [K][N] layout.  A Bt unit then
+// holds the slab's 64 weight rows, BN features each (2 BN bytes per row, four
+// or two rows per 1 KiB copy), in the staged-rows layout of gp_device.hpp
+// (16-byte chunk c of row r at chunk position c ^ 4 (r % 4)), and the MFMA A
+// fragments -- columns of W -- are read with ds_read_b64_tr_b16, two reads
+// per fragment.  No transposed copy of W is made.
+template <class C, int ACT, bool RESID, bool BROW = false>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_kernel(Args p) {
   __shared__ __attribute__((aligned(1024))) char ring[NU * C::UNIT];
 
@@ -134,13 +145,20 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   static_assert((RPC * NW / 2) % CPR == 0, "copies of one lane share a swizzle");
   const int vrow = RPC * wave + lane / CPR;
   const int vswz = ((lane % CPR) ^ ((vrow >> 1) & 7)) << 4;
-  const int voffa = vrow * p.lda * 2 + vswz, voffb = vrow * K * 2 + vswz;
+  const int voffa = vrow * p.lda * 2 + vswz;
+  // BROW copies: CPRB 16-byte chunks per weight row, RPCB rows per copy; copy
+  // j of a wave covers rows RPCB (j NW + w) .. + RPCB - 1 of the slab, whose
+  // row % 4 does not depend on j, so again only an SGPR offset changes.
+  constexpr int CPRB = C::BN / 8, RPCB = 64 / CPRB;
+  const int rq = RPCB * wave + lane / CPRB;
+  const int voffb = BROW ? rq * p.ldw * 2 + (((lane % CPRB) ^ (4 * (rq & 3))) << 4) : vrow * K * 2 + vswz;
   // A slabs that reach past column ka: a lane whose chunk starts at or past
   // ka reads from an offset beyond every descriptor's range, so the copy
   // writes zeros (the weight rows it meets are zero too).
   const int lck = (vswz >> 4) * 8;  // the lane's first column within a slab
   constexpr int kBeyond = 0x40000000;
-  const int jstra = RPC * NW * p.lda * 2, jstrb = RPC * NW * K * 2;
+  const int jstra = RPC * NW * p.lda * 2, jstrb = BROW ? RPCB * NW * p.ldw * 2 : RPC * NW * K * 2;
+  const int slabb = BROW ? 64 * p.ldw * 2 : ROWB;  // source offset of the next slab's B unit
   GP_LDS char* const lds = (GP_LDS char*)ring;
 
   struct Tile {
@@ -156,7 +174,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     const int64_t mrows = p.M - T.m0;
     T.rows = (int)(mrows < C::BM ? mrows : C::BM);
     T.ra = make_rsrc(p.a + T.m0 * p.lda, T.rows * p.lda * 2);
-    T.rb = make_rsrc(p.bt + (int64_t)T.n0 * K, C::BN * K * 2);
+    if constexpr (BROW)
+      T.rb = make_rsrc(p.w + T.n0, (int)((int64_t)p.kw * p.ldw * 2 - (int64_t)T.n0 * 2));
+    else
+      T.rb = make_rsrc(p.bt + (int64_t)T.n0 * K, C::BN * K * 2);
     return T;
   };
   // Copies [j0, j1) of unit u (default: all of them).
@@ -164,9 +185,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     GP_LDS char* const s = lds + (u % NU) * C::UNIT;
     const int so = (u >> 1) * ROWB;
     if (u & 1) {
+      const int sob = (u >> 1) * slabb;
 #pragma unroll
       for (int j = 0; j < C::UB; ++j)
-        if (j >= j0 && j < j1) dma16_buf_so(T.rb, voffb, j * jstrb + so, s + (j * NW + wave) * 1024);
+        if (j >= j0 && j < j1) dma16_buf_so(T.rb, voffb, j * jstrb + sob, s + (j * NW + wave) * 1024);
     } else {
       const int k0 = (u >> 1) * BK;
       const int vo = k0 + BK <= p.ka || k0 + lck < p.ka ? voffa : kBeyond;
@@ -187,11 +209,34 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   const int arow = 32 * C::MBW * wm + lr;  // A unit row of fragment mb: arow + 32 mb
   // Rows 32 apart share the unit_off swizzle, so fragment nb (mb) of step ks
   // is at a per-lane offset for ks plus the constant 32 nb ROWB (32 mb ROWB).
+  // BROW: lane part of the first transposed read of fragment nb (rows
+  // 8 lh + m / 4 of the step, features 32 (NBW wn + nb) + 16 (group % 2) +
+  // 4 (m % 4) .. +3, m = lane % 16); the second read is four rows further.
+  // With NBW = 4 the swizzled chunk of fragment nb is that of fragment 0
+  // with bits 2-3 xor-ed by nb, so lb(nb) = lb(0) ^ 64 nb.
+  static_assert(!BROW || C::NBW == 4, "fragment offsets assume four fragments per wave");
+  int lb0 = 0;
+  if constexpr (BROW) {
+    const int m = lane & 15, r4 = m >> 2;
+    const int f = 32 * C::NBW * wn + 16 * ((lane >> 4) & 1) + 4 * (m & 3);
+    lb0 = (8 * lh + r4) * (C::BN * 2) + (((f >> 3) ^ (4 * r4)) << 4) + (f & 7) * 2;
+  }
   auto load = [&](Frags& f, int kt, int ks) {
     GP_LDS const char* const ua = lds + ((2 * kt) % NU) * C::UNIT + unit_off(arow, 2 * ks + lh);
-    GP_LDS const char* const ub = lds + ((2 * kt + 1) % NU) * C::UNIT + unit_off(frow, 2 * ks + lh);
+    if constexpr (BROW) {
+      GP_LDS const char* const ub = lds + ((2 * kt + 1) % NU) * C::UNIT + ks * 16 * (C::BN * 2);
 #pragma unroll
-    for (int nb = 0; nb < C::NBW; ++nb) f.a[nb] = *(GP_LDS const h8*)(ub + 32 * nb * ROWB);
+      for (int nb = 0; nb < C::NBW; ++nb) {
+        const int lb = lb0 ^ (64 * nb);
+        const s4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GP_LDS s4*)(ub + lb));
+        const s4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GP_LDS s4*)(ub + lb + 4 * (C::BN * 2)));
+        f.a[nb] = __builtin_bit_cast(h8, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+    } else {
+      GP_LDS const char* const ub = lds + ((2 * kt + 1) % NU) * C::UNIT + unit_off(frow, 2 * ks + lh);
+#pragma unroll
+      for (int nb = 0; nb < C::NBW; ++nb) f.a[nb] = *(GP_LDS const h8*)(ub + 32 * nb * ROWB);
+    }
 #pragma unroll
     for (int mb = 0; mb < C::MBW; ++mb) f.b[mb] = *(GP_LDS const h8*)(ua + 32 * mb * ROWB);
   };
@@ -205,9 +250,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     for (int nb = 0; nb < C::NBW; ++nb)
 #pragma unroll
       for (int mb = 0; mb < C::MBW; ++mb) acc[nb][mb] = mfma32(f.a[nb], f.b[mb], acc[nb][mb]);
+    constexpr int nm = C::NBW * C::MBW;
 #pragma unroll
-    for (int i = 0; i < C::NBW * C::MBW; ++i) {
+    for (int i = 0; i < nm; ++i) {
       if (i < nfr) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (i + nm < nfr) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // more reads than MFMAs: two per MFMA
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       if (i < nv) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
     }
@@ -237,8 +284,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     }
   };
 
-  constexpr int NFR = C::NBW + C::MBW;  // fragment reads per step
-  static_assert(NFR <= C::NBW * C::MBW, "reads are spread one per MFMA");
+  constexpr int NFR = (BROW ? 2 : 1) * C::NBW + C::MBW;  // fragment reads per step
+  static_assert(NFR <= 2 * C::NBW * C::MBW, "reads are spread at most two per MFMA");
   Tile T = tile_at(t);
   prefetch(T);
 #pragma unroll
@@ -465,22 +512,22 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const half_t* a, int lda, in
   }
 }
 
-template <class C, int ACT, bool RESID>
+template <class C, int ACT, bool RESID, bool BROW>
 static hipError_t launch(const Args& a, int num_cus, hipStream_t s) {
   const int64_t tiles = ((a.M + C::BM - 1) / C::BM) * (a.N / C::BN);
   const int64_t grid = tiles < num_cus ? tiles : num_cus;  // one persistent workgroup per CU
-  hipLaunchKernelGGL((gemm_kernel<C, ACT, RESID>), dim3((unsigned)grid), dim3(NT), 0, s, a);
+  hipLaunchKernelGGL((gemm_kernel<C, ACT, RESID, BROW>), dim3((unsigned)grid), dim3(NT), 0, s, a);
   return hipGetLastError();
 }
 
-template <class C>
+template <class C, bool BROW>
 static hipError_t dispatch(const Args& g, int act, int ncu, hipStream_t s) {
-  if (g.r) return act == ACT_NONE ? launch<C, ACT_NONE, true>(g, ncu, s) : hipErrorInvalidValue;
+  if (g.r) return act == ACT_NONE ? launch<C, ACT_NONE, true, BROW>(g, ncu, s) : hipErrorInvalidValue;
   switch (act) {
-    case ACT_NONE: return launch<C, ACT_NONE, false>(g, ncu, s);
-    case ACT_RELU: return launch<C, ACT_RELU, false>(g, ncu, s);
-    case ACT_GELU_TANH: return launch<C, ACT_GELU_TANH, false>(g, ncu, s);
-    case ACT_SIGMOID: return launch<C, ACT_SIGMOID, false>(g, ncu, s);
+    case ACT_NONE: return launch<C, ACT_NONE, false, BROW>(g, ncu, s);
+    case ACT_RELU: return launch<C, ACT_RELU, false, BROW>(g, ncu, s);
+    case ACT_GELU_TANH: return launch<C, ACT_GELU_TANH, false, BROW>(g, ncu, s);
+    case ACT_SIGMOID: return launch<C, ACT_SIGMOID, false, BROW>(g, ncu, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -496,10 +543,16 @@ hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t s) {
   const int lda = a.lda ? (int)a.lda : ka, ldc = a.ldc ? (int)a.ldc : (int)a.N;
   const int ldr = a.ldr ? (int)a.ldr : (int)a.N;
   if (lda < ka || ldc < a.N || (a.r && ldr < a.N) || lda % 8 || ldc % 8 || ldr % 8) return hipErrorInvalidValue;
-  const Args g{(const half_t*)a.x, (const half_t*)a.wt, (const half_t*)a.b, (const half_t*)a.r, (half_t*)a.out,
-               a.M, (int)a.N, (int)a.K, ka, lda, ldc, ldr};
-  if (a.N % Wide::BN == 0) return dispatch<Wide>(g, a.act, num_cus, s);
-  return dispatch<Narrow>(g, a.act, num_cus, s);
+  const bool brow = a.w != nullptr;
+  const int ldw = a.ldw ? (int)a.ldw : (int)a.N, kw = a.kw ? (int)a.kw : (int)a.K;
+  if (brow && (ldw < a.N || ldw % 8 || kw < 1 || kw > a.K || (uintptr_t)a.w % 16 ||
+               (int64_t)kw * ldw * 2 > (int64_t(1) << 31) - 1))
+    return hipErrorInvalidValue;
+  if (!brow && !a.wt) return hipErrorInvalidValue;
+  const Args g{(const half_t*)a.x, (const half_t*)a.wt, (const half_t*)a.w, ldw, kw, (const half_t*)a.b,
+               (const half_t*)a.r, (half_t*)a.out, a.M, (int)a.N, (int)a.K, ka, lda, ldc, ldr};
+  if (a.N % Wide::BN == 0) return brow ? dispatch<Wide, true>(g, a.act, num_cus, s) : dispatch<Wide, false>(g, a.act, num_cus, s);
+  return brow ? dispatch<Narrow, true>(g, a.act, num_cus, s) : dispatch<Narrow, false>(g, a.act, num_cus, s);
 }
 
 hipError_t prep_launch(const PrepSpec* L, int n, hipStream_t s) {

@@ -103,8 +103,30 @@ struct GemmArgs {
   void* out;       // [M, ldc]
   int64_t lda = 0, ldc = 0, ldr = 0;
   int64_t ka = 0;  // columns of x read (a multiple of 8; 0 = K); columns [ka, K) count as zero
+  // Instead of wt: W in its own layout, w [kw, ldw] (k by feature, 16-byte
+  // aligned, ldw a multiple of 8, ldw >= N; kw defaults to K and ldw to N);
+  // rows [kw, K) count as zero.  No transposed copy is needed.
+  const void* w = nullptr;
+  int64_t ldw = 0, kw = 0;
 };
 hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t stream);
+// Whether a layer chain reads its weights in place instead of from
+// transposed copies.  In place, each weight fragment of the GEMM's k-loop
+// takes two transposing LDS reads instead of one 16-byte read, which slows
+// the loop by about 15% (BERT-large FFN 1.21 -> 1.38 ms); the copies cost one
+// transpose launch per call (5-9 us).  Below kInPlaceMaxFlop of GEMM work
+// (about 80 us) in place comes out ahead: the bert_addln_ffn chain at its
+// app's batch 0.1165 -> 0.1148 ms, nerf_a 0.1788 -> 0.1737 ms.
+constexpr double kInPlaceMaxFlop = 8e10;
+inline bool weights_in_place(double flop) { return flop < kInPlaceMaxFlop; }
+
+// GEMM arguments for W [K, N] read in place (row stride N).
+inline GemmArgs gemm_w(int64_t M, int64_t N, int64_t K, const void* x, const void* w, const void* b, const void* r,
+                       int act, void* out) {
+  GemmArgs g{M, N, K, x, nullptr, b, r, act, out};
+  g.w = w;
+  return g;
+}
 // out[Np, Kp] = in[K, N]^T, zero-padded (Kp, Np default to K, N); Kp and Np
 // multiples of 64.
 hipError_t transpose_launch(const void* in, void* out, int64_t K, int64_t N, hipStream_t stream, int64_t Kp = 0,

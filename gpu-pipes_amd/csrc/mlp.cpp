@@ -55,19 +55,33 @@ int act_ok(int act) {
   return act == GP_ACT_NONE || act == GP_ACT_RELU || act == GP_ACT_GELU_TANH || act == GP_ACT_SIGMOID;
 }
 
-// One dense layer prepared for the GEMM stage.
+// One dense layer prepared for the GEMM stage: either its weights in place
+// (w [kw][Np], read by the GEMM in their own layout) or a transposed,
+// zero-padded copy (wt) when the output width is not a multiple of 128.
 struct Prepared {
-  const void* wt;  // [Np][Kin], zero-padded
-  const void* b;   // [Np], zero-padded
+  const void* wt;  // [Np][Kin], zero-padded (nullptr: w in place)
+  const void* b;   // [Np], zero-padded; the caller's bias when w is in place
   int64_t Kin, Np;
   int act;
+  const void* w = nullptr;  // [kw][Np]
+  int64_t kw = 0;
 };
+
+// A layer of a chain small enough to read its weights in place
+// (weights_in_place) does so when its output width is a multiple of 128 and
+// weights and bias are 16-byte aligned; otherwise they are prepared
+// (transposed, zero-padded) into the workspace by the chain's prep launch.
+bool in_place(bool chain, int64_t N, const void* w, const void* b) {
+  return chain && N % 128 == 0 && aligned16(w) && (!b || aligned16(b));
+}
 
 
 // ka: columns of `a` read (a multiple of 8, <= L.Kin); the rest count as zero.
 hipError_t layer(const Prepared& L, int64_t rows, const void* a, int64_t lda, void* c, int64_t ldc, int ncu,
                  hipStream_t s, int64_t ka = 0) {
   GemmArgs g{rows, L.Np, L.Kin, a, L.wt, L.b, nullptr, L.act, c};
+  g.w = L.w;
+  g.kw = L.kw;
   g.lda = lda;
   g.ldc = ldc;
   g.ka = ka;
@@ -116,14 +130,24 @@ int run_chain(int64_t M, int nl, const int64_t* widths, const void* const* w, co
   char* ws = nullptr;
   if ((rc = workspace_acquire(dev, s, cv.off, (void**)&ws))) return rc;
 
-  // Transpose and pad every layer's weight and bias into the workspace.
+  // Layers whose weights cannot be read in place are transposed and padded
+  // into the workspace (one launch for all of them).
   std::vector<Prepared> L(nl);
-  std::vector<PrepSpec> ps(nl);
+  std::vector<PrepSpec> ps;
+  double flop = 0;
+  for (int i = 0; i < nl; ++i) flop += 2.0 * M * widths[i] * widths[i + 1];
+  const bool chain = weights_in_place(flop);
   for (int i = 0; i < nl; ++i) {
-    ps[i] = {w[i], ws + o_wt[i], b[i], ws + o_b[i], widths[i], widths[i + 1], kin[i], np[i]};
-    L[i] = {ws + o_wt[i], ws + o_b[i], kin[i], np[i], acts[i]};
+    if (in_place(chain, widths[i + 1], w[i], b[i])) {
+      L[i] = {nullptr, b[i], kin[i], np[i], acts[i], w[i], widths[i]};
+    } else {
+      ps.push_back({w[i], ws + o_wt[i], b[i], ws + o_b[i], widths[i], widths[i + 1], kin[i], np[i]});
+      L[i] = {ws + o_wt[i], ws + o_b[i], kin[i], np[i], acts[i]};
+    }
   }
-  if (hipError_t e = prep_launch(ps.data(), nl, s); e != hipSuccess) return fail_hip(e, "MLP weight preparation");
+  if (!ps.empty())
+    if (hipError_t e = prep_launch(ps.data(), (int)ps.size(), s); e != hipSuccess)
+      return fail_hip(e, "MLP weight preparation");
   char* hb[2] = {ws + o_h0, ws + o_h1};
   for (int64_t r0 = 0; r0 < M; r0 += CH) {
     const int64_t rows = M - r0 < CH ? M - r0 : CH;
@@ -286,11 +310,20 @@ int gp_nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb
   if ((rc = workspace_acquire(dev, s, cv.off, (void**)&ws))) return rc;
   Prepared L[12];
   PrepSpec ps[12];
+  int nps = 0;
+  double flop = 0;
+  for (int i = 0; i < 12; ++i) flop += 2.0 * M * sh[i].K * sh[i].N;
+  const bool chain = weights_in_place(flop);
   for (int i = 0; i < 12; ++i) {
-    ps[i] = {w[i], ws + o_wt[i], b[i], ws + o_b[i], sh[i].K, sh[i].N, sh[i].Kin, sh[i].Np};
-    L[i] = {ws + o_wt[i], ws + o_b[i], sh[i].Kin, sh[i].Np, sh[i].act};
+    if (in_place(chain, sh[i].N, w[i], b[i])) {
+      L[i] = {nullptr, b[i], sh[i].Kin, sh[i].Np, sh[i].act, w[i], sh[i].K};
+    } else {
+      ps[nps++] = {w[i], ws + o_wt[i], b[i], ws + o_b[i], sh[i].K, sh[i].N, sh[i].Kin, sh[i].Np};
+      L[i] = {ws + o_wt[i], ws + o_b[i], sh[i].Kin, sh[i].Np, sh[i].act};
+    }
   }
-  if (hipError_t e = prep_launch(ps, 12, s); e != hipSuccess) return fail_hip(e, "NeRF weight preparation");
+  if (nps)
+    if (hipError_t e = prep_launch(ps, nps, s); e != hipSuccess) return fail_hip(e, "NeRF weight preparation");
   char *xb = ws + o_x, *c1 = ws + o_c1, *c2 = ws + o_c2, *h0 = ws + o_h0, *h1 = ws + o_h1, *hd = ws + o_hd;
   for (int64_t r0 = 0; r0 < M; r0 += CH) {
     const int64_t rows = M - r0 < CH ? M - r0 : CH;
@@ -368,11 +401,20 @@ int gp_nerf_a_out(int64_t M, int64_t Kx, const void* x, const void* const* w, co
   if ((rc = workspace_acquire(dev, s, cv.off, (void**)&ws))) return rc;
   Prepared L[8];
   PrepSpec ps[8];
+  int nps = 0;
+  double flop = 0;
+  for (int i = 0; i < 8; ++i) flop += 2.0 * M * kreal[i] * H;
+  const bool chain = weights_in_place(flop);
   for (int i = 0; i < 8; ++i) {
-    ps[i] = {w[i], ws + o_wt[i], b[i], ws + o_b[i], kreal[i], H, kin[i], H};
-    L[i] = {ws + o_wt[i], ws + o_b[i], kin[i], H, GP_ACT_RELU};
+    if (in_place(chain, H, w[i], b[i])) {
+      L[i] = {nullptr, b[i], kin[i], H, GP_ACT_RELU, w[i], kreal[i]};
+    } else {
+      ps[nps++] = {w[i], ws + o_wt[i], b[i], ws + o_b[i], kreal[i], H, kin[i], H};
+      L[i] = {ws + o_wt[i], ws + o_b[i], kin[i], H, GP_ACT_RELU};
+    }
   }
-  if (hipError_t e = prep_launch(ps, 8, s); e != hipSuccess) return fail_hip(e, "NerfA weight preparation");
+  if (nps)
+    if (hipError_t e = prep_launch(ps, nps, s); e != hipSuccess) return fail_hip(e, "NerfA weight preparation");
   char *xb = ws + o_x, *c1 = ws + o_c1, *h0 = ws + o_h0, *h1 = ws + o_h1;
   for (int64_t r0 = 0; r0 < M; r0 += CH) {
     const int64_t rows = M - r0 < CH ? M - r0 : CH;

@@ -137,6 +137,26 @@ def test_gemm_residual(cuda, M, N, K):
     assert_parity(f(y0), oracle.linear(f(x), f(w), None) + f(r), f"gemm+residual no bias M={M}")
 
 
+def test_gemm_weight_paths_agree(cuda):
+    """Below 8e10 FLOP per call the GEMM reads the weights in their own [K, N]
+    layout (transposing LDS reads); above, it reads a transposed copy.  The
+    two compute the same products in the same order: a call above the limit
+    and the same rows in calls below it are bit-identical, and both match the
+    oracle on sampled rows."""
+    M, N, K = 16384, 2048, 1280  # 2 M N K = 8.6e10: the transposed copy
+    g = torch.Generator().manual_seed(17)
+    x = torch.randn((M, K), generator=g).to(torch.float16).to(cuda)
+    w = (torch.randn((K, N), generator=g) / np.sqrt(K)).to(torch.float16).to(cuda)
+    b = (torch.randn((N,), generator=g) * 0.5).to(torch.float16).to(cuda)
+    y = gpipes.gemm_out(x, w, b, act="gelu_tanh")
+    parts = torch.cat([gpipes.gemm_out(x[r:r + 2048].contiguous(), w, b, act="gelu_tanh") for r in range(0, M, 2048)])
+    assert torch.equal(y.view(torch.int16), parts.view(torch.int16))
+    rows = np.r_[0:32, 8000:8032, M - 32:M]
+    xs = f(x[torch.from_numpy(rows).to(cuda)])
+    assert_parity(f(y[torch.from_numpy(rows).to(cuda)]), oracle.linear(xs, f(w), f(b), ACT_ID["gelu_tanh"]),
+                  "gemm transposed-copy path, sampled rows")
+
+
 def test_gemm_identity_weight_is_exact(cuda):
     """x . I (+ 0) passes every fp16 value through the fp32 accumulator unchanged."""
     M, K = 700, 256
