@@ -37,8 +37,9 @@
 //  * Prologue: the weights are copied HBM->LDS in their own row-major shape
 //    (whole 1 KiB copies into the X buffers and hand-off slots) and every
 //    wave reads its MFMA A fragments -- columns of W -- with the transposing
-//    LDS read ds_read_b64_tr_b16; W3 follows into the X buffers once W1 is
-//    read.  Two copy latencies and no transposing LDS writes.
+//    LDS read ds_read_b64_tr_b16; W3 follows into the hand-off slots once W1
+//    and W2 are read, while the first X tile is copied into the X buffers.
+//    Two copy latencies and no transposing LDS writes.
 #include "gp_device.hpp"
 #include "gp_kernels.hpp"
 
@@ -219,24 +220,28 @@ __device__ __forceinline__ h8 w_col8(const WSpan& w, int kb, int fb, int m) {
 
 // Prologue shared by both stages: W1 (into the X buffers) and W2 (into the
 // hand-off slots) are copied at once; take12(w1, w2) then reads the caller's
-// fragments; W3 follows into the X buffers once every wave has its W1 / W2
-// fragments, and take3(w3) reads it.  pre() runs while the first copies are
-// in flight.
-template <int K, typename Pre, typename T12, typename T3>
+// fragments.  W3 follows into the hand-off slots once every wave has its W1
+// and W2 fragments, and early() -- the first X tile's copies, from the A waves
+// -- goes into the X buffers at the same time; take3(w3) reads W3.  pre()
+// runs while the first copies are in flight.  EARLY_OPS: the copies early()
+// issues, which the W3 wait leaves in flight (the barriers after it wait for
+// LDS traffic only).
+template <int K, int EARLY_OPS, typename Pre, typename T12, typename Early, typename T3>
 __device__ __forceinline__ void stage_weights_dma(const Params& p, WSpan xsp, WSpan hsp, int wave, int lane, Pre pre,
-                                                  T12 take12, T3 take3) {
+                                                  T12 take12, Early early, T3 take3) {
   weight_dma<K>(p.w1, xsp, wave, lane);
   weight_dma<D>(p.w2, hsp, wave, lane);
   pre();
   wait_vmcnt<0>();
   __syncthreads();
   take12(xsp, hsp);
-  __syncthreads();  // W1 read by every wave
-  weight_dma<D>(p.w3, xsp, wave, lane);
-  wait_vmcnt<0>();
-  __syncthreads();
-  take3(xsp);
-  __syncthreads();  // the buffers return to their tiles
+  __syncthreads();  // W1 and W2 read by every wave
+  weight_dma<D>(p.w3, hsp, wave, lane);
+  early();
+  wait_vmcnt<EARLY_OPS>();
+  lds_barrier();
+  take3(hsp);
+  lds_barrier();  // the hand-off slots return to their tiles
 }
 
 // Sum of a value over the four lanes l, l^16, l^32, l^48 (the lanes that
@@ -323,22 +328,13 @@ void mgn_fused_kernel(Params p) {
   const int arow0 = lr * ACT_STRIDE, arow1 = (32 + lr) * ACT_STRIDE;
   GP_LDS int* const ab = (GP_LDS int*)&sy.abort;
   const int lim = p.spin_limit;
-  // prologue weight staging: W1 / W3 in the X buffers, W2 in the hand-off slots
+  // prologue weight staging: W1 in the X buffers, W2 then W3 in the hand-off slots
   static_assert(2 * C::XBUF >= K * D * 2 && 2 * TM * ACT_STRIDE >= D * D * 2, "staged weights must fit");
   const WSpan xspan{(GP_LDS char*)xs0, C::XBUF / 1024, (GP_LDS char*)xs1};
   const WSpan hspan{(GP_LDS char*)hand0, TM * ACT_STRIDE / 1024, (GP_LDS char*)hand1};
 
   if (stage_a) {
     // ------------------------------------------------------------- stage A
-    // W1 fragment for k-step s: lane holds W1[16s + 8*lh + e][32n + lr].
-    h8 w1f[C::KS1];
-    stage_weights_dma<K>(p, xspan, hspan, wave, lane, load_prm, [&](const WSpan& w1, const WSpan&) {
-#pragma unroll
-      for (int s = 0; s < C::KS1; ++s) w1f[s] = w_col8(w1, 16 * s + 8 * lh, 32 * n + 16 * ((lane >> 4) & 1), lane & 15);
-    }, [](const WSpan&) {});
-#pragma unroll
-    for (int s = 0; s < C::KS1; ++s) asm volatile("" : "+a"(w1f[s]));
-
     // X tiles are copied HBM->LDS by the four A waves (wave n issues the
     // 1 KiB wave copies n, n+4, ...).  LDS chunk slot q = 64*i + lane holds
     // row r = q / CPR, physical chunk p = q % CPR, which is logical chunk
@@ -369,6 +365,21 @@ void mgn_fused_kernel(Params p) {
 #pragma unroll
       for (int ii = 0; ii < C::DMA_PER_WAVE; ++ii) dma16_buf_nt(rsrc, voff[ii], buf + (ii * 4 + n) * 1024);
     };
+
+    // W1 fragment for k-step s: lane holds W1[16s + 8*lh + e][32n + lr].
+    // (Non-gather: the first X tile is copied during the W3 part of the prologue.)
+    h8 w1f[C::KS1];
+    stage_weights_dma<K, GATHER ? 0 : C::DMA_PER_WAVE>(p, xspan, hspan, wave, lane, load_prm,
+        [&](const WSpan& w1, const WSpan&) {
+#pragma unroll
+          for (int s = 0; s < C::KS1; ++s) w1f[s] = w_col8(w1, 16 * s + 8 * lh, 32 * n + 16 * ((lane >> 4) & 1), lane & 15);
+        },
+        [&]() {
+          if constexpr (!GATHER) issue(0, (GP_LDS char*)xs0);
+        },
+        [](const WSpan&) {});
+#pragma unroll
+    for (int s = 0; s < C::KS1; ++s) asm volatile("" : "+a"(w1f[s]));
 
     int abar = 0;
     int& abar0 = abar;
@@ -431,8 +442,6 @@ void mgn_fused_kernel(Params p) {
       const __amdgpu_buffer_rsrc_t rsrc = tile_rsrc(0);
 #pragma unroll
       for (int ii = 0; ii < C::DMA_PER_WAVE; ++ii) gather_copy(ii, rsrc, (GP_LDS char*)xs0);
-    } else {
-      issue(0, (GP_LDS char*)xs0);
     }
 
     const int xa = lh ^ (lr & 15);  // chunk (2s+lh) of rows lr, lr+32 lands at (2s ^ xa) in its 16-group
@@ -483,10 +492,10 @@ void mgn_fused_kernel(Params p) {
     const int l16 = lane & 15, q4 = lane >> 4;
     h8 w2f[D / 16];
     h8 w3f[8][4];
-    stage_weights_dma<K>(p, xspan, hspan, wave, lane, load_prm, [&](const WSpan&, const WSpan& w2) {
+    stage_weights_dma<K, 0>(p, xspan, hspan, wave, lane, load_prm, [&](const WSpan&, const WSpan& w2) {
 #pragma unroll
       for (int s = 0; s < D / 16; ++s) w2f[s] = w_col8(w2, 16 * s + 8 * lh, 32 * n + 16 * ((lane >> 4) & 1), lane & 15);
-    }, [&](const WSpan& w3) {
+    }, []() {}, [&](const WSpan& w3) {
 #pragma unroll
       for (int fb = 0; fb < 8; ++fb)
 #pragma unroll
