@@ -255,50 +255,89 @@ hipError_t linear_launch(const LinearArgs& a, int num_cus, hipStream_t s) {
 }
 
 // Whole-matrix LayerNorm (host_layer_norm, common/layer_norm_v2.cuh:129-147)
-// with the same arithmetic as pipe_layer_norm, laid out for bandwidth: one
-// wave per row, D/64 consecutive features per lane (one 4- to 32-byte
-// vector), 64-lane butterfly reductions, and up to 32 waves per CU so that
-// many rows' loads are in flight (the kernel is HBM-bound).
+// with the same two-pass arithmetic as pipe_layer_norm, laid out for
+// bandwidth: a row is read by LPR lanes with 16 or 32 bytes each (LPR = D/8
+// up to 64: four rows per wave instruction at D = 128, one at D >= 512), the
+// sums over a row's lanes are DPP row rotations and v_permlane16/32_swap, and
+// each wave issues the loads of U row groups before it reduces the first, so
+// that several memory latencies overlap (the kernel is HBM-bound).
+template <int LPR>
+__device__ __forceinline__ float sum_lanes(float x) {
+  static_assert(LPR == 16 || LPR == 32 || LPR == 64, "16, 32 or 64 lanes per row");
+#define GP_DPP_F(v, ctrl) __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false))
+  x += GP_DPP_F(x, 0x128);  // row_ror:8
+  x += GP_DPP_F(x, 0x124);  // row_ror:4
+  x += GP_DPP_F(x, 0x4E);   // quad_perm [2,3,0,1]
+  x += GP_DPP_F(x, 0xB1);   // quad_perm [1,0,3,2]
+#undef GP_DPP_F
+  if constexpr (LPR >= 32) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    x = __builtin_bit_cast(float, (unsigned)a[0]) + __builtin_bit_cast(float, (unsigned)a[1]);
+  }
+  if constexpr (LPR == 64) x = sum_lane_halves(x);
+  return x;
+}
+
 template <int D>
 __global__ __launch_bounds__(kStageThreads) void layer_norm_rows_kernel(const half_t* x, const half_t* gamma,
                                                                         const half_t* beta, float eps, half_t* out,
                                                                         int64_t M) {
-  constexpr int EPL = D / kWave;
+  constexpr int LPR = D / 8 < kWave ? D / 8 : kWave;  // lanes per row
+  constexpr int EPL = D / LPR;                        // elements per lane: 8 or 16
+  constexpr int RPW = kWave / LPR;                    // rows per wave instruction
+  constexpr int U = EPL == 8 ? 4 : 1;                 // row groups in flight per wave
   typedef _Float16 hv __attribute__((ext_vector_type(EPL)));
   const int lane = threadIdx.x & 63;
-  const int64_t step = (int64_t)gridDim.x * (kStageThreads / kWave);
-  hv gv, bv;
+  const int sub = lane / LPR, c = lane % LPR;
+  float g[EPL], bb[EPL];
+  {
+    hv gv, bv;
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    gv[e] = (half_t)1.f;
-    bv[e] = (half_t)0.f;
+    for (int e = 0; e < EPL; ++e) {
+      gv[e] = (half_t)1.f;
+      bv[e] = (half_t)0.f;
+    }
+    if (gamma) gv = *(const hv*)(gamma + c * EPL);
+    if (beta) bv = *(const hv*)(beta + c * EPL);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      g[e] = (float)gv[e];
+      bb[e] = (float)bv[e];
+    }
   }
-  if (gamma) gv = *(const hv*)(gamma + lane * EPL);
-  if (beta) bv = *(const hv*)(beta + lane * EPL);
-  for (int64_t r = (int64_t)blockIdx.x * (kStageThreads / kWave) + (threadIdx.x >> 6); r < M; r += step) {
-    const hv v = *(const hv*)(x + r * D + lane * EPL);
-    float f[EPL], s = 0.f;
+  const int64_t waves = (int64_t)gridDim.x * (kStageThreads / kWave);
+  const int64_t w0 = (int64_t)blockIdx.x * (kStageThreads / kWave) + (threadIdx.x >> 6);
+  // wave w takes row groups w, w + waves, ...; a group is RPW consecutive rows
+  for (int64_t grp = w0; grp * RPW < M; grp += U * waves) {
+    hv v[U];
+    int64_t row[U];
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      f[e] = (float)v[e];
-      s += f[e];
+    for (int u = 0; u < U; ++u) {
+      row[u] = (grp + u * waves) * RPW + sub;
+      if (row[u] < M) v[u] = *(const hv*)(x + row[u] * D + c * EPL);
     }
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, kWave);
-    const float mean = s * (1.f / D);
-    float q = 0.f;
+    for (int u = 0; u < U; ++u) {
+      float f[EPL], s = 0.f;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      const float d = f[e] - mean;
-      q = __builtin_fmaf(d, d, q);
+      for (int e = 0; e < EPL; ++e) {
+        f[e] = (float)v[u][e];
+        s += f[e];
+      }
+      const float mean = sum_lanes<LPR>(s) * (1.f / D);
+      float q = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        f[e] -= mean;
+        q = __builtin_fmaf(f[e], f[e], q);
+      }
+      const float rstd = rsqrtf(sum_lanes<LPR>(q) * (1.f / D) + eps);
+      hv o;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) o[e] = (half_t)__builtin_fmaf(f[e] * rstd, g[e], bb[e]);
+      if (row[u] < M) *(hv*)(out + row[u] * D + c * EPL) = o;
     }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) q += __shfl_xor(q, m, kWave);
-    const float rstd = rsqrtf(q * (1.f / D) + eps);
-    hv o;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) o[e] = (half_t)((f[e] - mean) * rstd * (float)gv[e] + (float)bv[e]);
-    *(hv*)(out + r * D + lane * EPL) = o;
   }
 }
 
