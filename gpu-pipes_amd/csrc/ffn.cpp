@@ -49,6 +49,47 @@ int opt16(const void* p, const char* name) {
 
 const char* at_row(const void* base, int64_t row, int64_t width) { return (const char*)base + row * width * 2; }
 
+// The LayerNorm epilogues of one call.  Below 128 features a row stays in one
+// wave; wider rows exchange partial statistics through a queue arena, under
+// one epoch for the whole call (its launches are rounds of that epoch, so a
+// failed wait in any of them reads as a failure of the call), whose status
+// word gp_pipeline_check reads.
+struct LnEpilogue {
+  void* ws = nullptr;
+  uint32_t epoch = 0;
+  int64_t round = 0;
+
+  int init(int dev, hipStream_t s, int64_t rows, int64_t H) {
+    if (H == 128) return GP_OK;
+    const int rc = arena_acquire(dev, s, gemm_ln_ws_bytes(rows, H), kArenaLayoutGemmLn, &ws, &epoch);
+    if (rc) return rc;
+    status_note(dev, s, (unsigned long long*)ws, epoch);
+    return GP_OK;
+  }
+  GemmArgs apply(GemmArgs g, const void* gamma, const void* beta, float eps) {
+    g.ln = 1;
+    g.gamma = gamma;
+    g.beta = beta;
+    g.eps = eps;
+    if (ws) {
+      g.ln_ws = ws;
+      g.status = (unsigned long long*)ws;
+      g.epoch = epoch;
+      g.spin_limit = (int)wait_limit(0);
+      g.ln_round = round++;
+    }
+    return g;
+  }
+};
+
+// Rows per chunk of the FFN blocks: at most kFfnChunkRows, and with the
+// LayerNorm in the GEMM epilogue at most the rows whose tiles are all
+// resident at once.  0 when the epilogue cannot take the LayerNorm.
+int64_t ln_chunk_rows(int64_t H, int ncu) {
+  const int64_t r = gemm_ln_max_rows(H, ncu);
+  return r < 256 ? 0 : (r < kFfnChunkRows ? r : kFfnChunkRows);
+}
+
 }  // namespace
 }  // namespace gp
 
@@ -112,14 +153,17 @@ int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void*
   hipStream_t s = (hipStream_t)stream;
 
   // Workspace: w1^T [FF][H], w2^T [H][FF] (unless the GEMMs read w1 and w2
-  // in place), then one chunk of activations [CH][FF] and of pre-LayerNorm
-  // rows [CH][H].
+  // in place), then one chunk of activations [CH][FF] and, when the
+  // LayerNorm is a launch of its own, of pre-LayerNorm rows [CH][H].
   const bool inplace = weights_in_place(4.0 * M * H * FF);
-  const int64_t CH = M < kFfnChunkRows ? M : kFfnChunkRows;
+  const int64_t lnch = ln_chunk_rows(H, ncu);
+  const bool fuse_ln = lnch > 0;
+  const int64_t chmax = fuse_ln ? lnch : kFfnChunkRows;
+  const int64_t CH = M < chmax ? M : chmax;
   const size_t o_w2t = inplace ? 0 : round_up((size_t)FF * H * 2);
   const size_t o_act = o_w2t + (inplace ? 0 : round_up((size_t)FF * H * 2));
   const size_t o_y = o_act + round_up((size_t)CH * FF * 2);
-  const size_t total = o_y + round_up((size_t)CH * H * 2);
+  const size_t total = o_y + (fuse_ln ? 0 : round_up((size_t)CH * H * 2));
   char* ws = nullptr;
   if ((rc = workspace_acquire(dev, s, total, (void**)&ws))) return rc;
   void *w1t = ws, *w2t = ws + o_w2t, *hbuf = ws + o_act, *ybuf = ws + o_y;
@@ -135,14 +179,23 @@ int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void*
                const void* r, int ac, void* c) {
     return inplace ? gemm_w(rows, N, K, a, w, b, r, ac, c) : GemmArgs{rows, N, K, a, wt, b, r, ac, c};
   };
+  LnEpilogue lne;
+  if (fuse_ln && (rc = lne.init(dev, s, CH, H))) return rc;
   for (int64_t r0 = 0; r0 < M; r0 += CH) {
     const int64_t rows = M - r0 < CH ? M - r0 : CH;
     const void* xc = at_row(x, r0, H);
+    char* const oc = (char*)out + r0 * H * 2;
     e = gemm_launch(g(rows, FF, H, xc, w1, w1t, b1, nullptr, act, hbuf), ncu, s);
     if (e != hipSuccess) return fail_hip(e, "FFN GEMM1 launch");
+    if (fuse_ln) {
+      // GEMM2 + bias + residual + LayerNorm in one launch
+      e = gemm_launch(lne.apply(g(rows, H, FF, hbuf, w2, w2t, b2, xc, GP_ACT_NONE, oc), gamma, beta, eps), ncu, s);
+      if (e != hipSuccess) return fail_hip(e, "FFN GEMM2 + LayerNorm launch");
+      continue;
+    }
     e = gemm_launch(g(rows, H, FF, hbuf, w2, w2t, b2, xc, GP_ACT_NONE, ybuf), ncu, s);
     if (e != hipSuccess) return fail_hip(e, "FFN GEMM2 launch");
-    e = layer_norm_launch(rows, H, ybuf, gamma, beta, eps, (char*)out + r0 * H * 2, ncu, s);
+    e = layer_norm_launch(rows, H, ybuf, gamma, beta, eps, oc, ncu, s);
     if (e != hipSuccess) return fail_hip(e, "FFN LayerNorm launch");
   }
   return GP_OK;
@@ -183,7 +236,10 @@ int gp_bert_addln_ffn_out(int64_t M, int64_t H, int64_t FF, const void* attn, co
   // read the weights in place), then for one chunk the pre-LayerNorm rows
   // y [CH][H], h0 [CH][H] and the activations [CH][FF].
   const bool inplace = weights_in_place(2.0 * M * H * (H + 2.0 * FF));
-  const int64_t CH = M < kFfnChunkRows ? M : kFfnChunkRows;
+  const int64_t lnch = ln_chunk_rows(H, ncu);
+  const bool fuse_ln = lnch > 0;
+  const int64_t chmax = fuse_ln ? lnch : kFfnChunkRows;
+  const int64_t CH = M < chmax ? M : chmax;
   const size_t o_w1t = inplace ? 0 : round_up((size_t)H * H * 2);
   const size_t o_w2t = o_w1t + (inplace ? 0 : round_up((size_t)FF * H * 2));
   const size_t o_y = o_w2t + (inplace ? 0 : round_up((size_t)FF * H * 2));
@@ -205,8 +261,21 @@ int gp_bert_addln_ffn_out(int64_t M, int64_t H, int64_t FF, const void* attn, co
                const void* r, int ac, void* c) {
     return inplace ? gemm_w(rows, N, K, a, w, b, r, ac, c) : GemmArgs{rows, N, K, a, wt, b, r, ac, c};
   };
+  LnEpilogue lne;
+  if (fuse_ln && (rc = lne.init(dev, s, CH, H))) return rc;
   for (int64_t r0 = 0; r0 < M; r0 += CH) {
     const int64_t rows = M - r0 < CH ? M - r0 : CH;
+    if (fuse_ln) {
+      // GEMM0 + b0 + x + LN0, GEMM1 + b1 + act, GEMM2 + b2 + h0 + LN2
+      char* const oc = (char*)out + r0 * H * 2;
+      e = gemm_launch(lne.apply(g(rows, H, H, at_row(attn, r0, H), w0, w0t, b0, at_row(x, r0, H), GP_ACT_NONE, h0),
+                                ga0, be0, eps), ncu, s);
+      if (e == hipSuccess) e = gemm_launch(g(rows, FF, H, h0, w1, w1t, b1, nullptr, act, abuf), ncu, s);
+      if (e == hipSuccess)
+        e = gemm_launch(lne.apply(g(rows, H, FF, abuf, w2, w2t, b2, h0, GP_ACT_NONE, oc), ga2, be2, eps), ncu, s);
+      if (e != hipSuccess) return fail_hip(e, "bert_addln_ffn launch");
+      continue;
+    }
     e = gemm_launch(g(rows, H, H, at_row(attn, r0, H), w0, w0t, b0, at_row(x, r0, H), GP_ACT_NONE, ybuf), ncu, s);
     if (e == hipSuccess) e = layer_norm_launch(rows, H, ybuf, ga0, be0, eps, h0, ncu, s);
     if (e == hipSuccess) e = gemm_launch(g(rows, FF, H, h0, w1, w1t, b1, nullptr, act, abuf), ncu, s);

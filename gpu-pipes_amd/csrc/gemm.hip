@@ -88,6 +88,17 @@ struct Args {
   int K;
   int ka;              // columns of A read (a multiple of 8, <= K); columns [ka, K) read as zero
   int lda, ldc, ldr;   // row strides in elements
+  // LayerNorm epilogue (LNM kernels): gamma / beta [N] or null (1 / 0), eps.
+  const half_t* gamma;
+  const half_t* beta;
+  float eps;
+  // LNM 2: per-row partial statistics [M][N / 128] ((mean, M2) of one wave's
+  // 128 features, as 64-bit words), per-row-block commit counters, and the
+  // launch context (epoch, status word, poll bound).
+  unsigned long long* stats;
+  QCounter* cnt;
+  QueueCtx ctx;
+  uint32_t ln_target;  // count of a row block's counter once this launch's waves have all committed
 };
 
 // Byte offset of logical 16-byte chunk c of unit row r: the chunk position is
@@ -106,7 +117,14 @@ __device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&&
 // (16-byte chunk c of row r at chunk position c ^ 4 (r % 4)), and the MFMA A
 // fragments -- columns of W -- are read with ds_read_b64_tr_b16, two reads
 // per fragment.  No transposed copy of W is made.
-template <class C, int ACT, bool RESID, bool BROW = false>
+//
+// LNM (LayerNorm epilogue): 0 none; 1 the tile holds whole rows and each
+// wave all 128 features of its rows (N = 128), so the row statistics stay in
+// the wave; 2 a row spans N / 128 waves of N / BN workgroups, which publish
+// per-wave partial statistics and combine them (one tile per workgroup,
+// every tile resident).  Launches of one epoch share the counters: launch
+// round r of the epoch waits for (r + 1) N / BN NW commits.
+template <class C, int ACT, bool RESID, bool BROW = false, int LNM = 0>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_kernel(Args p) {
   __shared__ __attribute__((aligned(1024))) char ring[NU * C::UNIT];
 
@@ -130,9 +148,17 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   const int G = gridDim.x;
   const int NX = G < 8 ? G : 8;
   const int xcd = blockIdx.x % NX, wid = blockIdx.x / NX;
-  const int nwx = (G - xcd + NX - 1) / NX;
-  const int hi = (int)((int64_t)ntiles * (xcd + 1) / NX);
+  int nwx = (G - xcd + NX - 1) / NX;
+  int hi = (int)((int64_t)ntiles * (xcd + 1) / NX);
   int t = (int)((int64_t)ntiles * xcd / NX) + wid;
+  if constexpr (LNM == 2) {
+    // One tile per workgroup (the grid is the tile count).  With a grid of
+    // whole multiples of 8, XCD x takes tiles [x G/8, (x+1) G/8), so the
+    // workgroups of one row block mostly share an L2.
+    t = G % 8 == 0 ? (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+    hi = t + 1;
+    nwx = 1;
+  }
   if (t >= hi) return;
 
   // Copies.  Copy j of a wave fills unit rows RPC (j NW + w) .. + RPC-1; lane
@@ -352,6 +378,18 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 #pragma unroll
       for (int g = 0; g < 4; ++g)
         bias[nb][g] = p.bias ? *(const h4*)(p.bias + T.n0 + 32 * C::NBW * wn + 32 * nb + 8 * g + 4 * lh) : h4{};
+    // LayerNorm affine of the same features.
+    h4 gam[LNM ? C::NBW : 1][4], bet[LNM ? C::NBW : 1][4];
+    if constexpr (LNM != 0) {
+#pragma unroll
+      for (int nb = 0; nb < C::NBW; ++nb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int f = T.n0 + 32 * C::NBW * wn + 32 * nb + 8 * g + 4 * lh;
+          gam[nb][g] = p.gamma ? *(const h4*)(p.gamma + f) : h4{1, 1, 1, 1};
+          bet[nb][g] = p.beta ? *(const h4*)(p.beta + f) : h4{};
+        }
+    }
 
     // The next tile's first units go out before this tile's epilogue, once
     // every wave has read the last slab (the barrier), so their latency hides
@@ -376,7 +414,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     // tile's valid rows; the residual loads of one nb are all issued before
     // the first is used.
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.c + T.m0 * p.ldc, T.rows * p.ldc * 2);
-    const __amdgpu_buffer_rsrc_t rr = make_rsrc(RESID ? p.r + T.m0 * p.ldr : p.c, RESID ? T.rows * p.ldr * 2 : 0);
+    // (A LayerNorm kernel without a residual reads it through an empty
+    // descriptor: zeros.)
+    const bool hr = RESID && p.r != nullptr;
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(hr ? p.r + T.m0 * p.ldr : p.c, hr ? T.rows * p.ldr * 2 : 0);
     // Per-row byte offsets, computed here (opaque: not hoisted out of the tile
     // loop as 64 live registers); the nb / g part is an instruction offset.
     int ebase[C::MBW], rbase[C::MBW];
@@ -388,42 +429,211 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     }
     auto eoff = [&](int nb, int q, int mb) { return ebase[mb] + (32 * nb + 16 * q) * 2; };
     auto roff = [&](int nb, int g, int mb) { return rbase[mb] + (32 * nb + 8 * g) * 2; };
+    // Stores of the eight-feature groups of fragment (nb, mb), o[g] holding
+    // feature group g (the v_permlane32_swap pairing described above).
+    auto store_frag = [&](const u32x2 (&o)[4], int nb, int mb) {
 #pragma unroll
-    for (int nb = 0; nb < C::NBW; ++nb) {
-      // Pin the accumulators of block nb in place until here: the blocks are
-      // read one after another rather than all hoisted into VGPRs at once.
+      for (int q = 0; q < 2; ++q) {
+        const auto lo = __builtin_amdgcn_permlane32_swap(o[2 * q][0], o[2 * q + 1][0], false, false);
+        const auto hi = __builtin_amdgcn_permlane32_swap(o[2 * q][1], o[2 * q + 1][1], false, false);
+        const u32x4 w = {(unsigned)lo[0], (unsigned)hi[0], (unsigned)lo[1], (unsigned)hi[1]};
+        buf_store_u4(rc, eoff(nb, q, mb), w);
+      }
+    };
+    if constexpr (LNM != 0) {
+      // LayerNorm epilogue.  Pass 1: v = fp16(acc + bias + r) -- the value a
+      // separate LayerNorm launch would read -- and the row sums.  The fp16
+      // values go back into the first eight registers of their accumulator
+      // fragment as pairs, and every later use reads them through
+      // v_fma_mix_f32 (fp16 operands taken as they are), which keeps the
+      // epilogue's VALU work about half of an fp32 formulation's.  A lane
+      // holds 64 features of its row (16 per fragment nb), the lane 32 apart
+      // the other 64 of the wave's 128.
+      static_assert(C::NBW == 4, "a wave holds 128 features of its rows");
+      float s[C::MBW], mean[C::MBW], rstd[C::MBW];
 #pragma unroll
-      for (int mb = 0; mb < C::MBW; ++mb) asm volatile("" : "+a"(acc[nb][mb]));
-      h4 res[4][C::MBW];
-      if constexpr (RESID) {
+      for (int mb = 0; mb < C::MBW; ++mb) s[mb] = 0.f;
+      // 1.0 the compiler cannot see: fma(x, one, y) stays an fma (one
+      // v_fma_mix_f32 when x is an fp16 value) instead of becoming x + y.
+      float one = 1.f;
+      asm volatile("" : "+v"(one));
+#pragma unroll
+      for (int nb = 0; nb < C::NBW; ++nb) {
+#pragma unroll
+        for (int mb = 0; mb < C::MBW; ++mb) asm volatile("" : "+a"(acc[nb][mb]));
+        h4 res[4][C::MBW];
 #pragma unroll
         for (int g = 0; g < 4; ++g)
 #pragma unroll
           for (int mb = 0; mb < C::MBW; ++mb) res[g][mb] = buf_load_h4(rr, roff(nb, g, mb));
+#pragma unroll
+        for (int mb = 0; mb < C::MBW; ++mb) {
+          h2 pk[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            f2 t;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              // fma(x, 1, y) rounds x + y once: the sums of the plain epilogue
+              const int i = 2 * j + e;
+              t[e] = __builtin_fmaf((float)bias[nb][i / 4][i % 4], one, acc[nb][mb][i]);
+              t[e] = __builtin_fmaf((float)res[i / 4][mb][i % 4], one, t[e]);
+            }
+            // Rounded to fp16 from the fp32 sum, as the plain epilogue does (the
+            // barrier keeps the rounding out of the fma: one v_cvt_pk_f16_f32).
+            asm volatile("" : "+v"(t));
+            pk[j] = __builtin_convertvector(t, h2);
+#pragma unroll
+            for (int e = 0; e < 2; ++e) s[mb] = __builtin_fmaf((float)pk[j][e], one, s[mb]);
+          }
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[nb][mb][j] = __builtin_bit_cast(float, pk[j]);
+        }
+#pragma unroll
+        for (int mb = 0; mb < C::MBW; ++mb) asm volatile("" : "+a"(acc[nb][mb]));  // v back in AGPRs
       }
+      // (The element is copied out first: __builtin_bit_cast of a vector
+      // element lvalue reads element 0 of the vector in this compiler.)
+      auto vh = [&](int nb, int mb, int i) {
+        const float w = acc[nb][mb][i / 2];
+        return (float)__builtin_bit_cast(h2, w)[i % 2];
+      };
+      // Pass 2: the wave's mean and sum of squared deviations per row.
+      float q[C::MBW];
 #pragma unroll
       for (int mb = 0; mb < C::MBW; ++mb) {
-        u32x2 o[4];
+        mean[mb] = sum_lane_halves(s[mb]) * (1.f / 128);
+        q[mb] = 0.f;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          f4 v;
+        for (int nb = 0; nb < C::NBW; ++nb)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            v[e] = apply_act(acc[nb][mb][4 * g + e] + (float)bias[nb][g][e], ACT);
-            if constexpr (RESID) v[e] += (float)res[g][mb][e];
+          for (int i = 0; i < 16; ++i) {
+            const float d = __builtin_fmaf(vh(nb, mb, i), one, -mean[mb]);
+            q[mb] = __builtin_fmaf(d, d, q[mb]);
           }
-          o[g] = __builtin_bit_cast(u32x2, __builtin_convertvector(v, h4));
+        q[mb] = sum_lane_halves(q[mb]);
+      }
+      bool ok = true;
+      if constexpr (LNM == 1) {
+#pragma unroll
+        for (int mb = 0; mb < C::MBW; ++mb) rstd[mb] = rsqrtf(q[mb] * (1.f / 128) + p.eps);
+      } else {
+        // Publish (mean, M2) of this wave's 128 features for each of its
+        // rows, count the wave's commit on the row block, wait for all
+        // N / BN x NW commits, and combine the N / 128 partials (Chan et al.:
+        // M2 = sum M2_i + 128 sum (mean_i - mean)^2), P <= 8.
+        const int P = p.N >> 7;
+        const int pidx = (T.n0 >> 7) + wn;
+#pragma unroll
+        for (int mb = 0; mb < C::MBW; ++mb) {
+          const int r = arow + 32 * mb;
+          if (lh == 0 && r < T.rows)
+            __hip_atomic_store(p.stats + (T.m0 + r) * P + pidx, __builtin_bit_cast(unsigned long long, f2{mean[mb], q[mb]}),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_s_waitcnt(kWaitAll);
+        QCounter* const c = p.cnt + (int)(T.m0 / C::BM);
+        if (lane == 0) qcommit(c, p.ctx.epoch);
+        const uint32_t target = p.ln_target;
+        for (int it = 0;; ++it) {
+          const unsigned long long v = __hip_atomic_load(&c->v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (qcount(v, p.ctx.epoch) >= target) break;
+          if (q_aborted(p.ctx)) {
+            ok = false;
+            break;
+          }
+          if (it >= p.ctx.limit) {
+            if (lane == 0) q_fail(p.ctx, kErrTimeout);
+            ok = false;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(4);
         }
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const auto lo = __builtin_amdgcn_permlane32_swap(o[2 * q][0], o[2 * q + 1][0], false, false);
-          const auto hi = __builtin_amdgcn_permlane32_swap(o[2 * q][1], o[2 * q + 1][1], false, false);
-          const u32x4 w = {(unsigned)lo[0], (unsigned)hi[0], (unsigned)lo[1], (unsigned)hi[1]};
-          buf_store_u4(rc, eoff(nb, q, mb), w);
+        for (int mb = 0; mb < C::MBW; ++mb) {
+          const int r = arow + 32 * mb;
+          f2 part[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            part[i] = f2{0.f, 0.f};
+            if (i < P && r < T.rows && ok)
+              part[i] = __builtin_bit_cast(f2, __hip_atomic_load(p.stats + (T.m0 + r) * P + i, __ATOMIC_RELAXED,
+                                                                 __HIP_MEMORY_SCOPE_AGENT));
+          }
+          float m = 0.f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) m += part[i][0];
+          m /= (float)P;
+          float m2 = 0.f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (i < P) {
+              const float d = part[i][0] - m;
+              m2 += __builtin_fmaf(128.f * d, d, part[i][1]);
+            }
+          mean[mb] = m;
+          rstd[mb] = rsqrtf(m2 / (float)p.N + p.eps);
+        }
+      }
+      // Pass 3: normalise, affine, fp16, store.  After a failed wait nothing
+      // is stored.
+      if (ok) {
+#pragma unroll
+        for (int nb = 0; nb < C::NBW; ++nb) {
+#pragma unroll
+          for (int mb = 0; mb < C::MBW; ++mb) asm volatile("" : "+a"(acc[nb][mb]));
+#pragma unroll
+          for (int mb = 0; mb < C::MBW; ++mb) {
+            u32x2 o[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              f4 v;
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                v[e] = __builtin_fmaf(__builtin_fmaf(vh(nb, mb, 4 * g + e), one, -mean[mb]) * rstd[mb],
+                                      (float)gam[nb][g][e], (float)bet[nb][g][e]);
+              o[g] = __builtin_bit_cast(u32x2, __builtin_convertvector(v, h4));
+            }
+            store_frag(o, nb, mb);
+          }
         }
       }
 #pragma unroll
-      for (int mb = 0; mb < C::MBW; ++mb) acc[nb][mb] = f16x{};  // ready for the next tile
+      for (int nb = 0; nb < C::NBW; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < C::MBW; ++mb) acc[nb][mb] = f16x{};  // ready for the next tile
+    } else {
+#pragma unroll
+      for (int nb = 0; nb < C::NBW; ++nb) {
+        // Pin the accumulators of block nb in place until here: the blocks are
+        // read one after another rather than all hoisted into VGPRs at once.
+#pragma unroll
+        for (int mb = 0; mb < C::MBW; ++mb) asm volatile("" : "+a"(acc[nb][mb]));
+        h4 res[4][C::MBW];
+        if constexpr (RESID) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int mb = 0; mb < C::MBW; ++mb) res[g][mb] = buf_load_h4(rr, roff(nb, g, mb));
+        }
+#pragma unroll
+        for (int mb = 0; mb < C::MBW; ++mb) {
+          u32x2 o[4];
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            f4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v[e] = apply_act(acc[nb][mb][4 * g + e] + (float)bias[nb][g][e], ACT);
+              if constexpr (RESID) v[e] += (float)res[g][mb][e];
+            }
+            o[g] = __builtin_bit_cast(u32x2, __builtin_convertvector(v, h4));
+          }
+          store_frag(o, nb, mb);
+        }
+#pragma unroll
+        for (int mb = 0; mb < C::MBW; ++mb) acc[nb][mb] = f16x{};  // ready for the next tile
+      }
     }
     if (!more) break;
     wait_first(true);
@@ -512,11 +722,14 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const half_t* a, int lda, in
   }
 }
 
-template <class C, int ACT, bool RESID, bool BROW>
+template <class C, int ACT, bool RESID, bool BROW, int LNM = 0>
 static hipError_t launch(const Args& a, int num_cus, hipStream_t s) {
   const int64_t tiles = ((a.M + C::BM - 1) / C::BM) * (a.N / C::BN);
-  const int64_t grid = tiles < num_cus ? tiles : num_cus;  // one persistent workgroup per CU
-  hipLaunchKernelGGL((gemm_kernel<C, ACT, RESID, BROW>), dim3((unsigned)grid), dim3(NT), 0, s, a);
+  // One persistent workgroup per CU; the LNM 2 kernels take one tile each,
+  // all resident at once (the host keeps tiles <= num_cus).
+  if (LNM == 2 && tiles > num_cus) return hipErrorInvalidValue;
+  const int64_t grid = tiles < num_cus ? tiles : num_cus;
+  hipLaunchKernelGGL((gemm_kernel<C, ACT, RESID, BROW, LNM>), dim3((unsigned)grid), dim3(NT), 0, s, a);
   return hipGetLastError();
 }
 
@@ -532,7 +745,26 @@ static hipError_t dispatch(const Args& g, int act, int ncu, hipStream_t s) {
   }
 }
 
+// The LNM 2 exchange area: the status word's line, kLnMaxBlocks counter
+// lines (one per 256-row block of a launch), then 8 bytes per row and wave of
+// partial statistics.  The counters sit at the same place whatever the
+// launch's shape: the statistics of one call must never land where a later
+// call with more row blocks keeps a counter (a payload word there would
+// defeat the epoch test and the wait would run out).
+constexpr int64_t kLnMaxBlocks = 1024;
+size_t ln_ws_bytes(int64_t M, int64_t N) {
+  return sizeof(QCounter) * (size_t)(1 + kLnMaxBlocks) + (size_t)M * (size_t)(N / 128) * 8;
+}
+
 }  // namespace gemm
+
+int64_t gemm_ln_max_rows(int64_t N, int num_cus) {
+  if (N == 128) return int64_t(1) << 62;  // rows stay within a wave: any M
+  const int64_t tiles_n = N % gemm::Wide::BN == 0 ? N / gemm::Wide::BN : N / gemm::Narrow::BN;
+  return (num_cus / tiles_n) * 256;  // both configurations have 256-row tiles
+}
+
+size_t gemm_ln_ws_bytes(int64_t M, int64_t N) { return N == 128 ? 0 : gemm::ln_ws_bytes(M, N); }
 
 hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t s) {
   using namespace gemm;
@@ -549,8 +781,27 @@ hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t s) {
                (int64_t)kw * ldw * 2 > (int64_t(1) << 31) - 1))
     return hipErrorInvalidValue;
   if (!brow && !a.wt) return hipErrorInvalidValue;
-  const Args g{(const half_t*)a.x, (const half_t*)a.wt, (const half_t*)a.w, ldw, kw, (const half_t*)a.b,
-               (const half_t*)a.r, (half_t*)a.out, a.M, (int)a.N, (int)a.K, ka, lda, ldc, ldr};
+  Args g{(const half_t*)a.x, (const half_t*)a.wt, (const half_t*)a.w, ldw, kw, (const half_t*)a.b,
+         (const half_t*)a.r, (half_t*)a.out, a.M, (int)a.N, (int)a.K, ka, lda, ldc, ldr,
+         (const half_t*)a.gamma, (const half_t*)a.beta, a.eps, nullptr, nullptr, QueueCtx{}, 0};
+  if (a.ln) {
+    static_assert(Wide::BM == 256 && Narrow::BM == 256, "gemm_ln_max_rows assumes 256-row tiles");
+    if (a.act != ACT_NONE || a.N > 1024 || ((uintptr_t)a.gamma | (uintptr_t)a.beta) % 8) return hipErrorInvalidValue;
+    if (a.N == 128) return brow ? launch<Narrow, ACT_NONE, true, true, 1>(g, num_cus, s)
+                                : launch<Narrow, ACT_NONE, true, false, 1>(g, num_cus, s);
+    if (!a.ln_ws || !a.status || a.epoch == 0 || a.M > gemm_ln_max_rows(a.N, num_cus)) return hipErrorInvalidValue;
+    if ((a.M + 255) / 256 > kLnMaxBlocks) return hipErrorInvalidValue;
+    QCounter* const q = (QCounter*)a.ln_ws;
+    g.cnt = q + 1;
+    g.stats = (unsigned long long*)(q + 1 + kLnMaxBlocks);
+    g.ctx = QueueCtx{a.epoch, a.status, a.spin_limit > 0 ? a.spin_limit : kQueueSpinLimit};
+    const int64_t tiles_n = a.N % Wide::BN == 0 ? a.N / Wide::BN : a.N / Narrow::BN;
+    if (a.ln_round < 0 || (a.ln_round + 1) * tiles_n * NW > 0x7fffffff) return hipErrorInvalidValue;
+    g.ln_target = (uint32_t)((a.ln_round + 1) * tiles_n * NW);
+    if (a.N % Wide::BN == 0)
+      return brow ? launch<Wide, ACT_NONE, true, true, 2>(g, num_cus, s) : launch<Wide, ACT_NONE, true, false, 2>(g, num_cus, s);
+    return brow ? launch<Narrow, ACT_NONE, true, true, 2>(g, num_cus, s) : launch<Narrow, ACT_NONE, true, false, 2>(g, num_cus, s);
+  }
   if (a.N % Wide::BN == 0) return brow ? dispatch<Wide, true>(g, a.act, num_cus, s) : dispatch<Wide, false>(g, a.act, num_cus, s);
   return brow ? dispatch<Narrow, true>(g, a.act, num_cus, s) : dispatch<Narrow, false>(g, a.act, num_cus, s);
 }

@@ -38,6 +38,7 @@ constexpr uint32_t kArenaLayoutMgn = 1;    // mgn_pipelined Queues
 constexpr uint32_t kArenaLayoutRoute = 2;  // route kernels (+1 for the split layout)
 constexpr uint32_t kArenaLayoutBertAddln = 4;
 constexpr uint32_t kArenaLayoutNerfA = 5;
+constexpr uint32_t kArenaLayoutGemmLn = 6;  // LayerNorm-epilogue GEMMs: partial row statistics
 // GP_ERR_INVALID_ARG if `stream` is capturing into a graph: the queue-chained
 // launches call it before any other HIP call (a replay would reuse the
 // captured queue epoch).

@@ -108,8 +108,30 @@ struct GemmArgs {
   // rows [kw, K) count as zero.  No transposed copy is needed.
   const void* w = nullptr;
   int64_t ldw = 0, kw = 0;
+  // LayerNorm epilogue (ln != 0, act must be ACT_NONE): out = LayerNorm(x W +
+  // b + r) over each row's N features, gamma / beta (null: 1 / 0), eps.  For
+  // N > 128 a row spans several waves and workgroups, which exchange partial
+  // statistics through ln_ws (gemm_ln_ws_bytes(M, N) bytes of a queue arena,
+  // zeroed when allocated; the status word is its first 8 bytes) under an
+  // epoch; every tile must then be resident at once: at most num_cus tiles
+  // (gemm_ln_max_rows) and at most 1024 row blocks.  Launches of one epoch on
+  // one ln_ws are numbered by ln_round (0, 1, ...) and must cover a prefix of
+  // the same row blocks in every earlier round.
+  int ln = 0;
+  int64_t ln_round = 0;
+  const void* gamma = nullptr;
+  const void* beta = nullptr;
+  float eps = 0.f;
+  void* ln_ws = nullptr;
+  unsigned long long* status = nullptr;
+  uint32_t epoch = 0;
+  int spin_limit = 0;
 };
 hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t stream);
+// Rows one LayerNorm-epilogue launch may cover (all tiles resident), and the
+// size of its exchange area.
+int64_t gemm_ln_max_rows(int64_t N, int num_cus);
+size_t gemm_ln_ws_bytes(int64_t M, int64_t N);
 // Whether a layer chain reads its weights in place instead of from
 // transposed copies.  In place, each weight fragment of the GEMM's k-loop
 // takes two transposing LDS reads instead of one 16-byte read, which slows

@@ -88,6 +88,53 @@ def test_bert_ffn_no_affine_no_bias(cuda):
     assert_parity(f(y), want, "no biases, no affine")
 
 
+# ------------------------------------------------------------------ LayerNorm in GEMM2's epilogue
+@pytest.mark.parametrize("M,H,FF", [(300, 128, 512), (257, 256, 1024), (1000, 512, 2048), (20000, 1024, 4096)])
+def test_bert_ffn_ln_epilogue_matches_separate_launches(cuda, M, H, FF):
+    """gp_bert_ffn_out computes the LayerNorm in GEMM2's epilogue: within a wave
+    at H = 128, from per-wave partial statistics exchanged between waves and
+    workgroups above (M = 20,000 at H = 1024 is two row chunks, two rounds of
+    one exchange epoch).  Against GEMM2 + residual written out and the
+    LayerNorm launch reading it back, the pre-LayerNorm rows are the same fp16
+    values and only the summation order of the statistics differs, so every
+    output agrees to one fp16 rounding step and almost all bit for bit."""
+    print(f"[ln-epilogue] M={M} H={H} FF={FF}", flush=True)
+    p = dev(bert_params(H, FF, seed=H, init="bert", affine_random=True), cuda)
+    x = normal_fp16(M, H, seed=7, device=cuda)
+    y = ffn(x, p, "gelu_tanh", 1e-12)
+    h = gpipes.gemm_out(x, p["w1"], p["b1"], act="gelu_tanh")
+    pre = gpipes.gemm_out(h, p["w2"], p["b2"], r=x)
+    sep = gpipes.layer_norm_out(pre, p["gamma"], p["beta"], eps=1e-12)
+    gpipes.pipeline_check()
+    yf, sf = y.float(), sep.float()
+    step = torch.maximum(yf.abs(), sf.abs()) * 2.0 ** -10 + 2.0 ** -24
+    assert bool(((yf - sf).abs() <= step).all()), float((yf - sf).abs().max())
+    same = (y.view(torch.int16) == sep.view(torch.int16)).float().mean().item()
+    print(f"[ln-epilogue] bit-identical fraction {same:.5f}", flush=True)
+    assert same >= 0.99
+    rows = np.r_[0:min(M, 64), max(0, M - 64):M]
+    assert_parity(f(y)[rows], oracle_ffn(x[rows], p, "gelu_tanh", 1e-12), f"LN epilogue M={M} H={H}")
+
+
+def test_bert_ffn_ln_exchange_reused_across_shapes(cuda):
+    """The exchange area of the LayerNorm epilogue is one per stream and is reused
+    by calls of any shape: a call with fewer row blocks writes its partial
+    statistics, then calls with more row blocks and another width must still
+    find their counters clean (a regression test: with the statistics placed
+    right after the launch's own counters, the second call's counters held the
+    first call's statistics and its waits ran out)."""
+    H, FF = 1024, 1024
+    p = dev(bert_params(H, FF, seed=11, init="bert", affine_random=True), cuda)
+    p2 = dev(bert_params(256, 512, seed=12, init="bert", affine_random=True), cuda)
+    for M, q, width in [(77, p, H), (1000, p, H), (3000, p2, 256), (600, p, H), (1000, p, H)]:
+        print(f"[ln-exchange] M={M} H={width}", flush=True)
+        x = normal_fp16(M, width, seed=M, device=cuda)
+        y = ffn(x, q, "gelu_tanh", 1e-12)
+        gpipes.pipeline_check()
+        rows = np.r_[0:min(M, 40), max(0, M - 40):M]
+        assert_parity(f(y)[rows], oracle_ffn(x[rows], q, "gelu_tanh", 1e-12), f"reused exchange M={M} H={width}")
+
+
 # ------------------------------------------------------------------ full size (config 2)
 def test_bert_large_full_size(cuda):
     """M = 65,536 (128 x 512 tokens), H 1024, FF 4096, GELU(tanh), eps 1e-12: four

@@ -71,6 +71,39 @@ def test_fused_timeout_reported(cuda, restore_limit, K, ln):
     assert_parity(y.float().cpu().numpy()[idx], run_oracle(x.cpu()[idx], p), f"after timeout K={K}")
 
 
+def test_gemm_ln_exchange_timeout_reported(cuda, restore_limit):
+    """GEMM2's LayerNorm epilogue at H = 1024: each row's partial statistics come
+    from 16 waves of four workgroups.  With a one-poll bound the waits give up;
+    the call reports GP_ERR_TIMEOUT.  A wave stores its 128 features of a row
+    only after its own wait succeeded, so a row may be partly stored: every
+    element is either untouched or equal to a normal call's."""
+    from gpipes.synth import bert_params
+    M, H, FF = 16384, 1024, 1024
+    print(f"[timeout] bert_ffn LayerNorm exchange M={M} H={H} FF={FF}", flush=True)
+    p = {k: (None if v is None else v.to(cuda)) for k, v in bert_params(H, FF, seed=2, init="bert").items()}
+    x = normal_fp16(M, H, seed=3).to(cuda)
+
+    def call(out):
+        return gpipes.bert_ffn_out(x, p["w1"], p["b1"], p["w2"], p["b2"], p["gamma"], p["beta"], out, eps=1e-12,
+                                   act="gelu_tanh")
+
+    ref = call(torch.empty_like(x))
+    gpipes.pipeline_check()
+    out = torch.full((M, H), SENTINEL, dtype=torch.int16, device=cuda).view(torch.float16)
+    gpipes.set_wait_limit(1)
+    call(out)
+    expect_timeout()
+    g = out.view(torch.int16)
+    untouched = g == SENTINEL
+    print(f"[timeout] elements left untouched: {int(untouched.sum())} of {M * H}", flush=True)
+    assert bool((untouched | (g == ref.view(torch.int16))).all()), "an aborted launch stored values that differ"
+
+    gpipes.set_wait_limit(0)
+    y = call(torch.empty_like(x))
+    gpipes.pipeline_check()
+    assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+
+
 def test_gather_timeout_reported(cuda, restore_limit):
     E, N = 64 * 256 * 2 + 33, 5000
     print(f"[timeout] gather E={E} N={N}", flush=True)
