@@ -131,10 +131,14 @@ int gp_mgn_edge_gather_out(int64_t E, int64_t N, const void* nf, const void* ef,
  * Replaces bert_ffn_out(x, w1, b1, w2, b2, ga, be, out),
  * apps/bert_ffn/pipelined/bert_ffn_pl_ext.cu:24-56 (H = 128, FF = 512, ReLU,
  * eps 1e-5 fixed), and the bulk-sync chain gemm / gemm / add / LayerNorm of
- * apps/bert_ffn/bulksync/bert_ffn_bs.cuh:12-27.  The FF-wide activations pass
- * through a workspace kept per (device, stream), allocated on first use and
- * grown when needed (a grow synchronises the stream).  Any M >= 0 (the
- * reference needs M to be a multiple of its pipeline rows x 128).
+ * apps/bert_ffn/bulksync/bert_ffn_bs.cuh:12-27.  Per row chunk, two GEMM
+ * launches; the second computes the residual add and the LayerNorm in its
+ * epilogue.  Above H = 128 a row spans several workgroups, which exchange
+ * partial row statistics through the stream's queue arena with bounded waits:
+ * such calls report failures through gp_pipeline_check.  The FF-wide
+ * activations pass through a workspace kept per (device, stream), allocated
+ * on first use and grown when needed (a grow synchronises the stream).  Any
+ * M >= 0 (the reference needs M to be a multiple of its pipeline rows x 128).
  */
 int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void* w1, const void* b1,
                     const void* w2, const void* b2, const void* gamma, const void* beta, float eps, int act,
@@ -152,9 +156,10 @@ int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void*
  * Replaces bert_addln_ffn_out(attn_out, x, w0, b0, w1, b1, w2, b2, ga0, be0,
  * ga2, be2, out), apps/bert_addln_ffn/pipelined/bert_addln_ffn_pl_ext.cu:17-58
  * (H 128, FF 512, ReLU, M a multiple of 128).  impl GP_IMPL_FUSED (0, the
- * default) runs one GEMM launch per linear layer with bias, activation and
- * residual fused into its epilogue, plus two LayerNorm launches, over row
- * chunks in the per-stream workspace; GP_IMPL_PIPELINED runs the reference's
+ * default) runs one GEMM launch per linear layer with bias, activation,
+ * residual and LayerNorm fused into its epilogue, over row chunks in the
+ * per-stream workspace (above H = 128 with failures reported by
+ * gp_pipeline_check, as gp_bert_ffn_out); GP_IMPL_PIPELINED runs the reference's
  * queue-chained layout (bert_addln_ffn_pl.cuh:92-176: stage workgroups linked
  * by ring queues, both adds fed from queues) for H = 128, FF = 512 and ReLU or
  * GELU(tanh), with failures reported by gp_pipeline_check.  The reference's
@@ -346,8 +351,9 @@ int gp_pipe_route(int64_t M, const void* x, void* out, void* out2, int route, in
  * reports device-side failures failed (GP_ERR_TIMEOUT) or completed (GP_OK).
  * Those are the launches of gp_mgn_fullmlp_out, gp_mgn_linears_out,
  * gp_mgn_mlp_out (every impl), gp_mgn_edge_gather_out, gp_pipe_ident,
- * gp_pipe_route, and gp_bert_addln_ffn_out / gp_nerf_a_out with
- * GP_IMPL_PIPELINED: every wait between their workgroups or waves is bounded, and
+ * gp_pipe_route, gp_bert_addln_ffn_out / gp_nerf_a_out with
+ * GP_IMPL_PIPELINED, and gp_bert_ffn_out / gp_bert_addln_ffn_out (fused) with
+ * H > 128: every wait between their workgroups or waves is bounded, and
  * one that runs out makes the launch end early and leave its outputs invalid
  * (the fused kernels store nothing after it).  The pipelined layouts also fail
  * when no pipeline's workgroups shared an XCD.  GP_ERR_INVALID_ARG if no such
