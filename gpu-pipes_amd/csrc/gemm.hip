@@ -119,8 +119,9 @@ __device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&&
 // per fragment.  No transposed copy of W is made.
 //
 // LNM (LayerNorm epilogue): 0 none; 1 the tile holds whole rows and each
-// wave all 128 features of its rows (N = 128), so the row statistics stay in
-// the wave; 2 a row spans N / 128 waves of N / BN workgroups, which publish
+// wave all 128 features of its rows (N = 128, Narrow), so the row statistics
+// stay in the wave; 2 (Wide, N = 256 .. 1024) a row spans N / 128 waves of
+// N / BN workgroups, which publish
 // per-wave partial statistics and combine them (one tile per workgroup,
 // every tile resident).  Launches of one epoch share the counters: launch
 // round r of the epoch waits for (r + 1) N / BN NW commits.
@@ -746,8 +747,8 @@ static hipError_t dispatch(const Args& g, int act, int ncu, hipStream_t s) {
 }
 
 // The LNM 2 exchange area: the status word's line, kLnMaxBlocks counter
-// lines (one per 256-row block of a launch), then 8 bytes per row and wave of
-// partial statistics.  The counters sit at the same place whatever the
+// lines (one per row block of a launch: a Wide tile row), then 8 bytes per
+// row and wave of partial statistics.  The counters sit at the same place whatever the
 // launch's shape: the statistics of one call must never land where a later
 // call with more row blocks keeps a counter (a payload word there would
 // defeat the epoch test and the wait would run out).
@@ -760,8 +761,8 @@ size_t ln_ws_bytes(int64_t M, int64_t N) {
 
 int64_t gemm_ln_max_rows(int64_t N, int num_cus) {
   if (N == 128) return int64_t(1) << 62;  // rows stay within a wave: any M
-  const int64_t tiles_n = N % gemm::Wide::BN == 0 ? N / gemm::Wide::BN : N / gemm::Narrow::BN;
-  return (num_cus / tiles_n) * 256;  // both configurations have 256-row tiles
+  if (N % gemm::Wide::BN || N > 1024) return 0;
+  return (num_cus / (N / gemm::Wide::BN)) * gemm::Wide::BM;
 }
 
 size_t gemm_ln_ws_bytes(int64_t M, int64_t N) { return N == 128 ? 0 : gemm::ln_ws_bytes(M, N); }
@@ -785,22 +786,21 @@ hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t s) {
          (const half_t*)a.r, (half_t*)a.out, a.M, (int)a.N, (int)a.K, ka, lda, ldc, ldr,
          (const half_t*)a.gamma, (const half_t*)a.beta, a.eps, nullptr, nullptr, QueueCtx{}, 0};
   if (a.ln) {
-    static_assert(Wide::BM == 256 && Narrow::BM == 256, "gemm_ln_max_rows assumes 256-row tiles");
-    if (a.act != ACT_NONE || a.N > 1024 || ((uintptr_t)a.gamma | (uintptr_t)a.beta) % 8) return hipErrorInvalidValue;
+    // N = 128 (rows within a wave) or 256 .. 1024 in whole 256-feature tiles.
+    if (a.act != ACT_NONE || a.N > 1024 || (a.N != 128 && a.N % Wide::BN) || ((uintptr_t)a.gamma | (uintptr_t)a.beta) % 8)
+      return hipErrorInvalidValue;
     if (a.N == 128) return brow ? launch<Narrow, ACT_NONE, true, true, 1>(g, num_cus, s)
                                 : launch<Narrow, ACT_NONE, true, false, 1>(g, num_cus, s);
     if (!a.ln_ws || !a.status || a.epoch == 0 || a.M > gemm_ln_max_rows(a.N, num_cus)) return hipErrorInvalidValue;
-    if ((a.M + 255) / 256 > kLnMaxBlocks) return hipErrorInvalidValue;
+    if ((a.M + Wide::BM - 1) / Wide::BM > kLnMaxBlocks) return hipErrorInvalidValue;
     QCounter* const q = (QCounter*)a.ln_ws;
     g.cnt = q + 1;
     g.stats = (unsigned long long*)(q + 1 + kLnMaxBlocks);
     g.ctx = QueueCtx{a.epoch, a.status, a.spin_limit > 0 ? a.spin_limit : kQueueSpinLimit};
-    const int64_t tiles_n = a.N % Wide::BN == 0 ? a.N / Wide::BN : a.N / Narrow::BN;
+    const int64_t tiles_n = a.N / Wide::BN;
     if (a.ln_round < 0 || (a.ln_round + 1) * tiles_n * NW > 0x7fffffff) return hipErrorInvalidValue;
     g.ln_target = (uint32_t)((a.ln_round + 1) * tiles_n * NW);
-    if (a.N % Wide::BN == 0)
-      return brow ? launch<Wide, ACT_NONE, true, true, 2>(g, num_cus, s) : launch<Wide, ACT_NONE, true, false, 2>(g, num_cus, s);
-    return brow ? launch<Narrow, ACT_NONE, true, true, 2>(g, num_cus, s) : launch<Narrow, ACT_NONE, true, false, 2>(g, num_cus, s);
+    return brow ? launch<Wide, ACT_NONE, true, true, 2>(g, num_cus, s) : launch<Wide, ACT_NONE, true, false, 2>(g, num_cus, s);
   }
   if (a.N % Wide::BN == 0) return brow ? dispatch<Wide, true>(g, a.act, num_cus, s) : dispatch<Wide, false>(g, a.act, num_cus, s);
   return brow ? dispatch<Narrow, true>(g, a.act, num_cus, s) : dispatch<Narrow, false>(g, a.act, num_cus, s);
