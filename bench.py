@@ -248,8 +248,9 @@ def bench_bert(args):
 
     dev = torch.device("cuda:0")
     M, H, FF, eps = BERT["M"], BERT["H"], BERT["FF"], BERT["eps"]
-    p = {k: v.to(dev) for k, v in bert_params(H, FF, seed=0, init="bert").items()}
-    x = normal_fp16(M, H, seed=0, device=dev)
+    et = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    p = {k: v.to(et).to(dev) for k, v in bert_params(H, FF, seed=0, init="bert").items()}
+    x = normal_fp16(M, H, seed=0, device=dev, dtype=et)
     out = torch.empty_like(x)
 
     def step(i):
@@ -272,7 +273,7 @@ def bench_bert(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": args.dtype,
         "data": "synthetic (X~N(0,1), W~N(0,0.02), b=0, seed 0)",
         "config": {"workload": "bert_large_ffn", "M": M, "H": H, "FF": FF, "act": "gelu_tanh", "eps": eps,
                    "layers": f"{H}-{FF}-{H}+residual+LN", "accumulate": "f32", "row_chunk": 16384},
@@ -282,11 +283,11 @@ def bench_bert(args):
             "kernel_ms_avg": avg_ms, "kernel_ms_median": spread(call_ms)["median"],
             "flops_per_launch": flops, "algorithmic_bytes_per_launch": bytes_,
             "launch": "one gp_bert_ffn_out call (one weight-transpose launch, then per 16384-row chunk: "
-                      "GEMM1+bias+GELU, GEMM2+bias+residual, LayerNorm)",
+                      "GEMM1+bias+GELU, GEMM2+bias+residual+LayerNorm)",
         },
         "spread": spread(call_ms),
         "settle": settle,
-        "cpu_baseline": None if args.no_cpu else cpu_baseline_bert(),
+        "cpu_baseline": None if args.no_cpu or args.dtype != "f16" else cpu_baseline_bert(),
     }
     print(json.dumps(rec), flush=True)
 
@@ -506,7 +507,7 @@ def main():
                          "engine clock swings for tens of ms after a burst starts (launches run fast, then "
                          "up to 1.5x slower, then settle), so the timed region starts in the steady state")
     ap.add_argument("--dtype", choices=["f16", "bf16"], default="f16",
-                    help="element type of the MGN workloads (bf16: fused kernel, not the headline line)")
+                    help="element type of the MGN and BERT workloads (bf16: the fused kernels, not the headline line)")
     ap.add_argument("--eager", action="store_true",
                     help="MGN fused workloads: time the steps as eager calls only (by default `value` comes "
                          "from the same steps submitted as one HIP graph; the per-launch roofline times "

@@ -36,6 +36,11 @@ int check_act(int act) {
   return GP_OK;
 }
 
+int check_dtype(int dtype) {
+  if (dtype != GP_DTYPE_F16 && dtype != GP_DTYPE_BF16) return fail(GP_ERR_INVALID_ARG, "unknown dtype %d", dtype);
+  return GP_OK;
+}
+
 int need16(const void* p, const char* name) {
   if (!p) return fail(GP_ERR_INVALID_ARG, "%s is NULL", name);
   if (!aligned16(p)) return fail(GP_ERR_ALIGN, "%s must be 16-byte aligned", name);
@@ -97,10 +102,11 @@ using namespace gp;
 
 extern "C" {
 
-int gp_gemm_out(int64_t M, int64_t N, int64_t K, const void* x, const void* w, const void* b, const void* r,
-                int act, void* out, void* stream) {
+int gp_gemm_dtype_out(int64_t M, int64_t N, int64_t K, const void* x, const void* w, const void* b, const void* r,
+                      int act, void* out, int dtype, void* stream) {
   clear_error();
   int rc;
+  if ((rc = check_dtype(dtype))) return rc;
   if (M < 0) return fail(GP_ERR_INVALID_ARG, "M must be >= 0 (got %lld)", (long long)M);
   if (N < 128 || N > kMaxDim || N % 128)
     return fail(GP_ERR_SHAPE, "N must be a multiple of 128 in [128, %lld] (got %lld)", (long long)kMaxDim,
@@ -118,22 +124,32 @@ int gp_gemm_out(int64_t M, int64_t N, int64_t K, const void* x, const void* w, c
   if ((rc = current_device_info(&dev, &ncu))) return rc;
   hipStream_t s = (hipStream_t)stream;
   if (weights_in_place(2.0 * M * N * K)) {
-    const hipError_t e = gemm_launch(gemm_w(M, N, K, x, w, b, r, act, out), ncu, s);
+    GemmArgs g = gemm_w(M, N, K, x, w, b, r, act, out);
+    g.dtype = dtype;
+    const hipError_t e = gemm_launch(g, ncu, s);
     return e == hipSuccess ? GP_OK : fail_hip(e, "gemm launch");
   }
   void* ws = nullptr;
   if ((rc = workspace_acquire(dev, s, (size_t)N * K * 2, &ws))) return rc;
   hipError_t e = transpose_launch(w, ws, K, N, s);
   if (e != hipSuccess) return fail_hip(e, "transpose launch");
-  e = gemm_launch({M, N, K, x, ws, b, r, act, out}, ncu, s);
+  GemmArgs g{M, N, K, x, ws, b, r, act, out};
+  g.dtype = dtype;
+  e = gemm_launch(g, ncu, s);
   return e == hipSuccess ? GP_OK : fail_hip(e, "gemm launch");
 }
 
-int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void* w1, const void* b1,
-                    const void* w2, const void* b2, const void* gamma, const void* beta, float eps, int act,
-                    void* out, void* stream) {
+int gp_gemm_out(int64_t M, int64_t N, int64_t K, const void* x, const void* w, const void* b, const void* r,
+                int act, void* out, void* stream) {
+  return gp_gemm_dtype_out(M, N, K, x, w, b, r, act, out, GP_DTYPE_F16, stream);
+}
+
+int gp_bert_ffn_dtype_out(int64_t M, int64_t H, int64_t FF, const void* x, const void* w1, const void* b1,
+                          const void* w2, const void* b2, const void* gamma, const void* beta, float eps, int act,
+                          void* out, int dtype, void* stream) {
   clear_error();
   int rc;
+  if ((rc = check_dtype(dtype))) return rc;
   if (M < 0) return fail(GP_ERR_INVALID_ARG, "M must be >= 0 (got %lld)", (long long)M);
   if (H != 128 && H != 256 && H != 512 && H != 1024)
     return fail(GP_ERR_SHAPE, "H must be 128, 256, 512 or 1024 (got %lld)", (long long)H);
@@ -158,6 +174,8 @@ int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void*
   const bool inplace = weights_in_place(4.0 * M * H * FF);
   const int64_t lnch = ln_chunk_rows(H, ncu);
   const bool fuse_ln = lnch > 0;
+  if (!fuse_ln && dtype != GP_DTYPE_F16)
+    return fail(GP_ERR_SHAPE, "bf16 needs the LayerNorm in the GEMM epilogue, which this device's %d CUs cannot hold", ncu);
   const int64_t chmax = fuse_ln ? lnch : kFfnChunkRows;
   const int64_t CH = M < chmax ? M : chmax;
   const size_t o_w2t = inplace ? 0 : round_up((size_t)FF * H * 2);
@@ -177,7 +195,9 @@ int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void*
   // layer GEMM arguments: the weights in place or their transposed copies
   auto g = [&](int64_t rows, int64_t N, int64_t K, const void* a, const void* w, const void* wt, const void* b,
                const void* r, int ac, void* c) {
-    return inplace ? gemm_w(rows, N, K, a, w, b, r, ac, c) : GemmArgs{rows, N, K, a, wt, b, r, ac, c};
+    GemmArgs ga = inplace ? gemm_w(rows, N, K, a, w, b, r, ac, c) : GemmArgs{rows, N, K, a, wt, b, r, ac, c};
+    ga.dtype = dtype;
+    return ga;
   };
   LnEpilogue lne;
   if (fuse_ln && (rc = lne.init(dev, s, CH, H))) return rc;
@@ -201,12 +221,21 @@ int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void*
   return GP_OK;
 }
 
-int gp_bert_addln_ffn_out(int64_t M, int64_t H, int64_t FF, const void* attn, const void* x, const void* w0,
-                          const void* b0, const void* w1, const void* b1, const void* w2, const void* b2,
-                          const void* ga0, const void* be0, const void* ga2, const void* be2, float eps, int act,
-                          void* out, int impl, void* stream) {
+int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void* w1, const void* b1,
+                    const void* w2, const void* b2, const void* gamma, const void* beta, float eps, int act,
+                    void* out, void* stream) {
+  return gp_bert_ffn_dtype_out(M, H, FF, x, w1, b1, w2, b2, gamma, beta, eps, act, out, GP_DTYPE_F16, stream);
+}
+
+int gp_bert_addln_ffn_dtype_out(int64_t M, int64_t H, int64_t FF, const void* attn, const void* x,
+                                const void* w0, const void* b0, const void* w1, const void* b1, const void* w2,
+                                const void* b2, const void* ga0, const void* be0, const void* ga2, const void* be2,
+                                float eps, int act, void* out, int impl, int dtype, void* stream) {
   clear_error();
   int rc;
+  if ((rc = check_dtype(dtype))) return rc;
+  if (dtype != GP_DTYPE_F16 && impl != GP_IMPL_FUSED)
+    return fail(GP_ERR_INVALID_ARG, "bf16 runs the fused implementation only (the queue-chained layout is fp16)");
   if (M < 0) return fail(GP_ERR_INVALID_ARG, "M must be >= 0 (got %lld)", (long long)M);
   if (H != 128 && H != 256 && H != 512 && H != 1024)
     return fail(GP_ERR_SHAPE, "H must be 128, 256, 512 or 1024 (got %lld)", (long long)H);
@@ -238,6 +267,8 @@ int gp_bert_addln_ffn_out(int64_t M, int64_t H, int64_t FF, const void* attn, co
   const bool inplace = weights_in_place(2.0 * M * H * (H + 2.0 * FF));
   const int64_t lnch = ln_chunk_rows(H, ncu);
   const bool fuse_ln = lnch > 0;
+  if (!fuse_ln && dtype != GP_DTYPE_F16)
+    return fail(GP_ERR_SHAPE, "bf16 needs the LayerNorm in the GEMM epilogue, which this device's %d CUs cannot hold", ncu);
   const int64_t chmax = fuse_ln ? lnch : kFfnChunkRows;
   const int64_t CH = M < chmax ? M : chmax;
   const size_t o_w1t = inplace ? 0 : round_up((size_t)H * H * 2);
@@ -259,7 +290,9 @@ int gp_bert_addln_ffn_out(int64_t M, int64_t H, int64_t FF, const void* attn, co
   }
   auto g = [&](int64_t rows, int64_t N, int64_t K, const void* a, const void* w, const void* wt, const void* b,
                const void* r, int ac, void* c) {
-    return inplace ? gemm_w(rows, N, K, a, w, b, r, ac, c) : GemmArgs{rows, N, K, a, wt, b, r, ac, c};
+    GemmArgs ga = inplace ? gemm_w(rows, N, K, a, w, b, r, ac, c) : GemmArgs{rows, N, K, a, wt, b, r, ac, c};
+    ga.dtype = dtype;
+    return ga;
   };
   LnEpilogue lne;
   if (fuse_ln && (rc = lne.init(dev, s, CH, H))) return rc;
@@ -284,6 +317,14 @@ int gp_bert_addln_ffn_out(int64_t M, int64_t H, int64_t FF, const void* attn, co
     if (e != hipSuccess) return fail_hip(e, "bert_addln_ffn launch");
   }
   return GP_OK;
+}
+
+int gp_bert_addln_ffn_out(int64_t M, int64_t H, int64_t FF, const void* attn, const void* x, const void* w0,
+                          const void* b0, const void* w1, const void* b1, const void* w2, const void* b2,
+                          const void* ga0, const void* be0, const void* ga2, const void* be2, float eps, int act,
+                          void* out, int impl, void* stream) {
+  return gp_bert_addln_ffn_dtype_out(M, H, FF, attn, x, w0, b0, w1, b1, w2, b2, ga0, be0, ga2, be2, eps, act, out,
+                                     impl, GP_DTYPE_F16, stream);
 }
 
 }  // extern "C"

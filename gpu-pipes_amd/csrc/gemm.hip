@@ -75,6 +75,32 @@ struct Cfg {
 using Wide = Cfg<4, 4, 2>;    // 256 features x 256 rows
 using Narrow = Cfg<4, 2, 1>;  // 128 features x 256 rows
 
+// Element types.  Operands, bias, residual, affine and output are 16-bit
+// values held as raw bits in half_t containers; only the MFMA form, the
+// conversions to / from fp32 and the value 1.0 differ.  Arithmetic is fp32.
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+struct F16 {
+  static constexpr unsigned short kOne = 0x3C00;
+  __device__ static f16x mma(h8 a, h8 b, f16x c) { return mfma32(a, b, c); }
+  __device__ static float val(half_t h) { return (float)h; }
+  __device__ static h4 cvt4(f4 v) { return __builtin_convertvector(v, h4); }
+  __device__ static h2 cvt2(f2 v) { return __builtin_convertvector(v, h2); }
+};
+struct BF16 {
+  static constexpr unsigned short kOne = 0x3F80;
+  __device__ static f16x mma(h8 a, h8 b, f16x c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf8, a), __builtin_bit_cast(bf8, b), c, 0, 0, 0);
+  }
+  __device__ static float val(half_t h) {
+    return __builtin_bit_cast(float, (unsigned)__builtin_bit_cast(unsigned short, h) << 16);
+  }
+  // v_cvt_pk_bf16_f32: round to nearest even
+  __device__ static h4 cvt4(f4 v) { return __builtin_bit_cast(h4, __builtin_convertvector(v, bf4)); }
+  __device__ static h2 cvt2(f2 v) { return __builtin_bit_cast(h2, __builtin_convertvector(v, bf2)); }
+};
+
 struct Args {
   const half_t* a;     // [M][lda], the first K columns used
   const half_t* bt;    // [N][K] (transposed weights), or
@@ -125,7 +151,9 @@ __device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&&
 // per-wave partial statistics and combine them (one tile per workgroup,
 // every tile resident).  Launches of one epoch share the counters: launch
 // round r of the epoch waits for (r + 1) N / BN NW commits.
-template <class C, int ACT, bool RESID, bool BROW = false, int LNM = 0>
+//
+// E: the element type (F16 or BF16).
+template <class C, int ACT, bool RESID, bool BROW = false, int LNM = 0, typename E = F16>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_kernel(Args p) {
   __shared__ __attribute__((aligned(1024))) char ring[NU * C::UNIT];
 
@@ -276,7 +304,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 #pragma unroll
     for (int nb = 0; nb < C::NBW; ++nb)
 #pragma unroll
-      for (int mb = 0; mb < C::MBW; ++mb) acc[nb][mb] = mfma32(f.a[nb], f.b[mb], acc[nb][mb]);
+      for (int mb = 0; mb < C::MBW; ++mb) acc[nb][mb] = E::mma(f.a[nb], f.b[mb], acc[nb][mb]);
     constexpr int nm = C::NBW * C::MBW;
 #pragma unroll
     for (int i = 0; i < nm; ++i) {
@@ -387,7 +415,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int f = T.n0 + 32 * C::NBW * wn + 32 * nb + 8 * g + 4 * lh;
-          gam[nb][g] = p.gamma ? *(const h4*)(p.gamma + f) : h4{1, 1, 1, 1};
+          const half_t one_h = __builtin_bit_cast(half_t, E::kOne);
+          gam[nb][g] = p.gamma ? *(const h4*)(p.gamma + f) : h4{one_h, one_h, one_h, one_h};
           bet[nb][g] = p.beta ? *(const h4*)(p.beta + f) : h4{};
         }
     }
@@ -477,15 +506,15 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
             for (int e = 0; e < 2; ++e) {
               // fma(x, 1, y) rounds x + y once: the sums of the plain epilogue
               const int i = 2 * j + e;
-              t[e] = __builtin_fmaf((float)bias[nb][i / 4][i % 4], one, acc[nb][mb][i]);
-              t[e] = __builtin_fmaf((float)res[i / 4][mb][i % 4], one, t[e]);
+              t[e] = __builtin_fmaf(E::val(bias[nb][i / 4][i % 4]), one, acc[nb][mb][i]);
+              t[e] = __builtin_fmaf(E::val(res[i / 4][mb][i % 4]), one, t[e]);
             }
             // Rounded to fp16 from the fp32 sum, as the plain epilogue does (the
             // barrier keeps the rounding out of the fma: one v_cvt_pk_f16_f32).
             asm volatile("" : "+v"(t));
-            pk[j] = __builtin_convertvector(t, h2);
+            pk[j] = E::cvt2(t);
 #pragma unroll
-            for (int e = 0; e < 2; ++e) s[mb] = __builtin_fmaf((float)pk[j][e], one, s[mb]);
+            for (int e = 0; e < 2; ++e) s[mb] = __builtin_fmaf(E::val(pk[j][e]), one, s[mb]);
           }
 #pragma unroll
           for (int j = 0; j < 8; ++j) acc[nb][mb][j] = __builtin_bit_cast(float, pk[j]);
@@ -497,7 +526,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
       // element lvalue reads element 0 of the vector in this compiler.)
       auto vh = [&](int nb, int mb, int i) {
         const float w = acc[nb][mb][i / 2];
-        return (float)__builtin_bit_cast(h2, w)[i % 2];
+        return E::val(__builtin_bit_cast(h2, w)[i % 2]);
       };
       // Pass 2: the wave's mean and sum of squared deviations per row.
       float q[C::MBW];
@@ -592,8 +621,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 #pragma unroll
               for (int e = 0; e < 4; ++e)
                 v[e] = __builtin_fmaf(__builtin_fmaf(vh(nb, mb, 4 * g + e), one, -mean[mb]) * rstd[mb],
-                                      (float)gam[nb][g][e], (float)bet[nb][g][e]);
-              o[g] = __builtin_bit_cast(u32x2, __builtin_convertvector(v, h4));
+                                      E::val(gam[nb][g][e]), E::val(bet[nb][g][e]));
+              o[g] = __builtin_bit_cast(u32x2, E::cvt4(v));
             }
             store_frag(o, nb, mb);
           }
@@ -625,10 +654,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
             f4 v;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              v[e] = apply_act(acc[nb][mb][4 * g + e] + (float)bias[nb][g][e], ACT);
-              if constexpr (RESID) v[e] += (float)res[g][mb][e];
+              v[e] = apply_act(acc[nb][mb][4 * g + e] + E::val(bias[nb][g][e]), ACT);
+              if constexpr (RESID) v[e] += E::val(res[g][mb][e]);
             }
-            o[g] = __builtin_bit_cast(u32x2, __builtin_convertvector(v, h4));
+            o[g] = __builtin_bit_cast(u32x2, E::cvt4(v));
           }
           store_frag(o, nb, mb);
         }
@@ -723,27 +752,40 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const half_t* a, int lda, in
   }
 }
 
-template <class C, int ACT, bool RESID, bool BROW, int LNM = 0>
+template <class C, int ACT, bool RESID, bool BROW, int LNM = 0, typename E = F16>
 static hipError_t launch(const Args& a, int num_cus, hipStream_t s) {
   const int64_t tiles = ((a.M + C::BM - 1) / C::BM) * (a.N / C::BN);
   // One persistent workgroup per CU; the LNM 2 kernels take one tile each,
   // all resident at once (the host keeps tiles <= num_cus).
   if (LNM == 2 && tiles > num_cus) return hipErrorInvalidValue;
   const int64_t grid = tiles < num_cus ? tiles : num_cus;
-  hipLaunchKernelGGL((gemm_kernel<C, ACT, RESID, BROW, LNM>), dim3((unsigned)grid), dim3(NT), 0, s, a);
+  hipLaunchKernelGGL((gemm_kernel<C, ACT, RESID, BROW, LNM, E>), dim3((unsigned)grid), dim3(NT), 0, s, a);
   return hipGetLastError();
 }
 
-template <class C, bool BROW>
+template <class C, bool BROW, typename E>
 static hipError_t dispatch(const Args& g, int act, int ncu, hipStream_t s) {
-  if (g.r) return act == ACT_NONE ? launch<C, ACT_NONE, true, BROW>(g, ncu, s) : hipErrorInvalidValue;
+  if (g.r) return act == ACT_NONE ? launch<C, ACT_NONE, true, BROW, 0, E>(g, ncu, s) : hipErrorInvalidValue;
   switch (act) {
-    case ACT_NONE: return launch<C, ACT_NONE, false, BROW>(g, ncu, s);
-    case ACT_RELU: return launch<C, ACT_RELU, false, BROW>(g, ncu, s);
-    case ACT_GELU_TANH: return launch<C, ACT_GELU_TANH, false, BROW>(g, ncu, s);
-    case ACT_SIGMOID: return launch<C, ACT_SIGMOID, false, BROW>(g, ncu, s);
+    case ACT_NONE: return launch<C, ACT_NONE, false, BROW, 0, E>(g, ncu, s);
+    case ACT_RELU: return launch<C, ACT_RELU, false, BROW, 0, E>(g, ncu, s);
+    case ACT_GELU_TANH: return launch<C, ACT_GELU_TANH, false, BROW, 0, E>(g, ncu, s);
+    case ACT_SIGMOID: return launch<C, ACT_SIGMOID, false, BROW, 0, E>(g, ncu, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+// Every kernel of one element type.
+template <typename E>
+static hipError_t launch_typed(const GemmArgs& a, Args& g, bool brow, int num_cus, hipStream_t s) {
+  if (a.ln) {
+    if (a.N == 128) return brow ? launch<Narrow, ACT_NONE, true, true, 1, E>(g, num_cus, s)
+                                : launch<Narrow, ACT_NONE, true, false, 1, E>(g, num_cus, s);
+    return brow ? launch<Wide, ACT_NONE, true, true, 2, E>(g, num_cus, s)
+                : launch<Wide, ACT_NONE, true, false, 2, E>(g, num_cus, s);
+  }
+  if (a.N % Wide::BN == 0) return brow ? dispatch<Wide, true, E>(g, a.act, num_cus, s) : dispatch<Wide, false, E>(g, a.act, num_cus, s);
+  return brow ? dispatch<Narrow, true, E>(g, a.act, num_cus, s) : dispatch<Narrow, false, E>(g, a.act, num_cus, s);
 }
 
 // The LNM 2 exchange area: the status word's line, kLnMaxBlocks counter
@@ -785,25 +827,24 @@ hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t s) {
   Args g{(const half_t*)a.x, (const half_t*)a.wt, (const half_t*)a.w, ldw, kw, (const half_t*)a.b,
          (const half_t*)a.r, (half_t*)a.out, a.M, (int)a.N, (int)a.K, ka, lda, ldc, ldr,
          (const half_t*)a.gamma, (const half_t*)a.beta, a.eps, nullptr, nullptr, QueueCtx{}, 0};
+  if (a.dtype != GP_DTYPE_F16 && a.dtype != GP_DTYPE_BF16) return hipErrorInvalidValue;
   if (a.ln) {
     // N = 128 (rows within a wave) or 256 .. 1024 in whole 256-feature tiles.
     if (a.act != ACT_NONE || a.N > 1024 || (a.N != 128 && a.N % Wide::BN) || ((uintptr_t)a.gamma | (uintptr_t)a.beta) % 8)
       return hipErrorInvalidValue;
-    if (a.N == 128) return brow ? launch<Narrow, ACT_NONE, true, true, 1>(g, num_cus, s)
-                                : launch<Narrow, ACT_NONE, true, false, 1>(g, num_cus, s);
-    if (!a.ln_ws || !a.status || a.epoch == 0 || a.M > gemm_ln_max_rows(a.N, num_cus)) return hipErrorInvalidValue;
-    if ((a.M + Wide::BM - 1) / Wide::BM > kLnMaxBlocks) return hipErrorInvalidValue;
-    QCounter* const q = (QCounter*)a.ln_ws;
-    g.cnt = q + 1;
-    g.stats = (unsigned long long*)(q + 1 + kLnMaxBlocks);
-    g.ctx = QueueCtx{a.epoch, a.status, a.spin_limit > 0 ? a.spin_limit : kQueueSpinLimit};
-    const int64_t tiles_n = a.N / Wide::BN;
-    if (a.ln_round < 0 || (a.ln_round + 1) * tiles_n * NW > 0x7fffffff) return hipErrorInvalidValue;
-    g.ln_target = (uint32_t)((a.ln_round + 1) * tiles_n * NW);
-    return brow ? launch<Wide, ACT_NONE, true, true, 2>(g, num_cus, s) : launch<Wide, ACT_NONE, true, false, 2>(g, num_cus, s);
+    if (a.N != 128) {
+      if (!a.ln_ws || !a.status || a.epoch == 0 || a.M > gemm_ln_max_rows(a.N, num_cus)) return hipErrorInvalidValue;
+      if ((a.M + Wide::BM - 1) / Wide::BM > kLnMaxBlocks) return hipErrorInvalidValue;
+      QCounter* const q = (QCounter*)a.ln_ws;
+      g.cnt = q + 1;
+      g.stats = (unsigned long long*)(q + 1 + kLnMaxBlocks);
+      g.ctx = QueueCtx{a.epoch, a.status, a.spin_limit > 0 ? a.spin_limit : kQueueSpinLimit};
+      const int64_t tiles_n = a.N / Wide::BN;
+      if (a.ln_round < 0 || (a.ln_round + 1) * tiles_n * NW > 0x7fffffff) return hipErrorInvalidValue;
+      g.ln_target = (uint32_t)((a.ln_round + 1) * tiles_n * NW);
+    }
   }
-  if (a.N % Wide::BN == 0) return brow ? dispatch<Wide, true>(g, a.act, num_cus, s) : dispatch<Wide, false>(g, a.act, num_cus, s);
-  return brow ? dispatch<Narrow, true>(g, a.act, num_cus, s) : dispatch<Narrow, false>(g, a.act, num_cus, s);
+  return a.dtype == GP_DTYPE_BF16 ? launch_typed<BF16>(a, g, brow, num_cus, s) : launch_typed<F16>(a, g, brow, num_cus, s);
 }
 
 hipError_t prep_launch(const PrepSpec* L, int n, hipStream_t s) {

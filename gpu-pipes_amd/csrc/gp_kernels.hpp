@@ -119,6 +119,7 @@ struct GemmArgs {
   // the same row blocks in every earlier round.
   int ln = 0;
   int64_t ln_round = 0;
+  int dtype = GP_DTYPE_F16;  // element type of x, the weights, b, r, gamma, beta and out
   const void* gamma = nullptr;
   const void* beta = nullptr;
   float eps = 0.f;

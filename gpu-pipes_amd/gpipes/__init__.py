@@ -81,7 +81,9 @@ def _load():
     L.gp_mgn_edge_gather_out.argtypes = [i64, i64, vp, vp, vp, vp, i32] + [vp] * 8 + [f32, vp, vp]
     L.gp_mgn_edge_gather_out.restype = i32
     L.gp_gemm_out.argtypes = [i64, i64, i64, vp, vp, vp, vp, i32, vp, vp]
+    L.gp_gemm_dtype_out.argtypes = [i64, i64, i64, vp, vp, vp, vp, i32, vp, i32, vp]
     L.gp_bert_ffn_out.argtypes = [i64, i64, i64] + [vp] * 7 + [f32, i32, vp, vp]
+    L.gp_bert_ffn_dtype_out.argtypes = [i64, i64, i64] + [vp] * 7 + [f32, i32, vp, i32, vp]
     L.gp_mlp_out.argtypes = [i64, i32, vp, vp, vp, vp, vp, vp, vp]
     L.gp_dlrm_botmlp_out.argtypes = [i64, i64] + [vp] * 9
     L.gp_dlrm_topmlp_out.argtypes = [i64, i64, i64] + [vp] * 11 + [i32, vp, vp]
@@ -89,11 +91,13 @@ def _load():
     L.gp_nerf_full_out_noalloc.argtypes = [i64] * 5 + [vp] * 4 + [i32, vp, vp, vp]
     L.gp_bert_addln_ffn_out.argtypes = [i64, i64, i64] + [vp] * 12 + [f32, i32, vp, i32, vp]
     L.gp_bert_addln_ffn_out.restype = i32
+    L.gp_bert_addln_ffn_dtype_out.argtypes = [i64, i64, i64] + [vp] * 12 + [f32, i32, vp, i32, i32, vp]
+    L.gp_bert_addln_ffn_dtype_out.restype = i32
     L.gp_nerf_a_out.argtypes = [i64, i64, vp, vp, vp, vp, i32, vp]
     L.gp_nerf_a_out.restype = i32
     L.gp_nerf_full_out_noalloc.restype = i32
     for name in ("gp_mlp_out", "gp_dlrm_botmlp_out", "gp_dlrm_topmlp_out", "gp_nerf_full_out", "gp_gemm_out",
-                 "gp_bert_ffn_out", "gp_linear_out", "gp_linear_layer_norm_out", "gp_layer_norm_out", "gp_add_out",
+                 "gp_gemm_dtype_out", "gp_bert_ffn_out", "gp_bert_ffn_dtype_out", "gp_linear_out", "gp_linear_layer_norm_out", "gp_layer_norm_out", "gp_add_out",
                  "gp_concat_out", "gp_pipe_ident", "gp_pipeline_check"):
         getattr(L, name).restype = i32
     return L
@@ -208,11 +212,16 @@ def mgn_linears(x, w1, b1, w2, b2, w3, b3):
 # Stage-level operations (one library stage over a whole matrix)
 # ---------------------------------------------------------------------------
 
-def _opt(name, t, shape):
+def _opt(name, t, shape, dtype=torch.float16):
     if t is None:
         return None
-    _check_input(name, t, shape)
+    _check_input(name, t, shape, dtype)
     return t
+
+
+def _dtype_of(x):
+    """The element type a call runs in: x's, when it is float16 or bfloat16."""
+    return x.dtype if isinstance(x, torch.Tensor) and x.dtype in _DTYPES else torch.float16
 
 
 def _stream(t):
@@ -378,21 +387,23 @@ def mgn_edge_gather(nf, ef, src, dst, w1, b1, w2, b2, w3, b3, gamma=None, beta=N
 def gemm_out(x, w, b=None, r=None, act="none", out=None):
     """out[M,N] = act(x @ w + b), or x @ w + b + r -- the wide GEMM stage (any N multiple of
     128, K multiple of 64): the N-split PipeGemmBiasRelu / PipeGemmBias blocks of
-    apps/bert_ffn/pipelined/bert_ffn_pl.cuh:79-99 and bulksync_gemm."""
-    _check_input("x", x)
+    apps/bert_ffn/pipelined/bert_ffn_pl.cuh:79-99 and bulksync_gemm.  Every tensor float16,
+    or every tensor bfloat16 (gp_gemm_dtype_out)."""
+    dt = _dtype_of(x)
+    _check_input("x", x, dtype=dt)
     M, K = x.shape
-    _check_input("w", w)
+    _check_input("w", w, dtype=dt)
     if w.dim() != 2 or w.shape[0] != K:
         raise RuntimeError(f"w must be [{K}, N]")
     N = w.shape[1]
-    _opt("b", b, (N,))
-    _opt("r", r, (M, N))
+    _opt("b", b, (N,), dt)
+    _opt("r", r, (M, N), dt)
     if out is None:
-        out = torch.empty((M, N), dtype=torch.float16, device=x.device)
-    _check_input("out", out, (M, N))
+        out = torch.empty((M, N), dtype=dt, device=x.device)
+    _check_input("out", out, (M, N), dt)
     with torch.cuda.device(x.device):
-        _check(lib.gp_gemm_out(M, N, K, _ptr(x), _ptr(w), _ptr(b), _ptr(r), ACTS.get(act, act), _ptr(out),
-                               _stream(x)))
+        _check(lib.gp_gemm_dtype_out(M, N, K, _ptr(x), _ptr(w), _ptr(b), _ptr(r), ACTS.get(act, act), _ptr(out),
+                                     _DTYPES[dt], _stream(x)))
     return out
 
 
@@ -400,27 +411,30 @@ def bert_ffn_out(x, w1, b1, w2, b2, ga, be, out, eps=1e-5, act="relu"):
     """LayerNorm(Linear2(act(Linear1(x))) + x) into ``out`` -- bert_ffn_out of
     apps/bert_ffn/pipelined/bert_ffn_pl_ext.cu:24-56 (there H = 128, FF = 512, ReLU,
     eps 1e-5), for H in {128, 256, 512, 1024} and FF a multiple of 128.  Weights
-    [in, out] = ``nn.Linear.weight.t().contiguous()``; ga / be may be None (1 / 0)."""
-    _check_input("x", x)
+    [in, out] = ``nn.Linear.weight.t().contiguous()``; ga / be may be None (1 / 0).  Every
+    tensor float16, or every tensor bfloat16 (gp_bert_ffn_dtype_out)."""
+    dt = _dtype_of(x)
+    _check_input("x", x, dtype=dt)
     if x.dim() != 2:
         raise RuntimeError("x must be 2-D [M, H]")
     M, H = x.shape
-    _check_input("w1", w1)
+    _check_input("w1", w1, dtype=dt)
     if w1.dim() != 2 or w1.shape[0] != H:
         raise RuntimeError(f"w1 must be [{H}, FF]")
     FF = w1.shape[1]
-    _opt("b1", b1, (FF,))
-    _check_input("w2", w2, (FF, H))
-    _opt("b2", b2, (H,))
-    _opt("ga", ga, (H,))
-    _opt("be", be, (H,))
-    _check_input("out", out, (M, H))
+    _opt("b1", b1, (FF,), dt)
+    _check_input("w2", w2, (FF, H), dt)
+    _opt("b2", b2, (H,), dt)
+    _opt("ga", ga, (H,), dt)
+    _opt("be", be, (H,), dt)
+    _check_input("out", out, (M, H), dt)
     devs = {t.device for t in (x, w1, b1, w2, b2, ga, be, out) if t is not None}
     if len(devs) != 1:
         raise RuntimeError("all tensors must be on the same device")
     with torch.cuda.device(x.device):
-        _check(lib.gp_bert_ffn_out(M, H, FF, _ptr(x), _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2), _ptr(ga), _ptr(be),
-                                   float(eps), ACTS.get(act, act), _ptr(out), _stream(x)))
+        _check(lib.gp_bert_ffn_dtype_out(M, H, FF, _ptr(x), _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2), _ptr(ga),
+                                         _ptr(be), float(eps), ACTS.get(act, act), _ptr(out), _DTYPES[dt],
+                                         _stream(x)))
     return out
 
 
@@ -530,28 +544,31 @@ def bert_addln_ffn_out(attn_out, x, w0, b0, w1, b1, w2, b2, ga0, be0, ga2, be2, 
     there), for H in {128, 256, 512, 1024} and FF a multiple of 128.  Weights [in, out] =
     ``weight.t().contiguous()``; biases and LayerNorm affines may be None.  impl "fused" (one
     GEMM launch per layer with fused epilogues) or "pipelined" (the reference's queue-chained
-    layout, H 128 / FF 512 only)."""
-    _check_input("attn_out", attn_out)
+    layout, H 128 / FF 512 only).  Every tensor float16, or every tensor bfloat16 (fused impl
+    only: gp_bert_addln_ffn_dtype_out)."""
+    dt = _dtype_of(attn_out)
+    _check_input("attn_out", attn_out, dtype=dt)
     if attn_out.dim() != 2:
         raise RuntimeError("attn_out must be 2-D [M, H]")
     M, H = attn_out.shape
-    _check_input("x", x, (M, H))
-    _check_input("w0", w0, (H, H))
-    _check_input("w1", w1)
+    _check_input("x", x, (M, H), dt)
+    _check_input("w0", w0, (H, H), dt)
+    _check_input("w1", w1, dtype=dt)
     if w1.dim() != 2 or w1.shape[0] != H:
         raise RuntimeError(f"w1 must be [{H}, FF]")
     FF = w1.shape[1]
-    _check_input("w2", w2, (FF, H))
+    _check_input("w2", w2, (FF, H), dt)
     for name, t, n in (("b0", b0, H), ("b1", b1, FF), ("b2", b2, H), ("ga0", ga0, H), ("be0", be0, H),
                        ("ga2", ga2, H), ("be2", be2, H)):
-        _opt(name, t, (n,))
-    _check_input("out", out, (M, H))
+        _opt(name, t, (n,), dt)
+    _check_input("out", out, (M, H), dt)
     _same_device(attn_out, x, w0, b0, w1, b1, w2, b2, ga0, be0, ga2, be2, out)
     impl_id = _IMPLS.get(impl, impl)
     with torch.cuda.device(x.device):
-        _check(lib.gp_bert_addln_ffn_out(M, H, FF, _ptr(attn_out), _ptr(x), _ptr(w0), _ptr(b0), _ptr(w1), _ptr(b1),
-                                         _ptr(w2), _ptr(b2), _ptr(ga0), _ptr(be0), _ptr(ga2), _ptr(be2), float(eps),
-                                         ACTS.get(act, act), _ptr(out), int(impl_id), _stream(x)))
+        _check(lib.gp_bert_addln_ffn_dtype_out(M, H, FF, _ptr(attn_out), _ptr(x), _ptr(w0), _ptr(b0), _ptr(w1),
+                                               _ptr(b1), _ptr(w2), _ptr(b2), _ptr(ga0), _ptr(be0), _ptr(ga2),
+                                               _ptr(be2), float(eps), ACTS.get(act, act), _ptr(out), int(impl_id),
+                                               _DTYPES[dt], _stream(x)))
     return out
 
 

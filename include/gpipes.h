@@ -41,7 +41,7 @@ extern "C" {
 #define GP_IMPL_PIPELINED_SPLIT_LN 2 /* the reference's layout: layer 3 feeds five         */
                                      /* LayerNorm workers through a round-robin split queue */
 
-/* Element types of gp_mgn_mlp_dtype_out (16-bit storage, fp32 accumulation). */
+/* Element types of the *_dtype_out entry points (16-bit storage, fp32 accumulation). */
 #define GP_DTYPE_F16 0  /* IEEE binary16 */
 #define GP_DTYPE_BF16 1 /* bfloat16      */
 
@@ -145,6 +145,18 @@ int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void*
                     void* out, void* stream);
 
 /*
+ * gp_bert_ffn_out with the element type of x, the weights, biases, gamma,
+ * beta and out given by `dtype`: GP_DTYPE_F16 (the same call) or
+ * GP_DTYPE_BF16 (bf16 MFMAs, fp32 accumulation and epilogue arithmetic, the
+ * activations between the GEMMs and the output rounded to bf16).  No
+ * counterpart in the reference, whose extensions take fp16 tensors only; the
+ * bf16 form of the same block for callers that keep their activations in bf16.
+ */
+int gp_bert_ffn_dtype_out(int64_t M, int64_t H, int64_t FF, const void* x, const void* w1, const void* b1,
+                          const void* w2, const void* b2, const void* gamma, const void* beta, float eps, int act,
+                          void* out, int dtype, void* stream);
+
+/*
  * The add + LayerNorm + FFN block of the bert_addln_ffn app,
  * apps/bert_addln_ffn/torch/model.py:3-20:
  *   h0  = LayerNorm(attn . w0 + b0 + x) * ga0 + be0
@@ -170,6 +182,17 @@ int gp_bert_addln_ffn_out(int64_t M, int64_t H, int64_t FF, const void* attn, co
                           const void* b0, const void* w1, const void* b1, const void* w2, const void* b2,
                           const void* ga0, const void* be0, const void* ga2, const void* be2, float eps, int act,
                           void* out, int impl, void* stream);
+
+/*
+ * gp_bert_addln_ffn_out with every tensor's element type given by `dtype`
+ * (GP_DTYPE_F16 or GP_DTYPE_BF16, as gp_bert_ffn_dtype_out); bf16 runs the
+ * fused implementation only (GP_IMPL_PIPELINED with bf16 returns
+ * GP_ERR_INVALID_ARG).  No counterpart in the reference (fp16 only).
+ */
+int gp_bert_addln_ffn_dtype_out(int64_t M, int64_t H, int64_t FF, const void* attn, const void* x,
+                                const void* w0, const void* b0, const void* w1, const void* b1, const void* w2,
+                                const void* b2, const void* ga0, const void* be0, const void* ga2, const void* be2,
+                                float eps, int act, void* out, int impl, int dtype, void* stream);
 
 /*
  * NerfA, apps/nerf_a/torch/model.py:5-38 (hidden 256, skip after the fifth
@@ -293,6 +316,15 @@ int gp_linear_layer_norm_out(int64_t M, int64_t K, const void* x, const void* w,
  */
 int gp_gemm_out(int64_t M, int64_t N, int64_t K, const void* x, const void* w, const void* b, const void* r,
                 int act, void* out, void* stream);
+
+/*
+ * gp_gemm_out with the element type of x, w, b, r and out given by `dtype`
+ * (GP_DTYPE_F16: the same call; GP_DTYPE_BF16: bf16 MFMAs, fp32 accumulation,
+ * bias / activation / residual in fp32, output rounded to bf16).  No
+ * counterpart in the reference (fp16 only).
+ */
+int gp_gemm_dtype_out(int64_t M, int64_t N, int64_t K, const void* x, const void* w, const void* b, const void* r,
+                      int act, void* out, int dtype, void* stream);
 
 /*
  * out[M,D] = LayerNorm(x[M,D]) * gamma + beta, biased variance, eps as given;

@@ -30,7 +30,8 @@ repeated over 128 rows there, gamma = 1, beta = 0); its expected output is
 F.layer_norm in float64.
 
 The bf16 MGN fixtures are the same MgnMlp with inputs and parameters rounded to
-bfloat16 (stored as uint16 bit patterns), expected again from torch.nn in float64.
+bfloat16 (stored as uint16 bit patterns), expected again from torch.nn in float64;
+bert_ffn_gelu_bf16 is the BERT FFN block the same way.
 
 The bert_addln_ffn fixtures follow apps/bert_addln_ffn/torch/model.py:3-20 and the
 nerf_a fixture apps/nerf_a/torch/model.py:5-38, each evaluated with torch.nn modules in
@@ -154,6 +155,22 @@ def make_bert_fixture(name, M, H, FF, act, eps, init, seed, affine_random):
             "act": np.array(act)}
     for k, v in p.items():
         arrs[k] = v.numpy()
+    path = os.path.join(HERE, f"{name}.npz")
+    np.savez_compressed(path, **arrs)
+    return path
+
+
+def make_bert_bf16_fixture(name, M, H, FF, act, eps, seed):
+    """The BERT FFN block with bf16 inputs and parameters (stored as uint16 bit
+    patterns, key `dtype` = "bf16"); expected = torch.nn modules in float64 on
+    the bf16 values."""
+    p = {k: v.to(torch.bfloat16) for k, v in bert_params(H, FF, seed=seed, init="bert", affine_random=True).items()}
+    x = normal_fp16(M, H, seed=seed + 1000, dtype=torch.bfloat16)
+    y = torch_bert_ffn_f64(x, p, act, eps)
+    arrs = {"x": bf16_bits(x), "expected": y.numpy().astype(np.float64), "eps": np.float64(eps),
+            "act": np.array(act), "dtype": np.array("bf16")}
+    for k, v in p.items():
+        arrs[k] = bf16_bits(v)
     path = os.path.join(HERE, f"{name}.npz")
     np.savez_compressed(path, **arrs)
     return path
@@ -333,6 +350,9 @@ FIXTURES = {
     # MgnMlp in bfloat16 (edge and node widths)
     "mgn_edge_ln_bf16": lambda: make_mgn_bf16_fixture("mgn_edge_ln_bf16", 384, seed=40),
     "mgn_node_ln_bf16": lambda: make_mgn_bf16_fixture("mgn_node_ln_bf16", 256, seed=41),
+    # the BERT-large recipe in bfloat16 at a small width
+    "bert_ffn_gelu_bf16": lambda: make_bert_bf16_fixture("bert_ffn_gelu_bf16", 128, 256, 512, "gelu_tanh", 1e-12,
+                                                         seed=42),
 }
 
 

@@ -81,6 +81,24 @@ def test_dtype_entry_validates_like_the_fp16_call():
     assert _call_dtype(1, M=0) == 0
 
 
+def test_wide_dtype_entry_points_reject_before_any_device_call():
+    """gp_gemm_dtype_out, gp_bert_ffn_dtype_out and gp_bert_addln_ffn_dtype_out:
+    unknown dtypes, bf16 on the queue-chained bert_addln layout, and the fp16
+    calls' own shape checks all fail before touching a device."""
+    vp = ctypes.c_void_p
+    L = gpipes.lib
+    assert L.gp_gemm_dtype_out(16, 256, 64, vp(16), vp(16), None, None, 0, vp(16), 2, None) == -1
+    assert L.gp_gemm_dtype_out(16, 200, 64, vp(16), vp(16), None, None, 0, vp(16), 1, None) == -2
+    assert L.gp_gemm_dtype_out(0, 256, 64, None, vp(16), None, None, 0, None, 1, None) == 0
+    args = [vp(16)] * 7
+    assert L.gp_bert_ffn_dtype_out(16, 1024, 4096, *args, 1e-12, 2, vp(16), 5, None) == -1
+    assert L.gp_bert_ffn_dtype_out(16, 768, 4096, *args, 1e-12, 2, vp(16), 1, None) == -2
+    args12 = [vp(16)] * 12
+    assert L.gp_bert_addln_ffn_dtype_out(16, 128, 512, *args12, 1e-5, 1, vp(16), 1, 1, None) == -1  # bf16 + pipelined
+    assert L.gp_bert_addln_ffn_dtype_out(16, 128, 512, *args12, 1e-5, 1, vp(16), 0, 3, None) == -1
+    assert L.gp_last_error().decode() != ""
+
+
 def test_fullmlp_requires_affine():
     vp = ctypes.c_void_p
     rc = gpipes.lib.gp_mgn_fullmlp_out(16, vp(16), vp(16), vp(16), vp(16), vp(16), vp(16), vp(16), None,

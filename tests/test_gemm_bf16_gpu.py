@@ -1,0 +1,157 @@
+"""GPU parity of the bf16 forms of the wide GEMM stage, the BERT FFN block and
+the fused bert_addln_ffn chain (gp_gemm_dtype_out, gp_bert_ffn_dtype_out,
+gp_bert_addln_ffn_dtype_out; the Python mirrors follow the tensors' dtype).
+
+The oracle is the same fp32 restatement, run on the bf16 values (exact in
+fp32).  The bar is the fp16 bar scaled by the ratio of the unit roundoffs,
+oracle.BF16_MAX_ABS_TOL / BF16_REL_L2_TOL (max-abs 0.16, relative-L2 0.04): the
+kernels round the activations between GEMMs and the outputs to bf16 where the
+oracle keeps fp32.  The bf16 golden fixture (torch.nn in float64 on bf16
+parameters) pins the block; on the same values the bf16 and fp16 paths agree
+within the bf16 bar; the two weight paths (in place / transposed copy) are
+bit-identical in bf16 as in fp16.
+"""
+import numpy as np
+import pytest
+import torch
+
+import gpipes
+import oracle
+from conftest import load_golden
+from gpipes.synth import bert_addln_params, bert_params, normal_fp16
+
+pytestmark = pytest.mark.gpu
+
+ACT_ID = {"relu": oracle.ACT_RELU, "gelu_tanh": oracle.ACT_GELU_TANH, "none": oracle.ACT_NONE,
+          "sigmoid": oracle.ACT_SIGMOID}
+BF = torch.bfloat16
+
+
+def assert_bf16_parity(got, want, what):
+    max_abs, rel = oracle.errors(got, want)
+    print(f"[parity bf16] {what}: max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
+    assert max_abs <= oracle.BF16_MAX_ABS_TOL and rel <= oracle.BF16_REL_L2_TOL, (what, max_abs, rel)
+
+
+def f(t):
+    return None if t is None else t.detach().float().cpu().numpy()
+
+
+def to(p, cuda, dtype=BF):
+    return {k: (None if v is None else v.to(dtype).to(cuda)) for k, v in p.items()}
+
+
+# ------------------------------------------------------------------ wide GEMM stage
+@pytest.mark.parametrize("M,N,K", [(1, 128, 64), (257, 384, 1024), (1000, 4096, 1024), (513, 1024, 4096)])
+@pytest.mark.parametrize("act", ["none", "relu", "gelu_tanh", "sigmoid"])
+def test_gemm_bf16_vs_oracle(cuda, M, N, K, act):
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    x = torch.randn((M, K), generator=g).to(BF)
+    w = (torch.randn((K, N), generator=g) / np.sqrt(K)).to(BF)
+    b = (torch.randn((N,), generator=g) * 0.5).to(BF)
+    y = gpipes.gemm_out(x.to(cuda), w.to(cuda), b.to(cuda), act=act)
+    assert y.dtype == BF
+    assert_bf16_parity(f(y), oracle.linear(f(x), f(w), f(b), ACT_ID[act]), f"gemm M={M} N={N} K={K} {act}")
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 128, 512), (1000, 1024, 4096)])
+def test_gemm_bf16_residual(cuda, M, N, K):
+    g = torch.Generator().manual_seed(M + N)
+    x = torch.randn((M, K), generator=g).to(BF)
+    w = (torch.randn((K, N), generator=g) / np.sqrt(K)).to(BF)
+    b = (torch.randn((N,), generator=g) * 0.5).to(BF)
+    r = torch.randn((M, N), generator=g).to(BF)
+    y = gpipes.gemm_out(x.to(cuda), w.to(cuda), b.to(cuda), r.to(cuda))
+    assert_bf16_parity(f(y), oracle.linear(f(x), f(w), f(b)) + f(r), f"gemm+residual M={M} N={N} K={K}")
+
+
+def test_gemm_bf16_weight_paths_agree(cuda):
+    """Above 8e10 FLOP the GEMM reads a transposed copy of W, below it W in
+    place: the same products in the same order, bit-identical in bf16."""
+    M, N, K = 16384, 2048, 1280
+    g = torch.Generator().manual_seed(18)
+    x = torch.randn((M, K), generator=g).to(BF).to(cuda)
+    w = (torch.randn((K, N), generator=g) / np.sqrt(K)).to(BF).to(cuda)
+    b = (torch.randn((N,), generator=g) * 0.5).to(BF).to(cuda)
+    y = gpipes.gemm_out(x, w, b, act="gelu_tanh")
+    parts = torch.cat([gpipes.gemm_out(x[r:r + 2048].contiguous(), w, b, act="gelu_tanh") for r in range(0, M, 2048)])
+    assert torch.equal(y.view(torch.int16), parts.view(torch.int16))
+    rows = np.r_[0:32, M - 32:M]
+    assert_bf16_parity(f(y)[rows], oracle.linear(f(x[rows]), f(w), f(b), oracle.ACT_GELU_TANH), "both weight paths")
+
+
+def test_gemm_rejects_mixed_dtypes(cuda):
+    x = torch.zeros((64, 128), dtype=BF, device=cuda)
+    with pytest.raises(RuntimeError, match="bfloat16"):
+        gpipes.gemm_out(x, torch.zeros((128, 128), dtype=torch.float16, device=cuda))
+
+
+# ------------------------------------------------------------------ BERT FFN block
+def bert_ffn(x, p, act, eps):
+    return gpipes.bert_ffn(x, p["w1"], p["b1"], p["w2"], p["b2"], p["gamma"], p["beta"], eps=eps, act=act)
+
+
+def test_bert_ffn_bf16_golden(cuda):
+    z = load_golden("bert_ffn_gelu_bf16.npz")
+    assert str(z["dtype"]) == "bf16"
+    t = {k: torch.from_numpy(z[k].view(np.int16)).view(BF).to(cuda) for k in
+         ("x", "w1", "b1", "w2", "b2", "gamma", "beta")}
+    y = bert_ffn(t["x"], t, str(z["act"]), float(z["eps"]))
+    assert_bf16_parity(f(y), z["expected"], "golden bert_ffn_gelu_bf16")
+
+
+@pytest.mark.parametrize("M,H,FF,act", [(1, 128, 512, "relu"), (300, 128, 512, "relu"), (257, 256, 1024, "gelu_tanh"),
+                                        (1000, 1024, 4096, "gelu_tanh"), (20000, 1024, 1024, "gelu_tanh")])
+def test_bert_ffn_bf16_vs_oracle(cuda, M, H, FF, act):
+    """H 128 keeps the LayerNorm rows in a wave; H 256 and 1024 exchange partial
+    statistics between workgroups; M 20,000 is two row chunks."""
+    print(f"[bf16 bert_ffn] M={M} H={H} FF={FF} {act}", flush=True)
+    p = to(bert_params(H, FF, seed=M + H, init="bert", affine_random=True), cuda)
+    x = normal_fp16(M, H, seed=M, device=cuda, dtype=BF)
+    eps = 1e-12 if act == "gelu_tanh" else 1e-5
+    y = bert_ffn(x, p, act, eps)
+    if H > 128:
+        gpipes.pipeline_check()  # the LayerNorm exchange reports its waits
+    rows = np.r_[0:min(M, 200), max(0, M - 200):M]
+    want = oracle.bert_ffn(f(x[rows]), f(p["w1"]), f(p["b1"]), f(p["w2"]), f(p["b2"]), f(p["gamma"]), f(p["beta"]),
+                           act=ACT_ID[act], eps=eps)
+    assert_bf16_parity(f(y)[rows], want, f"bert_ffn bf16 M={M} H={H} FF={FF}")
+
+
+def test_bert_ffn_bf16_agrees_with_fp16(cuda):
+    """The same values through both element types (bf16 values are exact in
+    fp16 at these magnitudes): the results differ only by the bf16 rounding of
+    the activations and outputs."""
+    M, H, FF = 2000, 1024, 4096
+    p16 = to(bert_params(H, FF, seed=5, init="bert", affine_random=True), cuda, BF)
+    x16 = normal_fp16(M, H, seed=6, device=cuda, dtype=BF)
+    yb = bert_ffn(x16, p16, "gelu_tanh", 1e-12)
+    ph = {k: (None if v is None else v.to(torch.float16)) for k, v in p16.items()}
+    yh = bert_ffn(x16.to(torch.float16), ph, "gelu_tanh", 1e-12)
+    assert_bf16_parity(f(yb), f(yh), "bf16 against fp16 on the same values")
+
+
+# ------------------------------------------------------------------ bert_addln_ffn (fused)
+@pytest.mark.parametrize("M,H,FF,act", [(300, 128, 512, "relu"), (1000, 256, 384, "gelu_tanh")])
+def test_bert_addln_bf16_vs_oracle(cuda, M, H, FF, act):
+    p = to(bert_addln_params(H, FF, seed=H + FF, init="bert" if act == "gelu_tanh" else "torch",
+                             affine_random=True), cuda)
+    attn = normal_fp16(M, H, seed=M, device=cuda, dtype=BF)
+    x = normal_fp16(M, H, seed=M + 1, device=cuda, dtype=BF)
+    eps = 1e-12 if act == "gelu_tanh" else 1e-5
+    y = gpipes.bert_addln_ffn(attn, x, p["w0"], p["b0"], p["w1"], p["b1"], p["w2"], p["b2"], p["ga0"], p["be0"],
+                              p["ga2"], p["be2"], eps=eps, act=act)
+    if H > 128:
+        gpipes.pipeline_check()
+    want = oracle.bert_addln_ffn(f(attn), f(x), f(p["w0"]), f(p["b0"]), f(p["w1"]), f(p["b1"]), f(p["w2"]),
+                                 f(p["b2"]), f(p["ga0"]), f(p["be0"]), f(p["ga2"]), f(p["be2"]), act=ACT_ID[act],
+                                 eps=eps)
+    assert_bf16_parity(f(y), want, f"bert_addln_ffn bf16 M={M} H={H} FF={FF}")
+
+
+def test_bert_addln_bf16_pipelined_rejected(cuda):
+    p = to(bert_addln_params(128, 512, seed=1, init="torch", affine_random=True), cuda)
+    a = normal_fp16(128, 128, seed=1, device=cuda, dtype=BF)
+    with pytest.raises(gpipes.GpipesError):
+        gpipes.bert_addln_ffn(a, a, p["w0"], p["b0"], p["w1"], p["b1"], p["w2"], p["b2"], p["ga0"], p["be0"],
+                              p["ga2"], p["be2"], impl="pipelined")

@@ -262,6 +262,17 @@ def test_bert_ffn_golden(name):
     assert max_abs < 2e-4 and rel < 1e-5, (max_abs, rel)
 
 
+def test_bert_ffn_golden_bf16():
+    """The oracle on bf16 inputs (exact in fp32) against torch.nn in float64."""
+    z = load_golden("bert_ffn_gelu_bf16.npz")
+    assert str(z["dtype"]) == "bf16"
+    p = {k: bf16_to_f32(z[k]) for k in ("x", "w1", "b1", "w2", "b2", "gamma", "beta")}
+    got = oracle.bert_ffn(p["x"], p["w1"], p["b1"], p["w2"], p["b2"], p["gamma"], p["beta"],
+                          act=oracle.ACT_GELU_TANH, eps=float(z["eps"]))
+    max_abs, rel = oracle.errors(got, z["expected"])
+    assert max_abs < 2e-4 and rel < 1e-5, (max_abs, rel)
+
+
 @pytest.mark.parametrize("mutant", ["no_residual", "residual_after_ln", "w2_transposed_blocks", "relu_for_gelu",
                                     "eps_1e-5_instead"])
 def test_bert_ffn_golden_rejects_planted_mistakes(mutant):
