@@ -11,7 +11,7 @@
 // one streaming kernel over output tiles with its epilogue fused.
 //
 // Kernel design.
-//  * B is consumed transposed (Bt[N][K], from transpose_kernel / prep_kernel),
+//  * B is consumed transposed (Bt[N][K], from prep_kernel),
 //    so both MFMA operands are rows of consecutive k -- or, for calls small
 //    enough that the transpose launch would cost more than it saves, in its
 //    own [K][N] layout, its fragments read with the transposing LDS read
@@ -672,23 +672,55 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   }
 }
 
-// out[Np][Kp] = in[K][N] transposed, zero where n >= N or k >= K (fp16),
-// 64 x 64 tiles through LDS; Kp and Np multiples of 64, K <= Kp, N <= Np.
-__global__ __launch_bounds__(256) void transpose_kernel(const half_t* in, half_t* out, int K, int N, int Kp) {
-  __shared__ half_t tile[64][66];
-  const int k0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int r = ty; r < 64; r += 4) {
-    const int k = k0 + r, n = n0 + tx;
-    tile[r][tx] = (k < K && n < N) ? in[(int64_t)k * N + n] : (half_t)0.f;
+// One 64 x 64 tile of wt[Np][Kp] = w[K][N] transposed, zero where k >= K or
+// n >= N (16-bit values, any element type).  Rows of w come in as 16-byte
+// chunks (one 128-byte row segment per eight threads) into an LDS tile whose
+// chunk c of row r sits at chunk position c ^ (r % 8).  ds_read_b64_tr_b16
+// then hands lane j of a 16-lane group column j of the 4 x 16 block its lanes
+// point at (lane m at row r0 + m/4, columns c0 + 4 (m % 4) .. +3): two reads
+// give a lane eight consecutive k of one output row, stored as one 16-byte
+// chunk.  The swizzle keeps both the chunk writes and the transposing reads
+// free of bank conflicts.
+__device__ __forceinline__ void transpose_tile64(const half_t* w, int K, int N, half_t* wt, int Kp, int k0, int n0,
+                                                 GP_LDS char* tile) {
+  const int t = threadIdx.x;
+  const bool whole = N % 8 == 0 && (uintptr_t)w % 16 == 0 && k0 + 64 <= K && n0 + 64 <= N;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int c = t + 256 * h;  // row r = c / 8, 8-column chunk cg = c % 8
+    const int r = c >> 3, cg = c & 7;
+    h8 v;
+    if (whole) {
+      v = *(const h8*)(w + (int64_t)(k0 + r) * N + n0 + 8 * cg);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int k = k0 + r, n = n0 + 8 * cg + e;
+        v[e] = (k < K && n < N) ? w[(int64_t)k * N + n] : (half_t)0.f;
+      }
+    }
+    *(GP_LDS h8*)(tile + r * 128 + ((cg ^ (r & 7)) << 4)) = v;
   }
   __syncthreads();
-  for (int r = ty; r < 64; r += 4) out[(int64_t)(n0 + r) * Kp + k0 + tx] = tile[tx][r];
+  const int m = t & 15, grp = t >> 4;  // 16 groups of 16 lanes
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int nb = grp & 3, kg = (grp >> 2) + 4 * q;  // output rows n0 + 16 nb + m, k0 + 8 kg .. +7
+    s4 part[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int r = 8 * kg + 4 * hh + (m >> 2), col = 16 * nb + 4 * (m & 3);
+      part[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (GP_LDS s4*)(tile + r * 128 + (((col >> 3) ^ (r & 7)) << 4) + (col & 7) * 2));
+    }
+    *(h8*)(wt + (int64_t)(n0 + 16 * nb + m) * Kp + k0 + 8 * kg) =
+        __builtin_bit_cast(h8, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
+  }
 }
 
 // The weight preparation of a whole chain in one launch: for every layer,
-// wt[Np][Kp] = w[K][N] transposed and zero-padded (the 64 x 64 tiles of
-// transpose_kernel), and bp[Np] = b zero-padded (zeros for a null b).  Layer i
+// wt[Np][Kp] = w[K][N] transposed and zero-padded (transpose_tile64), and
+// bp[Np] = b zero-padded (zeros for a null b; skipped for a null bp).  Layer i
 // owns blocks [blk0_i, blk0_{i+1}); its first block also writes the bias.
 struct PrepLayer {
   const half_t* w;
@@ -704,20 +736,14 @@ struct PrepBatch {
 };
 
 __global__ __launch_bounds__(256) void prep_kernel(PrepBatch pb) {
-  __shared__ half_t tile[64][66];
+  __shared__ __attribute__((aligned(16))) char tile[64 * 128];
   int i = 0;
   while (i + 1 < pb.n && (int)blockIdx.x >= pb.L[i + 1].blk0) ++i;
   const PrepLayer& L = pb.L[i];
   const int local = (int)blockIdx.x - L.blk0;
   const int tn = L.Np / 64;
   const int n0 = (local % tn) * 64, k0 = (local / tn) * 64;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int r = ty; r < 64; r += 4) {
-    const int k = k0 + r, n = n0 + tx;
-    tile[r][tx] = (k < L.K && n < L.N) ? L.w[(int64_t)k * L.N + n] : (half_t)0.f;
-  }
-  __syncthreads();
-  for (int r = ty; r < 64; r += 4) L.wt[(int64_t)(n0 + r) * L.Kp + k0 + tx] = tile[tx][r];
+  transpose_tile64(L.w, L.K, L.N, L.wt, L.Kp, k0, n0, (GP_LDS char*)tile);
   if (local == 0 && L.bp)
     for (int j = threadIdx.x; j < L.Np; j += 256) L.bp[j] = (L.b && j < L.N) ? L.b[j] : (half_t)0.f;
 }
@@ -855,7 +881,8 @@ hipError_t prep_launch(const PrepSpec* L, int n, hipStream_t s) {
     pb.n = n - i0 < kMaxPrep ? n - i0 : kMaxPrep;
     for (int i = 0; i < pb.n; ++i) {
       const PrepSpec& q = L[i0 + i];
-      if (q.Kp % 64 != 0 || q.Np % 64 != 0 || q.K > q.Kp || q.N > q.Np || q.K < 1 || q.N < 1 || !q.w || !q.wt)
+      if (q.Kp % 64 != 0 || q.Np % 64 != 0 || q.K > q.Kp || q.N > q.Np || q.K < 1 || q.N < 1 || !q.w || !q.wt ||
+          (uintptr_t)q.wt % 16 != 0)
         return hipErrorInvalidValue;
       pb.L[i] = {(const half_t*)q.w, (half_t*)q.wt, (const half_t*)q.b, (half_t*)q.bp,
                  (int)q.K, (int)q.N, (int)q.Kp, (int)q.Np, blocks};
@@ -884,9 +911,8 @@ hipError_t transpose_launch(const void* in, void* out, int64_t K, int64_t N, hip
   if (Kp == 0) Kp = K;
   if (Np == 0) Np = N;
   if (Kp % 64 != 0 || Np % 64 != 0 || K > Kp || N > Np) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(gemm::transpose_kernel, dim3((unsigned)(Np / 64), (unsigned)(Kp / 64)), dim3(256), 0, s,
-                     (const half_t*)in, (half_t*)out, (int)K, (int)N, (int)Kp);
-  return hipGetLastError();
+  const PrepSpec one{in, out, nullptr, nullptr, K, N, Kp, Np};
+  return prep_launch(&one, 1, s);
 }
 
 }  // namespace gp
