@@ -135,7 +135,10 @@ int gp_mgn_edge_gather_out(int64_t E, int64_t N, const void* nf, const void* ef,
  * launches; the second computes the residual add and the LayerNorm in its
  * epilogue.  Above H = 128 a row spans several workgroups, which exchange
  * partial row statistics through the stream's queue arena with bounded waits:
- * such calls report failures through gp_pipeline_check.  The FF-wide
+ * such calls report failures through gp_pipeline_check.  Every workgroup of
+ * that launch (one per CU) must be resident at once, as for the queue-chained
+ * layouts: kernels of other streams or processes holding CUs meanwhile can
+ * make its waits run out (GP_ERR_TIMEOUT; never a hang).  The FF-wide
  * activations pass through a workspace kept per (device, stream), allocated
  * on first use and grown when needed (a grow synchronises the stream).  Any
  * M >= 0 (the reference needs M to be a multiple of its pipeline rows x 128).
