@@ -87,6 +87,7 @@ struct F16 {
   __device__ static float val(half_t h) { return (float)h; }
   __device__ static h4 cvt4(f4 v) { return __builtin_convertvector(v, h4); }
   __device__ static h2 cvt2(f2 v) { return __builtin_convertvector(v, h2); }
+  __device__ static half_t cvt1(float v) { return (half_t)v; }
 };
 struct BF16 {
   static constexpr unsigned short kOne = 0x3F80;
@@ -99,6 +100,7 @@ struct BF16 {
   // v_cvt_pk_bf16_f32: round to nearest even
   __device__ static h4 cvt4(f4 v) { return __builtin_bit_cast(h4, __builtin_convertvector(v, bf4)); }
   __device__ static h2 cvt2(f2 v) { return __builtin_bit_cast(h2, __builtin_convertvector(v, bf2)); }
+  __device__ static half_t cvt1(float v) { return __builtin_bit_cast(half_t, (__bf16)v); }
 };
 
 struct Args {
@@ -753,13 +755,14 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepBatch pb) {
 // MFMA and output on.  Each half of a wave takes one row and reads it as
 // 16-byte chunks (one 512-byte row per instruction at K = 256), then sums
 // its 32 partial dot products with lane exchanges.
+template <typename E>
 __global__ __launch_bounds__(256) void gemv1_kernel(const half_t* a, int lda, int64_t M, int K, const half_t* w,
                                                     const half_t* b, int act, half_t* out) {
   const int lane = threadIdx.x & 63, hw = lane >> 5, l32 = lane & 31;
   const int64_t wv = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int64_t nw = (int64_t)gridDim.x * 4;
   const int nc = K / 8;
-  const float bias = b ? (float)b[0] : 0.f;
+  const float bias = b ? E::val(b[0]) : 0.f;
   for (int64_t m0 = 2 * wv; m0 < M; m0 += 2 * nw) {
     const int64_t m = m0 + hw;
     float s = 0.f;
@@ -769,12 +772,12 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const half_t* a, int lda, in
         const h8 x = *(const h8*)(row + 8 * c);
         const h8 v = *(const h8*)(w + 8 * c);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s = __builtin_fmaf((float)x[e], (float)v[e], s);
+        for (int e = 0; e < 8; ++e) s = __builtin_fmaf(E::val(x[e]), E::val(v[e]), s);
       }
     }
 #pragma unroll
     for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 32);
-    if (l32 == 0 && m < M) out[m] = (half_t)apply_act(s + bias, act);
+    if (l32 == 0 && m < M) out[m] = E::cvt1(apply_act(s + bias, act));
   }
 }
 
@@ -896,13 +899,18 @@ hipError_t prep_launch(const PrepSpec* L, int n, hipStream_t s) {
 }
 
 hipError_t gemv1_launch(int64_t M, int64_t K, const void* a, int64_t lda, const void* w, const void* b, int act,
-                        void* out, int num_cus, hipStream_t s) {
+                        void* out, int num_cus, hipStream_t s, int dtype) {
   if (M <= 0) return hipSuccess;
   if (K < 8 || K % 8 || lda < K || lda % 8 || !a || !w || !out) return hipErrorInvalidValue;
   const int64_t want = (M + 7) / 8;  // eight rows per block and pass
   const int64_t grid = want < (int64_t)num_cus * 8 ? want : (int64_t)num_cus * 8;
-  hipLaunchKernelGGL(gemm::gemv1_kernel, dim3((unsigned)grid), dim3(256), 0, s, (const half_t*)a, (int)lda, M,
-                     (int)K, (const half_t*)w, (const half_t*)b, act, (half_t*)out);
+  if (dtype != GP_DTYPE_F16 && dtype != GP_DTYPE_BF16) return hipErrorInvalidValue;
+  if (dtype == GP_DTYPE_BF16)
+    hipLaunchKernelGGL(gemm::gemv1_kernel<gemm::BF16>, dim3((unsigned)grid), dim3(256), 0, s, (const half_t*)a,
+                       (int)lda, M, (int)K, (const half_t*)w, (const half_t*)b, act, (half_t*)out);
+  else
+    hipLaunchKernelGGL(gemm::gemv1_kernel<gemm::F16>, dim3((unsigned)grid), dim3(256), 0, s, (const half_t*)a,
+                       (int)lda, M, (int)K, (const half_t*)w, (const half_t*)b, act, (half_t*)out);
   return hipGetLastError();
 }
 

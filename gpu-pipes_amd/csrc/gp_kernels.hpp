@@ -157,7 +157,7 @@ hipError_t transpose_launch(const void* in, void* out, int64_t K, int64_t N, hip
 // out[m] = act(a[m, 0:K] . w[0:K] + b[0]) for m < M (a one-output layer); K
 // and lda multiples of 8, a and w 16-byte aligned, b may be null.
 hipError_t gemv1_launch(int64_t M, int64_t K, const void* a, int64_t lda, const void* w, const void* b, int act,
-                        void* out, int num_cus, hipStream_t stream);
+                        void* out, int num_cus, hipStream_t stream, int dtype = GP_DTYPE_F16);
 // One launch for the weights of a layer chain: wt[Np, Kp] = w[K, N]^T and
 // bp[Np] = b (zeros for a null b), both zero-padded; Kp and Np multiples of 64.
 // A null bp skips the bias.

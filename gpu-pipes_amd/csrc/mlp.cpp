@@ -78,8 +78,9 @@ bool in_place(bool chain, int64_t N, const void* w, const void* b) {
 
 // ka: columns of `a` read (a multiple of 8, <= L.Kin); the rest count as zero.
 hipError_t layer(const Prepared& L, int64_t rows, const void* a, int64_t lda, void* c, int64_t ldc, int ncu,
-                 hipStream_t s, int64_t ka = 0) {
+                 hipStream_t s, int64_t ka = 0, int dtype = GP_DTYPE_F16) {
   GemmArgs g{rows, L.Np, L.Kin, a, L.wt, L.b, nullptr, L.act, c};
+  g.dtype = dtype;
   g.w = L.w;
   g.kw = L.kw;
   g.lda = lda;
@@ -97,9 +98,10 @@ int common_checks(int64_t M, const void* x, const void* out) {
   return GP_OK;
 }
 
-// DlrmMlp-style chain: widths[0] -> widths[1] -> ... -> widths[nl], act[i] after layer i.
+// DlrmMlp-style chain: widths[0] -> widths[1] -> ... -> widths[nl], act[i] after layer i;
+// every tensor of element type dtype.
 int run_chain(int64_t M, int nl, const int64_t* widths, const void* const* w, const void* const* b, const int* acts,
-              const void* x, void* out, hipStream_t s) {
+              const void* x, void* out, hipStream_t s, int dtype = GP_DTYPE_F16) {
   int dev = 0, ncu = 0;
   int rc = current_device_info(&dev, &ncu);
   if (rc) return rc;
@@ -162,11 +164,11 @@ int run_chain(int64_t M, int nl, const int64_t* widths, const void* const* w, co
     for (int i = 0; i < nl && e == hipSuccess; ++i) {
       const bool last = i == nl - 1;
       if (last && gemv_head) {
-        e = gemv1_launch(rows, widths[i], a, lda, w[i], b[i], acts[i], (void*)row_ptr(out, r0, 1), ncu, s);
+        e = gemv1_launch(rows, widths[i], a, lda, w[i], b[i], acts[i], (void*)row_ptr(out, r0, 1), ncu, s, dtype);
         break;
       }
       void* c = last && direct_out ? (void*)row_ptr(out, r0, widths[nl]) : (void*)hb[i % 2];
-      e = layer(L[i], rows, a, lda, c, np[i], ncu, s, i == 0 && direct_in ? widths[0] : 0);
+      e = layer(L[i], rows, a, lda, c, np[i], ncu, s, i == 0 && direct_in ? widths[0] : 0, dtype);
       a = c;
       lda = np[i];
     }
@@ -197,16 +199,22 @@ using namespace gp;
 
 extern "C" {
 
-int gp_mlp_out(int64_t M, int nlayers, const int64_t* widths, const void* const* w, const void* const* b,
-               const int* acts, const void* x, void* out, void* stream) {
+int gp_mlp_dtype_out(int64_t M, int nlayers, const int64_t* widths, const void* const* w, const void* const* b,
+                     const int* acts, const void* x, void* out, int dtype, void* stream) {
   clear_error();
+  if (dtype != GP_DTYPE_F16 && dtype != GP_DTYPE_BF16) return fail(GP_ERR_INVALID_ARG, "unknown dtype %d", dtype);
   if (nlayers < 1 || nlayers > 32) return fail(GP_ERR_INVALID_ARG, "nlayers must be in [1, 32] (got %d)", nlayers);
   if (!widths || !w || !b || !acts) return fail(GP_ERR_INVALID_ARG, "widths, w, b and acts must be non-NULL");
   int rc = common_checks(M, x, out);
   if (rc) return rc;
   if ((rc = check_chain(nlayers, widths, w, acts))) return rc;
   if (M == 0) return GP_OK;
-  return run_chain(M, nlayers, widths, w, b, acts, x, out, (hipStream_t)stream);
+  return run_chain(M, nlayers, widths, w, b, acts, x, out, (hipStream_t)stream, dtype);
+}
+
+int gp_mlp_out(int64_t M, int nlayers, const int64_t* widths, const void* const* w, const void* const* b,
+               const int* acts, const void* x, void* out, void* stream) {
+  return gp_mlp_dtype_out(M, nlayers, widths, w, b, acts, x, out, GP_DTYPE_F16, stream);
 }
 
 int gp_dlrm_botmlp_out(int64_t M, int64_t K0, const void* x, const void* w1, const void* b1, const void* w2,

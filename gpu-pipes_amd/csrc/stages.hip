@@ -362,6 +362,8 @@ hipError_t layer_norm_launch(int64_t M, int64_t D, const void* x, const void* ga
 // block between matrices with zero padding (the concat inputs, padded inputs
 // and narrow heads of the MLP chains).  Strides in elements.  V elements per
 // thread: 8 (16-byte vectors) when every width, stride and base allows it.
+// Without an activation the values are copied as raw 16-bit patterns, so the
+// copy serves fp16 and bf16 alike.
 template <int V>
 __global__ __launch_bounds__(kStageThreads) void place_kernel(const half_t* src, int64_t lds, int w, half_t* dst,
                                                               int64_t ldd, int wpad, int act, int64_t M) {
@@ -375,8 +377,13 @@ __global__ __launch_bounds__(kStageThreads) void place_kernel(const half_t* src,
     hv v;
     if (j + V <= w) {
       v = *(const hv*)(src + m * lds + j);
+      if (act != ACT_NONE) {
 #pragma unroll
-      for (int e = 0; e < V; ++e) v[e] = (half_t)apply_act((float)v[e], act);
+        for (int e = 0; e < V; ++e) v[e] = (half_t)apply_act((float)v[e], act);
+      }
+    } else if (act == ACT_NONE) {  // a raw 16-bit copy: any element type
+#pragma unroll
+      for (int e = 0; e < V; ++e) v[e] = j + e < w ? src[m * lds + j + e] : (half_t)0.f;
     } else {
 #pragma unroll
       for (int e = 0; e < V; ++e) v[e] = j + e < w ? (half_t)apply_act((float)src[m * lds + j + e], act) : (half_t)0.f;

@@ -85,6 +85,8 @@ def _load():
     L.gp_bert_ffn_out.argtypes = [i64, i64, i64] + [vp] * 7 + [f32, i32, vp, vp]
     L.gp_bert_ffn_dtype_out.argtypes = [i64, i64, i64] + [vp] * 7 + [f32, i32, vp, i32, vp]
     L.gp_mlp_out.argtypes = [i64, i32, vp, vp, vp, vp, vp, vp, vp]
+    L.gp_mlp_dtype_out.argtypes = [i64, i32, vp, vp, vp, vp, vp, vp, i32, vp]
+    L.gp_mlp_dtype_out.restype = i32
     L.gp_dlrm_botmlp_out.argtypes = [i64, i64] + [vp] * 9
     L.gp_dlrm_topmlp_out.argtypes = [i64, i64, i64] + [vp] * 11 + [i32, vp, vp]
     L.gp_nerf_full_out.argtypes = [i64] * 5 + [vp] * 4 + [i32, vp, vp, vp]
@@ -456,8 +458,10 @@ def _same_device(*ts):
 
 def mlp_out(x, ws, bs, acts, out=None):
     """DlrmMlp-style chain (common/mlps.py:23-34): layer i = acts[i](h @ ws[i] + bs[i]).
-    ws[i] is [in, out] (``weight.t()``); bs[i] may be None; acts are names of ACTS or ids."""
-    _check_input("x", x)
+    ws[i] is [in, out] (``weight.t()``); bs[i] may be None; acts are names of ACTS or ids.
+    Every tensor float16, or every tensor bfloat16 (gp_mlp_dtype_out)."""
+    dt = _dtype_of(x)
+    _check_input("x", x, dtype=dt)
     if x.dim() != 2:
         raise RuntimeError("x must be 2-D [M, K]")
     if not (len(ws) == len(bs) == len(acts)) or not ws:
@@ -465,14 +469,14 @@ def mlp_out(x, ws, bs, acts, out=None):
     M, K = x.shape
     widths = [K]
     for i, (w, b) in enumerate(zip(ws, bs)):
-        _check_input(f"w{i + 1}", w)
+        _check_input(f"w{i + 1}", w, dtype=dt)
         if w.dim() != 2 or w.shape[0] != widths[-1]:
             raise RuntimeError(f"w{i + 1} must be [{widths[-1]}, N]")
         widths.append(w.shape[1])
-        _opt(f"b{i + 1}", b, (w.shape[1],))
+        _opt(f"b{i + 1}", b, (w.shape[1],), dt)
     if out is None:
-        out = torch.empty((M, widths[-1]), dtype=torch.float16, device=x.device)
-    _check_input("out", out, (M, widths[-1]))
+        out = torch.empty((M, widths[-1]), dtype=dt, device=x.device)
+    _check_input("out", out, (M, widths[-1]), dt)
     _same_device(x, out, *ws, *bs)
     n = len(ws)
     wa = (ctypes.c_int64 * (n + 1))(*widths)
@@ -480,7 +484,7 @@ def mlp_out(x, ws, bs, acts, out=None):
     bp = (ctypes.c_void_p * n)(*[0 if b is None else b.data_ptr() for b in bs])
     ap = (ctypes.c_int * n)(*[ACTS.get(a, a) for a in acts])
     with torch.cuda.device(x.device):
-        _check(lib.gp_mlp_out(M, n, wa, wp, bp, ap, _ptr(x), _ptr(out), _stream(x)))
+        _check(lib.gp_mlp_dtype_out(M, n, wa, wp, bp, ap, _ptr(x), _ptr(out), _DTYPES[dt], _stream(x)))
     return out
 
 

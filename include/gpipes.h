@@ -227,6 +227,16 @@ int gp_mlp_out(int64_t M, int nlayers, const int64_t* widths, const void* const*
                const int* acts, const void* x, void* out, void* stream);
 
 /*
+ * gp_mlp_out with every tensor's element type given by `dtype` (GP_DTYPE_F16:
+ * the same call; GP_DTYPE_BF16: bf16 MFMAs, fp32 accumulation and
+ * activations, each layer's output rounded to bf16).  No counterpart in the
+ * reference (fp16 only); the bf16 form of the DLRM towers for callers that
+ * keep their activations in bf16.
+ */
+int gp_mlp_dtype_out(int64_t M, int nlayers, const int64_t* widths, const void* const* w, const void* const* b,
+                     const int* acts, const void* x, void* out, int dtype, void* stream);
+
+/*
  * DLRM bottom MLP: x[M,K0] -> 512 -> 256 -> 128, ReLU after each layer.
  * Replaces dlrm_botmlp_out(x, w1, b1, w2, b2, w3, b3, out),
  * apps/dlrm_botmlp/pipelined/dlrm_botmlp_pl_ext.cu:24-66 (K0 = 32 there;

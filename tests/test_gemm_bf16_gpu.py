@@ -155,3 +155,24 @@ def test_bert_addln_bf16_pipelined_rejected(cuda):
     with pytest.raises(gpipes.GpipesError):
         gpipes.bert_addln_ffn(a, a, p["w0"], p["b0"], p["w1"], p["b1"], p["w2"], p["b2"], p["ga0"], p["be0"],
                               p["ga2"], p["be2"], impl="pipelined")
+
+
+# ------------------------------------------------------------------ DLRM towers (MLP chain)
+@pytest.mark.parametrize("widths,acts", [
+    ([13, 512, 256, 128], ["relu"] * 3),                               # the bottom MLP (unaligned input width)
+    ([479, 1024, 1024, 512, 256, 1], ["relu"] * 4 + ["sigmoid"]),      # the top MLP with its GEMV click head
+    ([256, 384, 200], ["gelu_tanh", "none"]),                          # a narrow, unaligned output
+])
+def test_mlp_bf16_vs_oracle(cuda, widths, acts):
+    """gp_mlp_dtype_out: the bf16 GEMM layers, the GEMV head and the raw
+    16-bit padding copies of the chain against the oracle on the bf16 values."""
+    from gpipes.synth import dlrm_params
+    M = 3000
+    ws, bs = dlrm_params(widths, seed=len(widths))
+    ws = [w.to(BF).to(cuda) for w in ws]
+    bs = [b.to(BF).to(cuda) for b in bs]
+    x = normal_fp16(M, widths[0], seed=7, device=cuda, dtype=BF)
+    y = gpipes.mlp_out(x, ws, bs, acts)
+    assert y.dtype == BF
+    want = oracle.mlp(f(x), [f(w) for w in ws], [f(b) for b in bs], [ACT_ID[a] for a in acts])
+    assert_bf16_parity(f(y), want, f"mlp bf16 {widths}")
