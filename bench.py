@@ -377,16 +377,21 @@ def bench_chain(args):
                               padded_normal, padded_uniform)
 
     dev = torch.device("cuda:0")
+    # element type of every tensor: the fp16 values drawn below, rounded to bf16 for --dtype bf16
+    et = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    if args.dtype == "bf16" and args.workload == "nerf_a":
+        raise SystemExit("the nerf_a workload runs in f16 only")
     if args.workload == "dlrm":
         M = 262144
         wb, bb = dlrm_params(DLRM_BOT, seed=0)
         wb[0][13:] = 0
         wt, bt = dlrm_params(DLRM_TOP, seed=1)
         wt[0][479:] = 0
-        wb, bb, wt, bt = ([t.to(dev) for t in ts] for ts in (wb, bb, wt, bt))
-        xb, xt = padded_uniform(M, 13, 16, seed=2, device=dev), padded_normal(M, 479, 480, seed=3, device=dev)
-        ob = torch.empty((M, 128), dtype=torch.float16, device=dev)
-        ot = torch.empty((M, 1), dtype=torch.float16, device=dev)
+        wb, bb, wt, bt = ([t.to(et).to(dev) for t in ts] for ts in (wb, bb, wt, bt))
+        xb = padded_uniform(M, 13, 16, seed=2, device=dev).to(et)
+        xt = padded_normal(M, 479, 480, seed=3, device=dev).to(et)
+        ob = torch.empty((M, 128), dtype=et, device=dev)
+        ot = torch.empty((M, 1), dtype=et, device=dev)
 
         def step(i):
             gpipes.mlp_out(xb, wb, bb, ["relu"] * 3, ob)
@@ -399,11 +404,13 @@ def bench_chain(args):
         unit = "rows/s"
     elif args.workload == "bert_addln":
         M, H, FF = ADDLN["M"], ADDLN["H"], ADDLN["FF"]
-        p = {k: v.to(dev) for k, v in bert_addln_params(H, FF, seed=0).items()}
-        attn, x = normal_fp16(M, H, seed=0, device=dev), normal_fp16(M, H, seed=1, device=dev)
+        p = {k: v.to(et).to(dev) for k, v in bert_addln_params(H, FF, seed=0).items()}
+        attn, x = normal_fp16(M, H, seed=0, device=dev, dtype=et), normal_fp16(M, H, seed=1, device=dev, dtype=et)
         out = torch.empty_like(x)
         keys = ("w0", "b0", "w1", "b1", "w2", "b2", "ga0", "be0", "ga2", "be2")
         impl = "pipelined" if args.impl == "pipelined" else "fused"
+        if et == torch.bfloat16 and impl == "pipelined":
+            raise SystemExit("the pipelined bert_addln layout runs in f16 only")
 
         def step(i):
             gpipes.bert_addln_ffn_out(attn, x, *(p[k] for k in keys), out, impl=impl)
@@ -432,9 +439,10 @@ def bench_chain(args):
     else:
         M = 1048576
         ws, bs = nerf_params(64, 27, 1, 3, seed=0, device=dev)
-        x, d = nerf_inputs(M, seed=0, device=dev)
-        o_r = torch.empty((M, 1), dtype=torch.float16, device=dev)
-        o_rgb = torch.empty((M, 3), dtype=torch.float16, device=dev)
+        ws, bs = [w.to(et) for w in ws], [b.to(et) for b in bs]
+        x, d = (t.to(et) for t in nerf_inputs(M, seed=0, device=dev))
+        o_r = torch.empty((M, 1), dtype=et, device=dev)
+        o_rgb = torch.empty((M, 3), dtype=et, device=dev)
         wb = [t for pair in zip(ws, bs) for t in pair]
 
         def step(i):
@@ -468,7 +476,7 @@ def bench_chain(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": args.dtype,
         "data": data,
         "config": config,
         "roofline": {
@@ -480,7 +488,7 @@ def bench_chain(args):
         },
         "spread": spread(call_ms),
         "settle": settle,
-        "cpu_baseline": None if args.no_cpu else cpu_baseline_chain(args.workload),
+        "cpu_baseline": None if args.no_cpu or args.dtype != "f16" else cpu_baseline_chain(args.workload),
     }
     print(json.dumps(rec), flush=True)
 
@@ -507,7 +515,8 @@ def main():
                          "engine clock swings for tens of ms after a burst starts (launches run fast, then "
                          "up to 1.5x slower, then settle), so the timed region starts in the steady state")
     ap.add_argument("--dtype", choices=["f16", "bf16"], default="f16",
-                    help="element type of the MGN and BERT workloads (bf16: the fused kernels, not the headline line)")
+                    help="element type of every workload but nerf_a (bf16: the fused / wide-GEMM kernels, not the "
+                         "headline line)")
     ap.add_argument("--eager", action="store_true",
                     help="MGN fused workloads: time the steps as eager calls only (by default `value` comes "
                          "from the same steps submitted as one HIP graph; the per-launch roofline times "

@@ -75,33 +75,8 @@ struct Cfg {
 using Wide = Cfg<4, 4, 2>;    // 256 features x 256 rows
 using Narrow = Cfg<4, 2, 1>;  // 128 features x 256 rows
 
-// Element types.  Operands, bias, residual, affine and output are 16-bit
-// values held as raw bits in half_t containers; only the MFMA form, the
-// conversions to / from fp32 and the value 1.0 differ.  Arithmetic is fp32.
-typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-struct F16 {
-  static constexpr unsigned short kOne = 0x3C00;
-  __device__ static f16x mma(h8 a, h8 b, f16x c) { return mfma32(a, b, c); }
-  __device__ static float val(half_t h) { return (float)h; }
-  __device__ static h4 cvt4(f4 v) { return __builtin_convertvector(v, h4); }
-  __device__ static h2 cvt2(f2 v) { return __builtin_convertvector(v, h2); }
-  __device__ static half_t cvt1(float v) { return (half_t)v; }
-};
-struct BF16 {
-  static constexpr unsigned short kOne = 0x3F80;
-  __device__ static f16x mma(h8 a, h8 b, f16x c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf8, a), __builtin_bit_cast(bf8, b), c, 0, 0, 0);
-  }
-  __device__ static float val(half_t h) {
-    return __builtin_bit_cast(float, (unsigned)__builtin_bit_cast(unsigned short, h) << 16);
-  }
-  // v_cvt_pk_bf16_f32: round to nearest even
-  __device__ static h4 cvt4(f4 v) { return __builtin_bit_cast(h4, __builtin_convertvector(v, bf4)); }
-  __device__ static h2 cvt2(f2 v) { return __builtin_bit_cast(h2, __builtin_convertvector(v, bf2)); }
-  __device__ static half_t cvt1(float v) { return __builtin_bit_cast(half_t, (__bf16)v); }
-};
+// Element types: F16 / BF16 (gp_device.hpp).
+
 
 struct Args {
   const half_t* a;     // [M][lda], the first K columns used
@@ -906,10 +881,10 @@ hipError_t gemv1_launch(int64_t M, int64_t K, const void* a, int64_t lda, const 
   const int64_t grid = want < (int64_t)num_cus * 8 ? want : (int64_t)num_cus * 8;
   if (dtype != GP_DTYPE_F16 && dtype != GP_DTYPE_BF16) return hipErrorInvalidValue;
   if (dtype == GP_DTYPE_BF16)
-    hipLaunchKernelGGL(gemm::gemv1_kernel<gemm::BF16>, dim3((unsigned)grid), dim3(256), 0, s, (const half_t*)a,
+    hipLaunchKernelGGL(gemm::gemv1_kernel<BF16>, dim3((unsigned)grid), dim3(256), 0, s, (const half_t*)a,
                        (int)lda, M, (int)K, (const half_t*)w, (const half_t*)b, act, (half_t*)out);
   else
-    hipLaunchKernelGGL(gemm::gemv1_kernel<gemm::F16>, dim3((unsigned)grid), dim3(256), 0, s, (const half_t*)a,
+    hipLaunchKernelGGL(gemm::gemv1_kernel<F16>, dim3((unsigned)grid), dim3(256), 0, s, (const half_t*)a,
                        (int)lda, M, (int)K, (const half_t*)w, (const half_t*)b, act, (half_t*)out);
   return hipGetLastError();
 }

@@ -216,6 +216,7 @@ __device__ __forceinline__ int wrow_voff(int lane, int stride) {
 // lanes of a wave half read four rows x 64 bytes that the swizzle puts in
 // four different chunk groups, so the read is conflict free.
 typedef short s4 __attribute__((ext_vector_type(4)));
+typedef short s8 __attribute__((ext_vector_type(8)));
 __device__ __forceinline__ s4 wrows_col4(const GP_LDS char* blk, int fb, int m) {
   const int r = m >> 2, f = fb + 4 * (m & 3);
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((GP_LDS s4*)(blk + r * 256 + (((f >> 3) ^ (4 * r)) * 16) + (f & 7) * 2));
@@ -226,5 +227,35 @@ __device__ __forceinline__ h8 wrows_col8(const GP_LDS char* blk0, const GP_LDS c
   const s4 a = wrows_col4(blk0, fb, m), b = wrows_col4(blk1, fb, m);
   return __builtin_bit_cast(h8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
 }
+
+// ---------------------------------------------------------------------------
+// Element types of the wide GEMM and the NeRF kernel.  Operands, bias,
+// residual, affine and output are 16-bit values held as raw bits in half_t
+// containers; only the MFMA form, the conversions to / from fp32 and the
+// value 1.0 differ.  Arithmetic is fp32.
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+struct F16 {
+  static constexpr unsigned short kOne = 0x3C00;
+  __device__ static f16x mma(h8 a, h8 b, f16x c) { return mfma32(a, b, c); }
+  __device__ static float val(half_t h) { return (float)h; }
+  __device__ static h4 cvt4(f4 v) { return __builtin_convertvector(v, h4); }
+  __device__ static h2 cvt2(f2 v) { return __builtin_convertvector(v, h2); }
+  __device__ static half_t cvt1(float v) { return (half_t)v; }
+};
+struct BF16 {
+  static constexpr unsigned short kOne = 0x3F80;
+  __device__ static f16x mma(h8 a, h8 b, f16x c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf8, a), __builtin_bit_cast(bf8, b), c, 0, 0, 0);
+  }
+  __device__ static float val(half_t h) {
+    return __builtin_bit_cast(float, (unsigned)__builtin_bit_cast(unsigned short, h) << 16);
+  }
+  // v_cvt_pk_bf16_f32: round to nearest even
+  __device__ static h4 cvt4(f4 v) { return __builtin_bit_cast(h4, __builtin_convertvector(v, bf4)); }
+  __device__ static h2 cvt2(f2 v) { return __builtin_bit_cast(h2, __builtin_convertvector(v, bf2)); }
+  __device__ static half_t cvt1(float v) { return __builtin_bit_cast(half_t, (__bf16)v); }
+};
 
 }  // namespace gp

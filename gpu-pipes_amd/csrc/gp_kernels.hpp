@@ -179,12 +179,13 @@ hipError_t place_launch(int64_t M, const void* src, int64_t lds, int64_t w, void
 // kernel: supported for Kx, Kd, Na, Nrgb <= 64; x and d 16-byte aligned.
 // w[i], b[i]: layer i+1's [K, N] weight and [N] bias (b may be null).  The
 // workspace (nerf_fused_workspace() bytes, 16-byte aligned) receives the
-// packed weight stream.
+// packed weight stream.  dtype: GP_DTYPE_F16 or GP_DTYPE_BF16, the element
+// type of every tensor.
 bool nerf_fused_supported(int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb);
 size_t nerf_fused_workspace();
 hipError_t nerf_fused_launch(int64_t M, int Kx, int Kd, int Na, int Nrgb, const void* x, const void* d,
                              const void* const* w, const void* const* b, int rgb_act, void* out_r, void* out_rgb,
-                             void* ws, int num_cus, hipStream_t stream);
+                             void* ws, int num_cus, hipStream_t stream, int dtype = GP_DTYPE_F16);
 // Device address and size of the NeRF kernel's static scratch on device `dev`
 // (the current device), for the allocation-free entry point.
 int nerf_static_scratch(int dev, void** ptr, size_t* bytes);

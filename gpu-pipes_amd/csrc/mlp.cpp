@@ -251,10 +251,11 @@ static int nerf_checks(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nr
   return GP_OK;
 }
 
-int gp_nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb, const void* x, const void* d,
-                     const void* const* w, const void* const* b, int rgb_act, void* out_r, void* out_rgb,
-                     void* stream) {
+int gp_nerf_full_dtype_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb, const void* x,
+                           const void* d, const void* const* w, const void* const* b, int rgb_act, void* out_r,
+                           void* out_rgb, int dtype, void* stream) {
   clear_error();
+  if (dtype != GP_DTYPE_F16 && dtype != GP_DTYPE_BF16) return fail(GP_ERR_INVALID_ARG, "unknown dtype %d", dtype);
   int rc = nerf_checks(M, Kx, Kd, Na, Nrgb, x, d, w, b, rgb_act, out_r, out_rgb);
   if (rc) return rc;
   if (M == 0) return GP_OK;
@@ -278,7 +279,7 @@ int gp_nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb
     if (e == hipSuccess && cd) e = hipMemcpyAsync(ws + o_d, d, (size_t)M * Kd * 2, hipMemcpyDeviceToDevice, s);
     if (e != hipSuccess) return fail_hip(e, "NeRF input alignment copy");
     e = nerf_fused_launch(M, (int)Kx, (int)Kd, (int)Na, (int)Nrgb, cx ? ws + o_x : x, cd ? ws + o_d : d, w, b,
-                          rgb_act, out_r, out_rgb, ws + o_st, ncu, s);
+                          rgb_act, out_r, out_rgb, ws + o_st, ncu, s, dtype);
     if (e != hipSuccess) return fail_hip(e, "NeRF fused kernel launch");
     return GP_OK;
   }
@@ -341,25 +342,33 @@ int gp_nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb
                                           ncu, s);
     if (e == hipSuccess) e = place_launch(rows, row_ptr(d, r0, Kd), Kd, Kd, c2 + H * 2, cat2, cat2 - H, GP_ACT_NONE,
                                           ncu, s);
-    if (e == hipSuccess) e = layer(L[0], rows, xb, kx, h0, H, ncu, s);
-    if (e == hipSuccess) e = layer(L[1], rows, h0, H, h1, H, ncu, s);
-    if (e == hipSuccess) e = layer(L[2], rows, h1, H, h0, H, ncu, s);
-    if (e == hipSuccess) e = layer(L[3], rows, h0, H, h1, H, ncu, s);
-    if (e == hipSuccess) e = layer(L[4], rows, h1, H, c1, cat1, ncu, s);  // h5 -> first 256 columns of [h5 | x]
-    if (e == hipSuccess) e = layer(L[5], rows, c1, cat1, h0, H, ncu, s);
-    if (e == hipSuccess) e = layer(L[6], rows, h0, H, h1, H, ncu, s);
-    if (e == hipSuccess) e = layer(L[7], rows, h1, H, h0, H, ncu, s);    // trunk output
-    if (e == hipSuccess) e = layer(L[8], rows, h0, H, hd, np9, ncu, s);  // density head
+    if (e == hipSuccess) e = layer(L[0], rows, xb, kx, h0, H, ncu, s, 0, dtype);
+    if (e == hipSuccess) e = layer(L[1], rows, h0, H, h1, H, ncu, s, 0, dtype);
+    if (e == hipSuccess) e = layer(L[2], rows, h1, H, h0, H, ncu, s, 0, dtype);
+    if (e == hipSuccess) e = layer(L[3], rows, h0, H, h1, H, ncu, s, 0, dtype);
+    // h5 -> the first 256 columns of [h5 | x]
+    if (e == hipSuccess) e = layer(L[4], rows, h1, H, c1, cat1, ncu, s, 0, dtype);
+    if (e == hipSuccess) e = layer(L[5], rows, c1, cat1, h0, H, ncu, s, 0, dtype);
+    if (e == hipSuccess) e = layer(L[6], rows, h0, H, h1, H, ncu, s, 0, dtype);
+    if (e == hipSuccess) e = layer(L[7], rows, h1, H, h0, H, ncu, s, 0, dtype);    // trunk output
+    if (e == hipSuccess) e = layer(L[8], rows, h0, H, hd, np9, ncu, s, 0, dtype);  // density head
     if (e == hipSuccess)
       e = place_launch(rows, hd, np9, Na, (void*)row_ptr(out_r, r0, Na), Na, Na, GP_ACT_NONE, ncu, s);
-    if (e == hipSuccess) e = layer(L[9], rows, h0, H, c2, cat2, ncu, s);  // bottleneck -> [bottleneck | d]
-    if (e == hipSuccess) e = layer(L[10], rows, c2, cat2, h1, H2, ncu, s);
-    if (e == hipSuccess) e = layer(L[11], rows, h1, H2, hd, np12, ncu, s);
+    // bottleneck -> the first 256 columns of [bottleneck | d]
+    if (e == hipSuccess) e = layer(L[9], rows, h0, H, c2, cat2, ncu, s, 0, dtype);
+    if (e == hipSuccess) e = layer(L[10], rows, c2, cat2, h1, H2, ncu, s, 0, dtype);
+    if (e == hipSuccess) e = layer(L[11], rows, h1, H2, hd, np12, ncu, s, 0, dtype);
     if (e == hipSuccess)
       e = place_launch(rows, hd, np12, Nrgb, (void*)row_ptr(out_rgb, r0, Nrgb), Nrgb, Nrgb, GP_ACT_NONE, ncu, s);
     if (e != hipSuccess) return fail_hip(e, "NeRF layer launch");
   }
   return GP_OK;
+}
+
+int gp_nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb, const void* x, const void* d,
+                     const void* const* w, const void* const* b, int rgb_act, void* out_r, void* out_rgb,
+                     void* stream) {
+  return gp_nerf_full_dtype_out(M, Kx, Kd, Na, Nrgb, x, d, w, b, rgb_act, out_r, out_rgb, GP_DTYPE_F16, stream);
 }
 
 int gp_nerf_a_out(int64_t M, int64_t Kx, const void* x, const void* const* w, const void* const* b, void* out, int impl,

@@ -130,6 +130,8 @@ __device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&&
   (f(std::integral_constant<int, I>{}), ...);
 }
 
+// E: F16 or BF16, the element type of x, d, the weights, biases and outputs.
+template <typename E>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void nerf_fused_kernel(Args p) {
   __shared__ __attribute__((aligned(1024))) char smem[LDS_BYTES];
   GP_LDS char* const ring = (GP_LDS char*)smem;
@@ -146,7 +148,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   const int my = (ntiles - (int)blockIdx.x + G - 1) / G;  // tiles blockIdx.x + k G, k < my
 
   for (int i = tid; i < BF_END / 8; i += NT) ((GP_LDS h8*)bfrag)[i] = ((const h8*)p.bias)[i];
-  if (tid < 128) bhead[tid] = (float)p.bias[BF_END + tid];
+  if (tid < 128) bhead[tid] = E::val(p.bias[BF_END + tid]);
   __syncthreads();
 
   auto tile_r0 = [&](int k) { return ((int64_t)blockIdx.x + (int64_t)k * G) * ROWS; };
@@ -226,7 +228,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   h8 fa[1][4];     // A fragments of the current group
   // B operand that is 1 at k = 0 and 0 elsewhere: lanes 0-31 hold k = 0..7.
   h8 ones = {};
-  ones[0] = lane0 < 32 ? (half_t)1.f : (half_t)0.f;
+  ones[0] = __builtin_bit_cast(half_t, lane0 < 32 ? E::kOne : (unsigned short)0);
 
   for (int k = 0; k < my; ++k) {
     const int64_t r0 = tile_r0(k);
@@ -290,7 +292,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
           h8 b;
           if constexpr (kb < K.next) b = xin[kb][rb];
           else b = act[kb - K.next][rb];
-          acc[fb][rb] = mfma32(fa[buf][i], b, (kb == 0 && !K.hb) ? f16x{} : acc[fb][rb]);
+          acc[fb][rb] = E::mma(fa[buf][i], b, (kb == 0 && !K.hb) ? f16x{} : acc[fb][rb]);
         }
       });
     };
@@ -303,7 +305,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         h8 a = {};
         a[0] = bfrag[off + 64 * fb + lane0];
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) acc[fb][rb] = mfma32(a, ones, f16x{});
+        for (int rb = 0; rb < RB; ++rb) acc[fb][rb] = E::mma(a, ones, f16x{});
       }
     };
     using G0 = std::integral_constant<int, 0>;
@@ -311,9 +313,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     using G2 = std::integral_constant<int, 2>;
     using G3 = std::integral_constant<int, 3>;
 
-    // Hidden-layer epilogue: act[2 fb + s][rb] = relu?(acc) in fp16.  Lane
-    // (row lr, half lh) holds, in element 4 g + e of block fb, feature
-    // 32 fb + 8 g + 4 lh + e.
+    // Hidden-layer epilogue: act[2 fb + s][rb] = relu?(acc) as 16-bit values.
+    // Lane (row lr, half lh) holds, in element 4 g + e of block fb, feature
+    // 32 fb + 8 g + 4 lh + e.  In bf16 the ReLU is a signed 16-bit integer
+    // max on the rounded bits: a bf16 value with its sign bit set is a
+    // negative integer and becomes +0, every other value stays.
     auto epi_hidden = [&](auto FBc, bool relu) {
       constexpr int FB = decltype(FBc)::value;
 #pragma unroll
@@ -321,14 +325,26 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
           h8 lo, hi;
+          if constexpr (std::is_same_v<E, F16>) {
 #pragma unroll
-          for (int r = 0; r < 8; ++r) {
-            lo[r] = (half_t)acc[fb][rb][r];
-            hi[r] = (half_t)acc[fb][rb][8 + r];
-          }
-          if (relu) {
-            lo = __builtin_elementwise_max(lo, h8{});
-            hi = __builtin_elementwise_max(hi, h8{});
+            for (int r = 0; r < 8; ++r) {
+              lo[r] = (half_t)acc[fb][rb][r];
+              hi[r] = (half_t)acc[fb][rb][8 + r];
+            }
+            if (relu) {
+              lo = __builtin_elementwise_max(lo, h8{});
+              hi = __builtin_elementwise_max(hi, h8{});
+            }
+          } else {
+            const f16x& a = acc[fb][rb];
+            lo = __builtin_shufflevector(E::cvt4(f4{a[0], a[1], a[2], a[3]}), E::cvt4(f4{a[4], a[5], a[6], a[7]}), 0, 1,
+                                         2, 3, 4, 5, 6, 7);
+            hi = __builtin_shufflevector(E::cvt4(f4{a[8], a[9], a[10], a[11]}), E::cvt4(f4{a[12], a[13], a[14], a[15]}),
+                                         0, 1, 2, 3, 4, 5, 6, 7);
+            if (relu) {
+              lo = __builtin_bit_cast(h8, __builtin_elementwise_max(__builtin_bit_cast(s8, lo), s8{}));
+              hi = __builtin_bit_cast(h8, __builtin_elementwise_max(__builtin_bit_cast(s8, hi), s8{}));
+            }
           }
           act[2 * fb][rb] = lo;
           act[2 * fb + 1][rb] = hi;
@@ -356,7 +372,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             f4 v;
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = apply_act(acc[fb][rb][4 * g + e] + bb[e], fn);
-            const h4 h = __builtin_convertvector(v, h4);
+            const h4 h = E::cvt4(v);
             const int off = (row * Nv + c) * 2;
             if (vec) {
               if (c < Nv) buf_store_h4(ro, off, h);
@@ -570,8 +586,9 @@ bool nerf_fused_supported(int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb) {
 
 hipError_t nerf_fused_launch(int64_t M, int Kx, int Kd, int Na, int Nrgb, const void* x, const void* d,
                              const void* const* w, const void* const* b, int rgb_act, void* out_r, void* out_rgb,
-                             void* ws, int num_cus, hipStream_t s) {
+                             void* ws, int num_cus, hipStream_t s, int dtype) {
   using namespace nerf;
+  if (dtype != GP_DTYPE_F16 && dtype != GP_DTYPE_BF16) return hipErrorInvalidValue;
   if (M <= 0) return hipSuccess;
   if (M > (int64_t(1) << 31) - 1) return hipErrorInvalidValue;
   if (((uintptr_t)x & 15) || ((uintptr_t)d & 15) || ((uintptr_t)ws & 15)) return hipErrorInvalidValue;
@@ -601,7 +618,10 @@ hipError_t nerf_fused_launch(int64_t M, int Kx, int Kd, int Na, int Nrgb, const 
                M, Kx, Kd, Na, Nrgb, rgb_act};
   const int64_t tiles = (M + ROWS - 1) / ROWS;
   const int64_t grid = tiles < num_cus ? tiles : num_cus;
-  hipLaunchKernelGGL(nerf_fused_kernel, dim3((unsigned)grid), dim3(NT), 0, s, a);
+  if (dtype == GP_DTYPE_BF16)
+    hipLaunchKernelGGL(nerf_fused_kernel<BF16>, dim3((unsigned)grid), dim3(NT), 0, s, a);
+  else
+    hipLaunchKernelGGL(nerf_fused_kernel<F16>, dim3((unsigned)grid), dim3(NT), 0, s, a);
   return hipGetLastError();
 }
 

@@ -91,6 +91,8 @@ def _load():
     L.gp_dlrm_topmlp_out.argtypes = [i64, i64, i64] + [vp] * 11 + [i32, vp, vp]
     L.gp_nerf_full_out.argtypes = [i64] * 5 + [vp] * 4 + [i32, vp, vp, vp]
     L.gp_nerf_full_out_noalloc.argtypes = [i64] * 5 + [vp] * 4 + [i32, vp, vp, vp]
+    L.gp_nerf_full_dtype_out.argtypes = [i64] * 5 + [vp] * 4 + [i32, vp, vp, i32, vp]
+    L.gp_nerf_full_dtype_out.restype = i32
     L.gp_bert_addln_ffn_out.argtypes = [i64, i64, i64] + [vp] * 12 + [f32, i32, vp, i32, vp]
     L.gp_bert_addln_ffn_out.restype = i32
     L.gp_bert_addln_ffn_dtype_out.argtypes = [i64, i64, i64] + [vp] * 12 + [f32, i32, vp, i32, i32, vp]
@@ -513,13 +515,15 @@ def dlrm_topmlp(x, w1, b1, w2, b2, w3, b3, w4, b4, w5, b5, act5="relu"):
 
 def nerf_full_out(x, d, *wb_and_outs, rgb_act="none"):
     """NeRF MLP (apps/nerf_full/pipelined/nerf_full_pl_ext.cu:24-97): arguments
-    x, d, w1, b1, ..., w12, b12, out_r, out_rgb; see gp_nerf_full_out for the shapes."""
+    x, d, w1, b1, ..., w12, b12, out_r, out_rgb; see gp_nerf_full_out for the shapes.
+    Every tensor float16, or every tensor bfloat16 (gp_nerf_full_dtype_out)."""
     if len(wb_and_outs) != 26:
         raise RuntimeError("expected w1, b1, ..., w12, b12, out_r, out_rgb")
     ws, bs = list(wb_and_outs[0:24:2]), list(wb_and_outs[1:24:2])
     out_r, out_rgb = wb_and_outs[24], wb_and_outs[25]
-    _check_input("x", x)
-    _check_input("d", d)
+    dt = _dtype_of(x)
+    _check_input("x", x, dtype=dt)
+    _check_input("d", d, dtype=dt)
     if x.dim() != 2 or d.dim() != 2 or d.shape[0] != x.shape[0]:
         raise RuntimeError("x and d must be 2-D with the same number of rows")
     M, Kx = x.shape
@@ -528,16 +532,16 @@ def nerf_full_out(x, d, *wb_and_outs, rgb_act="none"):
     shapes = [(Kx, 256)] + [(256, 256)] * 4 + [(256 + Kx, 256), (256, 256), (256, 256), (256, Na), (256, 256),
                                                 (256 + Kd, 128), (128, Nrgb)]
     for i, (w, b, shp) in enumerate(zip(ws, bs, shapes)):
-        _check_input(f"w{i + 1}", w, shp)
-        _opt(f"b{i + 1}", b, (shp[1],))
-    _check_input("out_r", out_r, (M, Na))
-    _check_input("out_rgb", out_rgb, (M, Nrgb))
+        _check_input(f"w{i + 1}", w, shp, dt)
+        _opt(f"b{i + 1}", b, (shp[1],), dt)
+    _check_input("out_r", out_r, (M, Na), dt)
+    _check_input("out_rgb", out_rgb, (M, Nrgb), dt)
     _same_device(x, d, out_r, out_rgb, *ws, *bs)
     wp = (ctypes.c_void_p * 12)(*[w.data_ptr() for w in ws])
     bp = (ctypes.c_void_p * 12)(*[0 if b is None else b.data_ptr() for b in bs])
     with torch.cuda.device(x.device):
-        _check(lib.gp_nerf_full_out(M, Kx, Kd, Na, Nrgb, _ptr(x), _ptr(d), wp, bp, ACTS.get(rgb_act, rgb_act),
-                                    _ptr(out_r), _ptr(out_rgb), _stream(x)))
+        _check(lib.gp_nerf_full_dtype_out(M, Kx, Kd, Na, Nrgb, _ptr(x), _ptr(d), wp, bp, ACTS.get(rgb_act, rgb_act),
+                                          _ptr(out_r), _ptr(out_rgb), _DTYPES[dt], _stream(x)))
     return out_r, out_rgb
 
 

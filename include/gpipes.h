@@ -279,6 +279,18 @@ int gp_nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb
                      void* stream);
 
 /*
+ * gp_nerf_full_out with the element type as an argument: no counterpart in
+ * the reference (its NeRF MLP is fp16 only).  dtype GP_DTYPE_F16 is
+ * gp_nerf_full_out; GP_DTYPE_BF16 takes x, d, every weight and bias and both
+ * outputs as bf16 (fp32 accumulation, activations rounded to bf16 between
+ * layers), on the same two paths: the fused kernel for the shapes above, one
+ * wide-GEMM launch per layer otherwise.
+ */
+int gp_nerf_full_dtype_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb, const void* x,
+                           const void* d, const void* const* w, const void* const* b, int rgb_act, void* out_r,
+                           void* out_rgb, int dtype, void* stream);
+
+/*
  * gp_nerf_full_out without any allocation: no reference counterpart.  For
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  Same arguments and

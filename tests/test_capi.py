@@ -82,8 +82,8 @@ def test_dtype_entry_validates_like_the_fp16_call():
 
 
 def test_wide_dtype_entry_points_reject_before_any_device_call():
-    """gp_gemm_dtype_out, gp_bert_ffn_dtype_out and gp_bert_addln_ffn_dtype_out:
-    unknown dtypes, bf16 on the queue-chained bert_addln layout, and the fp16
+    """gp_gemm_dtype_out, gp_bert_ffn_dtype_out, gp_bert_addln_ffn_dtype_out and
+    gp_nerf_full_dtype_out: unknown dtypes, bf16 on the queue-chained bert_addln layout, and the fp16
     calls' own shape checks all fail before touching a device."""
     vp = ctypes.c_void_p
     L = gpipes.lib
@@ -96,7 +96,12 @@ def test_wide_dtype_entry_points_reject_before_any_device_call():
     args12 = [vp(16)] * 12
     assert L.gp_bert_addln_ffn_dtype_out(16, 128, 512, *args12, 1e-5, 1, vp(16), 1, 1, None) == -1  # bf16 + pipelined
     assert L.gp_bert_addln_ffn_dtype_out(16, 128, 512, *args12, 1e-5, 1, vp(16), 0, 3, None) == -1
+    w = (vp * 12)(*([16] * 12))
+    b = (vp * 12)()
+    assert L.gp_nerf_full_dtype_out(16, 64, 27, 1, 3, vp(16), vp(16), w, b, 3, vp(16), vp(16), 7, None) == -1
+    assert L.gp_nerf_full_dtype_out(16, 0, 27, 1, 3, vp(16), vp(16), w, b, 3, vp(16), vp(16), 1, None) == -2
     assert L.gp_last_error().decode() != ""
+    assert L.gp_nerf_full_dtype_out(0, 64, 27, 1, 3, None, None, w, b, 3, None, None, 1, None) == 0
 
 
 def test_fullmlp_requires_affine():

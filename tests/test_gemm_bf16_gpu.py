@@ -1,6 +1,7 @@
-"""GPU parity of the bf16 forms of the wide GEMM stage, the BERT FFN block and
-the fused bert_addln_ffn chain (gp_gemm_dtype_out, gp_bert_ffn_dtype_out,
-gp_bert_addln_ffn_dtype_out; the Python mirrors follow the tensors' dtype).
+"""GPU parity of the bf16 forms of the wide GEMM stage, the BERT FFN block, the
+fused bert_addln_ffn chain, the MLP chains and the NeRF MLP (gp_gemm_dtype_out,
+gp_bert_ffn_dtype_out, gp_bert_addln_ffn_dtype_out, gp_mlp_dtype_out,
+gp_nerf_full_dtype_out; the Python mirrors follow the tensors' dtype).
 
 The oracle is the same fp32 restatement, run on the bf16 values (exact in
 fp32).  The bar is the fp16 bar scaled by the ratio of the unit roundoffs,
@@ -18,7 +19,7 @@ import torch
 import gpipes
 import oracle
 from conftest import load_golden
-from gpipes.synth import bert_addln_params, bert_params, normal_fp16
+from gpipes.synth import bert_addln_params, bert_params, nerf_inputs, nerf_params, normal_fp16
 
 pytestmark = pytest.mark.gpu
 
@@ -176,3 +177,56 @@ def test_mlp_bf16_vs_oracle(cuda, widths, acts):
     assert y.dtype == BF
     want = oracle.mlp(f(x), [f(w) for w in ws], [f(b) for b in bs], [ACT_ID[a] for a in acts])
     assert_bf16_parity(f(y), want, f"mlp bf16 {widths}")
+
+
+# ------------------------------------------------------------------ NeRF MLP
+def nerf_bf16(M, Kx, Kd, Na, Nrgb, seed, cuda):
+    """Parameters at 2x the default init (outputs of order 1 through all twelve
+    layers) and the positional-encoding inputs, cut or zero-padded to Kx / Kd."""
+    ws, bs = nerf_params(Kx, Kd, Na, Nrgb, seed=seed, zero_pad_rows=None)
+    ws = [(w.float() * 2).to(BF).to(cuda) for w in ws]
+    bs = [(b.float() * 2).to(BF).to(cuda) for b in bs]
+    x0, d0 = nerf_inputs(M, seed=seed)
+    x = torch.zeros((M, Kx))
+    x[:, :min(Kx, 63)] = x0[:, :min(Kx, 63)].float()
+    d = torch.zeros((M, Kd))
+    d[:, :min(Kd, 27)] = d0[:, :min(Kd, 27)].float()
+    return x.to(BF).to(cuda), d.to(BF).to(cuda), ws, bs
+
+
+@pytest.mark.parametrize("Kx,Kd,Na,Nrgb,act", [
+    (64, 27, 1, 3, "sigmoid"),   # the NeRF workload's widths (fused kernel)
+    (64, 32, 64, 64, "none"),    # the reference app's padded widths (fused kernel)
+    (63, 27, 4, 3, "sigmoid"),   # odd widths: rows copied to 16-byte aligned bases first
+    (72, 27, 1, 3, "sigmoid"),   # x wider than 64: one GEMM launch per layer
+    (64, 27, 65, 3, "none"),     # density head wider than 64: likewise
+])
+@pytest.mark.parametrize("M", [257, 4099])
+def test_nerf_bf16_vs_oracle(cuda, Kx, Kd, Na, Nrgb, act, M):
+    """gp_nerf_full_dtype_out on both of its paths against the oracle on the bf16 values."""
+    print(f"[bf16 nerf] M={M} Kx={Kx} Kd={Kd} Na={Na} Nrgb={Nrgb} {act}", flush=True)
+    x, d, ws, bs = nerf_bf16(M, Kx, Kd, Na, Nrgb, M + Kx, cuda)
+    wb = [t for pair in zip(ws, bs) for t in pair]
+    a, r = gpipes.nerf_full(x, d, *wb, rgb_act=act)
+    assert a.dtype == BF and r.dtype == BF
+    wa, wr = oracle.nerf(f(x), f(d), [f(w) for w in ws], [f(b) for b in bs], ACT_ID[act])
+    assert_bf16_parity(f(a), wa, f"nerf alpha bf16 M={M} Kx={Kx} Na={Na}")
+    assert_bf16_parity(f(r), wr, f"nerf rgb bf16 M={M} Kx={Kx} Nrgb={Nrgb}")
+
+
+def test_nerf_bf16_agrees_with_fp16_and_slices(cuda):
+    """The same bf16 values through both element types of the fused kernel agree
+    within the bf16 bar; a row slice of the batch (tiles at other offsets)
+    reproduces its rows bit for bit."""
+    M = 70000
+    x, d, ws, bs = nerf_bf16(M, 64, 27, 1, 3, 11, cuda)
+    wb = [t for pair in zip(ws, bs) for t in pair]
+    a, r = gpipes.nerf_full(x, d, *wb, rgb_act="sigmoid")
+    h = lambda t: t.to(torch.float16)  # noqa: E731
+    ah, rh = gpipes.nerf_full(h(x), h(d), *[h(t) for t in wb], rgb_act="sigmoid")
+    assert_bf16_parity(f(a), f(ah), "nerf alpha bf16 against fp16")
+    assert_bf16_parity(f(r), f(rh), "nerf rgb bf16 against fp16")
+    sa, sr = gpipes.nerf_full(x[1000:5000].contiguous(), d[1000:5000].contiguous(), *wb, rgb_act="sigmoid")
+    assert torch.equal(sa.view(torch.int16), a[1000:5000].view(torch.int16))
+    assert torch.equal(sr.view(torch.int16), r[1000:5000].view(torch.int16))
+    assert ((r.float() >= 0) & (r.float() <= 1)).all()
