@@ -379,8 +379,6 @@ def bench_chain(args):
     dev = torch.device("cuda:0")
     # element type of every tensor: the fp16 values drawn below, rounded to bf16 for --dtype bf16
     et = torch.bfloat16 if args.dtype == "bf16" else torch.float16
-    if args.dtype == "bf16" and args.workload == "nerf_a":
-        raise SystemExit("the nerf_a workload runs in f16 only")
     if args.workload == "dlrm":
         M = 262144
         wb, bb = dlrm_params(DLRM_BOT, seed=0)
@@ -423,10 +421,12 @@ def bench_chain(args):
     elif args.workload == "nerf_a":
         M, Kx = NERF_A["M"], NERF_A["Kx"]
         ws, bs = nerf_a_params(Kx, seed=0, device=dev)
-        x = normal_fp16(M, Kx, seed=0, device=dev)
-        out = torch.empty((M, 256), dtype=torch.float16, device=dev)
-        wb = [t for pair in zip(ws, bs) for t in pair]
+        x = normal_fp16(M, Kx, seed=0, device=dev, dtype=et)
+        out = torch.empty((M, 256), dtype=et, device=dev)
+        wb = [t.to(et) for pair in zip(ws, bs) for t in pair]
         impl = "pipelined" if args.impl == "pipelined" else "fused"
+        if et == torch.bfloat16 and impl == "pipelined":
+            raise SystemExit("the pipelined nerf_a layout runs in f16 only")
 
         def step(i):
             gpipes.nerf_a_out(x, *wb, out, impl=impl)
@@ -515,8 +515,8 @@ def main():
                          "engine clock swings for tens of ms after a burst starts (launches run fast, then "
                          "up to 1.5x slower, then settle), so the timed region starts in the steady state")
     ap.add_argument("--dtype", choices=["f16", "bf16"], default="f16",
-                    help="element type of every workload but nerf_a (bf16: the fused / wide-GEMM kernels, not the "
-                         "headline line)")
+                    help="element type of every tensor (bf16: the fused / wide-GEMM kernels only, not the headline "
+                         "line)")
     ap.add_argument("--eager", action="store_true",
                     help="MGN fused workloads: time the steps as eager calls only (by default `value` comes "
                          "from the same steps submitted as one HIP graph; the per-launch roofline times "

@@ -371,9 +371,10 @@ int gp_nerf_full_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb
   return gp_nerf_full_dtype_out(M, Kx, Kd, Na, Nrgb, x, d, w, b, rgb_act, out_r, out_rgb, GP_DTYPE_F16, stream);
 }
 
-int gp_nerf_a_out(int64_t M, int64_t Kx, const void* x, const void* const* w, const void* const* b, void* out, int impl,
-                  void* stream) {
+int gp_nerf_a_dtype_out(int64_t M, int64_t Kx, const void* x, const void* const* w, const void* const* b, void* out,
+                        int impl, int dtype, void* stream) {
   clear_error();
+  if (dtype != GP_DTYPE_F16 && dtype != GP_DTYPE_BF16) return fail(GP_ERR_INVALID_ARG, "unknown dtype %d", dtype);
   int rc = common_checks(M, x, out);
   if (rc) return rc;
   if (!w || !b) return fail(GP_ERR_INVALID_ARG, "w and b must be non-NULL");
@@ -381,6 +382,8 @@ int gp_nerf_a_out(int64_t M, int64_t Kx, const void* x, const void* const* w, co
   for (int i = 0; i < 8; ++i)
     if (!w[i]) return fail(GP_ERR_INVALID_ARG, "weight %d is NULL", i + 1);
   if (impl != GP_IMPL_FUSED && impl != GP_IMPL_PIPELINED) return fail(GP_ERR_INVALID_ARG, "unknown impl %d", impl);
+  if (impl == GP_IMPL_PIPELINED && dtype != GP_DTYPE_F16)
+    return fail(GP_ERR_INVALID_ARG, "the queue-chained NerfA layout runs in fp16 only");
   if (M == 0) return GP_OK;
   int dev = 0, ncu = 0;
   if ((rc = current_device_info(&dev, &ncu))) return rc;
@@ -438,17 +441,23 @@ int gp_nerf_a_out(int64_t M, int64_t Kx, const void* x, const void* const* w, co
     hipError_t e = place_launch(rows, row_ptr(x, r0, Kx), Kx, Kx, xb, kx, kx, GP_ACT_NONE, ncu, s);
     if (e == hipSuccess) e = place_launch(rows, row_ptr(x, r0, Kx), Kx, Kx, c1 + H * 2, cat1, cat1 - H, GP_ACT_NONE,
                                           ncu, s);
-    if (e == hipSuccess) e = layer(L[0], rows, xb, kx, h0, H, ncu, s);
-    if (e == hipSuccess) e = layer(L[1], rows, h0, H, h1, H, ncu, s);
-    if (e == hipSuccess) e = layer(L[2], rows, h1, H, h0, H, ncu, s);
-    if (e == hipSuccess) e = layer(L[3], rows, h0, H, h1, H, ncu, s);
-    if (e == hipSuccess) e = layer(L[4], rows, h1, H, c1, cat1, ncu, s);  // h5 -> first 256 columns of [h5 | x]
-    if (e == hipSuccess) e = layer(L[5], rows, c1, cat1, h0, H, ncu, s);
-    if (e == hipSuccess) e = layer(L[6], rows, h0, H, h1, H, ncu, s);
-    if (e == hipSuccess) e = layer(L[7], rows, h1, H, (void*)row_ptr(out, r0, H), H, ncu, s);
+    if (e == hipSuccess) e = layer(L[0], rows, xb, kx, h0, H, ncu, s, 0, dtype);
+    if (e == hipSuccess) e = layer(L[1], rows, h0, H, h1, H, ncu, s, 0, dtype);
+    if (e == hipSuccess) e = layer(L[2], rows, h1, H, h0, H, ncu, s, 0, dtype);
+    if (e == hipSuccess) e = layer(L[3], rows, h0, H, h1, H, ncu, s, 0, dtype);
+    // h5 -> the first 256 columns of [h5 | x]
+    if (e == hipSuccess) e = layer(L[4], rows, h1, H, c1, cat1, ncu, s, 0, dtype);
+    if (e == hipSuccess) e = layer(L[5], rows, c1, cat1, h0, H, ncu, s, 0, dtype);
+    if (e == hipSuccess) e = layer(L[6], rows, h0, H, h1, H, ncu, s, 0, dtype);
+    if (e == hipSuccess) e = layer(L[7], rows, h1, H, (void*)row_ptr(out, r0, H), H, ncu, s, 0, dtype);
     if (e != hipSuccess) return fail_hip(e, "NerfA layer launch");
   }
   return GP_OK;
+}
+
+int gp_nerf_a_out(int64_t M, int64_t Kx, const void* x, const void* const* w, const void* const* b, void* out, int impl,
+                  void* stream) {
+  return gp_nerf_a_dtype_out(M, Kx, x, w, b, out, impl, GP_DTYPE_F16, stream);
 }
 
 int gp_nerf_full_out_noalloc(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb, const void* x,

@@ -99,6 +99,8 @@ def _load():
     L.gp_bert_addln_ffn_dtype_out.restype = i32
     L.gp_nerf_a_out.argtypes = [i64, i64, vp, vp, vp, vp, i32, vp]
     L.gp_nerf_a_out.restype = i32
+    L.gp_nerf_a_dtype_out.argtypes = [i64, i64, vp, vp, vp, vp, i32, i32, vp]
+    L.gp_nerf_a_dtype_out.restype = i32
     L.gp_nerf_full_out_noalloc.restype = i32
     for name in ("gp_mlp_out", "gp_dlrm_botmlp_out", "gp_dlrm_topmlp_out", "gp_nerf_full_out", "gp_gemm_out",
                  "gp_gemm_dtype_out", "gp_bert_ffn_out", "gp_bert_ffn_dtype_out", "gp_linear_out", "gp_linear_layer_norm_out", "gp_layer_norm_out", "gp_add_out",
@@ -593,25 +595,27 @@ def nerf_a_out(x, *wb_and_out, impl="fused"):
     the order of nerf_a_out (apps/nerf_a/pipelined/nerf_a_pl_ext.cu:24-76).  w1 [Kx, 256],
     w6 [256 + Kx, 256], the others [256, 256]; biases may be None; out [M, 256].  impl "fused"
     (one GEMM launch per layer) or "pipelined" (the reference's queue-chained layout, Kx a
-    multiple of 8 up to 128)."""
+    multiple of 8 up to 128).  Every tensor float16, or every tensor bfloat16 (fused impl only:
+    gp_nerf_a_dtype_out)."""
     if len(wb_and_out) != 17:
         raise RuntimeError("expected w1, b1, ..., w8, b8, out")
     ws, bs, out = list(wb_and_out[0:16:2]), list(wb_and_out[1:16:2]), wb_and_out[16]
-    _check_input("x", x)
+    dt = _dtype_of(x)
+    _check_input("x", x, dtype=dt)
     if x.dim() != 2:
         raise RuntimeError("x must be 2-D [M, Kx]")
     M, Kx = x.shape
     shapes = [(Kx, 256)] + [(256, 256)] * 4 + [(256 + Kx, 256), (256, 256), (256, 256)]
     for i, (w, b, shp) in enumerate(zip(ws, bs, shapes)):
-        _check_input(f"w{i + 1}", w, shp)
-        _opt(f"b{i + 1}", b, (256,))
-    _check_input("out", out, (M, 256))
+        _check_input(f"w{i + 1}", w, shp, dt)
+        _opt(f"b{i + 1}", b, (256,), dt)
+    _check_input("out", out, (M, 256), dt)
     _same_device(x, out, *ws, *bs)
     wp = (ctypes.c_void_p * 8)(*[w.data_ptr() for w in ws])
     bp = (ctypes.c_void_p * 8)(*[0 if b is None else b.data_ptr() for b in bs])
     impl_id = _IMPLS.get(impl, impl)
     with torch.cuda.device(x.device):
-        _check(lib.gp_nerf_a_out(M, Kx, _ptr(x), wp, bp, _ptr(out), int(impl_id), _stream(x)))
+        _check(lib.gp_nerf_a_dtype_out(M, Kx, _ptr(x), wp, bp, _ptr(out), int(impl_id), _DTYPES[dt], _stream(x)))
     return out
 
 

@@ -214,6 +214,15 @@ int gp_nerf_a_out(int64_t M, int64_t Kx, const void* x, const void* const* w, co
                   int impl, void* stream);
 
 /*
+ * gp_nerf_a_out with the element type as an argument: no counterpart in the
+ * reference (fp16 only).  GP_DTYPE_BF16 takes x, every weight and bias and
+ * out as bf16 on the GEMM chain (impl GP_IMPL_FUSED); GP_IMPL_PIPELINED with
+ * bf16 returns GP_ERR_INVALID_ARG.
+ */
+int gp_nerf_a_dtype_out(int64_t M, int64_t Kx, const void* x, const void* const* w, const void* const* b, void* out,
+                        int impl, int dtype, void* stream);
+
+/*
  * Dense MLP chain: widths[0] -> widths[1] -> ... -> widths[nlayers], layer i
  * out = act_i(in . w[i] + b[i]) with w[i] [widths[i], widths[i+1]] (fp16,
  * weight.t()), b[i] [widths[i+1]] or NULL, acts[i] one of GP_ACT_*.  Any

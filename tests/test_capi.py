@@ -82,8 +82,8 @@ def test_dtype_entry_validates_like_the_fp16_call():
 
 
 def test_wide_dtype_entry_points_reject_before_any_device_call():
-    """gp_gemm_dtype_out, gp_bert_ffn_dtype_out, gp_bert_addln_ffn_dtype_out and
-    gp_nerf_full_dtype_out: unknown dtypes, bf16 on the queue-chained bert_addln layout, and the fp16
+    """gp_gemm_dtype_out, gp_bert_ffn_dtype_out, gp_bert_addln_ffn_dtype_out,
+    gp_nerf_full_dtype_out and gp_nerf_a_dtype_out: unknown dtypes, bf16 on the queue-chained bert_addln layout, and the fp16
     calls' own shape checks all fail before touching a device."""
     vp = ctypes.c_void_p
     L = gpipes.lib
@@ -102,6 +102,11 @@ def test_wide_dtype_entry_points_reject_before_any_device_call():
     assert L.gp_nerf_full_dtype_out(16, 0, 27, 1, 3, vp(16), vp(16), w, b, 3, vp(16), vp(16), 1, None) == -2
     assert L.gp_last_error().decode() != ""
     assert L.gp_nerf_full_dtype_out(0, 64, 27, 1, 3, None, None, w, b, 3, None, None, 1, None) == 0
+    w8 = (vp * 8)(*([16] * 8))
+    b8 = (vp * 8)()
+    assert L.gp_nerf_a_dtype_out(16, 64, vp(16), w8, b8, vp(16), 0, 9, None) == -1
+    assert L.gp_nerf_a_dtype_out(16, 64, vp(16), w8, b8, vp(16), 1, 1, None) == -1  # bf16 + pipelined
+    assert L.gp_nerf_a_dtype_out(0, 64, None, w8, b8, None, 0, 1, None) == 0
 
 
 def test_fullmlp_requires_affine():

@@ -1,7 +1,8 @@
 """GPU parity of the bf16 forms of the wide GEMM stage, the BERT FFN block, the
-fused bert_addln_ffn chain, the MLP chains and the NeRF MLP (gp_gemm_dtype_out,
-gp_bert_ffn_dtype_out, gp_bert_addln_ffn_dtype_out, gp_mlp_dtype_out,
-gp_nerf_full_dtype_out; the Python mirrors follow the tensors' dtype).
+fused bert_addln_ffn chain, the MLP chains, the NeRF MLP and the NerfA trunk
+(gp_gemm_dtype_out, gp_bert_ffn_dtype_out, gp_bert_addln_ffn_dtype_out,
+gp_mlp_dtype_out, gp_nerf_full_dtype_out, gp_nerf_a_dtype_out; the Python
+mirrors follow the tensors' dtype).
 
 The oracle is the same fp32 restatement, run on the bf16 values (exact in
 fp32).  The bar is the fp16 bar scaled by the ratio of the unit roundoffs,
@@ -19,7 +20,7 @@ import torch
 import gpipes
 import oracle
 from conftest import load_golden
-from gpipes.synth import bert_addln_params, bert_params, nerf_inputs, nerf_params, normal_fp16
+from gpipes.synth import bert_addln_params, bert_params, nerf_a_params, nerf_inputs, nerf_params, normal_fp16
 
 pytestmark = pytest.mark.gpu
 
@@ -230,3 +231,22 @@ def test_nerf_bf16_agrees_with_fp16_and_slices(cuda):
     assert torch.equal(sa.view(torch.int16), a[1000:5000].view(torch.int16))
     assert torch.equal(sr.view(torch.int16), r[1000:5000].view(torch.int16))
     assert ((r.float() >= 0) & (r.float() <= 1)).all()
+
+
+# ------------------------------------------------------------------ NerfA trunk
+@pytest.mark.parametrize("Kx,M", [(64, 300), (60, 4099), (72, 1000)])
+def test_nerf_a_bf16_vs_oracle(cuda, Kx, M):
+    """gp_nerf_a_dtype_out on the GEMM chain (the app's width, an unaligned one,
+    one wider than a k-block) against the oracle on the bf16 values; weights at
+    2x the default init keep every layer's signal visible."""
+    ws, bs = nerf_a_params(Kx, seed=M + Kx)
+    ws = [(w.float() * 2).to(BF).to(cuda) for w in ws]
+    bs = [(b.float() * 2).to(BF).to(cuda) for b in bs]
+    x = normal_fp16(M, Kx, seed=M, device=cuda, dtype=BF)
+    wb = [t for pair in zip(ws, bs) for t in pair]
+    y = gpipes.nerf_a(x, *wb)
+    assert y.dtype == BF
+    want = oracle.nerf_a(f(x), [f(w) for w in ws], [f(b) for b in bs])
+    assert_bf16_parity(f(y), want, f"nerf_a bf16 Kx={Kx} M={M}")
+    with pytest.raises(gpipes.GpipesError):
+        gpipes.nerf_a(x, *wb, impl="pipelined")
