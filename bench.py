@@ -459,8 +459,8 @@ def bench_chain(args):
               "nerf": "one step: the weight-packing kernel, then the fused 12-layer kernel over 256-row tiles",
               "bert_addln": "one step: one gp_bert_addln_ffn_out call (fused: weight transposes, then GEMM0 + b0 + x, "
                             "LN0, GEMM1 + act, GEMM2 + b2 + h0, LN2; pipelined: one queue-chained kernel)",
-              "nerf_a": "one step: one gp_nerf_a_out call (fused: weight preparation, input placement and eight "
-                        "GEMM launches; pipelined: one queue-chained kernel)"}
+              "nerf_a": "one step: one gp_nerf_a_out call (fused: the weight-packing kernel, then the NeRF kernel "
+                        "stopped after layer 8; pipelined: one queue-chained kernel)"}
 
     call_ms, ms_per_step, settle = timed_steps(step, args, dev)
     avg_ms = sum(call_ms) / len(call_ms)

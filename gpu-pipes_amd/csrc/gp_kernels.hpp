@@ -186,6 +186,12 @@ size_t nerf_fused_workspace();
 hipError_t nerf_fused_launch(int64_t M, int Kx, int Kd, int Na, int Nrgb, const void* x, const void* d,
                              const void* const* w, const void* const* b, int rgb_act, void* out_r, void* out_rgb,
                              void* ws, int num_cus, hipStream_t stream, int dtype = GP_DTYPE_F16);
+// NerfA (apps/nerf_a/torch/model.py:5-38): the same kernel stopped after
+// layer 8, out [M, 256] = the trunk's ReLU output; Kx <= 64, x 16-byte
+// aligned, w[0..7] / b[0..7], workspace as above.
+inline bool nerf_trunk_supported(int64_t Kx) { return Kx >= 1 && Kx <= 64; }
+hipError_t nerf_trunk_launch(int64_t M, int Kx, const void* x, const void* const* w, const void* const* b, void* out,
+                             void* ws, int num_cus, hipStream_t stream, int dtype = GP_DTYPE_F16);
 // Device address and size of the NeRF kernel's static scratch on device `dev`
 // (the current device), for the allocation-free entry point.
 int nerf_static_scratch(int dev, void** ptr, size_t* bytes);

@@ -400,7 +400,27 @@ int gp_nerf_a_dtype_out(int64_t M, int64_t Kx, const void* x, const void* const*
     return nerf_a_pipelined_run(a, dev, ncu, s);
   }
 
-  // Chain: one wide-GEMM launch per layer (apps/nerf_a/torch/model.py:5-38):
+  if (nerf_trunk_supported(Kx) && M <= (int64_t(1) << 31) - 1) {
+    // The NeRF kernel's trunk: all eight layers of a 256-row tile in one
+    // kernel.  x rows that do not start 16-byte aligned are copied into the
+    // workspace first (as gp_nerf_full_out does), so results never depend on
+    // how the input is sliced.
+    const bool cx = !aligned16(x);
+    Carve cv;
+    const size_t o_st = cv.take(nerf_fused_workspace());
+    const size_t o_x = cx ? cv.take((size_t)M * Kx * 2) : 0;
+    char* ws = nullptr;
+    if ((rc = workspace_acquire(dev, s, cv.off, (void**)&ws))) return rc;
+    if (cx)
+      if (hipError_t e = hipMemcpyAsync(ws + o_x, x, (size_t)M * Kx * 2, hipMemcpyDeviceToDevice, s); e != hipSuccess)
+        return fail_hip(e, "NerfA input alignment copy");
+    if (hipError_t e = nerf_trunk_launch(M, (int)Kx, cx ? ws + o_x : x, w, b, out, ws + o_st, ncu, s, dtype);
+        e != hipSuccess)
+      return fail_hip(e, "NerfA fused kernel launch");
+    return GP_OK;
+  }
+
+  // Wider inputs: one wide-GEMM launch per layer (apps/nerf_a/torch/model.py:5-38):
   // 1: Kx -> 256, 2-5: 256 -> 256; 6: [h5 | x] -> 256; 7-8: 256 -> 256; ReLU after each.
   const int64_t H = 256;
   const int64_t kx = rup(Kx, 64), cat1 = rup(H + Kx, 64);

@@ -131,8 +131,12 @@ __device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&&
 }
 
 // E: F16 or BF16, the element type of x, d, the weights, biases and outputs.
-template <typename E>
+// TRUNK: only layers 1-8 (NerfA, apps/nerf_a/torch/model.py:5-38): the weight
+// stream ends before the density head, no d is read, and out_r receives the
+// trunk's ReLU output, [M][256].
+template <typename E, bool TRUNK = false>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void nerf_fused_kernel(Args p) {
+  constexpr int ST = TRUNK ? S_L9 : S_TOTAL;  // slots per tile
   __shared__ __attribute__((aligned(1024))) char smem[LDS_BYTES];
   GP_LDS char* const ring = (GP_LDS char*)smem;
   GP_LDS half_t* const bfrag = (GP_LDS half_t*)(smem + L_B);
@@ -178,10 +182,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   };
 
   // ---------------------------------------------------------------- ring
-  // Global slot q = k S_TOTAL + l (tile k, local slot l) lives in ring slot
+  // Global slot q = k ST + l (tile k, local slot l) lives in ring slot
   // q % NS.  `cur` is the ring slot of the last acquired slot; (iss_k, iss_l)
   // the next slot to copy, which goes to ring slot (cur + NS - 1) % NS.
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.stream, S_TOTAL * SLOT);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.stream, ST * SLOT);
   int cur = NS - 1, iss_k = 0, iss_l = 0;
   // Copy the next slot into ring slot `rs` (ring waves; chunk c = RW i + wave
   // is copy i).  Branch-free apart from the wave test, so that a slot's MFMAs
@@ -199,13 +203,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         dma16_buf_so(r, 16 * lane0, base + c * FRAG, dst + c * FRAG);
       }
     }
-    const bool wrap = ++iss_l == S_TOTAL;
+    const bool wrap = ++iss_l == ST;
     iss_l = wrap ? 0 : iss_l;
     iss_k += wrap ? 1 : 0;
   };
   // Order of the first copies: x and d of tile 0, then the ring.
   copy_input(0, true);
-  copy_input(0, false);
+  if constexpr (!TRUNK) copy_input(0, false);
   for (int i = 0; i < NS - 1; ++i) issue(i);
   // Acquire the next slot in stream order: a ring wave waits for its own
   // copies of it (the CPW (NS - 2) copies issued after them may still be in
@@ -390,6 +394,37 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         }
     };
 
+    // Trunk output (TRUNK): out[row][f] = ReLU(acc) for the layer-8
+    // accumulators, f = 32 fb + 8 g + 4 lh + e.  v_permlane32_swap trades
+    // groups g = 2q+1 of the lower half-wave for groups g = 2q of the upper
+    // one, so each lane holds eight consecutive features 32 fb + 16 q + 8 lh +
+    // (0..7) and one 16-byte store per lane writes 32 bytes of each of 32 rows.
+    auto epi_out = [&] {
+      const __amdgpu_buffer_rsrc_t ro = make_rsrc(p.out_r + r0 * 256, vrows * 256 * 2);
+      const int lane = opaque(lane0), lr = lane & 31, lh = lane >> 5;
+#pragma unroll
+      for (int fb = 0; fb < 8; ++fb)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          const int row = 32 * RB * wave + 32 * rb + lr;
+          u32x2 o[4];
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            f4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = __builtin_fmaxf(acc[fb][rb][4 * g + e], 0.f);
+            o[g] = __builtin_bit_cast(u32x2, E::cvt4(v));
+          }
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const auto lo = __builtin_amdgcn_permlane32_swap(o[2 * q][0], o[2 * q + 1][0], false, false);
+            const auto hi = __builtin_amdgcn_permlane32_swap(o[2 * q][1], o[2 * q + 1][1], false, false);
+            const u32x4 w = {(unsigned)lo[0], (unsigned)hi[0], (unsigned)lo[1], (unsigned)hi[1]};
+            buf_store_u4(ro, (row * 256 + 32 * fb + 16 * q + 8 * lh) * 2, w);
+          }
+        }
+    };
+
     // Slot program.  A slot is 4 groups of 4 fragments, read and multiplied
     // in turn; the next slot is acquired and its first group read right after
     // the last group's MFMAs are issued -- across layer boundaries too, where
@@ -440,7 +475,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     // Layer 1: x -> 256, ReLU.  The input waves wait for this tile's x copies
     // (this tile's d copies, issued after them, may still be in flight); the
     // acquire's barrier then publishes the x tile.
-    if (!ring_wave) wait_vmcnt<DCPW>();
+    if (!ring_wave) wait_vmcnt<TRUNK ? 0 : DCPW>();
     advance();
     take_input(true, p.Kx);
     bias_init(E8{}, BF_L1);
@@ -448,8 +483,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     epi_hidden(E8{}, true);
     // Layers 2-5, 7, 8 (ReLU) and 10 (bottleneck, linear): 256 -> 256.
     // Layer 6 ([h5 | x] -> 256) runs before 7, the density head before 10.
+    // The trunk stops after layer 8 (i = 5) and stores it.
+    constexpr int NI = TRUNK ? 6 : 7;
 #pragma nounroll
-    for (int i = 0; i < 7; ++i) {
+    for (int i = 0; i < NI; ++i) {
       if (i == 4) {
         take_input(true, p.Kx);
         bias_init(E8{}, BF_L6);
@@ -465,11 +502,17 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       }
       bias_init(E8{}, i < 4 ? BF_L2 + 512 * i : i < 6 ? BF_L7 + 512 * (i - 4) : BF_L10);
       // what follows is another 256 -> 256 layer, layer 6 or the density
-      // head; layer 11 is acquired after the input waves' wait below
+      // head; layer 11 is acquired after the input waves' wait below (the
+      // trunk's next tile after its own)
       run_layer(C3{}, C8{}, [&] {
-        if (i != 6) advance();
+        if (i != NI - 1) advance();
       });
+      if (TRUNK && i == NI - 1) break;
       epi_hidden(E8{}, i != 6);
+    }
+    if constexpr (TRUNK) {
+      epi_out();
+      continue;
     }
     // Layer 11 ([bottleneck | d] -> 128, ReLU): the input waves wait for this
     // tile's d copies (the next tile's x copies may still be in flight).
@@ -484,6 +527,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     run_layer(C28{}, C1{}, nothing);
     epi_head(BH_L12 - BF_END, p.out_rgb, p.Nrgb, p.rgb_act);
   }
+  // The ring and input copies issued past the last tile (empty ranges that
+  // still write zeros into dead LDS slots) land before the waves exit.
+  wait_vmcnt<0>();
 }
 
 // ------------------------------------------------------------------ packing
@@ -584,9 +630,11 @@ bool nerf_fused_supported(int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb) {
   return Kx >= 1 && Kx <= 64 && Kd >= 1 && Kd <= 32 && Na >= 1 && Na <= 64 && Nrgb >= 1 && Nrgb <= 64;
 }
 
-hipError_t nerf_fused_launch(int64_t M, int Kx, int Kd, int Na, int Nrgb, const void* x, const void* d,
-                             const void* const* w, const void* const* b, int rgb_act, void* out_r, void* out_rgb,
-                             void* ws, int num_cus, hipStream_t s, int dtype) {
+// Packs the weight stream and bias tables (all twelve layers, or the trunk's
+// first eight), then launches the fused kernel.
+static hipError_t fused_launch(bool trunk, int64_t M, int Kx, int Kd, int Na, int Nrgb, const void* x, const void* d,
+                               const void* const* w, const void* const* b, int rgb_act, void* out_r, void* out_rgb,
+                               void* ws, int num_cus, hipStream_t s, int dtype) {
   using namespace nerf;
   if (dtype != GP_DTYPE_F16 && dtype != GP_DTYPE_BF16) return hipErrorInvalidValue;
   if (M <= 0) return hipSuccess;
@@ -603,11 +651,13 @@ hipError_t nerf_fused_launch(int64_t M, int Kx, int Kd, int Na, int Nrgb, const 
       {S_L9, 2, 16, 0, 0, 0, Na, BH_L9, 1},            {S_L10, 8, 16, 0, 0, 0, H, BF_L10, 0},
       {S_L11, 4, 20, 4, Kd, H, 128, BF_L11, 0},        {S_L12, 2, 8, 0, 0, 0, Nrgb, BH_L12, 1},
   };
-  for (int i = 0; i < 12; ++i) {
+  const int nl = trunk ? 8 : 12;
+  for (int i = 0; i < nl; ++i) {
     const int* sh = shape[i];
     pa.L[i] = {(const half_t*)w[i], (const half_t*)b[i], sh[0], sh[1], sh[2], sh[3], sh[4], sh[5], sh[6], sh[7],
                sh[8]};
   }
+  // (The trunk's layers 9-12 stay zero: no slots, no bias entries.)
   pa.stream = (char*)ws;
   pa.bias = (half_t*)((char*)ws + (size_t)S_TOTAL * SLOT);
   const int nthreads = S_TOTAL * FPS * kWave + B_TOTAL;
@@ -617,12 +667,30 @@ hipError_t nerf_fused_launch(int64_t M, int Kx, int Kd, int Na, int Nrgb, const 
   const Args a{(const half_t*)x, (const half_t*)d, (const char*)ws, pa.bias, (half_t*)out_r, (half_t*)out_rgb,
                M, Kx, Kd, Na, Nrgb, rgb_act};
   const int64_t tiles = (M + ROWS - 1) / ROWS;
-  const int64_t grid = tiles < num_cus ? tiles : num_cus;
-  if (dtype == GP_DTYPE_BF16)
-    hipLaunchKernelGGL(nerf_fused_kernel<BF16>, dim3((unsigned)grid), dim3(NT), 0, s, a);
-  else
-    hipLaunchKernelGGL(nerf_fused_kernel<F16>, dim3((unsigned)grid), dim3(NT), 0, s, a);
+  const dim3 grid((unsigned)(tiles < num_cus ? tiles : num_cus));
+  if (trunk) {
+    if (dtype == GP_DTYPE_BF16)
+      hipLaunchKernelGGL((nerf_fused_kernel<BF16, true>), grid, dim3(NT), 0, s, a);
+    else
+      hipLaunchKernelGGL((nerf_fused_kernel<F16, true>), grid, dim3(NT), 0, s, a);
+  } else {
+    if (dtype == GP_DTYPE_BF16)
+      hipLaunchKernelGGL((nerf_fused_kernel<BF16, false>), grid, dim3(NT), 0, s, a);
+    else
+      hipLaunchKernelGGL((nerf_fused_kernel<F16, false>), grid, dim3(NT), 0, s, a);
+  }
   return hipGetLastError();
+}
+
+hipError_t nerf_fused_launch(int64_t M, int Kx, int Kd, int Na, int Nrgb, const void* x, const void* d,
+                             const void* const* w, const void* const* b, int rgb_act, void* out_r, void* out_rgb,
+                             void* ws, int num_cus, hipStream_t s, int dtype) {
+  return fused_launch(false, M, Kx, Kd, Na, Nrgb, x, d, w, b, rgb_act, out_r, out_rgb, ws, num_cus, s, dtype);
+}
+
+hipError_t nerf_trunk_launch(int64_t M, int Kx, const void* x, const void* const* w, const void* const* b, void* out,
+                             void* ws, int num_cus, hipStream_t s, int dtype) {
+  return fused_launch(true, M, Kx, 0, 0, 0, x, nullptr, w, b, GP_ACT_NONE, out, nullptr, ws, num_cus, s, dtype);
 }
 
 }  // namespace gp

@@ -594,7 +594,8 @@ def nerf_a_out(x, *wb_and_out, impl="fused"):
     """NerfA (apps/nerf_a/torch/model.py:5-38) into ``out``: arguments x, w1, b1, ..., w8, b8, out,
     the order of nerf_a_out (apps/nerf_a/pipelined/nerf_a_pl_ext.cu:24-76).  w1 [Kx, 256],
     w6 [256 + Kx, 256], the others [256, 256]; biases may be None; out [M, 256].  impl "fused"
-    (one GEMM launch per layer) or "pipelined" (the reference's queue-chained layout, Kx a
+    (the NeRF kernel's first eight layers for Kx <= 64, else one GEMM launch per layer) or
+    "pipelined" (the reference's queue-chained layout, Kx a
     multiple of 8 up to 128).  Every tensor float16, or every tensor bfloat16 (fused impl only:
     gp_nerf_a_dtype_out)."""
     if len(wb_and_out) != 17:

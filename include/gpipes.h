@@ -204,8 +204,10 @@ int gp_bert_addln_ffn_dtype_out(int64_t M, int64_t H, int64_t FF, const void* at
  *   h = ReLU chain of w1 [Kx,256], w2..w5 [256,256];  h = [h | x];
  *   out [M,256] = ReLU chain of w6 [256+Kx,256], w7, w8 [256,256].
  * x [M,Kx], Kx in [1, 1024] (the app's is 64); biases may be NULL.  impl
- * GP_IMPL_FUSED (0, the default) runs one wide-GEMM launch per layer over row
- * chunks; GP_IMPL_PIPELINED runs the reference's queue-chained layout
+ * GP_IMPL_FUSED (0, the default) runs, for Kx <= 64, the NeRF MLP's fused
+ * kernel stopped after layer 8 (x rows not 16-byte aligned are first copied
+ * into the workspace), and for wider inputs one wide-GEMM launch per layer
+ * over row chunks; GP_IMPL_PIPELINED runs the reference's queue-chained layout
  * (nerf_a_pl.cuh:97-179: stage workgroups linked by ring queues, the skip
  * concatenation a pipe_concat stage fed from a queue) for Kx a multiple of 8
  * up to 128, with failures reported by gp_pipeline_check.
@@ -216,8 +218,8 @@ int gp_nerf_a_out(int64_t M, int64_t Kx, const void* x, const void* const* w, co
 /*
  * gp_nerf_a_out with the element type as an argument: no counterpart in the
  * reference (fp16 only).  GP_DTYPE_BF16 takes x, every weight and bias and
- * out as bf16 on the GEMM chain (impl GP_IMPL_FUSED); GP_IMPL_PIPELINED with
- * bf16 returns GP_ERR_INVALID_ARG.
+ * out as bf16 on the default implementation (both of its paths);
+ * GP_IMPL_PIPELINED with bf16 returns GP_ERR_INVALID_ARG.
  */
 int gp_nerf_a_dtype_out(int64_t M, int64_t Kx, const void* x, const void* const* w, const void* const* b, void* out,
                         int impl, int dtype, void* stream);

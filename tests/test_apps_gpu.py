@@ -1,7 +1,8 @@
 """GPU parity of the bert_addln_ffn and nerf_a drop-ins against the CPU oracle.
 
 Both implementations of each are checked: the default one (one GEMM launch per
-layer with fused epilogues) and the reference's queue-chained layout
+layer with fused epilogues; for nerf_a with Kx <= 64 the NeRF kernel's trunk,
+all eight layers in one kernel) and the reference's queue-chained layout
 (GP_IMPL_PIPELINED), whose adds (bert_addln_ffn) and skip concatenation
 (nerf_a) are stages fed from ring queues.  Bar (fp16 I/O, fp32 accumulate):
 max-abs <= 2e-2 and relative-L2 <= 5e-3 against the fp32 oracle on identical
@@ -170,6 +171,38 @@ def test_nerf_a_no_bias_and_agreement(cuda):
     assert_parity(f32(b), want, "pipelined no bias")
     b2 = nerf_a_gpu(x, ws, nb, "pipelined")
     assert torch.equal(b.view(torch.int16), b2.view(torch.int16))
+
+
+def test_nerf_a_fused_kernel_matches_layer_chain(cuda):
+    """Kx <= 64 runs the NeRF kernel's trunk (one kernel for all eight layers),
+    wider inputs one GEMM launch per layer: the same network with x
+    zero-padded from 64 to 72 columns (zero weight rows for the padding) takes
+    the chain, and both agree with each other and with the oracle.  A row slice
+    at an odd, unaligned offset (copied to an aligned base first) and a
+    second stream reproduce the rows bit for bit."""
+    M = 70001
+    ws, bs = scaled(*nerf_a_params(64, seed=21, device=cuda), 2.0)
+    x = normal_fp16(M, 64, seed=22).to(cuda)
+    x72 = torch.zeros((M, 72), dtype=torch.float16, device=cuda)
+    x72[:, :64] = x
+    w72 = list(ws)
+    w72[0] = torch.cat([ws[0], torch.zeros((8, 256), dtype=torch.float16, device=cuda)])
+    w72[5] = torch.cat([ws[5], torch.zeros((8, 256), dtype=torch.float16, device=cuda)])
+    a = nerf_a_gpu(x, ws, bs, "fused")
+    c = nerf_a_gpu(x72, w72, bs, "fused")
+    assert_parity(f32(a), f32(c), "nerf_a fused kernel vs GEMM chain")
+    rows = np.r_[0:300, 65400:65700, M - 300:M]
+    assert_parity(f32(a)[rows], nerf_a_oracle(x, ws, bs, rows), "nerf_a fused kernel vs oracle")
+    buf = torch.empty(M * 64 + 1, dtype=torch.float16, device=cuda)
+    xs = buf[1:1 + 3001 * 64].view(3001, 64)
+    xs.copy_(x[997:3998])
+    s = nerf_a_gpu(xs, ws, bs, "fused")
+    assert torch.equal(s.view(torch.int16), a[997:3998].view(torch.int16))
+    st = torch.cuda.Stream(device=cuda)
+    with torch.cuda.stream(st):
+        a2 = nerf_a_gpu(x, ws, bs, "fused")
+    st.synchronize()
+    assert torch.equal(a2.view(torch.int16), a.view(torch.int16))
 
 
 def test_nerf_a_rejects(cuda):
