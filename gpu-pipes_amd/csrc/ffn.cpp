@@ -11,8 +11,9 @@
 // residual epilogue, and the LayerNorm stage -- the shape of the reference's
 // bulk-sync variant (apps/bert_ffn/bulksync/bert_ffn_bs.cuh:12-27) with the add
 // fused.  Rows are processed in chunks so the FF-wide activations of one chunk
-// (128 MB at 16384 x 4096) can stay in the 256 MB Infinity Cache between the
-// two GEMMs rather than make a round trip through HBM.
+// (at most 128 MiB: 16384 x 4096 at BERT-large width) can stay in the 256 MB
+// Infinity Cache between the two GEMMs rather than make a round trip through
+// HBM.
 #include <hip/hip_runtime.h>
 
 #include "../../include/gpipes.h"
@@ -24,9 +25,16 @@ namespace {
 
 constexpr int64_t kMaxDim = 16384;
 constexpr int64_t kMaxRows = (int64_t(1) << 31) - 1;  // GEMM tile indices are 32-bit
-// 16384 rows: GEMM1 has 1024 tiles and GEMM2 256 tiles per chunk at
-// BERT-large width, whole multiples of the 256 CUs.
-constexpr int64_t kFfnChunkRows = 16384;
+// Row chunks hold their FF-wide activations within kFfnChunkBytes (128 MiB,
+// half the Infinity Cache): 16384 rows at BERT-large width, where GEMM1 has
+// 1024 tiles and GEMM2 256 tiles per chunk, whole multiples of the 256 CUs.
+// Narrower blocks take more rows per chunk, hence fewer, fuller launches (the
+// bert_addln_ffn app's 32,768 rows at FF 512 are one chunk).
+constexpr int64_t kFfnChunkBytes = int64_t(128) << 20;
+int64_t ffn_chunk_rows(int64_t FF) {
+  const int64_t r = kFfnChunkBytes / (FF * 2) / 256 * 256;
+  return r < 256 ? 256 : r;
+}
 
 size_t round_up(size_t v) { return (v + 255) & ~size_t(255); }
 
@@ -87,12 +95,12 @@ struct LnEpilogue {
   }
 };
 
-// Rows per chunk of the FFN blocks: at most kFfnChunkRows, and with the
+// Rows per chunk of the FFN blocks: at most ffn_chunk_rows(FF), and with the
 // LayerNorm in the GEMM epilogue at most the rows whose tiles are all
 // resident at once.  0 when the epilogue cannot take the LayerNorm.
-int64_t ln_chunk_rows(int64_t H, int ncu) {
-  const int64_t r = gemm_ln_max_rows(H, ncu);
-  return r < 256 ? 0 : (r < kFfnChunkRows ? r : kFfnChunkRows);
+int64_t ln_chunk_rows(int64_t H, int64_t FF, int ncu) {
+  const int64_t r = gemm_ln_max_rows(H, ncu), c = ffn_chunk_rows(FF);
+  return r < 256 ? 0 : (r < c ? r : c);
 }
 
 }  // namespace
@@ -172,11 +180,11 @@ int gp_bert_ffn_dtype_out(int64_t M, int64_t H, int64_t FF, const void* x, const
   // in place), then one chunk of activations [CH][FF] and, when the
   // LayerNorm is a launch of its own, of pre-LayerNorm rows [CH][H].
   const bool inplace = weights_in_place(4.0 * M * H * FF);
-  const int64_t lnch = ln_chunk_rows(H, ncu);
+  const int64_t lnch = ln_chunk_rows(H, FF, ncu);
   const bool fuse_ln = lnch > 0;
   if (!fuse_ln && dtype != GP_DTYPE_F16)
     return fail(GP_ERR_SHAPE, "bf16 needs the LayerNorm in the GEMM epilogue, which this device's %d CUs cannot hold", ncu);
-  const int64_t chmax = fuse_ln ? lnch : kFfnChunkRows;
+  const int64_t chmax = fuse_ln ? lnch : ffn_chunk_rows(FF);
   const int64_t CH = M < chmax ? M : chmax;
   const size_t o_w2t = inplace ? 0 : round_up((size_t)FF * H * 2);
   const size_t o_act = o_w2t + (inplace ? 0 : round_up((size_t)FF * H * 2));
@@ -265,11 +273,11 @@ int gp_bert_addln_ffn_dtype_out(int64_t M, int64_t H, int64_t FF, const void* at
   // read the weights in place), then for one chunk the pre-LayerNorm rows
   // y [CH][H], h0 [CH][H] and the activations [CH][FF].
   const bool inplace = weights_in_place(2.0 * M * H * (H + 2.0 * FF));
-  const int64_t lnch = ln_chunk_rows(H, ncu);
+  const int64_t lnch = ln_chunk_rows(H, FF, ncu);
   const bool fuse_ln = lnch > 0;
   if (!fuse_ln && dtype != GP_DTYPE_F16)
     return fail(GP_ERR_SHAPE, "bf16 needs the LayerNorm in the GEMM epilogue, which this device's %d CUs cannot hold", ncu);
-  const int64_t chmax = fuse_ln ? lnch : kFfnChunkRows;
+  const int64_t chmax = fuse_ln ? lnch : ffn_chunk_rows(FF);
   const int64_t CH = M < chmax ? M : chmax;
   const size_t o_w1t = inplace ? 0 : round_up((size_t)H * H * 2);
   const size_t o_w2t = o_w1t + (inplace ? 0 : round_up((size_t)FF * H * 2));
