@@ -74,6 +74,7 @@ struct Cfg {
 };
 using Wide = Cfg<4, 4, 2>;    // 256 features x 256 rows
 using Narrow = Cfg<4, 2, 1>;  // 128 features x 256 rows
+using Short = Cfg<4, 1, 1>;   // 128 features x 128 rows: N = 128 LayerNorm launches of fewer rows than 256 per CU
 
 // Element types: F16 / BF16 (gp_device.hpp).
 
@@ -287,6 +288,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     for (int i = 0; i < nm; ++i) {
       if (i < nfr) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       if (i + nm < nfr) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // more reads than MFMAs: two per MFMA
+      if (i + 2 * nm < nfr) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // (three: Short tiles reading W in place)
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       if (i < nv) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
     }
@@ -317,7 +319,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   };
 
   constexpr int NFR = (BROW ? 2 : 1) * C::NBW + C::MBW;  // fragment reads per step
-  static_assert(NFR <= 2 * C::NBW * C::MBW, "reads are spread at most two per MFMA");
+  static_assert(NFR <= 3 * C::NBW * C::MBW, "reads are spread at most three per MFMA");
   Tile T = tile_at(t);
   prefetch(T);
 #pragma unroll
@@ -783,6 +785,9 @@ static hipError_t dispatch(const Args& g, int act, int ncu, hipStream_t s) {
 template <typename E>
 static hipError_t launch_typed(const GemmArgs& a, Args& g, bool brow, int num_cus, hipStream_t s) {
   if (a.ln) {
+    if (a.N == 128 && (a.M + Narrow::BM - 1) / Narrow::BM < num_cus)
+      return brow ? launch<Short, ACT_NONE, true, true, 1, E>(g, num_cus, s)
+                  : launch<Short, ACT_NONE, true, false, 1, E>(g, num_cus, s);
     if (a.N == 128) return brow ? launch<Narrow, ACT_NONE, true, true, 1, E>(g, num_cus, s)
                                 : launch<Narrow, ACT_NONE, true, false, 1, E>(g, num_cus, s);
     return brow ? launch<Wide, ACT_NONE, true, true, 2, E>(g, num_cus, s)

@@ -135,6 +135,22 @@ def test_bert_ffn_ln_exchange_reused_across_shapes(cuda):
         assert_parity(f(y)[rows], oracle_ffn(x[rows], q, "gelu_tanh", 1e-12), f"reused exchange M={M} H={width}")
 
 
+def test_bert_ffn_h128_tile_heights_agree(cuda):
+    """At H = 128 a launch with fewer than 256 rows per CU runs its GEMM2 +
+    LayerNorm on 128-row tiles, a larger one on 256-row tiles: the same
+    products in the same order per row, so the rows of a small call equal the
+    same rows of a large one bit for bit (both against the oracle too)."""
+    M = 80000
+    p = dev(bert_params(128, 512, seed=13, init="torch", affine_random=True), cuda)
+    x = normal_fp16(M, 128, seed=14, device=cuda)
+    big = ffn(x, p, "relu", 1e-5)
+    for r0, n in ((0, 300), (40000, 5000), (M - 1000, 1000)):
+        small = ffn(x[r0:r0 + n].contiguous(), p, "relu", 1e-5)
+        assert torch.equal(small.view(torch.int16), big[r0:r0 + n].view(torch.int16)), (r0, n)
+    rows = np.r_[0:100, 40000:40100, M - 100:M]
+    assert_parity(f(big)[rows], oracle_ffn(x[rows], p, "relu", 1e-5), "H 128, 256-row tiles")
+
+
 # ------------------------------------------------------------------ full size (config 2)
 def test_bert_large_full_size(cuda):
     """M = 65,536 (128 x 512 tokens), H 1024, FF 4096, GELU(tanh), eps 1e-12: four
