@@ -19,7 +19,7 @@
 //   FF-wide layer split by columns because a stage workgroup computes 128
 //   outputs.  The reference computes it in one 512-wide block.
 // * The W2 stage keeps all of W2 (K = 512) in registers.
-// * Not reproduced: the reference's dispatcher never
+// * Not reproduced (defects of the reference): its dispatcher never
 //   reaches ln0 (:227 subtracts where it should add), ln2 reads q3 instead of
 //   the queue of add1 (:167), and its extension passes be0 for be2 (_ext.cu:71).
 //   Here ln0 runs on add0's output, ln2 on add1's, each with its own affine.

@@ -15,7 +15,7 @@
 // tile whose columns past 256 + Kx load as zeros.  Layer 1 reads x the same
 // way, as a K = 128 tile of Kx valid columns.
 //
-// Not reproduced: the reference's first layer uses a
+// Not reproduced (a defect of the reference): its first layer uses a
 // K = 256 block shape on the 64-wide input (nerf_a_pl.cuh:108); here each
 // layer takes its real input width.
 //

@@ -472,8 +472,9 @@ def test_bert_addln_ffn_golden(name):
 @pytest.mark.parametrize("mutant", ["be0_for_be2", "ln0_skipped", "residual_x_not_h0", "no_attn_residual",
                                     "ln2_affine_swapped", "w0_transposed"])
 def test_bert_addln_ffn_rejects_planted_mistakes(mutant):
-    """Plausible mistakes (among them the reference extension's, SURVEY App. B item 6:
-    be0 passed for be2, ln0 never run) must fail the fixture at the parity bar."""
+    """Plausible mistakes (among them the reference extension's own defects,
+    bert_addln_ffn_pl_ext.cu:71 and bert_addln_ffn_pl.cuh:227: be0 passed for be2,
+    ln0 never run) must fail the fixture at the parity bar."""
     z = load_golden("bert_addln_ffn.npz")
     p, act, eps = _addln_args(z)
     a = dict(p)
