@@ -9,14 +9,16 @@ stream, the HBM traffic per launch measured with rocprofv3 counters
 host cores.
 
   python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--settle-ms 1000]
-                  [--workload edge|node|edge_gather|bert|dlrm|nerf]
+                  [--workload edge|node|edge_gather|bert|dlrm|nerf|bert_addln|nerf_a|queue]
                   [--impl fused|pipelined|pipelined_split_ln] [--no-cpu]
 
 Every line carries "spread": the per-launch HIP-event times of the timed
 region in launch order (min, median, max, and the means of the first and last
 five launches), so a clock ramp or a slow box shows in the line itself.
 --settle-ms runs untimed launches for that long between the warm-up and the
-timed region; the line states it in "settle".
+timed region, with no synchronisation between them, so the timed region starts
+while the GPU is busy; the line states it in "settle".  ms_per_step is the
+HIP-event time between the first and the last timed step divided by K.
 
 --workload bert times the BERT-large FFN block of configs[2] instead
 (LayerNorm(GELU(x W1 + b1) W2 + b2 + x), M = 65,536, H 1024, FF 4096): a step is
@@ -49,6 +51,10 @@ WORKLOADS = {
     "edge_gather": (1048576, 384, True),
 }
 GATHER_NODES = 262144
+WORKLOAD_METRIC = {
+    "node": "rows/sec + % HBM roofline, MGN node MLP M=262144 (1×MI355X)",
+    "edge_gather": "rows/sec + % HBM roofline, MGN edge MLP with gather front end M=1M (1×MI355X)",
+}
 BERT = {"M": 65536, "H": 1024, "FF": 4096, "eps": 1e-12}
 BERT_METRIC = "rows/sec + % fp16 MFMA peak, BERT-large FFN+residual+LN M=65536 (1×MI355X)"
 
@@ -175,46 +181,78 @@ def spread(ms):
             "first5_mean": sum(ms[:k]) / k, "last5_mean": sum(ms[-k:]) / k}
 
 
+class _Pacer:
+    """Keeps the launch queue busy but bounded: after every 16 enqueued steps
+    an event is recorded, and the host waits for the event recorded `depth`
+    steps earlier, so the GPU never drains and the host never runs more than
+    about `depth` steps ahead."""
+
+    def __init__(self, stream, depth=64):
+        self.stream, self.depth, self.marks, self.n = stream, depth, [], 0
+
+    def tick(self):
+        import torch
+
+        self.n += 1
+        if self.n % 16 == 0:
+            e = torch.cuda.Event()
+            e.record(self.stream)
+            self.marks.append(e)
+            if len(self.marks) > self.depth // 16:
+                self.marks.pop(0).synchronize()
+
+
+def _settle(run_one, stream, settle_ms):
+    """Untimed submissions for settle_ms, paced by _Pacer (no synchronisation,
+    so the timed region that follows starts while the GPU is still busy)."""
+    pacer = _Pacer(stream)
+    t0 = time.perf_counter()
+    n = 0
+    while (time.perf_counter() - t0) * 1e3 < settle_ms:
+        run_one(n)
+        pacer.tick()
+        n += 1
+    return {"ms": (time.perf_counter() - t0) * 1e3, "launches": n}
+
+
 def timed_steps(step, args, dev):
-    """Warm-up, optional settle, then the timed region.  step(i) enqueues step
-    i on torch's current stream (the stream every entry point launches on).
-    Each step is bracketed by HIP events recorded on that stream.  Returns
-    (per-step ms in launch order, wall ms per step, settle record)."""
+    """Warm-up and synchronise, then a settle phase and the timed region back
+    to back: the settle launches keep the GPU busy up to the first timed step,
+    so the timed region starts in the steady state with no idle gap (after an
+    idle gap the engine clock overshoots and the first launches run up to 1.5x
+    slower).  step(i) enqueues step i on torch's current stream, the stream
+    every entry point launches on.  The K timed steps are bracketed by HIP
+    events on that stream (outer events around all K, and a pair around each
+    step); the host synchronises after the last one.  Returns (per-step ms in
+    launch order, ms per step between the outer events, settle record)."""
     import torch
 
     stream = torch.cuda.current_stream(dev)
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    outer = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
     settle = {"ms": 0.0, "launches": 0}
     if args.settle_ms > 0:
-        t0 = time.perf_counter()
-        n = 0
-        while (time.perf_counter() - t0) * 1e3 < args.settle_ms:
-            for _ in range(16):
-                step(args.warmup + n)
-                n += 1
-            torch.cuda.synchronize()
-        settle = {"ms": (time.perf_counter() - t0) * 1e3, "launches": n}
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
+        settle = _settle(lambda n: step(args.warmup + n), stream, args.settle_ms)
+    outer[0].record(stream)
     for i in range(args.steps):
         ev[i][0].record(stream)
         step(i)
         ev[i][1].record(stream)
+    outer[1].record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    return [a.elapsed_time(b) for a, b in ev], wall * 1e3 / args.steps, settle
+    return [a.elapsed_time(b) for a, b in ev], outer[0].elapsed_time(outer[1]) / args.steps, settle
 
 
 def graph_steps(step, args, dev):
     """The timed steps submitted as one HIP graph: args.steps calls of step(i)
     captured once (torch.cuda.CUDAGraph on torch's capture stream, which every
     entry point launches on), replayed untimed for --settle-ms, then one timed
-    replay between synchronisations.  Only entry points that allocate nothing
-    can be captured (the fused MGN kernels).  Returns (wall ms per step,
-    settle record)."""
+    replay right behind them, bracketed by HIP events.  Only entry points that
+    allocate nothing can be captured (the fused MGN kernels).  Returns (ms per
+    step, settle record)."""
     import torch
 
     g = torch.cuda.CUDAGraph()
@@ -222,21 +260,17 @@ def graph_steps(step, args, dev):
         for i in range(args.steps):
             step(i)
     torch.cuda.synchronize()
-    settle = {"ms": 0.0, "replays": 0}
+    stream = torch.cuda.current_stream(dev)
+    settle = {"ms": 0.0, "launches": 0}
     if args.settle_ms > 0:
-        t0 = time.perf_counter()
-        n = 0
-        while (time.perf_counter() - t0) * 1e3 < args.settle_ms:
-            g.replay()
-            torch.cuda.synchronize()
-            n += 1
-        settle = {"ms": (time.perf_counter() - t0) * 1e3, "replays": n}
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
+        settle = _settle(lambda n: g.replay(), stream, args.settle_ms)
+        settle["launches"] *= args.steps
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
     g.replay()
+    e1.record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    return wall * 1e3 / args.steps, settle
+    return e0.elapsed_time(e1) / args.steps, settle
 
 
 def bench_bert(args):
@@ -493,6 +527,67 @@ def bench_chain(args):
     print(json.dumps(rec), flush=True)
 
 
+QUEUE_METRIC = "GB/s of queue hand-off (producer writes + consumer reads), 32 KiB tiles (1×MI355X)"
+# The reference's A100 figures for the same 32 KiB payload (charts/qperf.py:8-21, the 32 KB
+# row at :14; measured with misc_tests/pipeperf/pipeperf.cu:125-215): one queue, 54 queues.
+QUEUE_REF_A100 = {"1_queue_gbs": 20.56, "54_queues_gbs": 1011.64}
+
+
+def bench_queue(args):
+    """Queue hand-off bandwidth over the ring queue (gp_pipe_route, GP_ROUTE_HANDOFF): one
+    producer / consumer pair, then every pair the GPU holds.  A step moves T generated
+    128 x 128 fp16 tiles (32 KiB) producer -> two-slot queue -> consumer in every pipeline;
+    bandwidth counts the producer's writes and the consumer's reads, as the reference's
+    "Bandwidth Total" does (pipeperf.cu:203-211).  The checksums of every step's tiles are
+    checked against the closed form after the timed region."""
+    import numpy as np
+    import torch
+
+    import gpipes
+
+    dev = torch.device("cuda:0")
+    tile = 128 * 128 * 2
+    legs = {}
+    for name, pipes, tiles in (("single_queue", 1, 20000), ("all_queues", 0, 262144)):
+        M = tiles * 128
+        out = torch.zeros(tiles, dtype=torch.int32, device=dev)
+
+        def step(i, pipes=pipes, M=M, out=out):
+            gpipes.pipe_handoff(M, max_pipes=pipes, out=out)
+
+        call_ms, ms_per_step, settle = timed_steps(step, args, dev)
+        gpipes.pipeline_check()
+        ok = bool(np.array_equal(out.cpu().numpy().view(np.uint32), gpipes.handoff_checksums(M)))
+        if not ok:
+            raise SystemExit(f"hand-off checksums wrong ({name})")
+        avg = sum(call_ms) / len(call_ms)
+        legs[name] = {"tiles": tiles, "max_pipes": pipes, "kernel_ms_avg": avg, "ms_per_step": ms_per_step,
+                      "gbs": 2 * tiles * tile / (avg * 1e-3) / 1e9, "spread": spread(call_ms), "settle": settle,
+                      "checksums": "all tiles match"}
+    full = legs["all_queues"]
+    rec = {
+        "metric": QUEUE_METRIC,
+        "value": 2 * full["tiles"] * tile / (full["ms_per_step"] * 1e-3) / 1e9,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": full["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u32",
+        "data": "synthetic (generated tile payloads, per-tile checksums verified)",
+        "config": {"workload": "queue_handoff", "payload_bytes": tile, "queue_slots": 2,
+                   "route": "GP_ROUTE_HANDOFF", "tiles_per_step": full["tiles"]},
+        "legs": legs,
+        "reference_a100": QUEUE_REF_A100,
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(rec), flush=True)
+
+
 def load_traffic(workload, impl):
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
@@ -507,7 +602,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["bert", "dlrm", "nerf", "bert_addln", "nerf_a"],
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["bert", "dlrm", "nerf", "bert_addln", "nerf_a", "queue"],
                     default="edge")
     ap.add_argument("--impl", choices=["fused", "pipelined", "pipelined_split_ln"], default="fused")
     ap.add_argument("--settle-ms", type=float, default=1000.0,
@@ -518,9 +613,9 @@ def main():
                     help="element type of every tensor (bf16: the fused / wide-GEMM kernels only, not the headline "
                          "line)")
     ap.add_argument("--eager", action="store_true",
-                    help="MGN fused workloads: time the steps as eager calls only (by default `value` comes "
-                         "from the same steps submitted as one HIP graph; the per-launch roofline times "
-                         "are eager in both cases)")
+                    help="MGN fused workloads: time the steps as eager calls only (by default the same steps "
+                         "are also timed as one HIP graph replay and `value` comes from the faster of the "
+                         "two; the per-launch roofline times are eager in both cases)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-ref", action="store_true",
                     help="first run one plain 1 GiB device copy (a known-size reference kernel "
@@ -537,6 +632,9 @@ def main():
         return
     if args.workload in ("dlrm", "nerf", "bert_addln", "nerf_a"):
         bench_chain(args)
+        return
+    if args.workload == "queue":
+        bench_queue(args)
         return
 
     import torch
@@ -586,19 +684,19 @@ def main():
 
     launch_ms, eager_ms_per_step, settle = timed_steps(step, args, dev)
     avg_launch_ms = sum(launch_ms) / len(launch_ms)
-    # The fused kernels allocate nothing, so the same steps can be submitted
-    # as one HIP graph, which removes the host's per-call launch gaps.
-    use_graph = args.impl == "fused" and not args.eager
-    graph_settle = None
-    ms_per_step = eager_ms_per_step
-    if use_graph:
-        ms_per_step, graph_settle = graph_steps(step, args, dev)
+    # The fused kernels allocate nothing, so the same steps can also be
+    # submitted as one HIP graph; `value` comes from the faster submission.
+    graph_ms_per_step, graph_settle = None, None
+    if args.impl == "fused" and not args.eager:
+        graph_ms_per_step, graph_settle = graph_steps(step, args, dev)
+    use_graph = graph_ms_per_step is not None and graph_ms_per_step < eager_ms_per_step
+    ms_per_step = graph_ms_per_step if use_graph else eager_ms_per_step
     bytes_, flops = algorithmic(M, K, ln, GATHER_NODES if gather else 0)
     achieved_gbs = bytes_ / (avg_launch_ms * 1e-3) / 1e9
     tflops = flops / (avg_launch_ms * 1e-3) / 1e12
 
     rec = {
-        "metric": METRIC,
+        "metric": METRIC if args.workload == "edge" else WORKLOAD_METRIC[args.workload],
         "value": M / (ms_per_step * 1e-3),
         "unit": "rows/s",
         "n_gpus": 1,
@@ -616,7 +714,11 @@ def main():
                    "accumulate": "f32",
                    "submission": (f"one HIP graph of the {args.steps} timed calls" if use_graph
                                   else "eager calls from Python")},
+        "timing": "HIP events on the launch stream around the timed steps, which follow the settle "
+                  "submissions with no synchronisation in between; synchronised before the settle phase "
+                  "and after the last step; value from the faster of eager and graph submission",
         "eager_ms_per_step": eager_ms_per_step,
+        "graph_ms_per_step": graph_ms_per_step,
         "roofline": {
             "bound": "hbm", "achieved": achieved_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": load_traffic(args.workload, args.impl),

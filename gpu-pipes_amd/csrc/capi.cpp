@@ -231,10 +231,19 @@ int gp_pipe_ident(int64_t M, const void* x, void* out, int max_pipes, void* stre
 
 int gp_pipe_route(int64_t M, const void* x, void* out, void* out2, int route, int max_pipes, void* stream) {
   int dev = 0, ncu = 0;
-  if (route != GP_ROUTE_IDENT && route != GP_ROUTE_BROADCAST && route != GP_ROUTE_SPLIT && route != GP_ROUTE_DRAIN)
+  if (route != GP_ROUTE_IDENT && route != GP_ROUTE_BROADCAST && route != GP_ROUTE_SPLIT && route != GP_ROUTE_DRAIN &&
+      route != GP_ROUTE_HANDOFF)
     return fail(GP_ERR_INVALID_ARG, "unknown route %d", route);
+  if (route == GP_ROUTE_HANDOFF) {
+    clear_error();
+    if (x != nullptr) return fail(GP_ERR_INVALID_ARG, "the hand-off route takes no input (x must be NULL)");
+    if (M > 0 && out == nullptr) return fail(GP_ERR_INVALID_ARG, "out is NULL");
+    if ((uintptr_t)out % 4 != 0) return fail(GP_ERR_ALIGN, "out (uint32 checksums) must be 4-byte aligned");
+  }
   int rc = stage_prologue(M, &dev, &ncu);
   if (rc) return rc < 0 ? rc : GP_OK;
+  if (route == GP_ROUTE_HANDOFF)
+    return pipe_route_run(M, nullptr, out, nullptr, route, max_pipes, dev, ncu, (hipStream_t)stream);
   if ((rc = need(x, "x")) || (rc = need(out, "out"))) return rc;
   if (route == GP_ROUTE_BROADCAST && (rc = need(out2, "out2"))) return rc;
   return pipe_route_run(M, x, out, out2, route, max_pipes, dev, ncu, (hipStream_t)stream);

@@ -516,10 +516,11 @@ void mgn_fused_kernel(Params p) {
     __builtin_amdgcn_s_setprio(1);
 
     auto tile_b = [&](GP_LDS char* hand, int k) {
+      // layer 2 bias: its LDS reads overlap the hand-off wait
+      f16x acc0 = bias_frag(prm[1], fq), acc1 = acc0;
       lds_wait_geq((GP_LDS int*)&sy.h_full, 4 * (k + 1), ab, lim);
 
       // layer 2, features [32n, 32n+32) of all 64 rows, from the handoff tile
-      f16x acc0 = bias_frag(prm[1], fq), acc1 = acc0;
       gemm_2blk<E, D / 16, PF_L2, 4>(w2f, [&](int rb, int s) {
         return *(const GP_LDS h8*)(hand + (rb ? arow1 : arow0) + (2 * s + lh) * 16);
       }, acc0, acc1);
@@ -530,20 +531,22 @@ void mgn_fused_kernel(Params p) {
       store_relu_row<E>((GP_LDS char*)act2 + arow0, fq, acc0);
       store_relu_row<E>((GP_LDS char*)act2 + arow1, fq, acc1);
       lds_signal((GP_LDS int*)&sy.x2_full, lane);
+      // layer 3 bias (features 16fb + 4q4 + (0..3)): its reads overlap the exchange wait
+      f4 y[8];
+#pragma unroll
+      for (int fb = 0; fb < 8; ++fb) y[fb] = *(const f4*)&prm[2][16 * fb + 4 * q4];
       lds_wait_geq((GP_LDS int*)&sy.x2_full, 4 * (k + 1), ab, lim);
 
-      // layer 3, all features of rows [16n, 16n+16)
+      // layer 3, all features of rows [16n, 16n+16): eight independent
+      // accumulator chains, issued k-step-major so no MFMA waits on the one before
       h8 bf[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) bf[ks] = *(const GP_LDS h8*)((GP_LDS char*)act2 + xrow3 + (32 * ks + 8 * q4) * 2);
       lds_signal((GP_LDS int*)&sy.x2_free, lane);
-      f4 y[8];
 #pragma unroll
-      for (int fb = 0; fb < 8; ++fb) {
-        y[fb] = *(const f4*)&prm[2][16 * fb + 4 * q4];  // bias of features 16fb + 4q4 + (0..3)
+      for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) y[fb] = E::mma16(w3f[fb][ks], bf[ks], y[fb]);
-      }
+        for (int fb = 0; fb < 8; ++fb) y[fb] = E::mma16(w3f[fb][ks], bf[ks], y[fb]);
 
       const int64_t grow = (t0 + (int64_t)k * G) * TM + 16 * n + l16;
       half_t* const orow = p.out + grow * D;

@@ -115,6 +115,8 @@ __global__ __launch_bounds__(kStageThreads) void concat_kernel(const half_t* a, 
 //  * ROUTE_SPLIT (5 stages): x -> q0 -> 3 workers (SplitQueueReader, round
 //    robin) -> q1 (SplitQueueWriter, round robin) -> one reader in sequence
 //    order -> out, the split write of bert_addln_ffn_pl.cuh:121.
+//  * ROUTE_HANDOFF (2 stages): generated tiles -> q -> per-tile checksums,
+//    the queue benchmark of misc_tests/pipeperf/pipeperf.cu:125-215.
 // ---------------------------------------------------------------------------
 using RouteEntry = QueueEntry2D<MBLK, 128>;
 using IdentQueue = RingQueue<RouteEntry, 2>;
@@ -144,8 +146,42 @@ struct RouteArgs {
 };
 
 constexpr int route_stages(int route) {
-  return route == GP_ROUTE_IDENT ? 2 : (route == GP_ROUTE_SPLIT ? 2 + kSplitWorkers : 3);
+  return route == GP_ROUTE_IDENT || route == GP_ROUTE_HANDOFF ? 2 : (route == GP_ROUTE_SPLIT ? 2 + kSplitWorkers : 3);
 }
+
+// Hand-off benchmark payload: word i of tile t (row-major, 64 words per
+// 128-wide fp16 row) is (t * 0x9E3779B1) ^ (i * 0x85EBCA77).  Thread j
+// handles 16-byte chunks j, j + 256, ... (chunk q holds words 4q .. 4q+3 and
+// lies in row q / 16); only the tile's valid rows are written and summed.
+constexpr int kHandoffChunks = MBLK * 128 * 2 / 16;
+__device__ __forceinline__ void handoff_fill(const TensorView& v, int64_t t) {
+  const unsigned a = (unsigned)t * 0x9E3779B1u;
+  for (int q = threadIdx.x; q < v.rows * 16; q += kStageThreads) {
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = a ^ ((unsigned)(4 * q + e) * 0x85EBCA77u);
+    *(u32x4*)((char*)v.data + (int64_t)q * 16) = w;
+  }
+}
+// Sum mod 2^32 of the tile's valid words, returned to thread 0.
+__device__ __forceinline__ unsigned handoff_sum(const TensorView& v) {
+  __shared__ unsigned part[kStageThreads / kWave];
+  unsigned s = 0;
+  for (int q = threadIdx.x; q < v.rows * 16; q += kStageThreads) {
+    const u32x4 w = *(const u32x4*)((const char*)v.data + (int64_t)q * 16);
+    s += (w[0] + w[1]) + (w[2] + w[3]);
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) s += (unsigned)__shfl_xor((int)s, m);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+  __syncthreads();
+  unsigned tot = 0;
+  if (threadIdx.x == 0)
+    for (int w = 0; w < kStageThreads / kWave; ++w) tot += part[w];
+  __syncthreads();  // `part` is reused by the next tile
+  return tot;
+}
+static_assert(kHandoffChunks % kStageThreads == 0, "whole chunks per thread");
 
 template <int ROUTE>
 __global__ __launch_bounds__(kStageThreads) void route_kernel(RouteArgs a) {
@@ -170,6 +206,29 @@ __global__ __launch_bounds__(kStageThreads) void route_kernel(RouteArgs a) {
       QueueReader<IdentQueue> ir(&q->ident, &a.ctx);
       MemoryWriter ow((half_t*)a.out + g * C * tile, tile, 128);
       pipe_copy_n(ir, ow, nc, 128);
+    }
+  } else if constexpr (ROUTE == GP_ROUTE_HANDOFF) {
+    // misc_tests/pipeperf/pipeperf.cu:125-163: sender / receiver over one
+    // two-slot queue per pipeline, with generated payloads instead of the
+    // reference's per-thread 4-byte stores and loads.
+    if (r.stage == 0) {
+      QueueWriter<IdentQueue> ow(&q->ident, &a.ctx);
+      for (int i = 0; i < nt; ++i) {
+        const int64_t t = g + (int64_t)i * P;
+        const int64_t left = a.M - t * MBLK;
+        const TensorView c = ow.write_acquire((int)(left < MBLK ? left : MBLK));
+        handoff_fill(c, t);
+        ow.write_release();
+      }
+    } else {
+      QueueReader<IdentQueue> ir(&q->ident, &a.ctx);
+      for (int i = 0; i < nt; ++i) {
+        const TensorView v = ir.read_acquire();
+        const unsigned sum = handoff_sum(v);
+        ir.read_release();
+        // a tile whose wait ran out has no rows: its checksum is not written
+        if (threadIdx.x == 0 && v.rows > 0) ((unsigned*)a.out)[g + (int64_t)i * P] = sum;
+      }
     }
   } else if constexpr (ROUTE == GP_ROUTE_BROADCAST || ROUTE == GP_ROUTE_DRAIN) {
     if (r.stage == 0) {
@@ -467,6 +526,7 @@ int pipe_route_run(int64_t M, const void* x, void* out, void* out2, int route, i
     case GP_ROUTE_BROADCAST: return route_launch<GP_ROUTE_BROADCAST>(M, x, out, out2, max_pipes, dev, num_cus, s);
     case GP_ROUTE_SPLIT: return route_launch<GP_ROUTE_SPLIT>(M, x, out, out2, max_pipes, dev, num_cus, s);
     case GP_ROUTE_DRAIN: return route_launch<GP_ROUTE_DRAIN>(M, x, out, out2, max_pipes, dev, num_cus, s);
+    case GP_ROUTE_HANDOFF: return route_launch<GP_ROUTE_HANDOFF>(M, x, out, out2, max_pipes, dev, num_cus, s);
     default: return fail(GP_ERR_INVALID_ARG, "unknown route %d", route);
   }
 }

@@ -39,7 +39,7 @@ IMPL_PIPELINED = 1
 IMPL_PIPELINED_SPLIT_LN = 2
 _IMPLS = {"fused": IMPL_FUSED, "pipelined": IMPL_PIPELINED, "pipelined_split_ln": IMPL_PIPELINED_SPLIT_LN}
 ACTS = {"none": 0, "relu": 1, "gelu_tanh": 2, "sigmoid": 3}
-ROUTES = {"ident": 0, "broadcast": 1, "split": 2, "drain": 3}
+ROUTES = {"ident": 0, "broadcast": 1, "split": 2, "drain": 3, "handoff": 4}
 
 
 class GpipesError(RuntimeError):
@@ -338,6 +338,45 @@ def pipe_route(x, route="ident", max_pipes=0):
     with torch.cuda.device(x.device):
         _check(lib.gp_pipe_route(M, _ptr(x), _ptr(out), _ptr(out2), int(rid), int(max_pipes), _stream(x)))
     return out, out2
+
+
+def pipe_handoff(M, max_pipes=0, device=None, out=None):
+    """Queue hand-off benchmark (misc_tests/pipeperf/pipeperf.cu:125-163): ceil(M/128)
+    generated 128 x 128 fp16 tiles (32 KiB each) pass producer -> two-slot queue ->
+    consumer in every pipeline; returns the consumer's per-tile checksums as int32 (uint32
+    bit patterns; handoff_checksums gives the expected values)."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    T = (int(M) + 127) // 128
+    if out is None:
+        out = torch.zeros(max(T, 1), dtype=torch.int32, device=dev)
+    if out.dtype != torch.int32 or not out.is_cuda or out.numel() < T or not out.is_contiguous():
+        raise RuntimeError("out must be a contiguous int32 CUDA tensor of ceil(M / 128) elements")
+    with torch.cuda.device(out.device):
+        _check(lib.gp_pipe_route(int(M), None, _ptr(out), None, ROUTES["handoff"], int(max_pipes), _stream(out)))
+    return out
+
+
+def handoff_checksums(M):
+    """Expected gp_pipe_route(GP_ROUTE_HANDOFF) checksums (numpy uint32): tile t sums the
+    words (t * 0x9E3779B1) ^ (i * 0x85EBCA77), i < 64 * rows, modulo 2^32.  Bit b of the
+    sum of a ^ w_i over n words is 2^b times (n - c_b if bit b of a is set, else c_b), c_b
+    being how many w_i have bit b set."""
+    import numpy as np
+
+    T = (int(M) + 127) // 128
+    t = np.arange(T, dtype=np.uint64)
+    rows = np.minimum(128, int(M) - 128 * t.astype(np.int64))
+    a = (t * np.uint64(0x9E3779B1)) & np.uint64(0xFFFFFFFF)
+    bits = np.arange(32, dtype=np.uint64)
+    abit = ((a[:, None] >> bits[None, :]) & np.uint64(1)).astype(np.int64)       # [T, 32]
+    w = (np.arange(128 * 64, dtype=np.uint64) * np.uint64(0x85EBCA77)) & np.uint64(0xFFFFFFFF)
+    wbit = ((w[:, None] >> bits[None, :]) & np.uint64(1)).astype(np.int64)      # [8192, 32]
+    cum = np.cumsum(wbit, axis=0)                                               # set bits among w_0..w_i
+    n = 64 * rows
+    c = cum[n - 1]                                                              # [T, 32]
+    ones = np.where(abit == 1, n[:, None] - c, c)
+    total = (ones.astype(np.uint64) << bits[None, :]).sum(axis=1)                # < 2^46: no overflow
+    return (total & np.uint64(0xFFFFFFFF)).astype(np.uint32)
 
 
 def pipeline_check(device=None):

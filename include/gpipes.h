@@ -404,13 +404,23 @@ int gp_pipe_ident(int64_t M, const void* x, void* out, int max_pipes, void* stre
 #define GP_ROUTE_DRAIN 3     /* the broadcast with the second consumer discarding its tiles  */
                              /* (NullWriter; dummy_consumer, bert_addln_ffn_pl.cuh:178-187);  */
                              /* out2 is not written                                          */
+#define GP_ROUTE_HANDOFF 4   /* queue hand-off benchmark (misc_tests/pipeperf/pipeperf.cu:     */
+                             /* 125-163): a producer writes generated 128 x 128 fp16 tiles   */
+                             /* (32 KiB) into a two-slot queue, the consumer reads each tile */
+                             /* and folds it into a checksum; no HBM input.  x must be NULL, */
+                             /* out is uint32[ceil(M / 128)]: out[t] = the sum mod 2^32 of   */
+                             /* the words w = (t * 0x9E3779B1) ^ (i * 0x85EBCA77) of tile t, */
+                             /* i < 64 * rows (word i of the tile in row-major order, rows = */
+                             /* min(128, M - 128 t)); tiles t = g, g + P, ... go through     */
+                             /* pipeline g of P                                              */
 
 /*
  * Copy pipelines over the queue topologies the reference's apps use; out
  * (and out2 for GP_ROUTE_BROADCAST) must equal x bit for bit.  The exercise
  * of the queue library's multi-consumer and split reader / writer paths,
  * the striped input reader (GP_ROUTE_IDENT) and the null writer
- * (GP_ROUTE_DRAIN; out2 may then be NULL).
+ * (GP_ROUTE_DRAIN; out2 may then be NULL).  GP_ROUTE_HANDOFF times the
+ * queue itself: x is NULL and out receives per-tile checksums (see above).
  */
 int gp_pipe_route(int64_t M, const void* x, void* out, void* out2, int route, int max_pipes, void* stream);
 

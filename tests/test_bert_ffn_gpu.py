@@ -3,8 +3,8 @@
 
 Checked against the golden fixtures (torch.nn modules in float64) and the CPU
 oracle at the fp16 I/O bar (max-abs 2e-2, relative-L2 5e-3).  At the full
-BERT-large size (M = 65,536) the oracle checks a sample of rows, and two
-size-independent properties are asserted: every row is computed independently,
+BERT-large size (M = 65,536) the oracle checks every row, and two
+size-independent properties are asserted beside it: every row is computed independently,
 so the rows of a small batch are bit-identical to the same rows inside a large
 (chunked) batch; and with gamma = 1, beta = 0 every output row has mean 0 and
 variance var / (var + eps) of its pre-LayerNorm row (~1).
@@ -154,7 +154,7 @@ def test_bert_ffn_h128_tile_heights_agree(cuda):
 # ------------------------------------------------------------------ full size (config 2)
 def test_bert_large_full_size(cuda):
     """M = 65,536 (128 x 512 tokens), H 1024, FF 4096, GELU(tanh), eps 1e-12: four
-    16,384-row chunks.  Oracle on sampled rows (first, chunk edges, last), bit
+    16,384-row chunks.  Oracle on every row (about 2 s on the box's cores), bit
     identity of a small batch with the same rows of the large one, and the
     LayerNorm row statistics."""
     M, H, FF = 65536, 1024, 4096
@@ -162,8 +162,7 @@ def test_bert_large_full_size(cuda):
     x = normal_fp16(M, H, seed=0, device=cuda)
     y = ffn(x, p, "gelu_tanh", 1e-12)
     torch.cuda.synchronize()
-    rows = np.r_[0:64, 16320:16448, 32700:32800, M - 64:M]
-    assert_parity(f(y)[rows], oracle_ffn(x[rows], p, "gelu_tanh", 1e-12), "BERT-large sampled rows")
+    assert_parity(f(y), oracle_ffn(x, p, "gelu_tanh", 1e-12), f"BERT-large all {M} rows")
     small = ffn(x[:1000].contiguous(), p, "gelu_tanh", 1e-12)
     assert torch.equal(small.view(torch.int16), y[:1000].view(torch.int16))
     tail = ffn(x[16000:17000].contiguous(), p, "gelu_tanh", 1e-12)  # crosses a chunk edge in the big batch

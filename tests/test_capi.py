@@ -221,3 +221,29 @@ def test_nerf_argument_errors():
     assert L.gp_nerf_full_out(16, 64, 27, 1, 3, vp(16), vp(16), w11, b, 3, vp(16), vp(16), None) == -1
     assert L.gp_nerf_full_out(16, 64, 27, 1, 3, vp(16), vp(16), w, b, 7, vp(16), vp(16), None) == -1
     assert L.gp_nerf_full_out(0, 64, 27, 1, 3, None, None, w, b, 3, None, None, None) == 0
+
+
+def _handoff_brute(M):
+    import numpy as np
+    out = []
+    for t in range((M + 127) // 128):
+        rows, a = min(128, M - 128 * t), (t * 0x9E3779B1) & 0xFFFFFFFF
+        out.append(sum(a ^ ((i * 0x85EBCA77) & 0xFFFFFFFF) for i in range(64 * rows)) & 0xFFFFFFFF)
+    return np.array(out, dtype=np.uint32)
+
+
+@pytest.mark.parametrize("M", [1, 2, 127, 128, 129, 255, 1000])
+def test_handoff_checksums_closed_form(M):
+    """The per-bit counting form of the hand-off checksums equals the plain sum."""
+    import numpy as np
+    assert np.array_equal(gpipes.handoff_checksums(M), _handoff_brute(M))
+
+
+def test_handoff_route_argument_errors():
+    vp = ctypes.c_void_p
+    L = gpipes.lib
+    assert L.gp_pipe_route(256, vp(16), vp(16), None, 4, 0, None) == -1   # takes no input
+    assert L.gp_pipe_route(256, None, None, None, 4, 0, None) == -1       # no checksum buffer
+    assert L.gp_pipe_route(256, None, vp(18), None, 4, 0, None) == -3     # misaligned
+    assert L.gp_pipe_route(256, None, vp(16), None, 9, 0, None) == -1     # unknown route
+    assert L.gp_pipe_route(0, None, None, None, 4, 0, None) == 0          # empty: no-op

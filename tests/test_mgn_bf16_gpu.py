@@ -94,16 +94,13 @@ def test_nondefault_stream_and_repeat(cuda):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
 
 
-def test_full_size_sampled_and_invariants(cuda):
-    """Edge MLP at the headline size, M = 1,048,576, in bf16."""
+def test_full_size_all_rows_and_invariants(cuda):
+    """Edge MLP at the headline size, M = 1,048,576, in bf16; the oracle runs over every row."""
     M, K = 1048576, 384
     p = to_dev(mgn_params(K, seed=11, dtype=BF), cuda)
     x = normal_fp16(M, K, seed=12, device=cuda, dtype=BF)
     y = run_gpu(x, p)
-    g = np.random.default_rng(13)
-    idx = np.unique(np.concatenate([np.arange(100), np.arange(M - 100, M), g.integers(0, M, 4096)]))
-    ti = torch.from_numpy(idx).to(cuda)
-    assert_parity_bf16(y[ti].float().cpu().numpy(), run_oracle(x[ti].cpu(), p), "edge bf16 sampled")
+    assert_parity_bf16(y.float().cpu().numpy(), run_oracle(x.cpu(), p), f"edge bf16 all {M} rows")
     yf = y.float()
     assert float(yf.mean(dim=1).abs().max()) < 8 * 5e-3
     assert float((yf.var(dim=1, unbiased=False) - 1).abs().max()) < 8 * 2e-2

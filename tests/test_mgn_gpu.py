@@ -1,10 +1,10 @@
 """GPU parity of the MGN MLP kernels against the CPU oracle (oracle/oracle.c).
 
 Bar (fp16 I/O, fp32 accumulate): max-abs <= 2e-2 and relative-L2 <= 5e-3
-against the fp32 oracle on identical fp16-rounded inputs.  At the full headline
-size the oracle checks a row sample, and size-independent properties cover
-every row: permutation equivariance (bit-exact), per-row LayerNorm moments,
-determinism, and untouched memory past the output.
+against the fp32 oracle on identical fp16-rounded inputs, over every row up to
+the full headline size.  Size-independent properties are checked beside it:
+permutation equivariance (bit-exact), per-row LayerNorm moments, determinism,
+and untouched memory past the output.
 """
 import numpy as np
 import pytest
@@ -114,17 +114,14 @@ def test_nondefault_stream_and_repeat(cuda):
 
 
 @pytest.mark.parametrize("which", ["edge", "node"])
-def test_full_size_sampled_and_invariants(cuda, which):
-    """Headline sizes: edge M=1,048,576 K=384; node M=262,144 K=256."""
+def test_full_size_all_rows_and_invariants(cuda, which):
+    """Headline sizes: edge M=1,048,576 K=384; node M=262,144 K=256.  The
+    oracle runs over every row (a few tenths of a second on the box's cores)."""
     M, K = (1048576, 384) if which == "edge" else (262144, 256)
     p = to_dev(mgn_params(K, seed=11), cuda)
     x = normal_fp16(M, K, seed=12, device=cuda)
     y = run_gpu(x, p)
-    # rows are independent: a row sample plus the first / last rows against the oracle
-    g = np.random.default_rng(13)
-    idx = np.unique(np.concatenate([np.arange(100), np.arange(M - 100, M), g.integers(0, M, 4096)]))
-    ti = torch.from_numpy(idx).to(cuda)
-    assert_parity(y[ti].float().cpu().numpy(), run_oracle(x[ti].cpu(), p), f"{which} sampled")
+    assert_parity(y.float().cpu().numpy(), run_oracle(x.cpu(), p), f"{which} all {M} rows")
     # every row: LayerNorm with gamma=1, beta=0 has mean 0 and variance v/(v+eps) ~ 1
     yf = y.float()
     mean = yf.mean(dim=1)

@@ -5,7 +5,6 @@ Same bar as the fused kernel: max-abs <= 2e-2, relative-L2 <= 5e-3.  After
 every launch gpipes.pipeline_check() confirms that no queue wait hit its
 spin bound.
 """
-import numpy as np
 import pytest
 import torch
 
@@ -62,16 +61,13 @@ def test_split_needs_layernorm(cuda):
 
 @pytest.mark.parametrize("impl", IMPLS)
 def test_full_size_edge(cuda, impl):
-    """Headline edge size through the queue pipelines: sampled rows vs the
+    """Headline edge size through the queue pipelines: every row vs the
     oracle, and a second launch bit-identical to the first (the tile-to-pipeline
     assignment may change between launches; the per-row arithmetic may not)."""
     M, K = 1048576, 384
     p = to_dev(mgn_params(K, seed=11), cuda)
     x = normal_fp16(M, K, seed=12, device=cuda)
     y = run_checked(x, p, impl)
-    g = np.random.default_rng(13)
-    idx = np.unique(np.concatenate([np.arange(100), np.arange(M - 100, M), g.integers(0, M, 4096)]))
-    ti = torch.from_numpy(idx).to(cuda)
-    assert_parity(y[ti].float().cpu().numpy(), run_oracle(x[ti].cpu(), p), f"{impl} edge sampled")
+    assert_parity(y.float().cpu().numpy(), run_oracle(x.cpu(), p), f"{impl} edge all {M} rows")
     y2 = run_checked(x, p, impl)
     assert torch.equal(y, y2)

@@ -164,6 +164,30 @@ def test_pipe_route_bit_exact(cuda, route, M, max_pipes):
         assert torch.equal(out2.view(torch.int16), x.view(torch.int16))
 
 
+@pytest.mark.parametrize("M", [1, 128, 129, 100003, 128 * 20000])
+@pytest.mark.parametrize("max_pipes", [1, 0, 5])
+def test_pipe_handoff_checksums(cuda, M, max_pipes):
+    """Queue hand-off benchmark route: every tile's checksum, computed by the consumer from
+    the payload the producer generated, equals the closed form (handoff_checksums is pinned
+    against a brute-force sum in test_capi.py)."""
+    got = gpipes.pipe_handoff(M, max_pipes=max_pipes)
+    gpipes.pipeline_check()
+    want = gpipes.handoff_checksums(M)
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), want)
+
+
+def test_pipe_handoff_back_to_back(cuda):
+    """Repeated hand-off launches over the arena the copy routes use."""
+    x = torch.randn((5000, 128), device=cuda).to(torch.float16)
+    for i, mp in enumerate([0, 1, 0, 3]):
+        got = gpipes.pipe_handoff(128 * 3000 + 77, max_pipes=mp)
+        gpipes.pipeline_check()
+        assert np.array_equal(got.cpu().numpy().view(np.uint32), gpipes.handoff_checksums(128 * 3000 + 77)), i
+        out, _ = gpipes.pipe_route(x, "ident")
+        gpipes.pipeline_check()
+        assert torch.equal(out, x), i
+
+
 def test_arena_shared_by_different_queue_layouts(cuda):
     """Launches with different queue layouts on one stream share the arena."""
     from gpipes.synth import mgn_params, normal_fp16
