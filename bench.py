@@ -617,11 +617,22 @@ def main():
                          "are also timed as one HIP graph replay and `value` comes from the faster of the "
                          "two; the per-launch roofline times are eager in both cases)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cus", type=int, default=0,
+                    help="size every launch for this many CUs instead of all of them (GPIPES_NUM_CUS); "
+                         "diagnostics only, with --phase-timers: the cycles per tile at 128, 192, 256 CUs")
+    ap.add_argument("--phase-timers", action="store_true",
+                    help="fused MGN workloads: load the diagnostic library (libgpipes_phase.so: the fused "
+                         "kernel with s_memtime phase timers, about 1%% slower) and add the last launch's "
+                         "cycles per tile and phase to the line as \"phase_cycles\"; not a headline run")
     ap.add_argument("--copy-ref", action="store_true",
                     help="first run one plain 1 GiB device copy (a known-size reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
 
+    if args.phase_timers:
+        os.environ["GPIPES_PHASE_TIMERS"] = "1"  # before gpipes is imported
+    if args.cus:
+        os.environ["GPIPES_NUM_CUS"] = str(args.cus)  # read when the library first queries the device
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the path needs no cross-GPU exchange; rows shard "
               f"trivially); --gpus {args.gpus} is not supported.", file=sys.stderr)
@@ -734,6 +745,12 @@ def main():
         "cpu_baseline": None if args.no_cpu or args.dtype != "f16" else cpu_baseline_torch_mgn(K, ln),
         "cpu_baseline_oracle": None if args.no_cpu or args.dtype != "f16" else cpu_baseline(K, ln),
     }
+    if args.phase_timers and args.impl == "fused":
+        step(0)  # the timers hold the last launch
+        rec["phase_cycles"] = gpipes.phase_timers()
+        rec["library"] = "libgpipes_phase.so (diagnostic build with phase timers)"
+    if args.cus:
+        rec["config"]["cus"] = args.cus
     print(json.dumps(rec), flush=True)
 
 

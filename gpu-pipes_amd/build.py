@@ -2,6 +2,9 @@
 
 Both are compiled in-tree so the shared objects travel with the source tree:
   gpu-pipes_amd/gpipes/libgpipes.so   HIP kernels + C ABI (include/gpipes.h)
+  gpu-pipes_amd/gpipes/libgpipes_phase.so  the same with the fused MGN kernels'
+                                      phase timers compiled in (diagnostics:
+                                      bench.py --phase-timers)
   oracle/liboracle.so                 CPU restatement used only by tests/bench
   gpu-pipes_amd/apps/mgn_mlp_cc       C++ driver of the operator (links libgpipes.so)
 
@@ -17,6 +20,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "gpipes", "libgpipes.so")
+PHASE_LIB = os.path.join(PKG, "gpipes", "libgpipes_phase.so")
 ORACLE_DIR = os.path.join(ROOT, "oracle")
 ORACLE_LIB = os.path.join(ORACLE_DIR, "liboracle.so")
 
@@ -63,12 +67,18 @@ def build_library(verbose=False):
         lang = ["-x", "hip"] if src.endswith(".hip") else []
         extra = SOURCE_FLAGS.get(src, VGPR_FORM)
         jobs.append([HIPCC] + HIP_FLAGS + extra + lang + ["-c", path, "-o", obj])
+    # the diagnostic build's fused MGN object, with the phase timers
+    phase_obj = os.path.join(BUILD, "mgn_fused_phase.o")
+    jobs.append([HIPCC] + HIP_FLAGS + VGPR_FORM + ["-DGP_PHASE_TIMERS", "-x", "hip", "-c",
+                                                   os.path.join(CSRC, "mgn_fused.hip"), "-o", phase_obj])
     with cf.ThreadPoolExecutor(max_workers=min(len(jobs), 8)) as ex:
         list(ex.map(lambda c: _run(c, verbose), jobs))
-    tmp = LIB + ".tmp"
-    # --no-undefined: a kernel whose host stub was not emitted fails here, not at load time
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", tmp] + objs, verbose)
-    os.replace(tmp, LIB)
+    for lib, lib_objs in ((LIB, objs), (PHASE_LIB, [phase_obj if o.endswith("mgn_fused.o") else o for o in objs])):
+        tmp = lib + ".tmp"
+        # --no-undefined: a kernel whose host stub was not emitted fails here, not at load time
+        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", tmp] + lib_objs,
+             verbose)
+        os.replace(tmp, lib)
     return LIB
 
 

@@ -10,6 +10,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 
@@ -58,6 +59,12 @@ int current_device_info(int* dev_out, int* num_cus) {
     e = hipGetDeviceProperties(&prop, dev);
     if (e != hipSuccess) return fail_hip(e, "hipGetDeviceProperties");
     d.num_cus = prop.multiProcessorCount;
+    // GPIPES_NUM_CUS=n sizes every launch for n CUs instead of all of them
+    // (a caller sharing the GPU, or a measurement on part of the chip).
+    if (const char* v = getenv("GPIPES_NUM_CUS")) {
+      const int n = atoi(v);
+      if (n >= 1 && n < d.num_cus) d.num_cus = n;
+    }
     d.gfx950 = std::string(prop.gcnArchName).rfind("gfx950", 0) == 0;
     d.valid = true;
   }
@@ -247,6 +254,16 @@ int gp_pipe_route(int64_t M, const void* x, void* out, void* out2, int route, in
   if ((rc = need(x, "x")) || (rc = need(out, "out"))) return rc;
   if (route == GP_ROUTE_BROADCAST && (rc = need(out2, "out2"))) return rc;
   return pipe_route_run(M, x, out, out2, route, max_pipes, dev, ncu, (hipStream_t)stream);
+}
+
+int gp_phase_timers_read(void* dst, int64_t bytes) {
+  clear_error();
+  switch (mgn_phase_timers_read(dst, bytes)) {
+    case 0: return GP_OK;
+    case -1: return fail(GP_ERR_INVALID_ARG, "dst must hold %d bytes", 256 * 8 * 12 * 8);
+    case -2: return fail(GP_ERR_HIP, "copy of the phase timers failed");
+    default: return fail(GP_ERR_INVALID_ARG, "this library was built without phase timers (libgpipes_phase.so has them)");
+  }
 }
 
 int gp_pipeline_check(void* stream) {

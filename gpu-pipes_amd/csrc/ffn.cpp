@@ -25,14 +25,16 @@ namespace {
 
 constexpr int64_t kMaxDim = 16384;
 constexpr int64_t kMaxRows = (int64_t(1) << 31) - 1;  // GEMM tile indices are 32-bit
-// Row chunks hold their FF-wide activations within kFfnChunkBytes (128 MiB,
-// half the Infinity Cache): 16384 rows at BERT-large width, where GEMM1 has
-// 1024 tiles and GEMM2 256 tiles per chunk, whole multiples of the 256 CUs.
-// Narrower blocks take more rows per chunk, hence fewer, fuller launches (the
-// bert_addln_ffn app's 32,768 rows at FF 512 are one chunk).
+// Row chunks hold their per-row workspace (the FF-wide activations plus any
+// H-wide intermediate rows, `row_elems` 16-bit values a row) within
+// kFfnChunkBytes (128 MiB, half the Infinity Cache): 16384 rows at BERT-large
+// width, where GEMM1 has 1024 tiles and GEMM2 256 tiles per chunk, whole
+// multiples of the 256 CUs.  Narrower blocks take more rows per chunk, hence
+// fewer, fuller launches (the bert_addln_ffn app's 32,768 rows at FF 512 are
+// one chunk).
 constexpr int64_t kFfnChunkBytes = int64_t(128) << 20;
-int64_t ffn_chunk_rows(int64_t FF) {
-  const int64_t r = kFfnChunkBytes / (FF * 2) / 256 * 256;
+int64_t ffn_chunk_rows(int64_t row_elems) {
+  const int64_t r = kFfnChunkBytes / (row_elems * 2) / 256 * 256;
   return r < 256 ? 256 : r;
 }
 
@@ -95,11 +97,11 @@ struct LnEpilogue {
   }
 };
 
-// Rows per chunk of the FFN blocks: at most ffn_chunk_rows(FF), and with the
-// LayerNorm in the GEMM epilogue at most the rows whose tiles are all
+// Rows per chunk of the FFN blocks with the LayerNorm in the GEMM epilogue:
+// at most ffn_chunk_rows(row_elems) and at most the rows whose tiles are all
 // resident at once.  0 when the epilogue cannot take the LayerNorm.
-int64_t ln_chunk_rows(int64_t H, int64_t FF, int ncu) {
-  const int64_t r = gemm_ln_max_rows(H, ncu), c = ffn_chunk_rows(FF);
+int64_t ln_chunk_rows(int64_t H, int64_t row_elems, int ncu) {
+  const int64_t r = gemm_ln_max_rows(H, ncu), c = ffn_chunk_rows(row_elems);
   return r < 256 ? 0 : (r < c ? r : c);
 }
 
@@ -184,7 +186,7 @@ int gp_bert_ffn_dtype_out(int64_t M, int64_t H, int64_t FF, const void* x, const
   const bool fuse_ln = lnch > 0;
   if (!fuse_ln && dtype != GP_DTYPE_F16)
     return fail(GP_ERR_SHAPE, "bf16 needs the LayerNorm in the GEMM epilogue, which this device's %d CUs cannot hold", ncu);
-  const int64_t chmax = fuse_ln ? lnch : ffn_chunk_rows(FF);
+  const int64_t chmax = fuse_ln ? lnch : ffn_chunk_rows(FF + H);
   const int64_t CH = M < chmax ? M : chmax;
   const size_t o_w2t = inplace ? 0 : round_up((size_t)FF * H * 2);
   const size_t o_act = o_w2t + (inplace ? 0 : round_up((size_t)FF * H * 2));
@@ -270,19 +272,20 @@ int gp_bert_addln_ffn_dtype_out(int64_t M, int64_t H, int64_t FF, const void* at
 
   // Chain: per row chunk, GEMM0 (+ b0 + x), LN0, GEMM1 (+ b1, act), GEMM2 (+ b2 + h0), LN2.
   // Workspace: w0^T [H][H], w1^T [FF][H], w2^T [H][FF] (unless the GEMMs
-  // read the weights in place), then for one chunk the pre-LayerNorm rows
-  // y [CH][H], h0 [CH][H] and the activations [CH][FF].
+  // read the weights in place), then for one chunk h0 [CH][H], the
+  // activations [CH][FF] and, when the LayerNorms are launches of their own,
+  // the pre-LayerNorm rows y [CH][H].
   const bool inplace = weights_in_place(2.0 * M * H * (H + 2.0 * FF));
-  const int64_t lnch = ln_chunk_rows(H, FF, ncu);
+  const int64_t lnch = ln_chunk_rows(H, FF + H, ncu);
   const bool fuse_ln = lnch > 0;
   if (!fuse_ln && dtype != GP_DTYPE_F16)
     return fail(GP_ERR_SHAPE, "bf16 needs the LayerNorm in the GEMM epilogue, which this device's %d CUs cannot hold", ncu);
-  const int64_t chmax = fuse_ln ? lnch : ffn_chunk_rows(FF);
+  const int64_t chmax = fuse_ln ? lnch : ffn_chunk_rows(FF + 2 * H);
   const int64_t CH = M < chmax ? M : chmax;
   const size_t o_w1t = inplace ? 0 : round_up((size_t)H * H * 2);
   const size_t o_w2t = o_w1t + (inplace ? 0 : round_up((size_t)FF * H * 2));
   const size_t o_y = o_w2t + (inplace ? 0 : round_up((size_t)FF * H * 2));
-  const size_t o_h0 = o_y + round_up((size_t)CH * H * 2);
+  const size_t o_h0 = o_y + (fuse_ln ? 0 : round_up((size_t)CH * H * 2));
   const size_t o_act = o_h0 + round_up((size_t)CH * H * 2);
   const size_t total = o_act + round_up((size_t)CH * FF * 2);
   char* ws = nullptr;

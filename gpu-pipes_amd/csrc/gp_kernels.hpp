@@ -42,6 +42,10 @@ struct MgnArgs {
 
 // Persistent fused kernel (all layers in one workgroup per CU).
 hipError_t mgn_fused_launch(const MgnArgs& a, int num_cus, hipStream_t stream);
+// Copies the fused MGN kernels' phase timers of the last launch (diagnostic
+// build only): 0, -1 (dst NULL or too small), -2 (copy failed), -3 (built
+// without GP_PHASE_TIMERS).
+int mgn_phase_timers_read(void* dst, int64_t bytes);
 
 // The add + LayerNorm + FFN block of apps/bert_addln_ffn (attn, x [M,H] ->
 // out [M,H]): h0 = LN0(attn w0 + b0 + x), out = LN2(act(h0 w1 + b1) w2 + b2 + h0).

@@ -272,6 +272,49 @@ __device__ __forceinline__ void store_row_pair(half_t* row, const h4 (&hv)[2], i
   if (ok) *(u32x4*)((char*)row + 64 * j + (q4 & 1) * 32 + (q4 >> 1) * 16) = w;
 }
 
+// Phase timers, compiled in only with GP_PHASE_TIMERS (libgpipes_phase.so, a
+// diagnostic build): every wave adds the s_memtime ticks (shader clock
+// cycles) of each phase of its tile loop into acc[], and at exit lane 0 of
+// wave w of workgroup b (b < kPhaseGroups) writes slot group (b * NWAVES + w):
+// acc[0..7], then the loop's total ticks, its s_memrealtime ticks (100 MHz),
+// the tiles it ran and the launch's grid size.  The product build's timer is
+// empty and costs nothing.
+constexpr int kPhaseGroups = 256;
+constexpr int kPhaseSlots = 12;
+#ifdef GP_PHASE_TIMERS
+__device__ unsigned long long g_phase[kPhaseGroups * NWAVES * kPhaseSlots];
+struct PhaseTimer {
+  unsigned long long acc[8] = {0, 0, 0, 0, 0, 0, 0, 0}, last = 0, t0 = 0, r0 = 0;
+  __device__ void start() {
+    t0 = last = __builtin_amdgcn_s_memtime();
+    r0 = __builtin_amdgcn_s_memrealtime();
+  }
+  __device__ void tile() { last = __builtin_amdgcn_s_memtime(); }
+  __device__ void mark(int i) {
+    const unsigned long long t = __builtin_amdgcn_s_memtime();
+    acc[i] += t - last;
+    last = t;
+  }
+  __device__ void finish(int wave, int lane, int nt) {
+    const unsigned long long t = __builtin_amdgcn_s_memtime(), r = __builtin_amdgcn_s_memrealtime();
+    if (lane != 0 || blockIdx.x >= kPhaseGroups) return;
+    unsigned long long* o = g_phase + ((int64_t)blockIdx.x * NWAVES + wave) * kPhaseSlots;
+    for (int i = 0; i < 8; ++i) o[i] = acc[i];
+    o[8] = t - t0;
+    o[9] = r - r0;
+    o[10] = (unsigned long long)nt;
+    o[11] = gridDim.x;
+  }
+};
+#else
+struct PhaseTimer {
+  __device__ void start() {}
+  __device__ void tile() {}
+  __device__ void mark(int) {}
+  __device__ void finish(int, int, int) {}
+};
+#endif
+
 // GATHER_IDX: 0 = X given; 4 / 8 = gather, index bytes.  E: ElemF16 / ElemBF16.
 template <int K, bool LN, int GATHER_IDX = 0, typename E = ElemF16>
 __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -447,12 +490,16 @@ void mgn_fused_kernel(Params p) {
     const int xa = lh ^ (lr & 15);  // chunk (2s+lh) of rows lr, lr+32 lands at (2s ^ xa) in its 16-group
     const int xrow = lr * XROW;
 
+    PhaseTimer pt;  // A phases: 0 X wait, 1 A barrier, 2 layer 1, 3 hand-off wait, 4 hand-off store
     auto tile_a = [&](GP_LDS char* xs, GP_LDS char* xnext, GP_LDS char* hand, int k) {
       // X(k) is the only copy in flight.  After the barrier it has landed for
       // every A wave and every A wave is done with tile k-1, whose buffer is
       // refilled with X(k+1) at once.
+      pt.tile();
       wait_vmcnt<0>();
+      pt.mark(0);
       group_barrier((GP_LDS int*)&sy.a_bar, abar, 4, lane, ab, lim);
+      pt.mark(1);
       // Layer 1; the copies of X(k+1) into xnext are issued between its
       // MFMAs, so a busy memory pipeline stalls the copies, not the MFMAs.
       // (Gather: tile k+1's indices landed with X(k); tile k+2's are copied
@@ -473,17 +520,22 @@ void mgn_fused_kernel(Params p) {
       });
 
       // Handoff slot k%2 was last read by stage B for tile k-2.
+      pt.mark(2);
       if (k >= 2) lds_wait_geq((GP_LDS int*)&sy.h_free, 4 * (k - 1), ab, lim);
+      pt.mark(3);
       store_relu_row<E>(hand + arow0, fq, acc0);
       store_relu_row<E>(hand + arow1, fq, acc1);
       lds_signal((GP_LDS int*)&sy.h_full, lane);
+      pt.mark(4);
     };
 
+    pt.start();
     for (int k = 0; k < nt; k += 2) {
       tile_a((GP_LDS char*)xs0, (GP_LDS char*)xs1, (GP_LDS char*)hand0, k);
       if (k + 1 < nt) tile_a((GP_LDS char*)xs1, (GP_LDS char*)xs0, (GP_LDS char*)hand1, k + 1);
     }
     wait_vmcnt<0>();  // the (empty) copy issued during the last tile has landed before the waves exit
+    pt.finish(wave, lane, nt);
   } else {
     // ------------------------------------------------------------- stage B
     // W2 (32x32x16 A operand): lane holds W2[16s + 8*lh + e][32n + lr].
@@ -515,27 +567,36 @@ void mgn_fused_kernel(Params p) {
     // keeps the four B waves in step, and A fills the gaps.
     __builtin_amdgcn_s_setprio(1);
 
+    // B phases: 0 hand-off wait, 1 layer 2, 2 exchange-free wait, 3 exchange
+    // store, 4 exchange-full wait, 5 layer 3 issue, 6 LayerNorm and stores
+    PhaseTimer pt;
     auto tile_b = [&](GP_LDS char* hand, int k) {
+      pt.tile();
       // layer 2 bias: its LDS reads overlap the hand-off wait
       f16x acc0 = bias_frag(prm[1], fq), acc1 = acc0;
       lds_wait_geq((GP_LDS int*)&sy.h_full, 4 * (k + 1), ab, lim);
+      pt.mark(0);
 
       // layer 2, features [32n, 32n+32) of all 64 rows, from the handoff tile
       gemm_2blk<E, D / 16, PF_L2, 4>(w2f, [&](int rb, int s) {
         return *(const GP_LDS h8*)(hand + (rb ? arow1 : arow0) + (2 * s + lh) * 16);
       }, acc0, acc1);
       lds_signal((GP_LDS int*)&sy.h_free, lane);  // B operands are in registers: release the slot
+      pt.mark(1);
 
       // exchange: act2 was last read (layer 3) for tile k-1
       if (k >= 1) lds_wait_geq((GP_LDS int*)&sy.x2_free, 4 * k, ab, lim);
+      pt.mark(2);
       store_relu_row<E>((GP_LDS char*)act2 + arow0, fq, acc0);
       store_relu_row<E>((GP_LDS char*)act2 + arow1, fq, acc1);
       lds_signal((GP_LDS int*)&sy.x2_full, lane);
+      pt.mark(3);
       // layer 3 bias (features 16fb + 4q4 + (0..3)): its reads overlap the exchange wait
       f4 y[8];
 #pragma unroll
       for (int fb = 0; fb < 8; ++fb) y[fb] = *(const f4*)&prm[2][16 * fb + 4 * q4];
       lds_wait_geq((GP_LDS int*)&sy.x2_full, 4 * (k + 1), ab, lim);
+      pt.mark(4);
 
       // layer 3, all features of rows [16n, 16n+16): eight independent
       // accumulator chains, issued k-step-major so no MFMA waits on the one before
@@ -548,6 +609,7 @@ void mgn_fused_kernel(Params p) {
 #pragma unroll
         for (int fb = 0; fb < 8; ++fb) y[fb] = E::mma16(w3f[fb][ks], bf[ks], y[fb]);
 
+      pt.mark(5);
       const int64_t grow = (t0 + (int64_t)k * G) * TM + 16 * n + l16;
       half_t* const orow = p.out + grow * D;
       // After a timed-out wait the tile's inputs are not trustworthy: store nothing.
@@ -590,12 +652,15 @@ void mgn_fused_kernel(Params p) {
           store_row_pair(orow, hv, j, q4, st);
         }
       }
+      pt.mark(6);
     };
 
+    pt.start();
     for (int k = 0; k < nt; k += 2) {
       tile_b((GP_LDS char*)hand0, k);
       if (k + 1 < nt) tile_b((GP_LDS char*)hand1, k + 1);
     }
+    pt.finish(wave, lane, nt);
   }
   // The abort word is sticky and is set before the wave that set it gets
   // here, so the workgroup's timeout is reported at least once.
@@ -615,6 +680,18 @@ static hipError_t launch_fused(const MgnArgs& a, int grid, hipStream_t stream) {
                   a.status, a.epoch, a.spin_limit > 0 ? a.spin_limit : kSpinLimit};
   hipLaunchKernelGGL((fused::mgn_fused_kernel<K, LN, GI, E>), dim3(grid), dim3(fused::NTHREADS), 0, stream, p);
   return hipGetLastError();
+}
+
+int mgn_phase_timers_read(void* dst, int64_t bytes) {
+#ifdef GP_PHASE_TIMERS
+  const int64_t need = (int64_t)sizeof(fused::g_phase);
+  if (dst == nullptr || bytes < need) return -1;
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(fused::g_phase), need, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -2;
+#else
+  (void)dst;
+  (void)bytes;
+  return -3;
+#endif
 }
 
 hipError_t mgn_fused_launch(const MgnArgs& a, int num_cus, hipStream_t stream) {

@@ -76,6 +76,7 @@ constexpr int CPW = FPS / RW;      // 1 KiB ring copies per copying wave per slo
 constexpr int XBUF = ROWS * 64 * 2;  // one tile of x (Kx <= 64)
 constexpr int DBUF = ROWS * 32 * 2;  // one tile of d (Kd <= 32)
 constexpr int XCPW = XBUF / FRAG / (NW - RW), DCPW = DBUF / FRAG / (NW - RW);  // input copies per wave
+constexpr int kOutStores = 8 * 2 * RB;  // trunk output stores per wave and tile (epi_out)
 
 // Local slot map of one tile's weight stream (76 slots, 1.25 MB).
 constexpr int S_L1 = 0, S_L2 = 2, S_L6 = 34, S_L7 = 44, S_L9 = 60, S_L10 = 62, S_L11 = 70, S_L12 = 75, S_TOTAL = 76;
@@ -219,8 +220,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   // refill(), after the first MFMAs of the new slot.  Every acquire is
   // followed by exactly one refill() before the next acquire.
   static_assert(XCPW + DCPW <= CPW * (NS - 2), "input copies in flight");
-  auto acquire = [&] {
-    wait_vmcnt<CPW * (NS - 2)>();
+  // OUT_STORES: the trunk's output stores of the previous tile (issued after
+  // every ring copy still in flight, and counted by vmcnt in issue order like
+  // them) are left in flight too.
+  auto acquire = [&](auto out_stores) {
+    wait_vmcnt<CPW * (NS - 2) + decltype(out_stores)::value>();
     lds_barrier();
     cur = cur == NS - 1 ? 0 : cur + 1;
   };
@@ -399,6 +403,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     // groups g = 2q+1 of the lower half-wave for groups g = 2q of the upper
     // one, so each lane holds eight consecutive features 32 fb + 16 q + 8 lh +
     // (0..7) and one 16-byte store per lane writes 32 bytes of each of 32 rows.
+    // Each wave issues kOutStores 16-byte stores (8 feature blocks x 2).
     auto epi_out = [&] {
       const __amdgpu_buffer_rsrc_t ro = make_rsrc(p.out_r + r0 * 256, vrows * 256 * 2);
       const int lane = opaque(lane0), lr = lane & 31, lh = lane >> 5;
@@ -430,8 +435,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     // the last group's MFMAs are issued -- across layer boundaries too, where
     // the epilogue runs after the next layer's first fragments were requested.
     // Acquire the next slot and read its first group.
+    using S0 = std::integral_constant<int, 0>;
     auto advance = [&] {
-      acquire();
+      acquire(S0{});
       fetch(G0{}, G0{});
     };
     // The N slots of one layer, of kinds KD0 .. KD0+N-1; `after` acquires what
@@ -473,10 +479,22 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     auto nothing = [] {};
 
     // Layer 1: x -> 256, ReLU.  The input waves wait for this tile's x copies
-    // (this tile's d copies, issued after them, may still be in flight); the
+    // (this tile's d copies, issued after them, may still be in flight; in the
+    // trunk, the previous tile's output stores, issued after them); the
     // acquire's barrier then publishes the x tile.
-    if (!ring_wave) wait_vmcnt<TRUNK ? 0 : DCPW>();
-    advance();
+    if constexpr (TRUNK) {
+      if (k == 0) {
+        if (!ring_wave) wait_vmcnt<0>();
+        advance();
+      } else {
+        if (!ring_wave) wait_vmcnt<kOutStores>();
+        acquire(std::integral_constant<int, kOutStores>{});
+        fetch(G0{}, G0{});
+      }
+    } else {
+      if (!ring_wave) wait_vmcnt<DCPW>();
+      advance();
+    }
     take_input(true, p.Kx);
     bias_init(E8{}, BF_L1);
     run_layer(C1{}, C2{}, [&] { advance(); });

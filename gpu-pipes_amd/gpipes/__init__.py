@@ -27,11 +27,14 @@ __all__ = [
     "pipeline_check", "set_wait_limit", "ACTS", "mgn_edge_gather", "mgn_edge_gather_out", "pipe_route", "ROUTES",
     "gemm_out", "bert_ffn", "bert_ffn_out", "mlp_out", "dlrm_botmlp", "dlrm_botmlp_out", "dlrm_topmlp",
     "dlrm_topmlp_out", "nerf_full", "nerf_full_out", "nerf_full_out_noalloc", "bert_addln_ffn",
-    "bert_addln_ffn_out", "nerf_a", "nerf_a_out",
+    "bert_addln_ffn_out", "nerf_a", "nerf_a_out", "pipe_handoff", "handoff_checksums", "phase_timers",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libgpipes.so")
+# GPIPES_PHASE_TIMERS=1 loads the diagnostic build (the same library with the
+# fused MGN kernels' phase timers compiled in, see gp_phase_timers_read).
+LIB_PATH = os.path.join(_HERE, "libgpipes_phase.so" if os.environ.get("GPIPES_PHASE_TIMERS") == "1"
+                        else "libgpipes.so")
 
 GP_OK = 0
 IMPL_FUSED = 0
@@ -78,6 +81,8 @@ def _load():
     L.gp_pipeline_check.argtypes = [vp]
     L.gp_set_wait_limit.argtypes = [i64]
     L.gp_set_wait_limit.restype = i32
+    L.gp_phase_timers_read.argtypes = [vp, i64]
+    L.gp_phase_timers_read.restype = i32
     L.gp_mgn_edge_gather_out.argtypes = [i64, i64, vp, vp, vp, vp, i32] + [vp] * 8 + [f32, vp, vp]
     L.gp_mgn_edge_gather_out.restype = i32
     L.gp_gemm_out.argtypes = [i64, i64, i64, vp, vp, vp, vp, i32, vp, vp]
@@ -377,6 +382,38 @@ def handoff_checksums(M):
     ones = np.where(abit == 1, n[:, None] - c, c)
     total = (ones.astype(np.uint64) << bits[None, :]).sum(axis=1)                # < 2^46: no overflow
     return (total & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+
+
+PHASE_NAMES = {
+    "layer1_waves": ["x_wait", "a_barrier", "layer1", "handoff_wait", "handoff_store"],
+    "layer23_waves": ["handoff_wait", "layer2", "exchange_free_wait", "exchange_store", "exchange_full_wait",
+                      "layer3_issue", "layernorm_store"],
+}
+
+
+def phase_timers():
+    """Per-phase shader-clock cycles per tile of the last fused MGN launch, averaged over the
+    launch's workgroups (diagnostic build only: GPIPES_PHASE_TIMERS=1); also the loop's
+    cycles per tile and the clock they imply (s_memtime ticks / s_memrealtime time)."""
+    import numpy as np
+
+    buf = np.zeros(256 * 8 * 12, dtype=np.uint64)
+    torch.cuda.synchronize()
+    _check(lib.gp_phase_timers_read(ctypes.c_void_p(buf.ctypes.data), buf.nbytes))
+    a = buf.reshape(256, 8, 12).astype(np.float64)
+    grid = int(a[0, 0, 11])
+    a = a[:grid]
+    res = {"grid": grid}
+    for kind, waves in (("layer1_waves", slice(0, 4)), ("layer23_waves", slice(4, 8))):
+        w = a[:, waves, :]
+        tiles = w[..., 10].sum()
+        total = w[..., 8].sum()
+        res[kind] = {
+            "cycles_per_tile": total / tiles,
+            "clock_ghz": total / (w[..., 9].sum() * 10.0),
+            "phases_per_tile": {nm: w[..., i].sum() / tiles for i, nm in enumerate(PHASE_NAMES[kind])},
+        }
+    return res
 
 
 def pipeline_check(device=None):

@@ -451,6 +451,22 @@ int gp_pipeline_check(void* stream);
  */
 int gp_set_wait_limit(int64_t polls);
 
+/*
+ * Diagnostics: copies into dst (at least 256 * 8 * 12 * 8 bytes) the phase
+ * timers of the last fused MGN launch (gp_mgn_fullmlp_out, gp_mgn_linears_out,
+ * gp_mgn_mlp_out with the fused implementation, gp_mgn_edge_gather_out).
+ * For wave w of workgroup b < 256 the 12 uint64 values at (b * 8 + w) * 12
+ * are: the shader-clock ticks (s_memtime) spent in each of the wave's 8
+ * phases summed over its tiles (waves 0-3, layer 1: X wait, stage-A barrier,
+ * layer 1, hand-off wait, hand-off store; waves 4-7, layers 2-3: hand-off
+ * wait, layer 2, exchange-free wait, exchange store, exchange-full wait,
+ * layer-3 issue, LayerNorm and stores), the loop's total ticks, its
+ * s_memrealtime ticks (100 MHz), its tiles and the launch's grid size.  Only
+ * the diagnostic build libgpipes_phase.so records them; the product library
+ * returns GP_ERR_INVALID_ARG.  No counterpart in the reference.
+ */
+int gp_phase_timers_read(void* dst, int64_t bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -146,7 +146,8 @@ def test_nerf_a_golden(cuda, impl, M):
     assert_parity(f32(nerf_a_gpu(x, ws, bs, impl)), z["expected"][:M], f"nerf_a {impl} M={M}")
 
 
-@pytest.mark.parametrize("impl,Kx", [("fused", 64), ("fused", 60), ("fused", 63), ("fused", 200),
+@pytest.mark.parametrize("impl,Kx", [("fused", 64), ("fused", 60), ("fused", 63), ("fused", 39), ("fused", 3),
+                                     ("fused", 200),
                                      ("pipelined", 64), ("pipelined", 8), ("pipelined", 120), ("pipelined", 128)])
 @pytest.mark.parametrize("scale", [1.0, 2.0])
 @pytest.mark.parametrize("M", [1, 65, 3000, 70001])
@@ -157,6 +158,23 @@ def test_nerf_a_shapes(cuda, impl, Kx, scale, M):
     got = f32(nerf_a_gpu(x.to(cuda), [w.to(cuda) for w in ws], [b.to(cuda) for b in bs], impl))
     rows = np.linspace(0, M - 1, min(M, 1200)).astype(np.int64)
     assert_parity(got[rows], nerf_a_oracle(x, ws, bs, rows), f"nerf_a {impl} Kx={Kx} x{scale} M={M}")
+
+
+def test_nerf_a_rejects_unaligned_out(cuda):
+    """Every NerfA path writes out in 16-byte stores: an out that starts 2 bytes past an
+    aligned base is rejected with GP_ERR_ALIGN for both implementations, and nothing is written."""
+    M = 300
+    ws, bs = nerf_a_params(64, seed=5, device=cuda)
+    x = normal_fp16(M, 64, seed=6).to(cuda)
+    buf = torch.full((M * 256 + 8,), 3.0, dtype=torch.float16, device=cuda)
+    out = buf[1:1 + M * 256].view(M, 256)
+    wb = [t for pair in zip(ws, bs) for t in pair]
+    for impl in ("fused", "pipelined"):
+        with pytest.raises(gpipes.GpipesError) as e:
+            gpipes.nerf_a_out(x, *wb, out, impl=impl)
+        assert e.value.code == -3, impl
+    torch.cuda.synchronize()
+    assert bool((buf == 3.0).all())
 
 
 def test_nerf_a_no_bias_and_agreement(cuda):

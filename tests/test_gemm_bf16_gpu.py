@@ -236,9 +236,10 @@ def test_nerf_bf16_agrees_with_fp16_and_slices(cuda):
 # ------------------------------------------------------------------ NerfA trunk
 @pytest.mark.parametrize("Kx,M", [(64, 300), (60, 4099), (72, 1000)])
 def test_nerf_a_bf16_vs_oracle(cuda, Kx, M):
-    """gp_nerf_a_dtype_out on the GEMM chain (the app's width, an unaligned one,
-    one wider than a k-block) against the oracle on the bf16 values; weights at
-    2x the default init keep every layer's signal visible."""
+    """gp_nerf_a_dtype_out in bf16 against the oracle on the bf16 values: Kx 64
+    and 60 run the NeRF kernel's trunk, Kx 72 (wider than the trunk's 64) the
+    GEMM chain; weights at 2x the default init keep every layer's signal
+    visible."""
     ws, bs = nerf_a_params(Kx, seed=M + Kx)
     ws = [(w.float() * 2).to(BF).to(cuda) for w in ws]
     bs = [(b.float() * 2).to(BF).to(cuda) for b in bs]

@@ -149,3 +149,35 @@ def test_linear_stage_graph_replays_match_eager(cuda):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), want.view(torch.int16)), f"replay {r}"
+
+
+def test_nerf_noalloc_graph_replays_match_eager(cuda):
+    """gp_nerf_full_out_noalloc under capture: the graph holds the weight-packing kernel and
+    the fused NeRF kernel, both on the static scratch.  Between replays x, d and the
+    weights change in place; every replay must equal the eager (workspace) call on the new
+    contents bit for bit, so the replay re-packs the weights it finds."""
+    from gpipes.synth import nerf_inputs, nerf_params
+    M = 5000
+    ws, bs = nerf_params(64, 27, 1, 3, seed=40, device=cuda)
+    x, d = nerf_inputs(M, seed=41, device=cuda)
+    out_r = torch.empty((M, 1), dtype=torch.float16, device=cuda)
+    out_rgb = torch.empty((M, 3), dtype=torch.float16, device=cuda)
+    wb = [t for pair in zip(ws, bs) for t in pair]
+    gpipes.nerf_full_out_noalloc(x, d, *wb, out_r, out_rgb, rgb_act="sigmoid")  # first call: symbol lookup
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        gpipes.nerf_full_out_noalloc(x, d, *wb, out_r, out_rgb, rgb_act="sigmoid")
+    for r in range(3):
+        ws2, bs2 = nerf_params(64, 27, 1, 3, seed=50 + r, device=cuda)
+        for t, n in zip(ws + bs, ws2 + bs2):
+            t.copy_(n)
+        x2, d2 = nerf_inputs(M, seed=60 + r, device=cuda)
+        x.copy_(x2)
+        d.copy_(d2)
+        want_r, want_rgb = gpipes.nerf_full(x, d, *wb, rgb_act="sigmoid")
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_r.view(torch.int16), want_r.view(torch.int16)), f"replay {r} density"
+        assert torch.equal(out_rgb.view(torch.int16), want_rgb.view(torch.int16)), f"replay {r} colour"
