@@ -437,19 +437,29 @@ void mgn_fused_kernel(Params p) {
     const int gc = (lane & 15) ^ (r0 & 15);
     const __amdgpu_buffer_rsrc_t nf_rsrc = make_rsrc(p.nf, GATHER ? (int)(p.N * (D * 2)) : 0);
     int goff[GATHER ? 8 : 1];  // [src q0..q3, dst q0..q3]
-    auto row_index_bytes = [&](int k, int which, int q) {  // nf byte offset of the gathered row
-      const GP_LDS char* ib = (const GP_LDS char*)idxs[k & 1] + which * 1024 + (16 * q + r0) * GATHER_IDX;
-      const unsigned lo = *(const GP_LDS unsigned*)ib;
-      const unsigned hi = GATHER_IDX == 8 ? *(const GP_LDS unsigned*)(ib + 4) : 0u;
-      const bool ok = hi == 0u && lo < (unsigned)p.N;
-      return ok ? (int)(lo * (unsigned)(D * 2) + gc * 16) : (int)0xFFFFFFF0u;
-    };
+    // All eight indices of a lane are read before any is used, with one LDS
+    // read each (both halves of an int64 index at once) and no branches, so
+    // their latencies overlap instead of adding up.
     auto gather_offsets = [&](int k) {
       if constexpr (GATHER) {
+        unsigned lo[8], hi[8];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          goff[q] = row_index_bytes(k, 0, q);
-          goff[4 + q] = row_index_bytes(k, 1, q);
+        for (int i = 0; i < 8; ++i) {
+          const GP_LDS char* ib =
+              (const GP_LDS char*)idxs[k & 1] + (i >> 2) * 1024 + (16 * (i & 3) + r0) * GATHER_IDX;
+          if constexpr (GATHER_IDX == 8) {
+            const u32x2 v = *(const GP_LDS u32x2*)ib;
+            lo[i] = v[0];
+            hi[i] = v[1];
+          } else {
+            lo[i] = *(const GP_LDS unsigned*)ib;
+            hi[i] = 0u;
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {  // [src q0..q3, dst q0..q3]
+          const bool ok = (hi[i] == 0u) & (lo[i] < (unsigned)p.N);
+          goff[i] = ok ? (int)(lo[i] * (unsigned)(D * 2) + gc * 16) : (int)0xFFFFFFF0u;
         }
       }
     };
