@@ -98,8 +98,8 @@ struct LnEpilogue {
 };
 
 // Rows per chunk of the FFN blocks with the LayerNorm in the GEMM epilogue:
-// at most ffn_chunk_rows(row_elems) and at most the rows whose tiles are all
-// resident at once.  0 when the epilogue cannot take the LayerNorm.
+// at most ffn_chunk_rows(row_elems) and at most the rows one LayerNorm-exchange
+// launch can take (gemm_ln_max_rows).  0 when the epilogue cannot take the LayerNorm.
 int64_t ln_chunk_rows(int64_t H, int64_t row_elems, int ncu) {
   const int64_t r = gemm_ln_max_rows(H, ncu), c = ffn_chunk_rows(row_elems);
   return r < 256 ? 0 : (r < c ? r : c);

@@ -58,6 +58,7 @@ constexpr int RPC = 1024 / ROWB;    // rows per 1 KiB copy instruction
 constexpr int KS = BK / 16;         // MFMA k-steps per slab
 constexpr int NU = 5;               // units in the LDS ring
 constexpr int NW = 4;               // waves per workgroup
+constexpr int kLnPasses = 4;        // passes over the grid one LayerNorm-exchange launch may run
 constexpr int NT = NW * kWave;
 static_assert(KS % 2 == 0, "fragments alternate between two register sets per step");
 
@@ -126,9 +127,10 @@ __device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&&
 // wave all 128 features of its rows (N = 128, Narrow), so the row statistics
 // stay in the wave; 2 (Wide, N = 256 .. 1024) a row spans N / 128 waves of
 // N / BN workgroups, which publish
-// per-wave partial statistics and combine them (one tile per workgroup,
-// every tile resident).  Launches of one epoch share the counters: launch
-// round r of the epoch waits for (r + 1) N / BN NW commits.
+// per-wave partial statistics and combine them (at most kLnPasses passes of
+// one tile per workgroup, every workgroup resident).  Launches of one epoch
+// share the counters: launch round r of the epoch waits for (r + 1) N / BN NW
+// commits.
 //
 // E: the element type (F16 or BF16).
 template <class C, int ACT, bool RESID, bool BROW = false, int LNM = 0, typename E = F16>
@@ -159,12 +161,17 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   int hi = (int)((int64_t)ntiles * (xcd + 1) / NX);
   int t = (int)((int64_t)ntiles * xcd / NX) + wid;
   if constexpr (LNM == 2) {
-    // One tile per workgroup (the grid is the tile count).  With a grid of
-    // whole multiples of 8, XCD x takes tiles [x G/8, (x+1) G/8), so the
-    // workgroups of one row block mostly share an L2.
+    // Passes of G tiles: workgroup b takes tile f(b) of every pass, j G +
+    // f(b).  A pass holds whole row blocks (the host keeps G a multiple of
+    // N / BN when there is more than one), so the N / BN tiles of a row block,
+    // which wait for each other's LayerNorm statistics, all run in the same
+    // pass on workgroups that are all resident; pass j + 1 waits on nothing
+    // that pass j has not finished.  With a grid of whole multiples of 8, XCD
+    // x takes tiles [x G/8, (x+1) G/8) of a pass, so the workgroups of one row
+    // block mostly share an L2.
     t = G % 8 == 0 ? (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
-    hi = t + 1;
-    nwx = 1;
+    hi = ntiles;
+    nwx = G;
   }
   if (t >= hi) return;
 
@@ -761,9 +768,10 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const half_t* a, int lda, in
 template <class C, int ACT, bool RESID, bool BROW, int LNM = 0, typename E = F16>
 static hipError_t launch(const Args& a, int num_cus, hipStream_t s) {
   const int64_t tiles = ((a.M + C::BM - 1) / C::BM) * (a.N / C::BN);
-  // One persistent workgroup per CU; the LNM 2 kernels take one tile each,
-  // all resident at once (the host keeps tiles <= num_cus).
-  if (LNM == 2 && tiles > num_cus) return hipErrorInvalidValue;
+  // One persistent workgroup per CU; the LNM 2 kernels run at most kLnPasses
+  // passes of one tile per workgroup, every pass of whole row blocks.
+  if (LNM == 2 && (tiles > kLnPasses * num_cus || (tiles > num_cus && num_cus % (a.N / C::BN) != 0)))
+    return hipErrorInvalidValue;
   const int64_t grid = tiles < num_cus ? tiles : num_cus;
   hipLaunchKernelGGL((gemm_kernel<C, ACT, RESID, BROW, LNM, E>), dim3((unsigned)grid), dim3(NT), 0, s, a);
   return hipGetLastError();
@@ -813,7 +821,9 @@ size_t ln_ws_bytes(int64_t M, int64_t N) {
 int64_t gemm_ln_max_rows(int64_t N, int num_cus) {
   if (N == 128) return int64_t(1) << 62;  // rows stay within a wave: any M
   if (N % gemm::Wide::BN || N > 1024) return 0;
-  return (num_cus / (N / gemm::Wide::BN)) * gemm::Wide::BM;
+  const int64_t tiles_n = N / gemm::Wide::BN;
+  const int64_t one_pass = (num_cus / tiles_n) * gemm::Wide::BM;
+  return num_cus % tiles_n == 0 ? gemm::kLnPasses * one_pass : one_pass;
 }
 
 size_t gemm_ln_ws_bytes(int64_t M, int64_t N) { return N == 128 ? 0 : gemm::ln_ws_bytes(M, N); }

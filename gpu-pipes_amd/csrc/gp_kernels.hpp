@@ -117,8 +117,9 @@ struct GemmArgs {
   // N > 128 a row spans several waves and workgroups, which exchange partial
   // statistics through ln_ws (gemm_ln_ws_bytes(M, N) bytes of a queue arena,
   // zeroed when allocated; the status word is its first 8 bytes) under an
-  // epoch; every tile must then be resident at once: at most num_cus tiles
-  // (gemm_ln_max_rows) and at most 1024 row blocks.  Launches of one epoch on
+  // epoch; every workgroup must then be resident at once: at most
+  // gemm_ln_max_rows(N, num_cus) rows (four passes of num_cus tiles when
+  // num_cus is a multiple of N / 256, else one) and at most 1024 row blocks.  Launches of one epoch on
   // one ln_ws are numbered by ln_round (0, 1, ...) and must cover a prefix of
   // the same row blocks in every earlier round.
   int ln = 0;
