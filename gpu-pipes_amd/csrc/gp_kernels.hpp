@@ -201,4 +201,21 @@ hipError_t nerf_trunk_launch(int64_t M, int Kx, const void* x, const void* const
 // (the current device), for the allocation-free entry point.
 int nerf_static_scratch(int dev, void** ptr, size_t* bytes);
 
+// The DLRM bottom MLP (K0 -> 512 -> 256 -> 128, apps/dlrm_botmlp) as one fused
+// kernel: supported for K0 <= 32, identity or ReLU after the first two layers
+// and any activation after the third (acts[0..2]); x and out 16-byte aligned.
+// w[i], b[i]: layer i+1's [K, N] weight and [N] bias (b may be null).  The
+// workspace (dlrm_bot_workspace() bytes, 16-byte aligned) receives the packed
+// weights.  dtype: GP_DTYPE_F16 or GP_DTYPE_BF16, the element type of every
+// tensor.
+inline bool dlrm_bot_supported(int64_t K0, const int* acts) {
+  auto hidden = [](int a) { return a == GP_ACT_NONE || a == GP_ACT_RELU; };
+  return K0 >= 1 && K0 <= 32 && hidden(acts[0]) && hidden(acts[1]) && acts[2] >= GP_ACT_NONE &&
+         acts[2] <= GP_ACT_SIGMOID;
+}
+size_t dlrm_bot_workspace();
+hipError_t dlrm_bot_launch(int64_t M, int K0, const void* x, const void* const* w, const void* const* b,
+                           const int* acts, void* out, void* ws, int num_cus, hipStream_t stream,
+                           int dtype = GP_DTYPE_F16);
+
 }  // namespace gp

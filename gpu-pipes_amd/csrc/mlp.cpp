@@ -105,6 +105,27 @@ int run_chain(int64_t M, int nl, const int64_t* widths, const void* const* w, co
   int dev = 0, ncu = 0;
   int rc = current_device_info(&dev, &ncu);
   if (rc) return rc;
+  if (nl == 3 && widths[1] == 512 && widths[2] == 256 && widths[3] == 128 && dlrm_bot_supported(widths[0], acts)) {
+    // The DLRM bottom MLP's shape: one fused kernel, activations on chip.  An
+    // input or output that is not 16-byte aligned (a row slice, say) goes
+    // through the workspace, so results never depend on how tensors are sliced.
+    const bool cx = !aligned16(x), co = !aligned16(out);
+    Carve cv;
+    const size_t o_pk = cv.take(dlrm_bot_workspace());
+    const size_t o_x = cx ? cv.take((size_t)M * widths[0] * 2) : 0;
+    const size_t o_o = co ? cv.take((size_t)M * widths[3] * 2) : 0;
+    char* ws = nullptr;
+    if ((rc = workspace_acquire(dev, s, cv.off, (void**)&ws))) return rc;
+    hipError_t e = hipSuccess;
+    if (cx) e = hipMemcpyAsync(ws + o_x, x, (size_t)M * widths[0] * 2, hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) return fail_hip(e, "DLRM input alignment copy");
+    e = dlrm_bot_launch(M, (int)widths[0], cx ? ws + o_x : x, w, b, acts, co ? ws + o_o : out, ws + o_pk, ncu, s,
+                        dtype);
+    if (e != hipSuccess) return fail_hip(e, "DLRM bottom MLP fused kernel launch");
+    if (co && (e = hipMemcpyAsync(out, ws + o_o, (size_t)M * widths[3] * 2, hipMemcpyDeviceToDevice, s)) != hipSuccess)
+      return fail_hip(e, "DLRM output copy");
+    return GP_OK;
+  }
   const int64_t CH = M < kChunkRows ? M : kChunkRows;
   std::vector<int64_t> kin(nl), np(nl);
   int64_t maxnp = 0;
