@@ -488,9 +488,10 @@ def bench_chain(args):
                   "accumulate": "f32", "tile_rows": 256}
         data = "synthetic (positional encodings of U(-1,1) points and unit directions, Kaiming-uniform, seed 0)"
         unit = "samples/s"
-    launch = {"dlrm": "one step: the bottom MLP as the weight-packing kernel plus one fused three-layer kernel "
-                      "over 256-row tiles; the top MLP as one weight-preparation launch, then a wide-GEMM launch "
-                      "per layer (the one-output click head a GEMV launch)",
+    launch = {"dlrm": "one step: the bottom MLP as a weight-packing launch plus one fused three-layer kernel "
+                      "over 256-row tiles; the top MLP as one weight-preparation launch, a wide-GEMM launch for "
+                      "each of its first three layers, then a weight-packing launch plus one fused kernel for "
+                      "512 -> 256 -> 1 (the click head)",
               "nerf": "one step: the weight-packing kernel, then the fused 12-layer kernel over 256-row tiles",
               "bert_addln": "one step: one gp_bert_addln_ffn_out call (fused: weight transposes, then GEMM0 + b0 + x, "
                             "LN0, GEMM1 + act, GEMM2 + b2 + h0, LN2; pipelined: one queue-chained kernel)",

@@ -454,7 +454,276 @@ __global__ __launch_bounds__(256) void dlrm_pack_kernel(PackArgs a) {
   ((half_t*)(a.pack + P_BIAS))[t] = (b && ln < 32) ? b[32 * fb + ln] : (half_t)0.f;
 }
 
+// ------------------------------------------------------------------ tail
+// The last two layers of the DLRM top MLP (apps/dlrm_topmlp: ... -> K -> 256
+// -> 1, the click head) as one persistent kernel: K -> 256 on MFMA with the
+// 256 accumulators of a wave's 32 rows in registers, then the one-output
+// layer as a dot product in the epilogue.  The reference chains these as
+// stage blocks linked by queues (apps/dlrm_topmlp/pipelined/
+// dlrm_topmlp_pl.cuh:185-224); here the 256-wide activations never leave the
+// CU and the click head needs no launch of its own.
+//
+//  * Eight waves (two per SIMD) own a 256-row tile, wave w its rows 32w ..
+//    32w+31.  The weights stream from L2 as in the bottom MLP: slot j holds
+//    k-blocks 2j, 2j+1 for the eight feature blocks (ST = K / 32 slots a
+//    tile), here in a ring of TS = 4 slots, every wave copying two of a
+//    slot's sixteen fragments.
+//  * The layer input comes from HBM straight into registers: the B operand of
+//    k-block kb for lane (row lr, half lh) is the 16 bytes x[row][16 kb + 8 lh
+//    ..], so each wave loads its own rows, two 16-byte loads per slot, into TS
+//    register sets (set = slot % TS; ST is a multiple of TS, so a slot's set
+//    does not depend on its tile).
+//  * While slot i is computed a wave issues the input loads of slot i + TS - 1
+//    and then its ring copies (OPS memory operations), the same order the
+//    prologue uses for slots 0 .. TS-2.  vmcnt counts them in issue order, so
+//    acquiring slot i waits until at most the (TS - 2) OPS operations issued
+//    after slot i's copies are in flight, which also covers slot i's input
+//    loads (issued just before its copies).
+//  * Epilogue: out[row] = act(sum_f relu?(fp16(acc_f)) w5[f] + b5) -- the
+//    hidden values rounded to the element type as a separate layer would
+//    store them -- each lane summing its 128 features, v_permlane32_swap
+//    adding the other half-wave's.
+namespace tail {
+
+constexpr int TS = 4;                 // ring slots = input register sets
+constexpr int TCPW = FPS / NW;        // ring copies per wave per slot
+constexpr int OPS = 2 + TCPW;         // memory operations per wave per slot
+constexpr int kWait = (TS - 2) * OPS;
+static_assert(FPS % NW == 0, "copies per wave");
+// LDS: ring, bias table (8 feature blocks), head weights (fp32).
+constexpr int L_B = TS * SLOT, L_W = L_B + 64 * FB2 * 2, LDS_BYTES = L_W + H2 * 4;
+static_assert(LDS_BYTES <= 160 * 1024, "LDS");
+
+// Packed block: ST slots, the bias table, then w5 [256] and b5 as fp32.
+constexpr size_t p_bias(int ST) { return (size_t)ST * SLOT; }
+constexpr size_t p_head(int ST) { return p_bias(ST) + 64 * FB2 * 2; }
+constexpr size_t p_total(int ST) { return p_head(ST) + (H2 + 4) * 4; }
+
+struct TailArgs {
+  const half_t* x;   // [M][K]
+  const char* pack;  // p_total(K / 32) bytes (dlrm_tail_pack_kernel)
+  half_t* out;       // [M] (one output per row)
+  int64_t M;
+  int relu;          // ReLU after the K -> 256 layer (else identity)
+  int act_out;       // activation of the click head (ACT_*)
+};
+
+__device__ __forceinline__ h8 buf_load_h8(__amdgpu_buffer_rsrc_t rsrc, int off) {
+  return __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
+}
+
+template <typename E, int ST>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void dlrm_tail_kernel(TailArgs p) {
+  static_assert(ST % TS == 0, "a slot's input register set must not depend on its tile");
+  constexpr int K = 32 * ST;
+  __shared__ __attribute__((aligned(1024))) char smem[LDS_BYTES];
+  GP_LDS char* const ring = (GP_LDS char*)smem;
+  GP_LDS half_t* const bfrag = (GP_LDS half_t*)(smem + L_B);
+  GP_LDS float* const w5 = (GP_LDS float*)(smem + L_W);
+
+  const int tid = threadIdx.x;
+  const int lane0 = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = gridDim.x;
+  const int ntiles = (int)((p.M + ROWS - 1) / ROWS);
+  const int my = (ntiles - (int)blockIdx.x + G - 1) / G;  // tiles blockIdx.x + k G, k < my
+
+  for (int i = tid; i < 64 * FB2 / 8; i += NT) ((GP_LDS h8*)bfrag)[i] = ((const h8*)(p.pack + p_bias(ST)))[i];
+  for (int i = tid; i < H2; i += NT) w5[i] = ((const float*)(p.pack + p_head(ST)))[i];
+  const float b5 = ((const float*)(p.pack + p_head(ST)))[H2];
+  __syncthreads();
+
+  auto tile_r0 = [&](int k) { return ((int64_t)blockIdx.x + (int64_t)k * G) * ROWS; };
+  const int lh = lane0 >> 5;
+  const int trow = 32 * wave + (lane0 & 31);  // this lane's row within a tile
+
+  // Input loads of global slot g (this workgroup's tile g / ST, k-blocks
+  // 2 (g % ST) and +1) into register set R.  Past the last tile the range is
+  // 0: the loads read zeros and every wave keeps the same count in flight.
+  h8 xin[TS][2];
+  auto load_input = [&](int g, auto rc) {
+    constexpr int R = decltype(rc)::value;
+    const int kk = g / ST, ls = g % ST;
+    const int64_t row0 = tile_r0(kk);
+    const int64_t left = kk < my ? p.M - row0 : 0;
+    const int rows = left <= 0 ? 0 : left < ROWS ? (int)left : ROWS;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.x + row0 * K, rows * K * 2);
+    const int off = (trow * K + 32 * ls + 8 * lh) * 2;
+    xin[R][0] = buf_load_h8(rs, off);
+    xin[R][1] = buf_load_h8(rs, off + 32);
+  };
+
+  // Ring of TS slots: global slot q lives in ring slot q % TS; copying slot q
+  // is every wave's TCPW fragments of it.  Past the last tile the range is 0.
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.pack, ST * SLOT);
+  auto issue = [&](int q) {
+    const int kk = q / ST, ls = q % ST;
+    const __amdgpu_buffer_rsrc_t r = kk < my ? rw : make_rsrc(p.pack, 0);
+    GP_LDS char* const dst = ring + (q % TS) * SLOT;
+#pragma unroll
+    for (int i = 0; i < TCPW; ++i) {
+      const int c = NW * i + wave;
+      dma16_buf_so(r, 16 * lane0, ls * SLOT + c * FRAG, dst + c * FRAG);
+    }
+  };
+  // Prologue: slots 0 .. TS-2, inputs then copies, as a slot's iteration
+  // issues them.
+  static_for(std::make_integer_sequence<int, TS - 1>{}, [&](auto uc) {
+    load_input(decltype(uc)::value, uc);
+    issue(decltype(uc)::value);
+  });
+
+  f16x acc[FB2];
+  h8 fa[4];
+  h8 ones = {};
+  ones[0] = __builtin_bit_cast(half_t, lane0 < 32 ? E::kOne : (unsigned short)0);
+
+  for (int k = 0; k < my; ++k) {
+    const int64_t r0 = tile_r0(k);
+    const int vrows = p.M - r0 < ROWS ? (int)(p.M - r0) : ROWS;
+#pragma unroll
+    for (int fb = 0; fb < FB2; ++fb) {
+      h8 a = {};
+      a[0] = bfrag[64 * fb + lane0];
+      acc[fb] = E::mma(a, ones, f16x{});
+    }
+#pragma nounroll
+    for (int grp = 0; grp < ST / TS; ++grp) {
+      const int i0 = k * ST + grp * TS;  // global slot of the group's first slot
+      static_for(std::make_integer_sequence<int, TS>{}, [&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        // acquire slot i0 + u (ring slot u)
+        wait_vmcnt<kWait>();
+        lds_barrier();
+        GP_LDS const char* const s = (GP_LDS const char*)(ring + u * SLOT) + 16 * lane0;
+        auto fetch = [&](int g) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) fa[i] = *(GP_LDS const h8*)(s + (4 * g + i) * FRAG);
+        };
+        fetch(0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = E::mma(fa[i], xin[u][0], acc[i]);
+        // slot i0 + u + TS - 1 goes into the ring slot and register set of
+        // slot i0 + u - 1, both dead since the barrier
+        load_input(i0 + u + TS - 1, std::integral_constant<int, (u + TS - 1) % TS>{});
+        issue(i0 + u + TS - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[4 + i] = E::mma(fa[i], xin[u][0], acc[4 + i]);
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(2);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = E::mma(fa[i], xin[u][1], acc[i]);
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(3);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[4 + i] = E::mma(fa[i], xin[u][1], acc[4 + i]);
+      });
+    }
+    // Click head.  Lane (row, half lh) holds features 32 fb + 8 g + 4 lh + e
+    // in element 4 g + e of block fb.
+    float sum = 0.f;
+#pragma unroll
+    for (int fb = 0; fb < FB2; ++fb) {
+      h8 lo, hi;
+      to_operands<E>(acc[fb], p.relu != 0, lo, hi);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f4 w = *(GP_LDS const f4*)(w5 + 32 * fb + 8 * g + 4 * lh);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum = __builtin_fmaf(E::val(g < 2 ? lo[4 * g + e] : hi[4 * g - 8 + e]), w[e], sum);
+      }
+    }
+    sum = sum_lane_halves(sum);
+    const unsigned short o = __builtin_bit_cast(unsigned short, E::cvt1(apply_act(sum + b5, p.act_out)));
+    // lanes of the upper half store past the range (dropped): one store
+    // instruction per wave and tile, whatever the row count
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(p.out + r0, vrows * 2);
+    __builtin_amdgcn_raw_buffer_store_b16(o, ro, lh == 0 ? 2 * trow : 2 * ROWS, 0, 0);
+  }
+  // The copies and loads issued past the last tile land before the waves exit.
+  wait_vmcnt<0>();
+}
+
+struct TailPackArgs {
+  const half_t* w4;  // [K][256]
+  const half_t* b4;  // [256] or null
+  const half_t* w5;  // [256] (the [256, 1] weight)
+  const half_t* b5;  // [1] or null
+  int ST;
+  char* pack;
+};
+
+// One thread per 16-byte lane chunk of the slot stream, then one per bias
+// entry, then one per head weight (and b5).
+template <typename E>
+__global__ __launch_bounds__(256) void dlrm_tail_pack_kernel(TailPackArgs a) {
+  const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+  const int nst = a.ST * SLOT / 16;
+  if (gid < nst) {
+    const int f = gid / kWave, lane = gid % kWave, h = lane >> 5;
+    const int kb = f / FB2, fb = f % FB2;  // slot j: k-blocks 2j, 2j+1 x feature blocks 0-7
+    const int out = 32 * fb + (lane & 31);
+    h8 v;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] = a.w4[(int64_t)(16 * kb + 8 * h + q) * H2 + out];
+    *(h8*)(a.pack + (size_t)gid * 16) = v;
+    return;
+  }
+  const int t = gid - nst;
+  if (t < 64 * FB2) {
+    const int fb = t / 64, ln = t % 64;
+    ((half_t*)(a.pack + p_bias(a.ST)))[t] = (a.b4 && ln < 32) ? a.b4[32 * fb + ln] : (half_t)0.f;
+    return;
+  }
+  const int hI = t - 64 * FB2;
+  float* const head = (float*)(a.pack + p_head(a.ST));
+  if (hI < H2) head[hI] = E::val(a.w5[hI]);
+  else if (hI == H2) head[H2] = a.b5 ? E::val(a.b5[0]) : 0.f;
+}
+
+}  // namespace tail
 }  // namespace dlrm
+
+size_t dlrm_tail_workspace(int64_t K) { return dlrm::tail::p_total((int)(K / 32)); }
+
+hipError_t dlrm_tail_launch(int64_t M, int64_t K, const void* x, const void* w4, const void* b4, int act4,
+                            const void* w5, const void* b5, int act5, void* out, void* ws, int num_cus,
+                            hipStream_t s, int dtype, bool pack) {
+  using namespace dlrm;
+  using namespace dlrm::tail;
+  if (dtype != GP_DTYPE_F16 && dtype != GP_DTYPE_BF16) return hipErrorInvalidValue;
+  if (M <= 0) return hipSuccess;
+  if (M > (int64_t(1) << 31) - 1 || !dlrm_tail_supported(K, act4, act5)) return hipErrorInvalidValue;
+  if (((uintptr_t)x & 15) || ((uintptr_t)ws & 15) || ((uintptr_t)out & 1)) return hipErrorInvalidValue;
+  const int ST = (int)(K / 32);
+  TailPackArgs pa{(const half_t*)w4, (const half_t*)b4, (const half_t*)w5, (const half_t*)b5, ST, (char*)ws};
+  const int nthreads = ST * SLOT / 16 + 64 * FB2 + H2 + 1;
+  if (pack) {
+    if (dtype == GP_DTYPE_BF16)
+      hipLaunchKernelGGL(dlrm_tail_pack_kernel<BF16>, dim3((nthreads + 255) / 256), dim3(256), 0, s, pa);
+    else
+      hipLaunchKernelGGL(dlrm_tail_pack_kernel<F16>, dim3((nthreads + 255) / 256), dim3(256), 0, s, pa);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  const TailArgs a{(const half_t*)x, (const char*)ws, (half_t*)out, M, act4 == GP_ACT_RELU, act5};
+  const int64_t tiles = (M + ROWS - 1) / ROWS;
+  const dim3 grid((unsigned)(tiles < num_cus ? tiles : num_cus));
+#define GP_TAIL(T, S) hipLaunchKernelGGL((dlrm_tail_kernel<T, S>), grid, dim3(NT), 0, s, a)
+  if (dtype == GP_DTYPE_BF16) {
+    if (ST == 8) GP_TAIL(BF16, 8);
+    else if (ST == 16) GP_TAIL(BF16, 16);
+    else GP_TAIL(BF16, 32);
+  } else {
+    if (ST == 8) GP_TAIL(F16, 8);
+    else if (ST == 16) GP_TAIL(F16, 16);
+    else GP_TAIL(F16, 32);
+  }
+#undef GP_TAIL
+  return hipGetLastError();
+}
 
 size_t dlrm_bot_workspace() { return dlrm::P_TOTAL; }
 

@@ -214,6 +214,21 @@ inline bool dlrm_bot_supported(int64_t K0, const int* acts) {
          acts[2] <= GP_ACT_SIGMOID;
 }
 size_t dlrm_bot_workspace();
+// The last two layers of the DLRM top MLP (K -> 256 -> 1, the click head,
+// apps/dlrm_topmlp) as one fused kernel: K 256, 512 or 1024 with x [M][K]
+// 16-byte aligned, identity or ReLU after the K -> 256 layer, any activation
+// after the click head; out [M] (2-byte aligned).  w4 [K][256], b4 [256], w5
+// [256] (the [256, 1] weight), b5 [1] (biases may be null).  The workspace
+// (dlrm_tail_workspace(K) bytes, 16-byte aligned) receives the packed weights
+// when `pack` is set (calls over row chunks of one set of weights pack once).
+inline bool dlrm_tail_supported(int64_t K, int act4, int act5) {
+  return (K == 256 || K == 512 || K == 1024) && (act4 == GP_ACT_NONE || act4 == GP_ACT_RELU) &&
+         act5 >= GP_ACT_NONE && act5 <= GP_ACT_SIGMOID;
+}
+size_t dlrm_tail_workspace(int64_t K);
+hipError_t dlrm_tail_launch(int64_t M, int64_t K, const void* x, const void* w4, const void* b4, int act4,
+                            const void* w5, const void* b5, int act5, void* out, void* ws, int num_cus,
+                            hipStream_t stream, int dtype = GP_DTYPE_F16, bool pack = true);
 hipError_t dlrm_bot_launch(int64_t M, int K0, const void* x, const void* const* w, const void* const* b,
                            const int* acts, void* out, void* ws, int num_cus, hipStream_t stream,
                            int dtype = GP_DTYPE_F16);

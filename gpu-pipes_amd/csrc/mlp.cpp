@@ -141,6 +141,13 @@ int run_chain(int64_t M, int nl, const int64_t* widths, const void* const* w, co
   // A one-output last layer (the DLRM click head) is a GEMV over the previous
   // activations, written straight to out.
   const bool gemv_head = widths[nl] == 1 && nl >= 2 && widths[nl - 1] % 8 == 0 && aligned16(w[nl - 1]);
+  // ... -> K -> 256 -> 1 (the DLRM top MLP's tail): the last two layers as one
+  // fused kernel, written straight to out.  Its input rows are K wide: the
+  // chain input (read in place or padded to kin[0] = K) or a previous layer's
+  // output (np = K).
+  const int tl = nl - 2;  // first layer of the fused tail
+  const bool fused_tail =
+      widths[nl] == 1 && nl >= 2 && widths[nl - 1] == 256 && dlrm_tail_supported(widths[tl], acts[tl], acts[nl - 1]);
   Carve cv;
   std::vector<size_t> o_wt(nl), o_b(nl);
   for (int i = 0; i < nl; ++i) {
@@ -150,17 +157,19 @@ int run_chain(int64_t M, int nl, const int64_t* widths, const void* const* w, co
   const size_t o_x = direct_in ? 0 : cv.take((size_t)CH * kin[0] * 2);
   const size_t o_h0 = cv.take((size_t)CH * maxnp * 2);
   const size_t o_h1 = cv.take((size_t)CH * maxnp * 2);
+  const size_t o_tail = fused_tail ? cv.take(dlrm_tail_workspace(widths[tl])) : 0;
   char* ws = nullptr;
   if ((rc = workspace_acquire(dev, s, cv.off, (void**)&ws))) return rc;
 
   // Layers whose weights cannot be read in place are transposed and padded
-  // into the workspace (one launch for all of them).
+  // into the workspace (one launch for all of them); the fused tail packs its
+  // own.
   std::vector<Prepared> L(nl);
   std::vector<PrepSpec> ps;
   double flop = 0;
   for (int i = 0; i < nl; ++i) flop += 2.0 * M * widths[i] * widths[i + 1];
   const bool chain = weights_in_place(flop);
-  for (int i = 0; i < nl; ++i) {
+  for (int i = 0; i < (fused_tail ? tl : nl); ++i) {
     if (in_place(chain, widths[i + 1], w[i], b[i])) {
       L[i] = {nullptr, b[i], kin[i], np[i], acts[i], w[i], widths[i]};
     } else {
@@ -184,6 +193,11 @@ int run_chain(int64_t M, int nl, const int64_t* widths, const void* const* w, co
     }
     for (int i = 0; i < nl && e == hipSuccess; ++i) {
       const bool last = i == nl - 1;
+      if (i == tl && fused_tail) {
+        e = dlrm_tail_launch(rows, widths[tl], a, w[tl], b[tl], acts[tl], w[nl - 1], b[nl - 1], acts[nl - 1],
+                             (void*)row_ptr(out, r0, 1), ws + o_tail, ncu, s, dtype, r0 == 0);
+        break;
+      }
       if (last && gemv_head) {
         e = gemv1_launch(rows, widths[i], a, lda, w[i], b[i], acts[i], (void*)row_ptr(out, r0, 1), ncu, s, dtype);
         break;
@@ -193,7 +207,7 @@ int run_chain(int64_t M, int nl, const int64_t* widths, const void* const* w, co
       a = c;
       lda = np[i];
     }
-    if (e == hipSuccess && !direct_out && !gemv_head)
+    if (e == hipSuccess && !direct_out && !gemv_head && !fused_tail)
       e = place_launch(rows, a, lda, widths[nl], (void*)row_ptr(out, r0, widths[nl]), widths[nl], widths[nl],
                        GP_ACT_NONE, ncu, s);
     if (e != hipSuccess) return fail_hip(e, "MLP layer launch");

@@ -1,9 +1,11 @@
-"""GPU parity of the fused DLRM bottom MLP (dlrm_fused.hip): every chain of
+"""GPU parity of the fused DLRM kernels (dlrm_fused.hip).  Every chain of
 gp_mlp_out / gp_mlp_dtype_out shaped K0 -> 512 -> 256 -> 128 with K0 <= 32,
 identity or ReLU after the first two layers, runs as one kernel whose
 activations never leave the CU (the reference's
 apps/dlrm_botmlp/pipelined/dlrm_botmlp_pl.cuh:79-173 runs the same tower as
-one queue-chained kernel).
+one queue-chained kernel); a chain ending K -> 256 -> 1 (K 256, 512 or 1024,
+the DLRM top MLP's tail with its click head, dlrm_topmlp_pl.cuh:185-224) runs
+its last two layers as one kernel.
 
 Checked against the CPU oracle at the fp16 I/O bar (max-abs 2e-2, rel-L2
 5e-3; bf16: 8x) over every row, for input widths that fill one or two MFMA
@@ -143,3 +145,85 @@ def test_dlrm_bottom_fused_back_to_back_weights(cuda):
         y, want, *_ = run(cuda, 513, 16, seed=30)
     torch.cuda.synchronize()
     check(f(y), want, "dlrm bottom second stream")
+
+
+# ------------------------------------------------------------------ top MLP tail: K -> 256 -> 1
+def run_tail(cuda, M, widths, acts, seed=0, bias=True, dtype=torch.float16, x=None):
+    ws, bs = dlrm_params(widths, seed=seed + widths[0], init="xavier")
+    if not bias:
+        bs = [None] * len(ws)
+    ws = [w.to(dtype) for w in ws]
+    bs = [None if b is None else b.to(dtype) for b in bs]
+    if x is None:
+        x = normal_fp16(M, widths[0], seed=seed + M, dtype=dtype)
+    y = gpipes.mlp_out(x.to(cuda), to(ws, cuda), to(bs, cuda), list(acts))
+    want = oracle.mlp(f(x), [f(w) for w in ws], [f(b) for b in bs], [ACT[a] for a in acts])
+    return y, want, x, ws, bs
+
+
+@pytest.mark.parametrize("K", [256, 512, 1024])
+@pytest.mark.parametrize("M", [1, 255, 257, 3000])
+def test_dlrm_tail_fused_vs_oracle(cuda, K, M):
+    """A chain ending K -> 256 -> 1 (K 256, 512, 1024) runs its last two layers
+    as the fused tail kernel: here the whole chain is the tail."""
+    print(f"[dlrm-tail] K={K} M={M}", flush=True)
+    y, want, *_ = run_tail(cuda, M, [K, 256, 1], ["relu", "sigmoid"])
+    assert y.shape == (M, 1)
+    check(f(y), want, f"tail K={K} M={M}")
+
+
+@pytest.mark.parametrize("acts", [("none", "none"), ("relu", "gelu_tanh"), ("none", "relu"), ("relu", "none")])
+def test_dlrm_tail_fused_activations(cuda, acts):
+    print(f"[dlrm-tail] acts={acts}", flush=True)
+    y, want, *_ = run_tail(cuda, 1000, [512, 256, 1], acts, seed=4)
+    check(f(y), want, f"tail acts={acts}")
+
+
+def test_dlrm_tail_fused_null_biases(cuda):
+    y, want, *_ = run_tail(cuda, 900, [512, 256, 1], ["relu", "sigmoid"], bias=False, seed=6)
+    check(f(y), want, "tail without biases")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, BF])
+def test_dlrm_top_mlp_with_fused_tail(cuda, dtype):
+    """The DLRM top MLP 480 -> 1024 -> 1024 -> 512 -> 256 -> 1: three GEMM
+    launches, then the tail kernel reading the 512-wide activations from the
+    workspace."""
+    print(f"[dlrm-tail] top MLP {dtype}", flush=True)
+    y, want, *_ = run_tail(cuda, 3000, [480, 1024, 1024, 512, 256, 1], ["relu"] * 4 + ["sigmoid"], seed=8,
+                           dtype=dtype)
+    assert y.dtype == dtype
+    check(f(y), want, f"top MLP {dtype}", bf16=dtype == BF)
+
+
+def test_dlrm_tail_fused_two_chunks_rows_independent(cuda):
+    """M = 300,077: two row chunks (262,144 + 37,933; the weights are packed once,
+    with the first), several tiles per workgroup and a partial last tile.  Every
+    row against the oracle; rows of small calls bit-identical to the same rows
+    of the large call."""
+    M = 300077
+    print(f"[dlrm-tail] two chunks M={M}", flush=True)
+    y, want, x, ws, bs = run_tail(cuda, M, [512, 256, 1], ["relu", "sigmoid"], seed=10)
+    check(f(y), want, f"tail all {M} rows")
+    wd, bd, xd = to(ws, cuda), to(bs, cuda), x.to(cuda)
+    for a, b in ((0, 300), (262000, 262400), (M - 77 - 256, M)):
+        small = gpipes.mlp_out(xd[a:b].contiguous(), wd, bd, ["relu", "sigmoid"])
+        assert torch.equal(small.view(torch.int16), y[a:b].view(torch.int16)), (a, b)
+
+
+def test_dlrm_tail_fused_unaligned_bit_exact(cuda):
+    """x at a 2-byte offset (copied into the workspace first) and out at a
+    2-byte offset (written in place, one 2-byte store per row): the result
+    equals the aligned call bit for bit."""
+    M, K = 777, 512
+    y, want, x, ws, bs = run_tail(cuda, M, [K, 256, 1], ["relu", "sigmoid"], seed=12)
+    wd, bd = to(ws, cuda), to(bs, cuda)
+    xbuf = torch.zeros(M * K + 8, dtype=torch.float16, device=cuda)
+    xu = xbuf[1:1 + M * K].view(M, K)
+    xu.copy_(x.to(cuda))
+    obuf = torch.zeros(M + 8, dtype=torch.float16, device=cuda)
+    ou = obuf[1:1 + M].view(M, 1)
+    gpipes.mlp_out(xu, wd, bd, ["relu", "sigmoid"], out=ou)
+    torch.cuda.synchronize()
+    assert torch.equal(ou.view(torch.int16), y.view(torch.int16))
+    assert float(obuf[0]) == 0.0 and float(obuf[1 + M]) == 0.0
