@@ -215,6 +215,36 @@ def _settle(run_one, stream, settle_ms):
     return {"ms": (time.perf_counter() - t0) * 1e3, "launches": n}
 
 
+def start_telemetry(delay_s=1.0):
+    """Start a child process that reads the board's telemetry (rocm-smi
+    --showmetrics: socket power, per-XCD engine clocks, activity; rocm-smi -M:
+    the power cap) delay_s from now, while the settle launches run."""
+    import subprocess
+
+    smi = "/opt/rocm/bin/rocm-smi"
+    cmd = f"sleep {delay_s}; {smi} --showmetrics; {smi} -M"
+    return subprocess.Popen(["bash", "-c", cmd], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+
+
+def finish_telemetry(child):
+    """Parse the telemetry child's output into a small record."""
+    import re
+
+    out, _ = child.communicate(timeout=120)
+
+    def field(name):
+        m = re.search(re.escape(name) + r"[^:]*:\s*(\[[^\]]*\]|[0-9.]+)", out)
+        if not m:
+            return None
+        v = m.group(1)
+        return [float(t) for t in v.strip("[]").split(",") if t.strip()] if v.startswith("[") else float(v)
+
+    return {"source": "rocm-smi --showmetrics and -M, read about 1 s into the settle phase",
+            "socket_power_w": field("current_socket_power"), "power_cap_w": field("Max Graphics Package Power"),
+            "gfxclk_mhz_per_xcd": field("current_gfxclks"), "gfx_activity_pct": field("average_gfx_activity"),
+            "umc_activity_pct": field("average_umc_activity")}
+
+
 def timed_steps(step, args, dev):
     """Warm-up and synchronise, then a settle phase and the timed region back
     to back: the settle launches keep the GPU busy up to the first timed step,
@@ -234,8 +264,11 @@ def timed_steps(step, args, dev):
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     outer = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
     settle = {"ms": 0.0, "launches": 0}
-    if args.settle_ms > 0:
-        settle = _settle(lambda n: step(args.warmup + n), stream, args.settle_ms)
+    settle_ms, tel = args.settle_ms, None
+    if getattr(args, "telemetry", False):
+        settle_ms, tel = max(settle_ms, 3000.0), start_telemetry()
+    if settle_ms > 0:
+        settle = _settle(lambda n: step(args.warmup + n), stream, settle_ms)
     outer[0].record(stream)
     for i in range(args.steps):
         ev[i][0].record(stream)
@@ -243,6 +276,8 @@ def timed_steps(step, args, dev):
         ev[i][1].record(stream)
     outer[1].record(stream)
     torch.cuda.synchronize()
+    if tel is not None:
+        settle["telemetry"] = finish_telemetry(tel)
     return [a.elapsed_time(b) for a, b in ev], outer[0].elapsed_time(outer[1]) / args.steps, settle
 
 
@@ -626,6 +661,10 @@ def main():
                     help="fused MGN workloads: load the diagnostic library (libgpipes_phase.so: the fused "
                          "kernel with s_memtime phase timers, about 1%% slower) and add the last launch's "
                          "cycles per tile and phase to the line as \"phase_cycles\"; not a headline run")
+    ap.add_argument("--telemetry", action="store_true",
+                    help="read the board's socket power, power cap and per-XCD engine clocks (rocm-smi, in a "
+                         "child process) during a settle phase of at least 3 s, and add them to the line's "
+                         "\"settle\" record (and, for the MGN workloads, as \"telemetry\")")
     ap.add_argument("--copy-ref", action="store_true",
                     help="first run one plain 1 GiB device copy (a known-size reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -753,6 +792,8 @@ def main():
         rec["library"] = "libgpipes_phase.so (diagnostic build with phase timers)"
     if args.cus:
         rec["config"]["cus"] = args.cus
+    if "telemetry" in settle:
+        rec["telemetry"] = settle["telemetry"]
     print(json.dumps(rec), flush=True)
 
 
