@@ -332,6 +332,10 @@ struct SplitQueueReader {
 // pipes.cuh:60-72
 struct MemoryWriter {
   static constexpr bool kReleaseBarrier = false;  // write_release passes no workgroup barrier
+  // A memory output is read by no later stage of the launch: stages may store
+  // it with the non-temporal policy in whole 128-byte lines, so that it does
+  // not take the L2 lines the queues live in.
+  static constexpr bool kStreamOut = true;
   half_t* base;
   int64_t stride;
   int tile_stride;

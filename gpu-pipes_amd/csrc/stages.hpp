@@ -25,6 +25,8 @@
 // offset 0; stage_lds_bytes<...>() gives the requirement.
 #pragma once
 
+#include <type_traits>
+
 #include "gp_device.hpp"
 #include "pipes.hpp"
 
@@ -182,6 +184,13 @@ __device__ __forceinline__ void stage_mfma_loop(const h8* wf, LD ld, f16x* acc) 
     }
   }
 }
+
+// Whether a writer's output may be stored non-temporally in whole lines
+// (W::kStreamOut; false when a writer does not say).
+template <typename W, typename = void>
+struct stream_out : std::false_type {};
+template <typename W>
+struct stream_out<W, std::void_t<decltype(W::kStreamOut)>> : std::bool_constant<W::kStreamOut> {};
 
 // One GEMM stage over num_iters tiles: out = act(in . W + b [+ acc]) or
 // LayerNorm(in . W + b).
@@ -403,7 +412,19 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
     // for groups g = 2q of the upper half, so each lane holds the eight
     // consecutive features 32 wave + 16 q + 8 lh + (0..7) of its row and
     // writes them with one 16-byte store.
+    //
+    // A LayerNorm stage writing memory (stream_out) stages the tile in its
+    // input tile buffer instead -- free since the LayerNorm barrier, which
+    // follows every wave's MFMAs -- and each wave then stores four whole
+    // 256-byte rows per instruction with the non-temporal policy.  16-byte
+    // chunk c of row r sits at chunk position c ^ (r % 16), so the 32 rows a
+    // wave writes at one chunk and the 16 chunks of a row it reads both
+    // spread over the banks.  Whole-line non-temporal stores keep the output
+    // out of L2, whose lines the queues need; 32-byte pieces would be
+    // written back as partial lines.
+    constexpr bool STAGED = LN && QPF && stream_out<OW>::value && MBLK * N * 2 <= PB;
     const TensorView ot = ow.write_acquire(cur.rows);
+    GP_LDS char* const st = xs + pb * PB;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       const int r = 32 * rb + lr;
@@ -420,13 +441,33 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
         const auto lo = __builtin_amdgcn_permlane32_swap(o[2 * q][0], o[2 * q + 1][0], false, false);
         const auto hi = __builtin_amdgcn_permlane32_swap(o[2 * q][1], o[2 * q + 1][1], false, false);
         const u32x4 w = {(unsigned)lo[0], (unsigned)hi[0], (unsigned)lo[1], (unsigned)hi[1]};
-        if (r < ot.rows) *(u32x4*)(ot.data + (int64_t)r * ot.stride + 32 * wave + 16 * q + 8 * lh) = w;
+        if constexpr (STAGED) {
+          const int c = 4 * wave + 2 * q + lh;
+          *(GP_LDS u32x4*)(st + r * (N * 2) + ((c ^ (r & 15)) << 4)) = w;
+        } else {
+          if (r < ot.rows) *(u32x4*)(ot.data + (int64_t)r * ot.stride + 32 * wave + 16 * q + 8 * lh) = w;
+        }
+      }
+    }
+    if constexpr (STAGED) {
+      __syncthreads();
+      const int j = lane & 15;
+#pragma unroll
+      for (int i = 0; i < MBLK / 16; ++i) {
+        const int row = (MBLK / 4) * wave + 4 * i + (lane >> 4);
+        const u32x4 v = *(const GP_LDS u32x4*)(st + row * (N * 2) + ((j ^ (row & 15)) << 4));
+        if (row < ot.rows) __builtin_nontemporal_store(v, (u32x4*)(ot.data + (int64_t)row * ot.stride + 8 * j));
       }
     }
     ow.write_release();
     // LDS tile / LN partials are reused by the next iteration; a queue
-    // writer's release already ends with a barrier after every wave's stores
-    if constexpr (!OW::kReleaseBarrier) __syncthreads();
+    // writer's release already ends with a barrier after every wave's stores.
+    // A staged tile needs none either: its barrier follows every wave's reads
+    // of the LN partials and the queue flags, and the next copy into the
+    // staging buffer comes after the next iteration's first barrier (the one
+    // after the tile wait when the next tile was prefetched into the other
+    // buffer, else the one in read_acquire).
+    if constexpr (!OW::kReleaseBarrier && !STAGED) __syncthreads();
     if constexpr (PF) {
       pb = npb;
       cur = nxt;
