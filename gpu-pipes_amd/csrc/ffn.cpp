@@ -237,6 +237,33 @@ int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void*
   return gp_bert_ffn_dtype_out(M, H, FF, x, w1, b1, w2, b2, gamma, beta, eps, act, out, GP_DTYPE_F16, stream);
 }
 
+int gp_bert_ffn_impl_out(int64_t M, int64_t H, int64_t FF, const void* x, const void* w1, const void* b1,
+                         const void* w2, const void* b2, const void* gamma, const void* beta, float eps, int act,
+                         void* out, int impl, void* stream) {
+  if (impl == GP_IMPL_FUSED)
+    return gp_bert_ffn_dtype_out(M, H, FF, x, w1, b1, w2, b2, gamma, beta, eps, act, out, GP_DTYPE_F16, stream);
+  clear_error();
+  int rc;
+  if (impl != GP_IMPL_PIPELINED) return fail(GP_ERR_INVALID_ARG, "unknown impl %d", impl);
+  if (M < 0) return fail(GP_ERR_INVALID_ARG, "M must be >= 0 (got %lld)", (long long)M);
+  if (H != 128 || FF != 512)
+    return fail(GP_ERR_SHAPE, "the pipelined layout is built for the app's shape H = 128, FF = 512 (got %lld, %lld)",
+                (long long)H, (long long)FF);
+  if (M > kMaxRows) return fail(GP_ERR_SHAPE, "M too large (%lld)", (long long)M);
+  if (act != GP_ACT_RELU && act != GP_ACT_GELU_TANH)
+    return fail(GP_ERR_INVALID_ARG, "the pipelined layout supports ReLU and GELU(tanh) only");
+  if (!(eps >= 0.f)) return fail(GP_ERR_INVALID_ARG, "eps must be >= 0");
+  if ((rc = need16(w1, "w1")) || (rc = need16(w2, "w2")) || (rc = opt16(b1, "b1")) || (rc = opt16(b2, "b2")) ||
+      (rc = opt16(gamma, "gamma")) || (rc = opt16(beta, "beta")))
+    return rc;
+  if (M == 0) return GP_OK;
+  if ((rc = need16(x, "x")) || (rc = need16(out, "out"))) return rc;
+  int dev = 0, ncu = 0;
+  if ((rc = current_device_info(&dev, &ncu))) return rc;
+  const BertFfnArgs a{M, H, FF, x, w1, b1, w2, b2, gamma, beta, eps, act, out};
+  return bert_ffn_pipelined_run(a, dev, ncu, (hipStream_t)stream);
+}
+
 int gp_bert_addln_ffn_dtype_out(int64_t M, int64_t H, int64_t FF, const void* attn, const void* x,
                                 const void* w0, const void* b0, const void* w1, const void* b1, const void* w2,
                                 const void* b2, const void* ga0, const void* be0, const void* ga2, const void* be2,

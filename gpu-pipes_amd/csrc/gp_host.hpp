@@ -26,6 +26,9 @@ int mgn_pipelined_run(const MgnArgs& a, bool split_ln, int dev, int num_cus, hip
 // (stage workgroups linked by L2 ring queues; pipe_add / pipe_concat stages
 // fed from queues).  H 128 / FF 512 and Kx a multiple of 8 up to 128 only.
 int bert_addln_pipelined_run(const BertAddlnArgs& a, int dev, int num_cus, hipStream_t stream);
+// The bert_ffn app's queue-chained layout (four W1 column slices, two W2 +
+// residual + LayerNorm workers), H 128 / FF 512 only.
+int bert_ffn_pipelined_run(const BertFfnArgs& a, int dev, int num_cus, hipStream_t stream);
 int nerf_a_pipelined_run(const NerfAArgs& a, int dev, int num_cus, hipStream_t stream);
 
 // Identity pipelines through ring queues (tests the queue protocol).
@@ -39,6 +42,7 @@ constexpr uint32_t kArenaLayoutRoute = 2;  // route kernels (+1 for the split la
 constexpr uint32_t kArenaLayoutBertAddln = 4;
 constexpr uint32_t kArenaLayoutNerfA = 5;
 constexpr uint32_t kArenaLayoutGemmLn = 6;  // LayerNorm-epilogue GEMMs: partial row statistics
+constexpr uint32_t kArenaLayoutBertFfn = 7;
 // GP_ERR_INVALID_ARG if `stream` is capturing into a graph: the queue-chained
 // launches call it before any other HIP call (a replay would reuse the
 // captured queue epoch).

@@ -61,6 +61,19 @@ struct BertAddlnArgs {
   void* out;
 };
 
+// The BERT FFN block of apps/bert_ffn (x [M,H] -> out [M,H]):
+// out = LayerNorm(act(x w1 + b1) w2 + b2 + x) * gamma + beta, w1 [H,FF], w2
+// [FF,H] (weight.t()); biases and affines may be null (gamma null: 1).
+struct BertFfnArgs {
+  int64_t M, H, FF;
+  const void* x;
+  const void *w1, *b1, *w2, *b2;
+  const void *gamma, *beta;
+  float eps;
+  int act;  // GP_ACT_*
+  void* out;
+};
+
 // NerfA of apps/nerf_a (x [M,Kx] -> out [M,256]): five Linear + ReLU layers,
 // the skip concatenation [h | x], three more Linear + ReLU layers.  w[0] is
 // [Kx,256], w[5] [256+Kx,256], the rest [256,256]; biases may be null.

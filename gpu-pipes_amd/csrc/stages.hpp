@@ -153,8 +153,10 @@ __device__ __forceinline__ void load_weight_frags(const TensorView& w, GP_LDS ch
 }
 
 // Parameter vectors (fp16 in memory, stride 0 or 1) -> fp32 LDS array.
-__device__ __forceinline__ void load_param(const TensorView& p, GP_LDS float* dst, int n) {
-  for (int i = threadIdx.x; i < n; i += kStageThreads) dst[i] = p.data ? (float)p.data[p.stride ? i : 0] : 0.f;
+// n parameters into LDS as fp32; a null view reads as `absent` (0 for a bias
+// or beta, 1 for gamma).
+__device__ __forceinline__ void load_param(const TensorView& p, GP_LDS float* dst, int n, float absent = 0.f) {
+  for (int i = threadIdx.x; i < n; i += kStageThreads) dst[i] = p.data ? (float)p.data[p.stride ? i : 0] : absent;
 }
 
 // The k-loop of a tile part: RBP 32-row blocks share the A operand (weight
@@ -242,7 +244,7 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
   for (int i = 0; i < K / 16; ++i) asm volatile("" : "+a"(wf[i]));
   load_param(bias, prm, N);
   if (LN) {
-    load_param(gamma, prm + N, N);
+    load_param(gamma, prm + N, N, 1.f);
     load_param(beta, prm + 2 * N, N);
   }
   __syncthreads();

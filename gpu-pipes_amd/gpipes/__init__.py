@@ -89,6 +89,7 @@ def _load():
     L.gp_gemm_dtype_out.argtypes = [i64, i64, i64, vp, vp, vp, vp, i32, vp, i32, vp]
     L.gp_bert_ffn_out.argtypes = [i64, i64, i64] + [vp] * 7 + [f32, i32, vp, vp]
     L.gp_bert_ffn_dtype_out.argtypes = [i64, i64, i64] + [vp] * 7 + [f32, i32, vp, i32, vp]
+    L.gp_bert_ffn_impl_out.argtypes = [i64, i64, i64] + [vp] * 7 + [f32, i32, vp, i32, vp]
     L.gp_mlp_out.argtypes = [i64, i32, vp, vp, vp, vp, vp, vp, vp]
     L.gp_mlp_dtype_out.argtypes = [i64, i32, vp, vp, vp, vp, vp, vp, i32, vp]
     L.gp_mlp_dtype_out.restype = i32
@@ -489,12 +490,14 @@ def gemm_out(x, w, b=None, r=None, act="none", out=None):
     return out
 
 
-def bert_ffn_out(x, w1, b1, w2, b2, ga, be, out, eps=1e-5, act="relu"):
+def bert_ffn_out(x, w1, b1, w2, b2, ga, be, out, eps=1e-5, act="relu", impl="fused"):
     """LayerNorm(Linear2(act(Linear1(x))) + x) into ``out`` -- bert_ffn_out of
     apps/bert_ffn/pipelined/bert_ffn_pl_ext.cu:24-56 (there H = 128, FF = 512, ReLU,
     eps 1e-5), for H in {128, 256, 512, 1024} and FF a multiple of 128.  Weights
     [in, out] = ``nn.Linear.weight.t().contiguous()``; ga / be may be None (1 / 0).  Every
-    tensor float16, or every tensor bfloat16 (gp_bert_ffn_dtype_out)."""
+    tensor float16, or every tensor bfloat16 (gp_bert_ffn_dtype_out).  impl="pipelined"
+    runs the reference app's queue-chained layout (gp_bert_ffn_impl_out; H 128, FF 512,
+    ReLU or GELU(tanh), float16)."""
     dt = _dtype_of(x)
     _check_input("x", x, dtype=dt)
     if x.dim() != 2:
@@ -513,17 +516,25 @@ def bert_ffn_out(x, w1, b1, w2, b2, ga, be, out, eps=1e-5, act="relu"):
     devs = {t.device for t in (x, w1, b1, w2, b2, ga, be, out) if t is not None}
     if len(devs) != 1:
         raise RuntimeError("all tensors must be on the same device")
+    impl_id = _IMPLS.get(impl, impl)
     with torch.cuda.device(x.device):
-        _check(lib.gp_bert_ffn_dtype_out(M, H, FF, _ptr(x), _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2), _ptr(ga),
-                                         _ptr(be), float(eps), ACTS.get(act, act), _ptr(out), _DTYPES[dt],
-                                         _stream(x)))
+        if impl_id == IMPL_FUSED:
+            _check(lib.gp_bert_ffn_dtype_out(M, H, FF, _ptr(x), _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2), _ptr(ga),
+                                             _ptr(be), float(eps), ACTS.get(act, act), _ptr(out), _DTYPES[dt],
+                                             _stream(x)))
+        else:
+            if dt != torch.float16:
+                raise RuntimeError("the pipelined layout takes float16 tensors only")
+            _check(lib.gp_bert_ffn_impl_out(M, H, FF, _ptr(x), _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2), _ptr(ga),
+                                            _ptr(be), float(eps), ACTS.get(act, act), _ptr(out), impl_id,
+                                            _stream(x)))
     return out
 
 
-def bert_ffn(x, w1, b1, w2, b2, ga, be, eps=1e-5, act="relu"):
+def bert_ffn(x, w1, b1, w2, b2, ga, be, eps=1e-5, act="relu", impl="fused"):
     """Allocating form (bert_ffn_pl_ext.cu:59-72)."""
     out = torch.zeros_like(x)
-    return bert_ffn_out(x, w1, b1, w2, b2, ga, be, out, eps=eps, act=act)
+    return bert_ffn_out(x, w1, b1, w2, b2, ga, be, out, eps=eps, act=act, impl=impl)
 
 
 # ---------------------------------------------------------------------------

@@ -148,6 +148,21 @@ int gp_bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void*
                     void* out, void* stream);
 
 /*
+ * gp_bert_ffn_out with a choice of implementation.  impl GP_IMPL_FUSED (0):
+ * the same call as gp_bert_ffn_out.  GP_IMPL_PIPELINED: the reference app's
+ * queue-chained layout (apps/bert_ffn/pipelined/bert_ffn_pl.cuh:79-162, the
+ * operator bert_ffn_out of bert_ffn_pl_ext.cu:24-56): stage workgroups linked
+ * by ring queues -- four W1 column slices write the FF-wide activations into
+ * one queue, two workers compute W2 + b2 + x and the LayerNorm -- for H = 128,
+ * FF = 512, ReLU or GELU(tanh), any M; failures (a wait that runs out) are
+ * reported by gp_pipeline_check, and the call is refused while the stream is
+ * capturing a graph.  fp16 tensors.
+ */
+int gp_bert_ffn_impl_out(int64_t M, int64_t H, int64_t FF, const void* x, const void* w1, const void* b1,
+                         const void* w2, const void* b2, const void* gamma, const void* beta, float eps, int act,
+                         void* out, int impl, void* stream);
+
+/*
  * gp_bert_ffn_out with the element type of x, the weights, biases, gamma,
  * beta and out given by `dtype`: GP_DTYPE_F16 (the same call) or
  * GP_DTYPE_BF16 (bf16 MFMAs, fp32 accumulation and epilogue arithmetic, the
@@ -429,8 +444,8 @@ int gp_pipe_route(int64_t M, const void* x, void* out, void* out2, int route, in
  * reports device-side failures failed (GP_ERR_TIMEOUT) or completed (GP_OK).
  * Those are the launches of gp_mgn_fullmlp_out, gp_mgn_linears_out,
  * gp_mgn_mlp_out (every impl), gp_mgn_edge_gather_out, gp_pipe_ident,
- * gp_pipe_route, gp_bert_addln_ffn_out / gp_nerf_a_out with
- * GP_IMPL_PIPELINED, and gp_bert_ffn_out / gp_bert_addln_ffn_out (fused) with
+ * gp_pipe_route, gp_bert_ffn_impl_out / gp_bert_addln_ffn_out / gp_nerf_a_out
+ * with GP_IMPL_PIPELINED, and gp_bert_ffn_out / gp_bert_addln_ffn_out (fused) with
  * H > 128: every wait between their workgroups or waves is bounded, and
  * one that runs out makes the launch end early and leave its outputs invalid
  * (the fused kernels store nothing after it).  The pipelined layouts also fail

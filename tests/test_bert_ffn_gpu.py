@@ -49,11 +49,17 @@ def oracle_ffn(x, p, act, eps):
 
 # ------------------------------------------------------------------ golden fixtures
 @pytest.mark.parametrize("name", ["bert_ffn_relu.npz", "bert_ffn_gelu.npz"])
-def test_bert_ffn_golden(cuda, name):
+@pytest.mark.parametrize("impl", ["fused", "pipelined"])
+def test_bert_ffn_golden(cuda, name, impl):
     z = load_golden(name)
     p = {k: torch.from_numpy(z[k]).to(cuda) for k in ("w1", "b1", "w2", "b2", "gamma", "beta")}
-    y = ffn(torch.from_numpy(z["x"]).to(cuda), p, str(z["act"]), float(z["eps"]))
-    assert_parity(f(y), z["expected"], f"golden {name}")
+    if impl == "pipelined" and tuple(p["w1"].shape) != (128, 512):
+        pytest.skip("the pipelined layout is built for the app's shape H 128, FF 512")
+    y = gpipes.bert_ffn(torch.from_numpy(z["x"]).to(cuda), p["w1"], p["b1"], p["w2"], p["b2"], p["gamma"], p["beta"],
+                        eps=float(z["eps"]), act=str(z["act"]), impl=impl)
+    if impl == "pipelined":
+        gpipes.pipeline_check()
+    assert_parity(f(y), z["expected"], f"golden {name} {impl}")
 
 
 def test_bert_ffn_reference_signature(cuda):
@@ -238,3 +244,86 @@ def test_gemm_identity_weight_is_exact(cuda):
     perm = torch.randperm(K, generator=torch.Generator().manual_seed(1)).to(cuda)
     y = gpipes.gemm_out(x, eye[:, perm].contiguous())
     assert torch.equal(y.view(torch.int16), x[:, perm].contiguous().view(torch.int16))
+
+
+# ------------------------------------------------------------------ the reference app's queue-chained layout
+@pytest.mark.parametrize("act", ["relu", "gelu_tanh"])
+@pytest.mark.parametrize("M", [1, 127, 129, 1000, 64 * 512, 100003])
+def test_bert_ffn_pipelined_vs_oracle(cuda, act, M):
+    """impl="pipelined" (gp_bert_ffn_impl_out): the app's layout of
+    apps/bert_ffn/pipelined/bert_ffn_pl.cuh:79-162 at its shape (H 128, FF 512),
+    four W1 column slices feeding two W2 + residual + LayerNorm workers through
+    ring queues, against the oracle over every row; partial last tiles (any M)
+    travel as the queues' row counts."""
+    print(f"[bert-ffn-pipelined] act={act} M={M}", flush=True)
+    p = dev(bert_params(128, 512, seed=M, init="torch", affine_random=True), cuda)
+    x = normal_fp16(M, 128, seed=M + 1, device=cuda)
+    y = gpipes.bert_ffn(x, p["w1"], p["b1"], p["w2"], p["b2"], p["gamma"], p["beta"], eps=1e-5, act=act,
+                        impl="pipelined")
+    gpipes.pipeline_check()
+    assert_parity(f(y), oracle_ffn(x, p, act, 1e-5), f"pipelined {act} M={M}")
+
+
+def test_bert_ffn_pipelined_null_params(cuda):
+    """No biases, no affine (gamma 1, beta 0), in the queue-chained layout."""
+    M = 1500
+    p = dev(bert_params(128, 512, seed=3, init="torch"), cuda)
+    x = normal_fp16(M, 128, seed=4, device=cuda)
+    y = gpipes.bert_ffn(x, p["w1"], None, p["w2"], None, None, None, eps=1e-5, act="relu", impl="pipelined")
+    gpipes.pipeline_check()
+    want = oracle.bert_ffn(f(x), f(p["w1"]), None, f(p["w2"]), None, None, None, act=oracle.ACT_RELU, eps=1e-5)
+    assert_parity(f(y), want, "pipelined without biases or affine")
+
+
+def test_bert_ffn_pipelined_deterministic_and_agrees_with_fused(cuda):
+    """Two calls, and a call on a second stream, are bit-identical (each tile's
+    arithmetic does not depend on which pipeline ran it); the fused (GEMM) form
+    sums in another order and agrees at the fp16 bar."""
+    M = 64 * 512
+    p = dev(bert_params(128, 512, seed=8, init="torch", affine_random=True), cuda)
+    x = normal_fp16(M, 128, seed=9, device=cuda)
+    args = (x, p["w1"], p["b1"], p["w2"], p["b2"], p["gamma"], p["beta"])
+    a = gpipes.bert_ffn(*args, eps=1e-5, act="relu", impl="pipelined")
+    b = gpipes.bert_ffn(*args, eps=1e-5, act="relu", impl="pipelined")
+    s2 = torch.cuda.Stream()
+    with torch.cuda.stream(s2):
+        c = gpipes.bert_ffn(*args, eps=1e-5, act="relu", impl="pipelined")
+        gpipes.pipeline_check()
+    torch.cuda.synchronize()
+    gpipes.pipeline_check()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.equal(a.view(torch.int16), c.view(torch.int16))
+    fused = gpipes.bert_ffn(*args, eps=1e-5, act="relu")
+    assert_parity(f(a), f(fused).astype(np.float64), "pipelined vs fused")
+
+
+def test_bert_ffn_pipelined_rejects_other_shapes(cuda):
+    p = dev(bert_params(256, 1024, seed=1, init="torch"), cuda)
+    x = normal_fp16(300, 256, seed=2, device=cuda)
+    with pytest.raises(gpipes.GpipesError) as ei:
+        gpipes.bert_ffn(x, p["w1"], p["b1"], p["w2"], p["b2"], p["gamma"], p["beta"], impl="pipelined")
+    assert ei.value.code == -2
+
+
+def test_bert_ffn_pipelined_refuses_capture(cuda):
+    """The queue-chained launch takes a new queue epoch per call, which a graph
+    replay would repeat: under capture it fails with GP_ERR_INVALID_ARG and the
+    stream stays usable."""
+    p = dev(bert_params(128, 512, seed=5, init="torch"), cuda)
+    x = normal_fp16(512, 128, seed=6, device=cuda)
+    out = torch.zeros_like(x)
+    args = (x, p["w1"], p["b1"], p["w2"], p["b2"], p["gamma"], p["beta"], out)
+    gpipes.bert_ffn_out(*args, impl="pipelined")
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    err = None
+    with torch.cuda.graph(g):
+        try:
+            gpipes.bert_ffn_out(*args, impl="pipelined")
+        except gpipes.GpipesError as e:
+            err = e
+    assert err is not None and err.code == -1 and "graph" in str(err)
+    out2 = torch.zeros_like(out)
+    gpipes.bert_ffn_out(*args[:-1], out2, impl="pipelined")
+    gpipes.pipeline_check()
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))

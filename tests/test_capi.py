@@ -180,6 +180,32 @@ def test_bert_ffn_empty_batch_is_a_noop():
     assert gpipes.lib.gp_last_error().decode() == ""
 
 
+def _ffn_impl(M=16, H=128, FF=512, x=16, w1=16, b1=16, w2=16, b2=16, g=16, bt=16, eps=1e-5, act=1, out=16, impl=1):
+    """Call gp_bert_ffn_impl_out with fake (never dereferenced) pointers."""
+    vp = ctypes.c_void_p
+    P = lambda v: vp(v) if v else None  # noqa: E731
+    return gpipes.lib.gp_bert_ffn_impl_out(M, H, FF, P(x), P(w1), P(b1), P(w2), P(b2), P(g), P(bt), eps, act,
+                                           P(out), impl, None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(impl=5), -1), (dict(impl=-1), -1), (dict(H=256), -2), (dict(FF=1024), -2), (dict(M=-1), -1),
+    (dict(act=3), -1), (dict(act=0), -1), (dict(eps=-1.0), -1), (dict(w1=0), -1), (dict(x=0), -1),
+    (dict(x=24), -3), (dict(out=8), -3), (dict(w2=40), -3), (dict(g=8), -3),
+    (dict(impl=0, H=768), -2),  # impl 0 is gp_bert_ffn_out's own validation
+])
+def test_bert_ffn_impl_argument_errors(kw, code):
+    """gp_bert_ffn_impl_out: the queue-chained layout is the app's shape (H 128,
+    FF 512) with ReLU or GELU(tanh); bad arguments fail before any device call."""
+    assert _ffn_impl(**kw) == code
+    assert gpipes.lib.gp_last_error().decode() != ""
+
+
+def test_bert_ffn_impl_empty_batch_is_a_noop():
+    assert _ffn_impl(M=0, x=0, out=0) == 0
+    assert _ffn_impl(M=0, x=0, out=0, impl=0) == 0
+
+
 @pytest.mark.parametrize("M,N,K,x,w,r,act,out,code", [
     (16, 100, 128, 16, 16, 0, 0, 16, -2), (16, 128, 96, 16, 16, 0, 0, 16, -2), (16, 32768, 128, 16, 16, 0, 0, 16, -2),
     (-1, 128, 128, 16, 16, 0, 0, 16, -1), (16, 128, 128, 16, 0, 0, 0, 16, -1), (16, 128, 128, 16, 16, 16, 1, 16, -1),
