@@ -9,7 +9,7 @@ stream, the HBM traffic per launch measured with rocprofv3 counters
 host cores.
 
   python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--settle-ms 1000]
-                  [--workload edge|node|edge_gather|bert|dlrm|nerf|bert_addln|nerf_a|queue]
+                  [--workload edge|node|edge_gather|bert|dlrm|nerf|bert_addln|bert_app|nerf_a|queue]
                   [--impl fused|pipelined|pipelined_split_ln] [--no-cpu]
 
 Every line carries "spread": the per-launch HIP-event times of the timed
@@ -368,6 +368,7 @@ CHAIN_METRIC = {
     "nerf": "samples/sec + % fp16 MFMA peak, NeRF full MLP M=1048576 (1×MI355X)",
     "bert_addln": "rows/sec + % fp16 MFMA peak, bert_addln_ffn H=128 FF=512 M=32768 (1×MI355X)",
     "nerf_a": "samples/sec + % fp16 MFMA peak, NerfA trunk M=65536 (1×MI355X)",
+    "bert_app": "rows/sec + % fp16 MFMA peak, bert_ffn app H=128 FF=512 M=32768 (1×MI355X)",
 }
 # The reference apps' own batches: apps/bert_addln_ffn/pipelined/perf.py (64 x 512 rows)
 # and apps/nerf_a/pipelined/val.py (65,536 samples).
@@ -421,6 +422,16 @@ def cpu_baseline_chain(workload, budget_s=10.0):
         def run():
             oracle.bert_addln_ffn(attn, x, *(p[k] for k in keys))
         what = f"oracle bert_addln_ffn fp32 on {Ms} rows"
+    elif workload == "bert_app":
+        from gpipes.synth import bert_params
+        Ms = 4096
+        p = {k: v.float().numpy() for k, v in bert_params(128, 512, seed=0, init="torch").items()}
+        x = normal_fp16(Ms, 128, seed=0).float().numpy()
+
+        def run():
+            oracle.bert_ffn(x, p["w1"], p["b1"], p["w2"], p["b2"], p["gamma"], p["beta"], act=oracle.ACT_RELU,
+                            eps=1e-5)
+        what = f"oracle BertFfn fp32 on {Ms} rows"
     else:
         Ms = 2048
         ws, bs = nerf_a_params(64, seed=0)
@@ -442,8 +453,8 @@ def bench_chain(args):
     import torch
 
     import gpipes
-    from gpipes.synth import (bert_addln_params, dlrm_params, nerf_a_params, nerf_inputs, nerf_params, normal_fp16,
-                              padded_normal, padded_uniform)
+    from gpipes.synth import (bert_addln_params, bert_params, dlrm_params, nerf_a_params, nerf_inputs, nerf_params,
+                              normal_fp16, padded_normal, padded_uniform)
 
     dev = torch.device("cuda:0")
     # element type of every tensor: the fp16 values drawn below, rounded to bf16 for --dtype bf16
@@ -486,6 +497,24 @@ def bench_chain(args):
         config = {"workload": "bert_addln_ffn", "M": M, "H": H, "FF": FF, "act": "relu", "eps": 1e-5,
                   "impl": impl, "accumulate": "f32"}
         data = "synthetic (attn_out, x ~ N(0,1), nn.Linear default init, seed 0)"
+        unit = "rows/s"
+    elif args.workload == "bert_app":
+        # the bert_ffn app at its batch (apps/bert_ffn/pipelined/val.py: 64 x 512 rows, H 128, FF 512, ReLU)
+        M, H, FF = ADDLN["M"], ADDLN["H"], ADDLN["FF"]
+        p = {k: v.to(et).to(dev) for k, v in bert_params(H, FF, seed=0, init="torch").items()}
+        x = normal_fp16(M, H, seed=0, device=dev, dtype=et)
+        out = torch.empty_like(x)
+        impl = "pipelined" if args.impl == "pipelined" else "fused"
+        if et == torch.bfloat16 and impl == "pipelined":
+            raise SystemExit("the pipelined bert_ffn layout runs in f16 only")
+
+        def step(i):
+            gpipes.bert_ffn_out(x, p["w1"], p["b1"], p["w2"], p["b2"], p["gamma"], p["beta"], out, impl=impl)
+        flops = 4 * M * H * FF
+        bytes_ = M * H * 2 * 2
+        config = {"workload": "bert_ffn_app", "M": M, "H": H, "FF": FF, "act": "relu", "eps": 1e-5,
+                  "impl": impl, "accumulate": "f32"}
+        data = "synthetic (x ~ N(0,1), nn.Linear default init, seed 0)"
         unit = "rows/s"
     elif args.workload == "nerf_a":
         M, Kx = NERF_A["M"], NERF_A["Kx"]
@@ -531,7 +560,9 @@ def bench_chain(args):
               "bert_addln": "one step: one gp_bert_addln_ffn_out call (fused: weight transposes, then GEMM0 + b0 + x, "
                             "LN0, GEMM1 + act, GEMM2 + b2 + h0, LN2; pipelined: one queue-chained kernel)",
               "nerf_a": "one step: one gp_nerf_a_out call (fused: the weight-packing kernel, then the NeRF kernel "
-                        "stopped after layer 8; pipelined: one queue-chained kernel)"}
+                        "stopped after layer 8; pipelined: one queue-chained kernel)",
+              "bert_app": "one step: one gp_bert_ffn_impl_out call (fused: GEMM1 + b1 + act, GEMM2 + b2 + x with "
+                          "the LayerNorm in its epilogue; pipelined: one queue-chained kernel)"}
 
     call_ms, ms_per_step, settle = timed_steps(step, args, dev)
     avg_ms = sum(call_ms) / len(call_ms)
@@ -639,7 +670,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["bert", "dlrm", "nerf", "bert_addln", "nerf_a", "queue"],
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["bert", "dlrm", "nerf", "bert_addln", "bert_app", "nerf_a",
+                                                               "queue"],
                     default="edge")
     ap.add_argument("--impl", choices=["fused", "pipelined", "pipelined_split_ln"], default="fused")
     ap.add_argument("--settle-ms", type=float, default=1000.0,
@@ -682,7 +714,7 @@ def main():
     if args.workload == "bert":
         bench_bert(args)
         return
-    if args.workload in ("dlrm", "nerf", "bert_addln", "nerf_a"):
+    if args.workload in ("dlrm", "nerf", "bert_addln", "bert_app", "nerf_a"):
         bench_chain(args)
         return
     if args.workload == "queue":
