@@ -9,7 +9,7 @@ stream, the HBM traffic per launch measured with rocprofv3 counters
 host cores.
 
   python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--settle-ms 1000]
-                  [--workload edge|node|edge_gather|bert|dlrm|nerf|bert_addln|bert_app|nerf_a|queue]
+                  [--workload edge|node|edge_gather|bert|dlrm|nerf|bert_addln|bert_app|nerf_a|queue|mfma_peak]
                   [--impl fused|pipelined|pipelined_split_ln] [--no-cpu]
 
 Every line carries "spread": the per-launch HIP-event times of the timed
@@ -656,6 +656,44 @@ def bench_queue(args):
     print(json.dumps(rec), flush=True)
 
 
+def bench_mfma_peak(args):
+    """The dense MFMA ceiling of the board as it runs: the probe kernel (gp_probe_mfma:
+    two waves per SIMD of back-to-back 32x32x16 MFMAs on register data, no memory
+    traffic), one launch a step, timed like the other workloads.  With --telemetry the
+    line also carries the socket power and engine clocks it ran at."""
+    import torch
+
+    import gpipes
+
+    dev = torch.device("cuda:0")
+    et = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    iters = 4096
+    flops = gpipes.probe_mfma(iters, et)
+
+    def step(i):
+        gpipes.probe_mfma(iters, et)
+    call_ms, ms_per_step, settle = timed_steps(step, args, dev)
+    avg_ms = sum(call_ms) / len(call_ms)
+    tflops = flops / (avg_ms * 1e-3) / 1e12
+    rec = {
+        "metric": f"TFLOP/s, dense {args.dtype} MFMA probe without memory traffic (1×MI355X)",
+        "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": args.dtype, "data": "synthetic register operands in [-1, 1)",
+        "config": {"workload": "mfma_peak_probe", "iters": iters, "waves_per_simd": 2, "accumulators_per_wave": 8,
+                   "instruction": "v_mfma_f32_32x32x16"},
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tflops / MFMA_F16_PEAK_TFLOPS, "traffic": None, "kernel_ms_avg": avg_ms,
+                     "flops_per_launch": flops},
+        "spread": spread(call_ms),
+        "settle": settle,
+        "cpu_baseline": None,
+    }
+    if "telemetry" in settle:
+        rec["telemetry"] = settle["telemetry"]
+    print(json.dumps(rec), flush=True)
+
+
 def load_traffic(workload, impl):
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
@@ -671,7 +709,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["bert", "dlrm", "nerf", "bert_addln", "bert_app", "nerf_a",
-                                                               "queue"],
+                                                               "queue", "mfma_peak"],
                     default="edge")
     ap.add_argument("--impl", choices=["fused", "pipelined", "pipelined_split_ln"], default="fused")
     ap.add_argument("--settle-ms", type=float, default=1000.0,
@@ -719,6 +757,9 @@ def main():
         return
     if args.workload == "queue":
         bench_queue(args)
+        return
+    if args.workload == "mfma_peak":
+        bench_mfma_peak(args)
         return
 
     import torch

@@ -38,7 +38,7 @@ HIP_FLAGS = [
 VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 
 SOURCES = ["mgn_fused.hip", "mgn_pipelined.hip", "stages.hip", "gemm.hip", "nerf_fused.hip", "dlrm_fused.hip", "status.hip",
-           "bert_addln_pipelined.hip", "bert_ffn_pipelined.hip", "nerf_a_pipelined.hip", "capi.cpp", "ffn.cpp", "mlp.cpp", "arena.cpp"]
+           "bert_addln_pipelined.hip", "bert_ffn_pipelined.hip", "nerf_a_pipelined.hip", "probe.hip", "capi.cpp", "ffn.cpp", "mlp.cpp", "arena.cpp"]
 SOURCE_FLAGS = {"gemm.hip": [], "nerf_fused.hip": [], "dlrm_fused.hip": []}
 
 

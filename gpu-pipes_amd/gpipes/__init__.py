@@ -28,6 +28,7 @@ __all__ = [
     "gemm_out", "bert_ffn", "bert_ffn_out", "mlp_out", "dlrm_botmlp", "dlrm_botmlp_out", "dlrm_topmlp",
     "dlrm_topmlp_out", "nerf_full", "nerf_full_out", "nerf_full_out_noalloc", "bert_addln_ffn",
     "bert_addln_ffn_out", "nerf_a", "nerf_a_out", "pipe_handoff", "handoff_checksums", "phase_timers",
+    "probe_mfma",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -90,6 +91,7 @@ def _load():
     L.gp_bert_ffn_out.argtypes = [i64, i64, i64] + [vp] * 7 + [f32, i32, vp, vp]
     L.gp_bert_ffn_dtype_out.argtypes = [i64, i64, i64] + [vp] * 7 + [f32, i32, vp, i32, vp]
     L.gp_bert_ffn_impl_out.argtypes = [i64, i64, i64] + [vp] * 7 + [f32, i32, vp, i32, vp]
+    L.gp_probe_mfma.argtypes = [i64, i32, vp, i64, ctypes.POINTER(i64), vp]
     L.gp_mlp_out.argtypes = [i64, i32, vp, vp, vp, vp, vp, vp, vp]
     L.gp_mlp_dtype_out.argtypes = [i64, i32, vp, vp, vp, vp, vp, vp, i32, vp]
     L.gp_mlp_dtype_out.restype = i32
@@ -390,6 +392,23 @@ PHASE_NAMES = {
     "layer23_waves": ["handoff_wait", "layer2", "exchange_free_wait", "exchange_store", "exchange_full_wait",
                       "layer3_issue", "layernorm_store"],
 }
+
+
+_probe_out = {}
+
+
+def probe_mfma(iters, dtype=torch.float16, device=None):
+    """Launch the dense-MFMA throughput probe (gp_probe_mfma) on the current stream and
+    return the launch's FLOP count; time it with events on that stream.  Diagnostics."""
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    out = _probe_out.get(dev)
+    if out is None:
+        out = _probe_out[dev] = torch.empty(2 * 1024 * 256, dtype=torch.float32, device=dev)
+    flops = ctypes.c_int64(0)
+    with torch.cuda.device(dev):
+        _check(lib.gp_probe_mfma(int(iters), _DTYPES[dtype], _ptr(out), out.numel(), ctypes.byref(flops),
+                                 ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
+    return flops.value
 
 
 def phase_timers():

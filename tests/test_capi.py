@@ -273,3 +273,15 @@ def test_handoff_route_argument_errors():
     assert L.gp_pipe_route(256, None, vp(18), None, 4, 0, None) == -3     # misaligned
     assert L.gp_pipe_route(256, None, vp(16), None, 9, 0, None) == -1     # unknown route
     assert L.gp_pipe_route(0, None, None, None, 4, 0, None) == 0          # empty: no-op
+
+
+@pytest.mark.parametrize("iters,dtype,out,flops,code", [
+    (0, 0, 16, True, -1), (16, 5, 16, True, -1), (16, 0, 0, True, -1), (16, 0, 16, False, -1),
+])
+def test_probe_argument_errors(iters, dtype, out, flops, code):
+    """gp_probe_mfma rejects bad arguments before any device call."""
+    f = ctypes.c_int64(0)
+    rc = gpipes.lib.gp_probe_mfma(iters, dtype, ctypes.c_void_p(out) if out else None, 1 << 20,
+                                  ctypes.byref(f) if flops else None, None)
+    assert rc == code
+    assert gpipes.lib.gp_last_error().decode() != ""
