@@ -9,7 +9,7 @@ stream, the HBM traffic per launch measured with rocprofv3 counters
 host cores.
 
   python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--settle-ms 1000]
-                  [--workload edge|node|edge_gather|bert|dlrm|nerf|bert_addln|bert_app|nerf_a|queue|mfma_peak]
+                  [--workload edge|node|edge_gather|bert|dlrm|nerf|bert_addln|bert_app|nerf_a|queue|mfma_peak|gemm]
                   [--impl fused|pipelined|pipelined_split_ln] [--no-cpu]
 
 Every line carries "spread": the per-launch HIP-event times of the timed
@@ -694,6 +694,52 @@ def bench_mfma_peak(args):
     print(json.dumps(rec), flush=True)
 
 
+GEMM_SHAPES = [(16384, 1024, 4096), (16384, 4096, 1024), (262144, 1024, 1024), (262144, 512, 1024),
+               (262144, 1024, 512), (8192, 8192, 8192)]
+
+
+def bench_gemm(args):
+    """The wide GEMM stage (gp_gemm_out, bias + ReLU epilogue, weights [K, N] as a caller
+    holds them) against torch.matmul (hipBLASLt, no epilogue) on the BERT-large and DLRM
+    layer shapes: one line per shape, HIP events over 20 calls after 5 untimed ones."""
+    import torch
+
+    import gpipes
+
+    dev = torch.device("cuda:0")
+
+    def timed(fn, n=20):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    for (M, K, N) in GEMM_SHAPES:
+        g = torch.Generator(device=dev).manual_seed(M + K + N)
+        a = torch.randn(M, K, device=dev, generator=g).half()
+        w = (torch.randn(K, N, device=dev, generator=g) * K ** -0.5).half()
+        b = torch.randn(N, device=dev, generator=g).half()
+        out = torch.empty(M, N, device=dev, dtype=torch.float16)
+        ours = timed(lambda: gpipes.gemm_out(a, w, b, act="relu", out=out))
+        lib_ms = timed(lambda: torch.matmul(a, w))
+        flops = 2 * M * K * N
+        print(json.dumps({
+            "metric": "TFLOP/s, wide GEMM stage (bias + ReLU epilogue) against hipBLASLt (torch.matmul)",
+            "value": flops / (ours * 1e-3) / 1e12, "unit": "TFLOP/s", "n_gpus": 1, "ms_per_step": ours,
+            "higher_is_better": True, "dtype": "f16", "data": "synthetic (N(0,1) inputs, N(0,1/K) weights)",
+            "config": {"workload": "gemm", "M": M, "K": K, "N": N,
+                       "weights": "in place" if 2.0 * M * N * K < 8e10 else "transposed copy made by the call"},
+            "library": {"name": f"torch {torch.__version__} matmul (hipBLASLt), no epilogue", "ms": lib_ms,
+                        "tflops": flops / (lib_ms * 1e-3) / 1e12},
+        }), flush=True)
+
+
 def load_traffic(workload, impl):
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
@@ -709,7 +755,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["bert", "dlrm", "nerf", "bert_addln", "bert_app", "nerf_a",
-                                                               "queue", "mfma_peak"],
+                                                               "queue", "mfma_peak", "gemm"],
                     default="edge")
     ap.add_argument("--impl", choices=["fused", "pipelined", "pipelined_split_ln"], default="fused")
     ap.add_argument("--settle-ms", type=float, default=1000.0,
@@ -760,6 +806,9 @@ def main():
         return
     if args.workload == "mfma_peak":
         bench_mfma_peak(args)
+        return
+    if args.workload == "gemm":
+        bench_gemm(args)
         return
 
     import torch
