@@ -103,6 +103,14 @@ inline void bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const 
   check(gp_bert_ffn_out(M, H, FF, x, w1, b1, w2, b2, ga, be, eps, act, out, stream));
 }
 
+// the same with a choice of layout: GP_IMPL_PIPELINED is the app's
+// queue-chained layout (bert_ffn_pl.cuh:79-162; H 128, FF 512)
+inline void bert_ffn_out(int64_t M, int64_t H, int64_t FF, const void* x, const void* w1, const void* b1,
+                         const void* w2, const void* b2, const void* ga, const void* be, void* out, float eps,
+                         int act, int impl, void* stream) {
+  check(gp_bert_ffn_impl_out(M, H, FF, x, w1, b1, w2, b2, ga, be, eps, act, out, impl, stream));
+}
+
 // the wide GEMM stage (bert_ffn_pl.cuh:79-99, bulksync_gemm)
 inline void gemm_out(int64_t M, int64_t N, int64_t K, const void* x, const void* w, const void* b, const void* r,
                      int act, void* out, void* stream = nullptr) {
