@@ -227,3 +227,30 @@ def test_dlrm_tail_fused_unaligned_bit_exact(cuda):
     torch.cuda.synchronize()
     assert torch.equal(ou.view(torch.int16), y.view(torch.int16))
     assert float(obuf[0]) == 0.0 and float(obuf[1 + M]) == 0.0
+
+
+def test_dlrm_fused_randomized_sweep(cuda):
+    """Twenty seeded random cases per kernel: input width, row count (partial
+    last tiles, one to several tiles per workgroup), activations, null biases
+    and element type, each against the oracle over every row."""
+    rng = np.random.default_rng(2024)
+    hidden = ["none", "relu"]
+    heads = ["none", "relu", "sigmoid", "gelu_tanh"]
+    for i in range(20):
+        K0 = int(rng.integers(1, 33))
+        M = int(rng.integers(1, 70000))
+        acts = (hidden[rng.integers(2)], hidden[rng.integers(2)], heads[rng.integers(4)])
+        bias = bool(rng.integers(2))
+        dtype = BF if rng.integers(4) == 0 else torch.float16
+        print(f"[dlrm-fused] sweep {i}: K0={K0} M={M} acts={acts} bias={bias} {dtype}", flush=True)
+        y, want, *_ = run(cuda, M, K0, acts=acts, seed=100 + i, bias=bias, dtype=dtype)
+        check(f(y), want, f"sweep {i}", bf16=dtype == BF)
+    for i in range(20):
+        K = int(rng.choice([256, 512, 1024]))
+        M = int(rng.integers(1, 70000))
+        acts = (hidden[rng.integers(2)], heads[rng.integers(4)])
+        bias = bool(rng.integers(2))
+        dtype = BF if rng.integers(4) == 0 else torch.float16
+        print(f"[dlrm-tail] sweep {i}: K={K} M={M} acts={acts} bias={bias} {dtype}", flush=True)
+        y, want, *_ = run_tail(cuda, M, [K, 256, 1], acts, seed=200 + i, bias=bias, dtype=dtype)
+        check(f(y), want, f"tail sweep {i}", bf16=dtype == BF)
