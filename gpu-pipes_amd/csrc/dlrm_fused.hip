@@ -228,27 +228,35 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   f16x acc1;      // the first-layer block in flight
   h8 act[KB3];    // second-layer outputs as third-layer B operands
   h8 xin[NKB1];   // the input rows as first-layer B operands
-  h8 fa[4];       // A fragments of the current group
+  // A fragments, double-buffered: group g + 1 of a slot is read while group
+  // g's MFMAs issue, and a slot's last group issues after the next slot's
+  // barrier, so neither the LDS latency nor the barrier leaves the wave
+  // without MFMAs to issue.
+  h8 fa[2][4];
   // B operand that is 1 at k = 0 and 0 elsewhere: lanes 0-31 hold k = 0..7.
   h8 ones = {};
   ones[0] = __builtin_bit_cast(half_t, lane0 < 32 ? E::kOne : (unsigned short)0);
 
   using S0 = std::integral_constant<int, 0>;
   using SO = std::integral_constant<int, kOutStores>;
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
 
   for (int k = 0; k < my; ++k) {
     const int64_t r0 = tile_r0(k);
     const int vrows = p.M - r0 < ROWS ? (int)(p.M - r0) : ROWS;
     auto cur_slot = [&] { return (GP_LDS const char*)(ring + cur * SLOT); };
-    // Read group g (fragments 4g .. 4g+3) of the current slot.
-    auto fetch = [&](int g) {
+    // Read group g (fragments 4g .. 4g+3) of the current slot into fa[BUF].
+    auto fetch = [&](int g, auto bufc) {
+      constexpr int BUF = decltype(bufc)::value;
       GP_LDS const char* const s = cur_slot() + 4 * g * FRAG + 16 * lane0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) fa[i] = *(GP_LDS const h8*)(s + i * FRAG);
+      for (int i = 0; i < 4; ++i) fa[BUF][i] = *(GP_LDS const h8*)(s + i * FRAG);
     };
+    // Acquire the next slot and read its group 0 into fa[0].
     auto advance = [&] {
       acquire(S0{});
-      fetch(0);
+      fetch(0, B0{});
     };
     // acc[fb] = bias (x) ones for the FB feature blocks of a layer.
     auto bias_init = [&](auto FBc, int off) {
@@ -282,7 +290,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     } else {
       if (!ring_wave) wait_vmcnt<kOutStores>();
       acquire(SO{});
-      fetch(0);
+      fetch(0, B0{});
     }
     // This wave's rows of the input tile, K0 columns each, as NKB1 k-blocks
     // (zero past K0).
@@ -319,25 +327,27 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       to_operands<E>(acc1, p.relu1 != 0, a0, a1);
       // (block FB1 - 1 is recomputed once at the end: branch-free)
       acc1 = layer1(j + 1 < FB1 ? j + 1 : j);
+      fetch(1, B1{});
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = E::mma(fa[i], a0, acc[i]);
+      for (int i = 0; i < 4; ++i) acc[i] = E::mma(fa[0][i], a0, acc[i]);
       refill();
       // Every wave has read this tile's input rows (a barrier has passed
       // since): the next tile's go into the buffer now.
       if (j == 1) copy_input(k + 1);
       __builtin_amdgcn_sched_barrier(0);
-      fetch(1);
+      fetch(2, B0{});
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[4 + i] = E::mma(fa[i], a0, acc[4 + i]);
+      for (int i = 0; i < 4; ++i) acc[4 + i] = E::mma(fa[1][i], a0, acc[4 + i]);
       __builtin_amdgcn_sched_barrier(0);
-      fetch(2);
+      fetch(3, B1{});
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = E::mma(fa[i], a1, acc[i]);
+      for (int i = 0; i < 4; ++i) acc[i] = E::mma(fa[0][i], a1, acc[i]);
       __builtin_amdgcn_sched_barrier(0);
-      fetch(3);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[4 + i] = E::mma(fa[i], a1, acc[4 + i]);
+      // The next slot (the first third-layer slot after j = 15); group 3's
+      // fragments are in registers, so its MFMAs issue after the barrier.
       advance();
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[4 + i] = E::mma(fa[1][i], a1, acc[4 + i]);
     }
     // Second-layer epilogue, then the third layer: slot S_W3 + s holds
     // k-blocks 4s .. 4s+3 (group g: k-block 4s + g) for the four feature
@@ -347,18 +357,23 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     bias_init(std::integral_constant<int, FB3>{}, BF_3);
     static_for(std::make_integer_sequence<int, KB3 * FB3 / FPS>{}, [&](auto sc) {
       constexpr int s = decltype(sc)::value;
+      fetch(1, B1{});
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = E::mma(fa[i], act[4 * s], acc[i]);
+      for (int i = 0; i < 4; ++i) acc[i] = E::mma(fa[0][i], act[4 * s], acc[i]);
       refill();
-      static_for(std::make_integer_sequence<int, 3>{}, [&](auto gc) {
-        constexpr int g = decltype(gc)::value + 1;
-        __builtin_amdgcn_sched_barrier(0);
-        fetch(g);
+      __builtin_amdgcn_sched_barrier(0);
+      fetch(2, B0{});
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = E::mma(fa[i], act[4 * s + g], acc[i]);
-      });
+      for (int i = 0; i < 4; ++i) acc[i] = E::mma(fa[1][i], act[4 * s + 1], acc[i]);
+      __builtin_amdgcn_sched_barrier(0);
+      fetch(3, B1{});
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = E::mma(fa[0][i], act[4 * s + 2], acc[i]);
+      __builtin_amdgcn_sched_barrier(0);
       // the next tile's first slot is acquired after this tile's stores
       if constexpr (s + 1 < KB3 * FB3 / FPS) advance();
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = E::mma(fa[1][i], act[4 * s + 3], acc[i]);
     });
 
     // Output: out[row][f] = act3(acc) for f = 32 fb + 8 g + 4 lh + e.
@@ -574,9 +589,29 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   });
 
   f16x acc[FB2];
-  h8 fa[4];
+  // A fragments, double-buffered as in the bottom MLP: group g + 1 is read
+  // while group g's MFMAs issue, and a slot's last group issues after the
+  // next slot's barrier.
+  h8 fa[2][4];
   h8 ones = {};
   ones[0] = __builtin_bit_cast(half_t, lane0 < 32 ? E::kOne : (unsigned short)0);
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  // Read group g of ring slot RS into fa[BUF].
+  auto fetch = [&](auto rsc, int g, auto bufc) {
+    constexpr int RS = decltype(rsc)::value, BUF = decltype(bufc)::value;
+    GP_LDS const char* const s = (GP_LDS const char*)(ring + RS * SLOT) + 16 * lane0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[BUF][i] = *(GP_LDS const h8*)(s + (4 * g + i) * FRAG);
+  };
+  // Acquire the next slot in stream order (all but the kWait operations
+  // issued after its copies have landed -- its input loads among them -- then
+  // a barrier) and read its group 0.
+  auto acquire = [&](auto rsc) {
+    wait_vmcnt<kWait>();
+    lds_barrier();
+    fetch(rsc, 0, B0{});
+  };
 
   for (int k = 0; k < my; ++k) {
     const int64_t r0 = tile_r0(k);
@@ -587,38 +622,37 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       a[0] = bfrag[64 * fb + lane0];
       acc[fb] = E::mma(a, ones, f16x{});
     }
+    // the tile's first slot (ring slot 0: ST is a multiple of TS)
+    acquire(std::integral_constant<int, 0>{});
 #pragma nounroll
     for (int grp = 0; grp < ST / TS; ++grp) {
       const int i0 = k * ST + grp * TS;  // global slot of the group's first slot
+      const bool last_grp = grp + 1 == ST / TS;
       static_for(std::make_integer_sequence<int, TS>{}, [&](auto uc) {
         constexpr int u = decltype(uc)::value;
-        // acquire slot i0 + u (ring slot u)
-        wait_vmcnt<kWait>();
-        lds_barrier();
-        GP_LDS const char* const s = (GP_LDS const char*)(ring + u * SLOT) + 16 * lane0;
-        auto fetch = [&](int g) {
+        using RS = std::integral_constant<int, u>;
+        // slot i0 + u is acquired (ring slot u) and its group 0 is in fa[0]
+        fetch(RS{}, 1, B1{});
 #pragma unroll
-          for (int i = 0; i < 4; ++i) fa[i] = *(GP_LDS const h8*)(s + (4 * g + i) * FRAG);
-        };
-        fetch(0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = E::mma(fa[i], xin[u][0], acc[i]);
+        for (int i = 0; i < 4; ++i) acc[i] = E::mma(fa[0][i], xin[u][0], acc[i]);
         // slot i0 + u + TS - 1 goes into the ring slot and register set of
         // slot i0 + u - 1, both dead since the barrier
         load_input(i0 + u + TS - 1, std::integral_constant<int, (u + TS - 1) % TS>{});
         issue(i0 + u + TS - 1);
         __builtin_amdgcn_sched_barrier(0);
-        fetch(1);
+        fetch(RS{}, 2, B0{});
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[4 + i] = E::mma(fa[i], xin[u][0], acc[4 + i]);
+        for (int i = 0; i < 4; ++i) acc[4 + i] = E::mma(fa[1][i], xin[u][0], acc[4 + i]);
         __builtin_amdgcn_sched_barrier(0);
-        fetch(2);
+        fetch(RS{}, 3, B1{});
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = E::mma(fa[i], xin[u][1], acc[i]);
+        for (int i = 0; i < 4; ++i) acc[i] = E::mma(fa[0][i], xin[u][1], acc[i]);
         __builtin_amdgcn_sched_barrier(0);
-        fetch(3);
+        // the next slot of this tile (the next tile's first is acquired after
+        // this tile's output store)
+        if (u + 1 < TS || !last_grp) acquire(std::integral_constant<int, (u + 1) % TS>{});
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[4 + i] = E::mma(fa[i], xin[u][1], acc[4 + i]);
+        for (int i = 0; i < 4; ++i) acc[4 + i] = E::mma(fa[1][i], xin[u][1], acc[4 + i]);
       });
     }
     // Click head.  Lane (row, half lh) holds features 32 fb + 8 g + 4 lh + e
