@@ -233,7 +233,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   f16x acc[8][RB];  // [feature block][row block]
   h8 act[16][RB];   // B operands of register-fed k-blocks: [k-block][row block]
   h8 xin[4][RB];    // B operands of the x / d k-blocks: [k-block][row block]
-  h8 fa[1][4];     // A fragments of the current group
+  h8 fa[2][4];     // A fragments, double-buffered (see run_layer)
   // B operand that is 1 at k = 0 and 0 elsewhere: lanes 0-31 hold k = 0..7.
   h8 ones = {};
   ones[0] = __builtin_bit_cast(half_t, lane0 < 32 ? E::kOne : (unsigned short)0);
@@ -447,21 +447,22 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       static_for(std::make_integer_sequence<int, N>{}, [&](auto jc) {
         constexpr int j = decltype(jc)::value;
         using KD = std::integral_constant<int, KD0 + j>;
-        constexpr int NG = 4;
-        // One fragment buffer: the other wave on the SIMD covers the read
-        // latency while this one waits.
+        // Two fragment buffers: group g + 1 is read while group g's MFMAs
+        // issue, and the slot's last group issues after the next slot's
+        // barrier (its fragments are in registers by then).
+        fetch(G1{}, G1{});
         mma(KD{}, G0{}, G0{});
         refill();
-        static_for(std::make_integer_sequence<int, NG - 1>{}, [&](auto gc) {
-          using G = std::integral_constant<int, decltype(gc)::value + 1>;
-          // keep each group's reads below the previous group's MFMAs: reads
-          // hoisted further ahead run out of registers and spill
-          __builtin_amdgcn_sched_barrier(0);
-          fetch(G{}, G0{});
-          mma(KD{}, G{}, G0{});
-        });
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(G2{}, G0{});
+        mma(KD{}, G1{}, G1{});
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(G3{}, G1{});
+        mma(KD{}, G2{}, G0{});
+        __builtin_amdgcn_sched_barrier(0);
         if constexpr (j + 1 < N) advance();
         else after();
+        mma(KD{}, G3{}, G1{});
       });
     };
     using C1 = std::integral_constant<int, 1>;
