@@ -137,6 +137,7 @@ __device__ __forceinline__ void stores_complete() {
 // mgn_fullmlp_pl.cuh:13-21: a queue entry is an [M][D] fp16 tile.
 template <int MBLK, int D>
 struct QueueEntry2D {
+  static constexpr int kRows = MBLK, kCols = D;
   half_t buf[MBLK][D];
   __device__ half_t* as_ptr() { return &buf[0][0]; }
   __device__ TensorView as_view(int rows) { return {as_ptr(), D, rows < 0 ? 0 : (rows > MBLK ? MBLK : rows)}; }
@@ -403,6 +404,43 @@ struct SplitQueueWriter {
     seq_n += seq_stride;
   }
   __device__ void reset() { seq_n = seq_off; }
+};
+
+// Producer w of np writes rows [w R, (w + 1) R) of every entry, R = the
+// entry's rows / np; an entry is full once all np have committed.  The row
+// count an entry carries is its whole tile's, which every producer derives
+// from the rows left in the input at that entry (rows_left, falling by
+// row_step per entry), so the producers store the same value.
+template <typename QT>
+struct RowSplitQueueWriter {
+  static constexpr bool kReleaseBarrier = true;
+  using Queue = QT;
+  using Entry = typename QT::Item;
+  Queue* q;
+  const QueueCtx* ctx;
+  int64_t seq_n = 0;
+  int row0;
+  int64_t rows_left, rows_left0, row_step;
+
+  __device__ RowSplitQueueWriter(Queue* q_, const QueueCtx* ctx_, int w, int np, int64_t rows_left_, int64_t row_step_)
+      : q(q_), ctx(ctx_), row0(w * (Entry::kRows / np)), rows_left(rows_left_), rows_left0(rows_left_),
+        row_step(row_step_) {}
+  __device__ TensorView write_acquire(int rows_) {
+    TensorView v = q->write_wait(seq_n, *ctx)->as_view(Entry::kRows);
+    v.data += (int64_t)row0 * Entry::kCols;
+    v.rows = rows_ < 0 ? 0 : rows_;
+    return v;
+  }
+  __device__ void write_release() {
+    const int64_t r = rows_left < Entry::kRows ? rows_left : Entry::kRows;
+    q->write_commit(seq_n, r > 0 ? (int)r : 0, *ctx);
+    ++seq_n;
+    rows_left -= row_step;
+  }
+  __device__ void reset() {
+    seq_n = 0;
+    rows_left = rows_left0;
+  }
 };
 
 // pipes.cuh:104-108

@@ -84,6 +84,12 @@ constexpr int gemm_param_lds() {
   return 3 * 128 * 4 + MBLK * 4 * 8;
 }
 constexpr int kGemmParamLds = gemm_param_lds<128>();
+// Extra LDS of a stage that chains a second 128 -> 128 layer: the first
+// layer's MBLK x 128 fp16 output tile and the second layer's bias.
+template <int MBLK>
+constexpr int gemm_chain_lds() {
+  return MBLK * 128 * 2 + 128 * 4;
+}
 
 // Copy rows [0, MBLK) x K halves of a tile view into LDS.  LDS row r holds
 // 16-byte chunk c at chunk position (c & ~15) | ((c ^ r) & 15), so the 16
@@ -94,18 +100,20 @@ constexpr int kGemmParamLds = gemm_param_lds<128>();
 // columns are zero, never the next row's data.
 // NT: copy with the non-temporal cache policy -- for an input streamed from
 // memory once, so that it does not evict the L2 lines of the ring queues.
-template <int MBLK, int K, bool NT = false>
+// NW: the copies are issued by waves 0 .. NW-1 (the others issue none).
+template <int MBLK, int K, bool NT = false, int NW = 4>
 __device__ __forceinline__ void load_tile_swz(const TensorView& v, GP_LDS char* dst, int kv = K) {
   static_assert(K % 128 == 0, "K must be a multiple of 128");
   constexpr int CPR = K / 8;
   constexpr int NI = MBLK * K * 2 / 1024;
-  static_assert(NI % 4 == 0, "tile must split over four waves");
+  static_assert(NI % NW == 0, "tile must split over the copying waves");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (wave >= NW) return;
   const int rows = v.rows < MBLK ? (v.rows > 0 ? v.rows : 0) : MBLK;
   const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(v.data, rows * v.stride * 2);
 #pragma unroll
-  for (int ii = 0; ii < NI / 4; ++ii) {
-    const int i = ii * 4 + wave;
+  for (int ii = 0; ii < NI / NW; ++ii) {
+    const int i = ii * NW + wave;
     const int q = i * kWave + lane;
     const int r = q / CPR;
     const int c = (q - r * CPR) ^ (r & 15);
@@ -187,6 +195,28 @@ __device__ __forceinline__ void stage_mfma_loop(const h8* wf, LD ld, f16x* acc) 
   }
 }
 
+// A 32-row block's accumulators (lane (lr, lh) of wave w holds features
+// 32 w + 4 lh + 8 g + (0..3), g = 0..3, of row lr) as two 16-byte words of
+// fp16 after the activation: v_permlane32_swap trades groups g = 2q+1 of the
+// lower wave half for groups g = 2q of the upper half, so word q holds the
+// eight consecutive features 32 w + 16 q + 8 lh + (0..7) of the lane's row.
+__device__ __forceinline__ void fp16_row_words(const f16x& a, int act, u32x4 (&w)[2]) {
+  u32x2 o[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    f4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = apply_act(a[4 * g + e], act);
+    o[g] = __builtin_bit_cast(u32x2, __builtin_convertvector(v, h4));
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const auto lo = __builtin_amdgcn_permlane32_swap(o[2 * q][0], o[2 * q + 1][0], false, false);
+    const auto hi = __builtin_amdgcn_permlane32_swap(o[2 * q][1], o[2 * q + 1][1], false, false);
+    w[q] = u32x4{(unsigned)lo[0], (unsigned)hi[0], (unsigned)lo[1], (unsigned)hi[1]};
+  }
+}
+
 // Whether a writer's output may be stored non-temporally in whole lines
 // (W::kStreamOut; false when a writer does not say).
 template <typename W, typename = void>
@@ -211,9 +241,17 @@ struct stream_out<W, std::void_t<decltype(W::kStreamOut)>> : std::bool_constant<
 // stage never waits for a next tile before its current one is out.  LPF is
 // the depth (k-steps) of the LDS fragment prefetch of the MFMA loop; 0 picks
 // 2 for four row blocks per part, else 4.
-template <int MBLK, int K, int ACT, bool LN, int NB, int LPF, typename IR, typename AR, typename OW>
+//
+// CH: a second 128 -> 128 layer follows in the same workgroup (weight2,
+// bias2).  The first layer's output act(in . W + b) goes, rounded to fp16 as
+// a queue entry would hold it, into an LDS tile laid out as a 128-wide input
+// tile, and the second layer reads its B operands from there; the epilogue
+// (LayerNorm, or the plain store) applies to the second layer's result.  Two
+// layers then cost one queue hand-off instead of two.
+template <int MBLK, int K, int ACT, bool LN, int NB, int LPF, typename IR, typename AR, typename OW, bool CH = false>
 __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView gamma, TensorView beta, float eps,
-                                IR& ir, AR& ar, OW& ow, int num_iters) {
+                                IR& ir, AR& ar, OW& ow, int num_iters, TensorView weight2 = {},
+                                TensorView bias2 = {}) {
   constexpr int N = 128;
   constexpr int RB = MBLK / 32;
   static_assert(MBLK % 32 == 0 && MBLK <= 128, "MBLK must be 32, 64, 96 or 128");
@@ -225,8 +263,12 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
   constexpr int PROWS = PF ? 64 : MBLK;                      // rows per part
   constexpr int PB = PROWS * K * 2;                 // bytes per part buffer
   constexpr int RBP = PROWS / 32;                   // 32-row blocks per part
+  static_assert(!CH || !PF, "a chained stage takes whole tiles");
+  constexpr int ACT_OUT = CH ? ACT_NONE : ACT;      // activation of the stored result
   GP_LDS char* xs = dyn_lds();
-  GP_LDS float* prm = (GP_LDS float*)(xs + gemm_stage_lds<MBLK, K, NB>());
+  GP_LDS char* const chb = xs + gemm_stage_lds<MBLK, K, NB>();  // CH: the first layer's output tile
+  GP_LDS float* const prm2 = (GP_LDS float*)(chb + MBLK * N * 2);  // CH: the second layer's bias
+  GP_LDS float* prm = (GP_LDS float*)(xs + gemm_stage_lds<MBLK, K, NB>() + (CH ? gemm_chain_lds<MBLK>() : 0));
   // The weight view's row count is the layer's real K: input columns past it
   // are zero-filled (their weight rows are zero too).
   const int kv = weight.rows < K ? weight.rows : K;
@@ -238,10 +280,17 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
 
   h8 wf[K / 16];
   load_weight_frags<K, gemm_stage_lds<MBLK, K, NB>()>(weight, xs, wf);
+  h8 wf2[CH ? N / 16 : 1];
+  if constexpr (CH) load_weight_frags<N, gemm_stage_lds<MBLK, K, NB>()>(weight2, xs, wf2);
   // The weight fragments live in AGPRs (MFMA A operands are read from there
   // directly), which leaves the VGPRs to the accumulators and the epilogue.
 #pragma unroll
   for (int i = 0; i < K / 16; ++i) asm volatile("" : "+a"(wf[i]));
+  if constexpr (CH) {
+#pragma unroll
+    for (int i = 0; i < N / 16; ++i) asm volatile("" : "+a"(wf2[i]));
+    load_param(bias2, prm2, N);
+  }
   load_param(bias, prm, N);
   if (LN) {
     load_param(gamma, prm + N, N, 1.f);
@@ -250,10 +299,11 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
   __syncthreads();
   // This lane's 16 features' bias (and LayerNorm gamma, beta) are kept in
   // registers for all tiles -- except in 64-row stages, which are built to
-  // run three workgroups per CU and have no registers to spare; they read
-  // them from LDS for every tile.
-  constexpr bool RP = MBLK >= 128;
-  float bias_r[RP ? 16 : 1], gm_r[RP && LN ? 16 : 1], bt_r[RP && LN ? 16 : 1];
+  // run three workgroups per CU, and in chained stages, which hold two
+  // weight matrices and run two workgroups per CU: they have no registers to
+  // spare and read them from LDS for every tile.
+  constexpr bool RP = MBLK >= 128 && !CH;
+  float bias_r[RP ? 16 : 1], gm_r[RP && LN ? 16 : 1], bt_r[RP && LN ? 16 : 1], b2_r[RP && CH ? 16 : 1];
   if constexpr (RP) {
 #pragma unroll
     for (int g = 0; g < 4; ++g)
@@ -264,14 +314,19 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
           gm_r[4 * g + e] = prm[N + fq + 8 * g + e];
           bt_r[4 * g + e] = prm[2 * N + fq + 8 * g + e];
         }
+        if constexpr (CH) b2_r[4 * g + e] = prm2[fq + 8 * g + e];
       }
   }
-  // parameter j (0 bias, 1 gamma, 2 beta) of this lane's feature i (0..15)
+  // parameter j (0 bias, 1 gamma, 2 beta, 3 the second layer's bias) of
+  // this lane's feature i (0..15)
   auto param = [&](int j, int i) -> float {
-    if constexpr (RP) return j == 0 ? bias_r[i] : (j == 1 ? gm_r[LN ? i : 0] : bt_r[LN ? i : 0]);
-    else return prm[j * N + fq + 8 * (i / 4) + i % 4];
+    if constexpr (RP) {
+      if (j == 3) return b2_r[CH ? i : 0];
+      return j == 0 ? bias_r[i] : (j == 1 ? gm_r[LN ? i : 0] : bt_r[LN ? i : 0]);
+    } else {
+      return j == 3 ? prm2[fq + 8 * (i / 4) + i % 4] : prm[j * N + fq + 8 * (i / 4) + i % 4];
+    }
   };
-
   // Part h of a tile view: rows [PROWS h, PROWS h + PROWS) into buffer `buf`.
   auto copy_part = [&](const TensorView& v, int h, int buf) {
     const int r0 = PROWS * h;
@@ -376,6 +431,34 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
       }
     }
 
+    if constexpr (CH) {
+      // The first layer's output into the chain tile: chunk c of row r at
+      // chunk position (c ^ r) & 15, the layout load_tile_swz gives a
+      // 128-wide tile.  The tile is free: the last reads of the previous
+      // tile's second layer came before that tile's epilogue barriers.
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const int r = 32 * rb + lr;
+        u32x4 w[2];
+        fp16_row_words(acc[rb], ACT, w);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int c = 4 * wave + 2 * q + lh;
+          *(GP_LDS u32x4*)(chb + r * (N * 2) + ((c ^ (r & 15)) << 4)) = w[q];
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[rb][i] = param(3, i);
+      const GP_LDS char* xp = chb + lr * (N * 2);
+      stage_mfma_loop<N / 16, RB, (RB >= 4 ? 2 : 4)>(wf2, [&](int rp, int s) {
+        const int off = (((2 * s) ^ xa) & 15) * 16;
+        return *(const GP_LDS h8*)(xp + rp * (32 * N * 2) + off);
+      }, acc);
+    }
+
     if constexpr (LN) {
       // per-wave (mean, M2) over 32 features, combined over the four waves
 #pragma unroll
@@ -410,44 +493,34 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
       }
     }
 
-    // Stores: v_permlane32_swap trades groups g = 2q+1 of the lower wave half
-    // for groups g = 2q of the upper half, so each lane holds the eight
-    // consecutive features 32 wave + 16 q + 8 lh + (0..7) of its row and
-    // writes them with one 16-byte store.
+    // Stores: each lane writes the eight consecutive features of each word
+    // of fp16_row_words with one 16-byte store.
     //
-    // A LayerNorm stage writing memory (stream_out) stages the tile in its
-    // input tile buffer instead -- free since the LayerNorm barrier, which
-    // follows every wave's MFMAs -- and each wave then stores four whole
-    // 256-byte rows per instruction with the non-temporal policy.  16-byte
+    // A LayerNorm or chained stage writing memory (stream_out) stages the
+    // tile in its input tile buffer instead -- free since the LayerNorm or
+    // chain barrier, which follows every wave's MFMAs on that buffer -- and
+    // each wave then stores four whole 256-byte rows per instruction with
+    // the non-temporal policy.  16-byte
     // chunk c of row r sits at chunk position c ^ (r % 16), so the 32 rows a
     // wave writes at one chunk and the 16 chunks of a row it reads both
     // spread over the banks.  Whole-line non-temporal stores keep the output
     // out of L2, whose lines the queues need; 32-byte pieces would be
     // written back as partial lines.
-    constexpr bool STAGED = LN && QPF && stream_out<OW>::value && MBLK * N * 2 <= PB;
+    constexpr bool STAGED = ((LN && QPF) || (CH && !PF)) && stream_out<OW>::value && MBLK * N * 2 <= PB;
     const TensorView ot = ow.write_acquire(cur.rows);
     GP_LDS char* const st = xs + pb * PB;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       const int r = 32 * rb + lr;
-      u32x2 o[4];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        f4 v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = LN ? acc[rb][4 * g + e] : apply_act(acc[rb][4 * g + e], ACT);
-        o[g] = __builtin_bit_cast(u32x2, __builtin_convertvector(v, h4));
-      }
+      u32x4 w[2];
+      fp16_row_words(acc[rb], LN ? ACT_NONE : ACT_OUT, w);
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        const auto lo = __builtin_amdgcn_permlane32_swap(o[2 * q][0], o[2 * q + 1][0], false, false);
-        const auto hi = __builtin_amdgcn_permlane32_swap(o[2 * q][1], o[2 * q + 1][1], false, false);
-        const u32x4 w = {(unsigned)lo[0], (unsigned)hi[0], (unsigned)lo[1], (unsigned)hi[1]};
         if constexpr (STAGED) {
           const int c = 4 * wave + 2 * q + lh;
-          *(GP_LDS u32x4*)(st + r * (N * 2) + ((c ^ (r & 15)) << 4)) = w;
+          *(GP_LDS u32x4*)(st + r * (N * 2) + ((c ^ (r & 15)) << 4)) = w[q];
         } else {
-          if (r < ot.rows) *(u32x4*)(ot.data + (int64_t)r * ot.stride + 32 * wave + 16 * q + 8 * lh) = w;
+          if (r < ot.rows) *(u32x4*)(ot.data + (int64_t)r * ot.stride + 32 * wave + 16 * q + 8 * lh) = w[q];
         }
       }
     }
@@ -509,6 +582,20 @@ template <int MBLK, int K, int NB = 0, int LPF = 0, typename IR, typename AR, ty
 __device__ void pipe_gemm_bias_layer_norm(TensorView weight, TensorView bias, TensorView gamma, TensorView beta,
                                           float eps, IR& ir, AR& ar, OW& ow, int num_iters) {
   gemm_stage_impl<MBLK, K, ACT_NONE, true, NB, LPF>(weight, bias, gamma, beta, eps, ir, ar, ow, num_iters);
+}
+
+// pipe_gemm_bias_relu followed by pipe_gemm_bias_layer_norm (LN) or
+// pipe_gemm_bias in one workgroup: out = LayerNorm(relu(in . W + b) . W2 + b2)
+// * gamma + beta, or relu(in . W + b) . W2 + b2.  The 128-wide intermediate
+// tile passes through LDS (rounded to fp16, as a queue entry holds it), not a
+// queue.  Whole input tiles (a queue input with NB >= 2 MBLK / 64 copies the
+// next tile under this one).
+template <int MBLK, int K, bool LN, int NB = 0, typename IR, typename AR, typename OW>
+__device__ void pipe_gemm_bias_relu_chain(TensorView weight, TensorView bias, TensorView weight2, TensorView bias2,
+                                          TensorView gamma, TensorView beta, float eps, IR& ir, AR& ar, OW& ow,
+                                          int num_iters) {
+  gemm_stage_impl<MBLK, K, ACT_RELU, LN, NB, 0, IR, AR, OW, true>(weight, bias, gamma, beta, eps, ir, ar, ow,
+                                                                  num_iters, weight2, bias2);
 }
 
 // ---------------------------------------------------------------------------
