@@ -56,9 +56,13 @@ constexpr int kHalf = MBLK / 2;  // rows of a layer-1 worker's tile in the defau
 using QEntry = QueueEntry2D<MBLK, D>;
 
 // Default layout: q12 with the two layer-1 workers as producers of every
-// entry (row halves).  Two slots: a deeper q12 kept more queue lines in L2,
-// so more of them were written back to HBM.
-using HalfQueue = RingQueue<QEntry, 2, 2, 1>;
+// entry (row halves).  One slot: the consumer hands it back as soon as the
+// tile is in its LDS, so the producers write the next tile while it computes.
+// A slot that is rewritten within a tile's time stays in L2; with two slots
+// each line waited two tiles, long enough for the X stream to evict about
+// half of them dirty (WRITE_SIZE 406 MB per call against 276 MB, the output
+// being 268 MB), and the call was 1-2% slower.
+using HalfQueue = RingQueue<QEntry, 1, 2, 1>;
 struct Queues {
   HalfQueue q12;
 };

@@ -41,7 +41,9 @@ def test_golden_fixtures(cuda, impl, name, K, M):
 
 @pytest.mark.parametrize("impl", IMPLS)
 @pytest.mark.parametrize("K", [384, 256, 128])
-@pytest.mark.parametrize("M", [127, 128, 129, 5000, 16384 * 3 + 17])
+# 64 and 192: a last tile whose second 64-row half (the second layer-1
+# worker's share in the default layout) is empty
+@pytest.mark.parametrize("M", [64, 127, 128, 129, 192, 5000, 16384 * 3 + 17])
 def test_random_shapes(cuda, impl, K, M):
     for ln in (True, False):
         if impl == "pipelined_split_ln" and not ln:
