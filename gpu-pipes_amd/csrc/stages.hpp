@@ -100,20 +100,18 @@ constexpr int gemm_chain_lds() {
 // columns are zero, never the next row's data.
 // NT: copy with the non-temporal cache policy -- for an input streamed from
 // memory once, so that it does not evict the L2 lines of the ring queues.
-// NW: the copies are issued by waves 0 .. NW-1 (the others issue none).
-template <int MBLK, int K, bool NT = false, int NW = 4>
+template <int MBLK, int K, bool NT = false>
 __device__ __forceinline__ void load_tile_swz(const TensorView& v, GP_LDS char* dst, int kv = K) {
   static_assert(K % 128 == 0, "K must be a multiple of 128");
   constexpr int CPR = K / 8;
   constexpr int NI = MBLK * K * 2 / 1024;
-  static_assert(NI % NW == 0, "tile must split over the copying waves");
+  static_assert(NI % 4 == 0, "tile must split over four waves");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (wave >= NW) return;
   const int rows = v.rows < MBLK ? (v.rows > 0 ? v.rows : 0) : MBLK;
   const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(v.data, rows * v.stride * 2);
 #pragma unroll
-  for (int ii = 0; ii < NI / NW; ++ii) {
-    const int i = ii * NW + wave;
+  for (int ii = 0; ii < NI / 4; ++ii) {
+    const int i = ii * 4 + wave;
     const int q = i * kWave + lane;
     const int r = q / CPR;
     const int c = (q - r * CPR) ^ (r & 15);
