@@ -269,6 +269,33 @@ void scenario_columns(uint32_t epoch, std::atomic<uint64_t>& err, int64_t M) {
   check_once(seen, T, 1, "column blocks");
 }
 
+// two producers write the row halves of each entry of a one-slot queue
+// (RowSplitQueueWriter: NP = 2), both committing the whole tile's row count;
+// one consumer.  Mutant 6: each producer commits only its own half's rows.
+void scenario_rows(uint32_t epoch, std::atomic<uint64_t>& err, int64_t M) {
+  constexpr int NP = 2, RH = R / NP;
+  static RingQueue<E, 1, NP, 1> q;
+  if (epoch == 1) dirty(q, 0);
+  const Ctx ctx{epoch, &err, g_limit};
+  const int64_t T = (M + R - 1) / R;
+  std::vector<int> seen(T, 0);
+  std::vector<std::function<void()>> fns;
+  for (int j = 0; j < NP; ++j)
+    fns.push_back([&, j] {
+      for (int64_t seq = 0; seq < T; ++seq) {
+        E* e = q.write_wait(seq, ctx);
+        const int rows = rows_of(seq, M);
+        const int mine = rows - j * RH < 0 ? 0 : (rows - j * RH > RH ? RH : rows - j * RH);
+        for (int r = j * RH; r < j * RH + mine; ++r)
+          for (int c = 0; c < C; ++c) e->buf[r][c] = tag(seq, r, c);
+        q.write_commit(seq, g_mutant == 6 ? mine : rows, ctx);
+      }
+    });
+  fns.push_back([&] { consume(q, ctx, M, T, 0, 1, seen, true); });
+  run_threads(fns);
+  check_once(seen, T, 1, "row halves");
+}
+
 // the producer stops after `stop` tiles: the consumer's bounded wait must end
 // the launch with the error set; no tile that never came may be counted.
 void scenario_stuck(uint32_t epoch, std::atomic<uint64_t>& err, int64_t M, int64_t stop) {
@@ -298,6 +325,7 @@ int main(int argc, char** argv) {
       scenario_broadcast(epoch++, err, M);
       scenario_split(epoch++, err, M);
       scenario_columns(epoch++, err, M);
+      scenario_rows(epoch++, err, M);
     }
   }
   // a timed-out launch, then a clean launch on the same queues and error word

@@ -5,7 +5,7 @@ std::thread workgroups and std::atomic counters: epoch-tagged full / empty
 counters, the epoch lift on a slot's first round, the NP / NC wait targets,
 split round robin, row counts, and bounded waits with an epoch-tagged error
 word.  It must pass its scenarios (1:1, broadcast, split / merge, four
-column producers, partial tiles, back-to-back launches over garbage from
+column producers, two row-half producers of a one-slot queue, partial tiles, back-to-back launches over garbage from
 older launches, a stuck producer) both as a plain build and under
 ThreadSanitizer, and each planted protocol mistake must be caught.
 """
@@ -46,7 +46,8 @@ def test_protocol_scenarios_pass(exes, kind):
 
 @pytest.mark.parametrize("mutant,what", [(1, "no epoch lift"), (2, "producer waits one round short"),
                                          (4, "split worker with the wrong stride"),
-                                         (5, "consumer commits before reading")])
+                                         (5, "consumer commits before reading"),
+                                         (6, "row-half producers commit their own rows")])
 def test_planted_protocol_mistakes_are_caught(exes, mutant, what):
     r = run(exes["plain"], mutant)
     assert r.returncode != 0, f"{what} went undetected: {r.stdout}"
