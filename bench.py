@@ -658,30 +658,32 @@ def bench_queue(args):
 
 def bench_mfma_peak(args):
     """The dense MFMA ceiling of the board as it runs: the probe kernel (gp_probe_mfma:
-    two waves per SIMD of back-to-back 32x32x16 MFMAs on register data, no memory
-    traffic), one launch a step, timed like the other workloads.  With --telemetry the
-    line also carries the socket power and engine clocks it ran at."""
+    two waves per SIMD of back-to-back MFMAs on register data, no memory traffic;
+    --mfma-shape picks 32x32x16 or 16x16x32), one launch a step, timed like the other
+    workloads.  With --telemetry the line also carries the socket power and engine
+    clocks it ran at."""
     import torch
 
     import gpipes
 
     dev = torch.device("cuda:0")
     et = torch.bfloat16 if args.dtype == "bf16" else torch.float16
-    iters = 4096
-    flops = gpipes.probe_mfma(iters, et)
+    iters, shape = 4096, args.mfma_shape
+    flops = gpipes.probe_mfma(iters, et, shape=shape)
+    instr = "v_mfma_f32_32x32x16" if shape == 32 else "v_mfma_f32_16x16x32"
 
     def step(i):
-        gpipes.probe_mfma(iters, et)
+        gpipes.probe_mfma(iters, et, shape=shape)
     call_ms, ms_per_step, settle = timed_steps(step, args, dev)
     avg_ms = sum(call_ms) / len(call_ms)
     tflops = flops / (avg_ms * 1e-3) / 1e12
     rec = {
-        "metric": f"TFLOP/s, dense {args.dtype} MFMA probe without memory traffic (1×MI355X)",
+        "metric": f"TFLOP/s, dense {args.dtype} {instr} probe without memory traffic (1×MI355X)",
         "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": args.dtype, "data": "synthetic register operands in [-1, 1)",
-        "config": {"workload": "mfma_peak_probe", "iters": iters, "waves_per_simd": 2, "accumulators_per_wave": 8,
-                   "instruction": "v_mfma_f32_32x32x16"},
+        "config": {"workload": "mfma_peak_probe", "iters": iters, "waves_per_simd": 2,
+                   "accumulators_per_wave": 8 if shape == 32 else 16, "instruction": instr},
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": tflops / MFMA_F16_PEAK_TFLOPS, "traffic": None, "kernel_ms_avg": avg_ms,
                      "flops_per_launch": flops},
@@ -781,6 +783,9 @@ def main():
                     help="read the board's socket power, power cap and per-XCD engine clocks (rocm-smi, in a "
                          "child process) during a settle phase of at least 3 s, and add them to the line's "
                          "\"settle\" record (and, for the MGN workloads, as \"telemetry\")")
+    ap.add_argument("--mfma-shape", type=int, choices=[32, 16], default=32,
+                    help="--workload mfma_peak: the probe's MFMA form, 32 (v_mfma_f32_32x32x16, the form the "
+                         "fused kernels and the wide GEMM use) or 16 (v_mfma_f32_16x16x32)")
     ap.add_argument("--copy-ref", action="store_true",
                     help="first run one plain 1 GiB device copy (a known-size reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")

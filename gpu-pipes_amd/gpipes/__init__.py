@@ -91,7 +91,7 @@ def _load():
     L.gp_bert_ffn_out.argtypes = [i64, i64, i64] + [vp] * 7 + [f32, i32, vp, vp]
     L.gp_bert_ffn_dtype_out.argtypes = [i64, i64, i64] + [vp] * 7 + [f32, i32, vp, i32, vp]
     L.gp_bert_ffn_impl_out.argtypes = [i64, i64, i64] + [vp] * 7 + [f32, i32, vp, i32, vp]
-    L.gp_probe_mfma.argtypes = [i64, i32, vp, i64, ctypes.POINTER(i64), vp]
+    L.gp_probe_mfma.argtypes = [i64, i32, i32, vp, i64, ctypes.POINTER(i64), vp]
     L.gp_mlp_out.argtypes = [i64, i32, vp, vp, vp, vp, vp, vp, vp]
     L.gp_mlp_dtype_out.argtypes = [i64, i32, vp, vp, vp, vp, vp, vp, i32, vp]
     L.gp_mlp_dtype_out.restype = i32
@@ -397,17 +397,18 @@ PHASE_NAMES = {
 _probe_out = {}
 
 
-def probe_mfma(iters, dtype=torch.float16, device=None):
-    """Launch the dense-MFMA throughput probe (gp_probe_mfma) on the current stream and
-    return the launch's FLOP count; time it with events on that stream.  Diagnostics."""
+def probe_mfma(iters, dtype=torch.float16, device=None, shape=32):
+    """Launch the dense-MFMA throughput probe (gp_probe_mfma; shape 32: 32x32x16 MFMAs,
+    16: 16x16x32) on the current stream and return the launch's FLOP count; time it with
+    events on that stream.  Diagnostics."""
     dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
     out = _probe_out.get(dev)
     if out is None:
         out = _probe_out[dev] = torch.empty(2 * 1024 * 256, dtype=torch.float32, device=dev)
     flops = ctypes.c_int64(0)
     with torch.cuda.device(dev):
-        _check(lib.gp_probe_mfma(int(iters), _DTYPES[dtype], _ptr(out), out.numel(), ctypes.byref(flops),
-                                 ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
+        _check(lib.gp_probe_mfma(int(iters), _DTYPES[dtype], int(shape), _ptr(out), out.numel(),
+                                 ctypes.byref(flops), ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
     return flops.value
 
 

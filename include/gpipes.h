@@ -441,15 +441,17 @@ int gp_pipe_route(int64_t M, const void* x, void* out, void* out2, int route, in
 
 /*
  * Diagnostics, no counterpart in the reference: one launch of a probe kernel
- * in which every SIMD runs two waves of back-to-back dense 32x32x16 MFMAs
- * (GP_DTYPE_F16 or GP_DTYPE_BF16 operands, fp32 accumulation) on register
+ * in which every SIMD runs two waves of back-to-back dense MFMAs -- `shape`
+ * 32: v_mfma_f32_32x32x16, 16: v_mfma_f32_16x16x32, the same FLOPs per round
+ * -- (GP_DTYPE_F16 or GP_DTYPE_BF16 operands, fp32 accumulation) on register
  * data for `iters` rounds, with no memory traffic but one 4-byte store per
  * lane into `out` (at least 2 x CUs x 256 floats, `out_floats` of them).
  * *flops receives the launch's FLOP count; timed on the stream, it gives the
- * dense MFMA rate the device sustains (under its power cap), the ceiling for
- * the MFMA-bound kernels' measured rates.
+ * dense MFMA rate the device sustains with that instruction (the engine clock
+ * is set by the board's power and current limits), the ceiling for the
+ * MFMA-bound kernels' measured rates.
  */
-int gp_probe_mfma(int64_t iters, int dtype, void* out, int64_t out_floats, int64_t* flops, void* stream);
+int gp_probe_mfma(int64_t iters, int dtype, int shape, void* out, int64_t out_floats, int64_t* flops, void* stream);
 
 /*
  * Waits for `stream`, then reports whether the last launch on it that

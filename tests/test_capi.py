@@ -275,13 +275,14 @@ def test_handoff_route_argument_errors():
     assert L.gp_pipe_route(0, None, None, None, 4, 0, None) == 0          # empty: no-op
 
 
-@pytest.mark.parametrize("iters,dtype,out,flops,code", [
-    (0, 0, 16, True, -1), (16, 5, 16, True, -1), (16, 0, 0, True, -1), (16, 0, 16, False, -1),
+@pytest.mark.parametrize("iters,dtype,shape,out,flops,code", [
+    (0, 0, 32, 16, True, -1), (16, 5, 32, 16, True, -1), (16, 0, 32, 0, True, -1), (16, 0, 32, 16, False, -1),
+    (16, 0, 8, 16, True, -1),
 ])
-def test_probe_argument_errors(iters, dtype, out, flops, code):
+def test_probe_argument_errors(iters, dtype, shape, out, flops, code):
     """gp_probe_mfma rejects bad arguments before any device call."""
     f = ctypes.c_int64(0)
-    rc = gpipes.lib.gp_probe_mfma(iters, dtype, ctypes.c_void_p(out) if out else None, 1 << 20,
+    rc = gpipes.lib.gp_probe_mfma(iters, dtype, shape, ctypes.c_void_p(out) if out else None, 1 << 20,
                                   ctypes.byref(f) if flops else None, None)
     assert rc == code
     assert gpipes.lib.gp_last_error().decode() != ""
