@@ -113,16 +113,30 @@ __device__ __forceinline__ bool qwait(QCounter* c, uint32_t target, const QueueC
   return res;
 }
 
-// Acquire side: drop this CU's vector L1 lines, so the payload loads that
-// follow are served by the L2 the producer wrote to.  `buffer_inv sc0` is the
-// L1-only invalidate (the one gfx950 uses for a workgroup-scope acquire when
-// a workgroup's waves may sit on different CUs).  The agent-scope acquire
-// fence (`buffer_inv sc1`) would also invalidate the L2's lines of other
-// memory types, which a queue whose producer and consumer share one L2 does
-// not need: with it the pipelined MGN edge MLP took 0.88 ms per call instead
-// of 0.63 ms.  The caller has already observed the counter (a load that has
-// returned: qwait's barrier follows its s_waitcnt).
-__device__ __forceinline__ void l1_invalidate() { asm volatile("buffer_inv sc0" ::: "memory"); }
+// Acquire side.  A queue's producers and consumers run on different CUs of one
+// XCD, and the vector L1 of a CU is not kept coherent with stores from other
+// CUs.  `buffer_inv sc0` (the L1 invalidate of a workgroup-scope acquire) does
+// not drop those lines either: a one-slot queue of 16 KiB entries, re-read by
+// its consumer every tile, delivered the slot's previous round from L1.  So
+// every load of a queue payload carries the agent-scope cache policy (SC1),
+// which reads the L2 that the producer's stores reached, and no invalidate is
+// issued: the agent-scope acquire fence (`buffer_inv sc1`) would also drop the
+// L2's lines of other memory types, which cost the pipelined MGN edge MLP 0.88
+// against 0.63 ms per call.  The counters and the row count are read with
+// agent-scope atomic / volatile loads, which bypass the L1 as well.
+constexpr int kQueueLoadAux = 16;  // cache-policy bits of a buffer load: SC1
+
+// 16 bytes at element `off` of a tile view, from a queue payload (Q, the SC1
+// policy) or from memory.  Loads of a queue view stay below its row count.
+template <bool Q>
+__device__ __forceinline__ h8 view_load_h8(const TensorView& v, int64_t off) {
+  if constexpr (Q) {
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(v.data, v.rows * v.stride * 2);
+    return __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(off * 2), 0, kQueueLoadAux));
+  } else {
+    return *(const h8*)(v.data + off);
+  }
+}
 
 // Release side, workgroup-collective: every store of every wave is complete
 // in L2 once this returns.
@@ -179,7 +193,6 @@ struct RingQueue {
   __device__ Entry* read_wait(int64_t seq, int* rows, const QueueCtx& ctx) {
     QueueSlot<Entry>& s = slot(seq);
     const bool ok = qwait(&s.full, (uint32_t)(seq / N + 1) * NP, ctx);
-    l1_invalidate();
     *rows = ok ? *(volatile int*)&s.rows : 0;
     return &s.data;
   }
@@ -193,7 +206,7 @@ struct RingQueue {
     if (threadIdx.x == 0) qcommit(&slot(seq).empty, ctx.epoch, seq < N);
   }
   // Thread-level, no wait: have all NP producers of `seq` committed?  A
-  // consumer that sees true may load the payload after l1_invalidate().
+  // consumer that sees true may load the payload (with the SC1 policy).
   __device__ bool full_peek(int64_t seq, const QueueCtx& ctx) {
     const unsigned long long v = __hip_atomic_load(&slot(seq).full.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return qcount(v, ctx.epoch) >= (uint32_t)(seq / N + 1) * NP;

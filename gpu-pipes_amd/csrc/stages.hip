@@ -168,7 +168,7 @@ __device__ __forceinline__ unsigned handoff_sum(const TensorView& v) {
   __shared__ unsigned part[kStageThreads / kWave];
   unsigned s = 0;
   for (int q = threadIdx.x; q < v.rows * 16; q += kStageThreads) {
-    const u32x4 w = *(const u32x4*)((const char*)v.data + (int64_t)q * 16);
+    const u32x4 w = __builtin_bit_cast(u32x4, view_load_h8<true>(v, (int64_t)q * 8));  // a queue payload
     s += (w[0] + w[1]) + (w[2] + w[3]);
   }
 #pragma unroll

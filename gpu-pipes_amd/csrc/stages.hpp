@@ -99,7 +99,9 @@ constexpr int gemm_chain_lds() {
 // NeRF encoding, a 320-wide concatenation) runs as a K-wide tile whose extra
 // columns are zero, never the next row's data.
 // NT: copy with the non-temporal cache policy -- for an input streamed from
-// memory once, so that it does not evict the L2 lines of the ring queues.
+// memory once, so that it does not evict the L2 lines of the ring queues;
+// otherwise the tile is a queue payload, copied with the agent-scope policy
+// (kQueueLoadAux: read from L2, never from a stale L1 line).
 template <int MBLK, int K, bool NT = false>
 __device__ __forceinline__ void load_tile_swz(const TensorView& v, GP_LDS char* dst, int kv = K) {
   static_assert(K % 128 == 0, "K must be a multiple of 128");
@@ -119,7 +121,7 @@ __device__ __forceinline__ void load_tile_swz(const TensorView& v, GP_LDS char* 
     if constexpr (NT)
       dma16_buf_nt(rsrc, off, dst + i * 1024);
     else
-      dma16_buf(rsrc, off, dst + i * 1024);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst + i * 1024, 16, off, 0, 0, kQueueLoadAux);
   }
 }
 
@@ -262,6 +264,7 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
   constexpr int PB = PROWS * K * 2;                 // bytes per part buffer
   constexpr int RBP = PROWS / 32;                   // 32-row blocks per part
   static_assert(!CH || !PF, "a chained stage takes whole tiles");
+  static_assert(!AR::kFromQueue, "accumulator tiles are read from memory");
   constexpr int ACT_OUT = CH ? ACT_NONE : ACT;      // activation of the stored result
   GP_LDS char* xs = dyn_lds();
   GP_LDS char* const chb = xs + gemm_stage_lds<MBLK, K, NB>();  // CH: the first layer's output tile
@@ -379,7 +382,6 @@ __device__ void gemm_stage_impl(TensorView weight, TensorView bias, TensorView g
       if (qnext) {
         // the peeked tile is now the reader's current one; copy all MBLK rows
         // (rows past its count are never stored)
-        l1_invalidate();
         copy_part(ir.view(MBLK), 0, pb ^ 1);
       }
     } else {
@@ -630,7 +632,7 @@ __device__ void pipe_layer_norm(TensorView gamma, TensorView beta, IR& ir, OW& o
 #pragma unroll
       for (int j = 0; j < NV; ++j) {
         h8 v = {};
-        if (valid) v = *(const h8*)(in.data + (int64_t)r * in.stride + 128 * j + 8 * g16);
+        if (valid) v = view_load_h8<IR::kFromQueue>(in, (int64_t)r * in.stride + 128 * j + 8 * g16);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           x[j][e] = (float)v[e];
@@ -682,8 +684,8 @@ __device__ void pipe_add_n(IR0& ir0, IR1& ir1, OW& ow, int num_iters, int n) {
     const int n = rows < c.rows ? rows : c.rows;  // a NullWriter takes no rows
     for (int i = threadIdx.x; i < n * vpr; i += kStageThreads) {
       const int r = i / vpr, v = i - r * vpr;
-      const h8 x = *(const h8*)(a.data + (int64_t)r * a.stride + 8 * v);
-      const h8 y = *(const h8*)(b.data + (int64_t)r * b.stride + 8 * v);
+      const h8 x = view_load_h8<IR0::kFromQueue>(a, (int64_t)r * a.stride + 8 * v);
+      const h8 y = view_load_h8<IR1::kFromQueue>(b, (int64_t)r * b.stride + 8 * v);
       *(h8*)(c.data + (int64_t)r * c.stride + 8 * v) = x + y;
     }
     ir0.read_release();
@@ -713,8 +715,8 @@ __device__ void pipe_concat_n(IR0& ir0, IR1& ir1, OW& ow, int num_iters, int n0,
     const int n = rows < c.rows ? rows : c.rows;  // a NullWriter takes no rows
     for (int i = threadIdx.x; i < n * vo; i += kStageThreads) {
       const int r = i / vo, v = i - r * vo;
-      const h8 x = v < v0 ? *(const h8*)(a.data + (int64_t)r * a.stride + 8 * v)
-                          : *(const h8*)(b.data + (int64_t)r * b.stride + 8 * (v - v0));
+      const h8 x = v < v0 ? view_load_h8<IR0::kFromQueue>(a, (int64_t)r * a.stride + 8 * v)
+                          : view_load_h8<IR1::kFromQueue>(b, (int64_t)r * b.stride + 8 * (v - v0));
       *(h8*)(c.data + (int64_t)r * c.stride + 8 * v) = x;
     }
     ir0.read_release();
@@ -740,7 +742,7 @@ __device__ void pipe_copy_n(IR& ir, OW& ow, int num_iters, int n) {
     const int n = a.rows < c.rows ? a.rows : c.rows;  // a NullWriter takes no rows
     for (int i = threadIdx.x; i < n * vpr; i += kStageThreads) {
       const int r = i / vpr, v = i - r * vpr;
-      *(h8*)(c.data + (int64_t)r * c.stride + 8 * v) = *(const h8*)(a.data + (int64_t)r * a.stride + 8 * v);
+      *(h8*)(c.data + (int64_t)r * c.stride + 8 * v) = view_load_h8<IR::kFromQueue>(a, (int64_t)r * a.stride + 8 * v);
     }
     ir.read_release();
     ow.write_release();
