@@ -18,8 +18,9 @@
 //    memset: a counter from an older epoch reads as zero.
 //  * Release: the producer's payload stores are complete in L2 (vmcnt(0) in
 //    every wave, then a barrier) before the commit atomic.  Acquire: after the
-//    consumer observes the counter it invalidates its CU's L1 (buffer_inv sc0)
-//    so payload loads are served by L2.  The reference has no fences at all
+//    consumer observes the counter, its payload loads carry the agent-scope
+//    cache policy (SC1), so they are served by L2, not by a stale L1 line.
+//    The reference has no fences at all
 //    (mpmcq.cuh:34-40).  Producer and consumer must share an XCD (one L2):
 //    the pipelined kernels assign stage roles by the hardware XCC id.
 //  * Waits are bounded: on timeout an error word is set and every later wait
