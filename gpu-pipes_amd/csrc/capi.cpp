@@ -239,7 +239,7 @@ int gp_pipe_ident(int64_t M, const void* x, void* out, int max_pipes, void* stre
 int gp_pipe_route(int64_t M, const void* x, void* out, void* out2, int route, int max_pipes, void* stream) {
   int dev = 0, ncu = 0;
   if (route != GP_ROUTE_IDENT && route != GP_ROUTE_BROADCAST && route != GP_ROUTE_SPLIT && route != GP_ROUTE_DRAIN &&
-      route != GP_ROUTE_HANDOFF)
+      route != GP_ROUTE_HANDOFF && route != GP_ROUTE_RELOAD)
     return fail(GP_ERR_INVALID_ARG, "unknown route %d", route);
   if (route == GP_ROUTE_HANDOFF) {
     clear_error();

@@ -44,6 +44,7 @@ constexpr uint32_t kArenaLayoutNerfA = 5;
 constexpr uint32_t kArenaLayoutGemmLn = 6;  // LayerNorm-epilogue GEMMs: partial row statistics
 constexpr uint32_t kArenaLayoutBertFfn = 7;
 constexpr uint32_t kArenaLayoutMgnSplit = 8;  // mgn_pipelined's split-LayerNorm layout
+constexpr uint32_t kArenaLayoutRouteReload = 9;  // the one-slot route of 64-row entries
 // GP_ERR_INVALID_ARG if `stream` is capturing into a graph: the queue-chained
 // launches call it before any other HIP call (a replay would reuse the
 // captured queue epoch).

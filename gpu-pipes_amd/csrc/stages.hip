@@ -117,12 +117,17 @@ __global__ __launch_bounds__(kStageThreads) void concat_kernel(const half_t* a, 
 //    order -> out, the split write of bert_addln_ffn_pl.cuh:121.
 //  * ROUTE_HANDOFF (2 stages): generated tiles -> q -> per-tile checksums,
 //    the queue benchmark of misc_tests/pipeperf/pipeperf.cu:125-215.
+//  * ROUTE_RELOAD (2 stages): x -> q (one slot, 64-row entries) -> out.  The
+//    consumer reads the same 16 KiB of slot every tile, which fits its CU's
+//    L1: payload loads served by L1 would return the slot's previous round.
 // ---------------------------------------------------------------------------
 using RouteEntry = QueueEntry2D<MBLK, 128>;
 using IdentQueue = RingQueue<RouteEntry, 2>;
 using BcastQueue = RingQueue<RouteEntry, 2, 1, 2>;
 constexpr int kSplitWorkers = 3;
 using SplitQueue = RingQueue<RouteEntry, kSplitWorkers + 1>;
+constexpr int kReloadRows = 64;
+using ReloadQueue = RingQueue<QueueEntry2D<kReloadRows, 128>, 1>;
 
 struct RouteQueues {
   union {
@@ -131,6 +136,7 @@ struct RouteQueues {
     struct {
       SplitQueue q0, q1;
     } split;
+    ReloadQueue reload;
   };
 };
 
@@ -146,7 +152,9 @@ struct RouteArgs {
 };
 
 constexpr int route_stages(int route) {
-  return route == GP_ROUTE_IDENT || route == GP_ROUTE_HANDOFF ? 2 : (route == GP_ROUTE_SPLIT ? 2 + kSplitWorkers : 3);
+  return route == GP_ROUTE_IDENT || route == GP_ROUTE_HANDOFF || route == GP_ROUTE_RELOAD
+             ? 2
+             : (route == GP_ROUTE_SPLIT ? 2 + kSplitWorkers : 3);
 }
 
 // Hand-off benchmark payload: word i of tile t (row-major, 64 words per
@@ -206,6 +214,20 @@ __global__ __launch_bounds__(kStageThreads) void route_kernel(RouteArgs a) {
       QueueReader<IdentQueue> ir(&q->ident, &a.ctx);
       MemoryWriter ow((half_t*)a.out + g * C * tile, tile, 128);
       pipe_copy_n(ir, ow, nc, 128);
+    }
+  } else if constexpr (ROUTE == GP_ROUTE_RELOAD) {
+    // 64-row tiles g, g + P, ... of pipeline g
+    const int64_t T2 = (a.M + kReloadRows - 1) / kReloadRows;
+    const int n2 = g < T2 ? (int)((T2 - 1 - g) / P + 1) : 0;
+    const int64_t t2 = (int64_t)kReloadRows * 128;
+    if (r.stage == 0) {
+      MemoryReader ir((half_t*)a.x + g * t2, P * t2, 128, kReloadRows, a.M - g * kReloadRows, P * kReloadRows);
+      QueueWriter<ReloadQueue> ow(&q->reload, &a.ctx);
+      pipe_copy_n(ir, ow, n2, 128);
+    } else {
+      QueueReader<ReloadQueue> ir(&q->reload, &a.ctx);
+      MemoryWriter ow((half_t*)a.out + g * t2, P * t2, 128);
+      pipe_copy_n(ir, ow, n2, 128);
     }
   } else if constexpr (ROUTE == GP_ROUTE_HANDOFF) {
     // misc_tests/pipeperf/pipeperf.cu:125-163: sender / receiver over one
@@ -501,7 +523,8 @@ static int route_launch(int64_t M, const void* x, void* out, void* out2, int max
   const size_t bytes = sizeof(PipeCtl) + (size_t)(grid / S) * sizeof(RouteQueues);
   void* base = nullptr;
   uint32_t epoch = 0;
-  int rc = arena_acquire(dev, s, bytes, kArenaLayoutRoute + (ROUTE == GP_ROUTE_SPLIT), &base, &epoch);
+  const uint32_t layout = ROUTE == GP_ROUTE_RELOAD ? kArenaLayoutRouteReload : kArenaLayoutRoute + (ROUTE == GP_ROUTE_SPLIT);
+  int rc = arena_acquire(dev, s, bytes, layout, &base, &epoch);
   if (rc != GP_OK) return rc;
   RouteArgs a;
   a.x = (const half_t*)x;
@@ -527,6 +550,7 @@ int pipe_route_run(int64_t M, const void* x, void* out, void* out2, int route, i
     case GP_ROUTE_SPLIT: return route_launch<GP_ROUTE_SPLIT>(M, x, out, out2, max_pipes, dev, num_cus, s);
     case GP_ROUTE_DRAIN: return route_launch<GP_ROUTE_DRAIN>(M, x, out, out2, max_pipes, dev, num_cus, s);
     case GP_ROUTE_HANDOFF: return route_launch<GP_ROUTE_HANDOFF>(M, x, out, out2, max_pipes, dev, num_cus, s);
+    case GP_ROUTE_RELOAD: return route_launch<GP_ROUTE_RELOAD>(M, x, out, out2, max_pipes, dev, num_cus, s);
     default: return fail(GP_ERR_INVALID_ARG, "unknown route %d", route);
   }
 }

@@ -43,7 +43,7 @@ IMPL_PIPELINED = 1
 IMPL_PIPELINED_SPLIT_LN = 2
 _IMPLS = {"fused": IMPL_FUSED, "pipelined": IMPL_PIPELINED, "pipelined_split_ln": IMPL_PIPELINED_SPLIT_LN}
 ACTS = {"none": 0, "relu": 1, "gelu_tanh": 2, "sigmoid": 3}
-ROUTES = {"ident": 0, "broadcast": 1, "split": 2, "drain": 3, "handoff": 4}
+ROUTES = {"ident": 0, "broadcast": 1, "split": 2, "drain": 3, "handoff": 4, "reload": 5}
 
 
 class GpipesError(RuntimeError):
@@ -333,7 +333,7 @@ def pipe_ident(x, max_pipes=0, out=None):
 
 
 def pipe_route(x, route="ident", max_pipes=0):
-    """Copy x[M,128] through a queue topology (ident / broadcast / split / drain); returns
+    """Copy x[M,128] through a queue topology (ident / broadcast / split / drain / reload); returns
     (out, out2) -- out2 is None except for the two-consumer broadcast (the drain's second
     consumer discards its tiles)."""
     _check_input("x", x)

@@ -428,6 +428,10 @@ int gp_pipe_ident(int64_t M, const void* x, void* out, int max_pipes, void* stre
                              /* i < 64 * rows (word i of the tile in row-major order, rows = */
                              /* min(128, M - 128 t)); tiles t = g, g + P, ... go through     */
                              /* pipeline g of P                                              */
+#define GP_ROUTE_RELOAD 5    /* x -> one-slot queue of 64-row entries -> out: the consumer   */
+                             /* reads the same slot addresses every tile, so stale L1 lines  */
+                             /* of its previous round would show (the check of the queue's   */
+                             /* agent-scope payload loads); no counterpart in the reference  */
 
 /*
  * Copy pipelines over the queue topologies the reference's apps use; out

@@ -149,13 +149,15 @@ def test_pipe_ident_back_to_back(cuda):
         assert torch.equal(y.view(torch.int16), x.view(torch.int16)), i
 
 
-@pytest.mark.parametrize("route", ["ident", "broadcast", "split", "drain"])
+@pytest.mark.parametrize("route", ["ident", "broadcast", "split", "drain", "reload"])
 @pytest.mark.parametrize("M", [1, 129, 100003, 1048576])
 @pytest.mark.parametrize("max_pipes", [1, 0, 5])
 def test_pipe_route_bit_exact(cuda, route, M, max_pipes):
     """Queue topologies: 1:1 over striped input chunks (read_striped_input), one producer /
-    two consumers, split / merge, and the broadcast whose second consumer is a NullWriter
-    (it must keep the two-consumer queue draining, or the launch times out)."""
+    two consumers, split / merge, the broadcast whose second consumer is a NullWriter
+    (it must keep the two-consumer queue draining, or the launch times out), and a one-slot
+    queue of 64-row entries whose consumer re-reads the same 16 KiB every tile (payload
+    loads served by its L1 would return the slot's previous round)."""
     x = torch.randn((M, 128), device=cuda, generator=torch.Generator(device=cuda).manual_seed(M + 1)).to(torch.float16)
     out, out2 = gpipes.pipe_route(x, route, max_pipes=max_pipes)
     gpipes.pipeline_check()
@@ -197,7 +199,7 @@ def test_arena_shared_by_different_queue_layouts(cuda):
     ref = gpipes.mgn_mlp(xe, p["w1"], p["b1"], p["w2"], p["b2"], p["w3"], p["b3"], p["gamma"], p["beta"],
                          impl="pipelined")
     gpipes.pipeline_check()
-    for route in ["split", "ident", "broadcast", "drain", "split", "ident"]:
+    for route in ["split", "ident", "reload", "broadcast", "drain", "split", "reload", "ident"]:
         out, _ = gpipes.pipe_route(x, route)
         gpipes.pipeline_check()
         assert torch.equal(out, x), route

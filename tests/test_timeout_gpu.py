@@ -146,7 +146,7 @@ def test_pipelined_timeout_reported(cuda, restore_limit, impl):
     assert_parity(y.float().cpu().numpy()[idx], run_oracle(x.cpu()[idx], p), f"{impl} after timeout")
 
 
-@pytest.mark.parametrize("route", ["ident", "broadcast", "split", "drain"])
+@pytest.mark.parametrize("route", ["ident", "broadcast", "split", "drain", "reload"])
 def test_route_timeout_reported(cuda, restore_limit, route):
     M = 128 * 200 + 3
     print(f"[timeout] route {route} M={M}", flush=True)
