@@ -48,11 +48,9 @@
 //    through buffer descriptors bounded to the tile's valid rows.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
 #include <type_traits>
 #include <utility>
-
-#include "../../include/gpipes.h"
-#include <mutex>
 
 #include "../../include/gpipes.h"
 #include "gp_device.hpp"
