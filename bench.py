@@ -202,14 +202,21 @@ class _Pacer:
                 self.marks.pop(0).synchronize()
 
 
-def _settle(run_one, stream, settle_ms):
+def _settle(run_one, stream, settle_ms, bracket=None):
     """Untimed submissions for settle_ms, paced by _Pacer (no synchronisation,
-    so the timed region that follows starts while the GPU is still busy)."""
+    so the timed region that follows starts while the GPU is still busy).
+    bracket: a pair of timing events recorded around every launch, as the
+    timed region records its per-step events, so that the submission pattern
+    does not change where the timed region starts."""
     pacer = _Pacer(stream)
     t0 = time.perf_counter()
     n = 0
     while (time.perf_counter() - t0) * 1e3 < settle_ms:
+        if bracket is not None:
+            bracket[0].record(stream)
         run_one(n)
+        if bracket is not None:
+            bracket[1].record(stream)
         pacer.tick()
         n += 1
     return {"ms": (time.perf_counter() - t0) * 1e3, "launches": n}
@@ -268,7 +275,8 @@ def timed_steps(step, args, dev):
     if getattr(args, "telemetry", False):
         settle_ms, tel = max(settle_ms, 3000.0), start_telemetry()
     if settle_ms > 0:
-        settle = _settle(lambda n: step(args.warmup + n), stream, settle_ms)
+        bracket = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        settle = _settle(lambda n: step(args.warmup + n), stream, settle_ms, bracket)
     outer[0].record(stream)
     for i in range(args.steps):
         ev[i][0].record(stream)
