@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/gpipes.h"
 
 namespace gp {
@@ -210,9 +212,18 @@ hipError_t nerf_fused_launch(int64_t M, int Kx, int Kd, int Na, int Nrgb, const 
 inline bool nerf_trunk_supported(int64_t Kx) { return Kx >= 1 && Kx <= 64; }
 hipError_t nerf_trunk_launch(int64_t M, int Kx, const void* x, const void* const* w, const void* const* b, void* out,
                              void* ws, int num_cus, hipStream_t stream, int dtype = GP_DTYPE_F16);
-// Device address and size of the NeRF kernel's static scratch on device `dev`
-// (the current device), for the allocation-free entry point.
-int nerf_static_scratch(int dev, void** ptr, size_t* bytes);
+// The NeRF kernel's static scratch on device `dev` (the current device), for
+// the allocation-free entry point: its device address and size, the event
+// that chains the calls on that device (each eager call's stream waits for it
+// and records it after its own kernels) and the lock that keeps the wait,
+// the launches and the record of one call together.
+struct NerfScratch {
+  void* ptr;
+  size_t bytes;
+  hipEvent_t last;
+  std::mutex* lock;
+};
+int nerf_static_scratch(int dev, NerfScratch* out);
 
 // The DLRM bottom MLP (K0 -> 512 -> 256 -> 128, apps/dlrm_botmlp) as one fused
 // kernel: supported for K0 <= 32, identity or ReLU after the first two layers

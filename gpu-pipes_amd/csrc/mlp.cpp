@@ -23,6 +23,7 @@
 // contribute nothing.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
 #include <vector>
 
 #include "../../include/gpipes.h"
@@ -534,15 +535,24 @@ int gp_nerf_full_out_noalloc(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int6
     return fail(GP_ERR_ALIGN, "x and d must be 16-byte aligned (the allocation-free call cannot copy them)");
   int dev = 0, ncu = 0;
   if ((rc = current_device_info(&dev, &ncu))) return rc;
-  void* ws = nullptr;
-  size_t bytes = 0;
-  if ((rc = nerf_static_scratch(dev, &ws, &bytes))) return rc;
-  if (bytes < nerf_fused_workspace())
-    return fail(GP_ERR_SHAPE, "static scratch of %zu bytes is below the %zu the kernel needs", bytes,
+  NerfScratch sc{};
+  if ((rc = nerf_static_scratch(dev, &sc))) return rc;
+  if (sc.bytes < nerf_fused_workspace())
+    return fail(GP_ERR_SHAPE, "static scratch of %zu bytes is below the %zu the kernel needs", sc.bytes,
                 nerf_fused_workspace());
-  hipError_t e = nerf_fused_launch(M, (int)Kx, (int)Kd, (int)Na, (int)Nrgb, x, d, w, b, rgb_act, out_r, out_rgb, ws,
-                                   ncu, (hipStream_t)stream);
+  // An eager call waits for the previous call's kernels on this GPU (whatever
+  // its stream) and records the event after its own; a call under capture is
+  // not chained (a graph cannot wait on an event recorded outside it).
+  const hipStream_t s = (hipStream_t)stream;
+  std::lock_guard<std::mutex> lk(*sc.lock);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(s, &cs);
+  if (e != hipSuccess) return fail_hip(e, "hipStreamIsCapturing");
+  const bool eager = cs == hipStreamCaptureStatusNone;
+  if (eager && (e = hipStreamWaitEvent(s, sc.last, 0)) != hipSuccess) return fail_hip(e, "hipStreamWaitEvent");
+  e = nerf_fused_launch(M, (int)Kx, (int)Kd, (int)Na, (int)Nrgb, x, d, w, b, rgb_act, out_r, out_rgb, sc.ptr, ncu, s);
   if (e != hipSuccess) return fail_hip(e, "NeRF fused kernel launch");
+  if (eager && (e = hipEventRecord(sc.last, s)) != hipSuccess) return fail_hip(e, "hipEventRecord");
   return GP_OK;
 }
 

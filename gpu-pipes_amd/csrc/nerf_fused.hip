@@ -618,28 +618,36 @@ size_t nerf_fused_workspace() { return (size_t)nerf::S_TOTAL * nerf::SLOT + (siz
 // packed weight stream and bias tables, in a file-scope device array instead
 // of the per-stream workspace.  Every GPU the library runs on holds its own
 // copy until the process ends.  The packing kernel rewrites every byte the
-// fused kernel reads on each call, so nothing has to start at zero; calls that
-// overlap on one GPU share the array and race.
+// fused kernel reads on each call, so nothing has to start at zero.  All
+// calls on one GPU share the array: eager calls are chained through one event
+// per device, so that calls on different streams run one after the other
+// (calls captured into a graph are not chained: replays that overlap race).
 constexpr size_t kNerfScratchBytes =
     ((size_t)nerf::S_TOTAL * nerf::SLOT + (size_t)nerf::B_TOTAL * 2 + 255) & ~size_t(255);
 static __device__ __align__(256) char scratch[kNerfScratchBytes];
 
-int nerf_static_scratch(int dev, void** ptr, size_t* bytes) {
+int nerf_static_scratch(int dev, NerfScratch* out) {
   // In host code `scratch` names a host-side stand-in, never the device
   // memory: its device address is looked up once per device (with that device
-  // current) and only that address is handed to kernels.
+  // current) and only that address is handed to kernels.  The device's event
+  // is created at the same set-up step, so later calls create nothing.
   static std::mutex mu;
   static void* dev_ptr[64];
+  static hipEvent_t dev_ev[64];
+  static std::mutex dev_lock[64];
   if (dev < 0 || dev >= 64) return fail(GP_ERR_NO_DEVICE, "device index %d out of range", dev);
   std::lock_guard<std::mutex> lk(mu);
   if (dev_ptr[dev] == nullptr) {
     void* p = nullptr;
     hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return fail_hip(e, "hipGetSymbolAddress (NeRF static scratch)");
+    hipEvent_t ev = nullptr;
+    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) return fail_hip(e, "hipEventCreateWithFlags (NeRF static scratch)");
+    dev_ev[dev] = ev;
     dev_ptr[dev] = p;
   }
-  *ptr = dev_ptr[dev];
-  *bytes = kNerfScratchBytes;
+  *out = NerfScratch{dev_ptr[dev], kNerfScratchBytes, dev_ev[dev], &dev_lock[dev]};
   return GP_OK;
 }
 

@@ -738,7 +738,9 @@ def nerf_a(x, *wb, impl="fused"):
 def nerf_full_out_noalloc(x, d, *wb_and_outs, rgb_act="none"):
     """nerf_full_out through the allocation-free entry point (gp_nerf_full_out_noalloc): the
     fused kernel's shapes only (Kx <= 64, Kd <= 32, Na <= 64, Nrgb <= 64), x and d 16-byte
-    aligned; its scratch is a static per-GPU array, so calls that overlap on one GPU race."""
+    aligned; its scratch is a static per-GPU array shared by every call on the GPU: eager
+    calls are chained by the library (each waits for the previous call's kernels, whatever
+    its stream), graph replays are not and race if they overlap."""
     if len(wb_and_outs) != 26:
         raise RuntimeError("expected w1, b1, ..., w12, b12, out_r, out_rgb")
     ws, bs = list(wb_and_outs[0:24:2]), list(wb_and_outs[1:24:2])

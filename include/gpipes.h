@@ -325,8 +325,14 @@ int gp_nerf_full_dtype_out(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_
  * 16-byte aligned x and d; other shapes are rejected with GP_ERR_SHAPE /
  * GP_ERR_ALIGN.  Its scratch (the packed weight stream, 1,255,168 bytes) is a
  * static device array that every GPU the library runs on holds until the
- * process ends; every call on a GPU shares it, so calls that overlap on one
- * GPU race.  Calls no hipMalloc, hipFree or allocating library routine.
+ * process ends, shared by every call on that GPU.  Eager calls are chained
+ * through one event per GPU: each call's stream waits for the previous call's
+ * kernels (on whatever stream) and records the event after its own, so calls
+ * on different streams run in turn.  Calls under graph capture are not
+ * chained: graph replays that overlap each other or an eager call race for
+ * the scratch.  The first call on a GPU looks up the array's address and
+ * creates the event; no call makes hipMalloc, hipFree or an allocating
+ * library routine.
  */
 int gp_nerf_full_out_noalloc(int64_t M, int64_t Kx, int64_t Kd, int64_t Na, int64_t Nrgb, const void* x,
                              const void* d, const void* const* w, const void* const* b, int rgb_act, void* out_r,

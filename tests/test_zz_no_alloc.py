@@ -2,8 +2,9 @@
 through the C ABI: its outputs must be bit-identical to gp_nerf_full_out's on
 the same inputs (the same kernels run; only the scratch differs), on two calls
 in a row, the second with a smaller batch, so that the shared static scratch
-is reused with what the first call left in it.  Shapes it cannot run are
-rejected before any launch."""
+is reused with what the first call left in it.  Calls on two streams are
+chained by the library, so they do not race on that scratch.  Shapes it
+cannot run are rejected before any launch."""
 import ctypes
 
 import numpy as np
@@ -84,3 +85,36 @@ def test_noalloc_rejects_what_it_cannot_run(cuda):
     # M = 0 is a no-op
     z = torch.empty((0, 64), dtype=torch.float16, device=cuda)
     assert call_noalloc(z, d[:0], ws, bs, out_r[:0], out_rgb[:0]) == 0
+
+
+def test_noalloc_calls_on_two_streams_are_chained(cuda):
+    """Calls on two streams, issued back to back without a host wait, share the
+    static scratch; the library chains them (each call's stream waits for the
+    previous call's kernels), so each output is bit-identical to the default
+    entry point's on its own inputs and weights."""
+    M = 120000
+    cases = []
+    for seed in (11, 12):
+        ws, bs = nerf_params(64, 27, 1, 3, seed=seed, device=cuda)
+        x, d = nerf_inputs(M, seed=seed, device=cuda)
+        ref_r, ref_rgb = call_default(x, d, ws, bs)
+        out_r = torch.empty((M, 1), dtype=torch.float16, device=cuda)
+        out_rgb = torch.empty((M, 3), dtype=torch.float16, device=cuda)
+        cases.append((x, d, ws, bs, ref_r, ref_rgb, out_r, out_rgb))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(cuda), torch.cuda.Stream(cuda)]
+    for rnd in range(3):
+        print(f"[noalloc two streams] round {rnd}", flush=True)
+        for _, _, _, _, _, _, out_r, out_rgb in cases:
+            out_r.fill_(float("nan"))
+            out_rgb.fill_(float("nan"))
+        torch.cuda.synchronize()
+        order = (0, 1) if rnd % 2 == 0 else (1, 0)
+        for i in order:
+            x, d, ws, bs, _, _, out_r, out_rgb = cases[i]
+            with torch.cuda.stream(streams[i]):
+                assert call_noalloc(x, d, ws, bs, out_r, out_rgb) == 0, L.gp_last_error().decode()
+        torch.cuda.synchronize()
+        for i, (_, _, _, _, ref_r, ref_rgb, out_r, out_rgb) in enumerate(cases):
+            assert np.array_equal(bits(out_r), bits(ref_r)), f"density of call {i} differs (round {rnd})"
+            assert np.array_equal(bits(out_rgb), bits(ref_rgb)), f"colour of call {i} differs (round {rnd})"
