@@ -209,8 +209,12 @@ template <int R>
 __device__ __forceinline__ void weight_dma(const half_t* W, WSpan dst, int wave, int lane) {
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(W, R * D * 2);
   const int voff = wrow_voff(lane, D * 2);
+  static_assert((R / 4) % NWAVES == 0, "every wave issues the same number of copies");
 #pragma unroll
-  for (int j = wave; j < R / 4; j += NWAVES) dma16_buf_so(rs, voff, j * (4 * D * 2), dst.block(j));
+  for (int i = 0; i < R / 4 / NWAVES; ++i) {
+    const int j = wave + NWAVES * i;
+    dma16_buf_so(rs, voff, j * (4 * D * 2), dst.block(j));
+  }
 }
 // Lane j of each 16-lane group receives W[kb + e][fb + j], e = 0..7 (kb a
 // multiple of 8, fb of 16).
