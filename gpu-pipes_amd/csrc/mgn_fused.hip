@@ -222,6 +222,19 @@ __device__ __forceinline__ h8 w_col8(const WSpan& w, int kb, int fb, int m) {
   return wrows_col8(w.block(kb >> 2), w.block((kb >> 2) + 1), fb, m);
 }
 
+// s_memrealtime at five points of the weight prologue, in the phase-timer
+// build only (the product build's marks are empty).
+#ifdef GP_PHASE_TIMERS
+struct PrologueMarks {
+  unsigned long long t[5] = {0, 0, 0, 0, 0};
+  __device__ void mark(int i) { t[i] = __builtin_amdgcn_s_memrealtime(); }
+};
+#else
+struct PrologueMarks {
+  __device__ void mark(int) {}
+};
+#endif
+
 // Prologue shared by both stages: W1 (into the X buffers) and W2 (into the
 // hand-off slots) are copied at once; take12(w1, w2) then reads the caller's
 // fragments.  W3 follows into the hand-off slots once every wave has its W1
@@ -231,21 +244,26 @@ __device__ __forceinline__ h8 w_col8(const WSpan& w, int kb, int fb, int m) {
 // issues, which the W3 wait leaves in flight (the barriers after it wait for
 // LDS traffic only).
 template <int K, int EARLY_OPS, typename Pre, typename T12, typename Early, typename T3>
-__device__ __forceinline__ void stage_weights_dma(const Params& p, WSpan xsp, WSpan hsp, int wave, int lane, Pre pre,
-                                                  T12 take12, Early early, T3 take3) {
+__device__ __forceinline__ void stage_weights_dma(const Params& p, WSpan xsp, WSpan hsp, PrologueMarks& pm, int wave,
+                                                  int lane, Pre pre, T12 take12, Early early, T3 take3) {
   weight_dma<K>(p.w1, xsp, wave, lane);
   weight_dma<D>(p.w2, hsp, wave, lane);
   pre();
   wait_vmcnt<0>();
+  pm.mark(0);
   __syncthreads();
+  pm.mark(1);
   take12(xsp, hsp);
   __syncthreads();  // W1 and W2 read by every wave
+  pm.mark(2);
   weight_dma<D>(p.w3, hsp, wave, lane);
   early();
   wait_vmcnt<EARLY_OPS>();
+  pm.mark(3);
   lds_barrier();
   take3(hsp);
   lds_barrier();  // the hand-off slots return to their tiles
+  pm.mark(4);
 }
 
 // Sum of a value over the four lanes l, l^16, l^32, l^48 (the lanes that
@@ -281,10 +299,11 @@ __device__ __forceinline__ void store_row_pair(half_t* row, const h4 (&hv)[2], i
 // cycles) of each phase of its tile loop into acc[], and at exit lane 0 of
 // wave w of workgroup b (b < kPhaseGroups) writes slot group (b * NWAVES + w):
 // acc[0..7], then the loop's total ticks, its s_memrealtime ticks (100 MHz),
-// the tiles it ran and the launch's grid size.  The product build's timer is
-// empty and costs nothing.
+// the tiles it ran, the launch's grid size, the s_memrealtime values at
+// kernel entry, at the loop's start and at its end, and the five prologue
+// marks.  The product build's timer is empty and costs nothing.
 constexpr int kPhaseGroups = 256;
-constexpr int kPhaseSlots = 12;
+constexpr int kPhaseSlots = 20;
 #ifdef GP_PHASE_TIMERS
 __device__ unsigned long long g_phase[kPhaseGroups * NWAVES * kPhaseSlots];
 struct PhaseTimer {
@@ -299,7 +318,7 @@ struct PhaseTimer {
     acc[i] += t - last;
     last = t;
   }
-  __device__ void finish(int wave, int lane, int nt) {
+  __device__ void finish(int wave, int lane, int nt, unsigned long long entry, const PrologueMarks& pm) {
     const unsigned long long t = __builtin_amdgcn_s_memtime(), r = __builtin_amdgcn_s_memrealtime();
     if (lane != 0 || blockIdx.x >= kPhaseGroups) return;
     unsigned long long* o = g_phase + ((int64_t)blockIdx.x * NWAVES + wave) * kPhaseSlots;
@@ -308,21 +327,29 @@ struct PhaseTimer {
     o[9] = r - r0;
     o[10] = (unsigned long long)nt;
     o[11] = gridDim.x;
+    o[12] = entry;
+    o[13] = r0;
+    o[14] = r;
+    for (int i = 0; i < 5; ++i) o[15 + i] = pm.t[i];
   }
 };
+__device__ __forceinline__ unsigned long long phase_entry() { return __builtin_amdgcn_s_memrealtime(); }
 #else
 struct PhaseTimer {
   __device__ void start() {}
   __device__ void tile() {}
   __device__ void mark(int) {}
-  __device__ void finish(int, int, int) {}
+  __device__ void finish(int, int, int, unsigned long long, const PrologueMarks&) {}
 };
+__device__ __forceinline__ unsigned long long phase_entry() { return 0; }
 #endif
 
 // GATHER_IDX: 0 = X given; 4 / 8 = gather, index bytes.  E: ElemF16 / ElemBF16.
 template <int K, bool LN, int GATHER_IDX = 0, typename E = ElemF16>
 __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void mgn_fused_kernel(Params p) {
+  const unsigned long long t_entry = phase_entry();  // phase-timer build only (0 otherwise)
+  PrologueMarks pro_t;
   using C = Cfg<K>;
   constexpr bool GATHER = GATHER_IDX != 0;
   static_assert(!GATHER || K == 3 * D, "the gather front end builds 384-wide rows");
@@ -416,7 +443,7 @@ void mgn_fused_kernel(Params p) {
     // W1 fragment for k-step s: lane holds W1[16s + 8*lh + e][32n + lr].
     // (Non-gather: the first X tile is copied during the W3 part of the prologue.)
     h8 w1f[C::KS1];
-    stage_weights_dma<K, GATHER ? 0 : C::DMA_PER_WAVE>(p, xspan, hspan, wave, lane, load_prm,
+    stage_weights_dma<K, GATHER ? 0 : C::DMA_PER_WAVE>(p, xspan, hspan, pro_t, wave, lane, load_prm,
         [&](const WSpan& w1, const WSpan&) {
 #pragma unroll
           for (int s = 0; s < C::KS1; ++s) w1f[s] = w_col8(w1, 16 * s + 8 * lh, 32 * n + 16 * ((lane >> 4) & 1), lane & 15);
@@ -549,7 +576,7 @@ void mgn_fused_kernel(Params p) {
       if (k + 1 < nt) tile_a((GP_LDS char*)xs1, (GP_LDS char*)xs0, (GP_LDS char*)hand1, k + 1);
     }
     wait_vmcnt<0>();  // the (empty) copy issued during the last tile has landed before the waves exit
-    pt.finish(wave, lane, nt);
+    pt.finish(wave, lane, nt, t_entry, pro_t);
   } else {
     // ------------------------------------------------------------- stage B
     // W2 (32x32x16 A operand): lane holds W2[16s + 8*lh + e][32n + lr].
@@ -558,7 +585,7 @@ void mgn_fused_kernel(Params p) {
     const int l16 = lane & 15, q4 = lane >> 4;
     h8 w2f[D / 16];
     h8 w3f[8][4];
-    stage_weights_dma<K, 0>(p, xspan, hspan, wave, lane, load_prm, [&](const WSpan&, const WSpan& w2) {
+    stage_weights_dma<K, 0>(p, xspan, hspan, pro_t, wave, lane, load_prm, [&](const WSpan&, const WSpan& w2) {
 #pragma unroll
       for (int s = 0; s < D / 16; ++s) w2f[s] = w_col8(w2, 16 * s + 8 * lh, 32 * n + 16 * ((lane >> 4) & 1), lane & 15);
     }, []() {}, [&](const WSpan& w3) {
@@ -674,7 +701,7 @@ void mgn_fused_kernel(Params p) {
       tile_b((GP_LDS char*)hand0, k);
       if (k + 1 < nt) tile_b((GP_LDS char*)hand1, k + 1);
     }
-    pt.finish(wave, lane, nt);
+    pt.finish(wave, lane, nt, t_entry, pro_t);
   }
   // The abort word is sticky and is set before the wave that set it gets
   // here, so the workgroup's timeout is reported at least once.

@@ -415,13 +415,17 @@ def probe_mfma(iters, dtype=torch.float16, device=None, shape=32):
 def phase_timers():
     """Per-phase shader-clock cycles per tile of the last fused MGN launch, averaged over the
     launch's workgroups (diagnostic build only: GPIPES_PHASE_TIMERS=1); also the loop's
-    cycles per tile and the clock they imply (s_memtime ticks / s_memrealtime time)."""
+    cycles per tile and the clock they imply (s_memtime ticks / s_memrealtime time), and how
+    the workgroups' tile loops end: the loop time of each workgroup (its slowest wave, in µs of
+    s_memrealtime) over the launch and averaged per XCD (workgroup b runs on XCD b % 8), with
+    each XCD's clock; the weight prologue (kernel entry to loop start) of each workgroup; and
+    how far apart the workgroups start and end."""
     import numpy as np
 
-    buf = np.zeros(256 * 8 * 12, dtype=np.uint64)
+    buf = np.zeros(256 * 8 * 20, dtype=np.uint64)
     torch.cuda.synchronize()
     _check(lib.gp_phase_timers_read(ctypes.c_void_p(buf.ctypes.data), buf.nbytes))
-    a = buf.reshape(256, 8, 12).astype(np.float64)
+    a = buf.reshape(256, 8, 20).astype(np.float64)
     grid = int(a[0, 0, 11])
     a = a[:grid]
     res = {"grid": grid}
@@ -434,6 +438,27 @@ def phase_timers():
             "clock_ghz": total / (w[..., 9].sum() * 10.0),
             "phases_per_tile": {nm: w[..., i].sum() / tiles for i, nm in enumerate(PHASE_NAMES[kind])},
         }
+    loop_us = a[:, :, 9].max(axis=1) / 100.0  # s_memrealtime runs at 100 MHz
+    xcd = np.arange(grid) % 8
+    clock = a[:, :, 8].sum(axis=1) / (a[:, :, 9].sum(axis=1) * 10.0)
+    res["workgroup_loop_us"] = {"min": float(loop_us.min()), "median": float(np.median(loop_us)),
+                                "mean": float(loop_us.mean()), "max": float(loop_us.max())}
+    res["xcd_loop_us_mean"] = [float(loop_us[xcd == i].mean()) for i in range(8) if (xcd == i).any()]
+    res["xcd_clock_ghz"] = [float(clock[xcd == i].mean()) for i in range(8) if (xcd == i).any()]
+    # s_memrealtime at kernel entry, loop start and loop end (one GPU-wide 100 MHz counter)
+    entry, start, end = a[:, :, 12].min(axis=1), a[:, :, 13].max(axis=1), a[:, :, 14].max(axis=1)
+    pro = (start - entry) / 100.0
+    res["prologue_us"] = {"min": float(pro.min()), "median": float(np.median(pro)), "max": float(pro.max())}
+    res["entry_spread_us"] = float((entry.max() - entry.min()) / 100.0)
+    res["end_spread_us"] = float((end.max() - end.min()) / 100.0)
+    res["entry_to_last_end_us"] = float((end.max() - entry.min()) / 100.0)
+    # prologue steps (median over workgroups of the slowest wave's time per step, µs):
+    # copies of W1 and W2 landed, barrier, their fragments read + barrier, W3 (and the
+    # first X tile) landed, W3's fragments read + barriers, then on to the loop
+    m = np.concatenate([entry[:, None], a[:, :, 15:20].max(axis=1), start[:, None]], axis=1)
+    steps = np.diff(m, axis=1) / 100.0
+    names = ("w12_landed", "barrier", "take12", "w3_landed", "take3", "to_loop")
+    res["prologue_steps_us"] = {nm: float(np.median(steps[:, i])) for i, nm in enumerate(names)}
     return res
 
 
