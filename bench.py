@@ -18,7 +18,10 @@ five launches), so a clock ramp or a slow box shows in the line itself.
 --settle-ms runs untimed launches for that long between the warm-up and the
 timed region, with no synchronisation between them, so the timed region starts
 while the GPU is busy; the line states it in "settle".  ms_per_step is the
-HIP-event time between the first and the last timed step divided by K.
+HIP-event time between the first and the last timed step divided by K.  For
+the MGN workloads, "repeats" also gives the ms per step of --repeats blocks of
+K steps per submission (the timed block and the blocks that follow it back to
+back) and their median; value comes from the first block.
 
 --workload bert times the BERT-large FFN block of configs[2] instead
 (LayerNorm(GELU(x W1 + b1) W2 + b2 + x), M = 65,536, H 1024, FF 4096): a step is
@@ -30,6 +33,7 @@ samples) are measured the same way.
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -252,7 +256,7 @@ def finish_telemetry(child):
             "umc_activity_pct": field("average_umc_activity")}
 
 
-def timed_steps(step, args, dev):
+def timed_steps(step, args, dev, with_repeats=False):
     """Warm-up and synchronise, then a settle phase and the timed region back
     to back: the settle launches keep the GPU busy up to the first timed step,
     so the timed region starts in the steady state with no idle gap (after an
@@ -261,7 +265,10 @@ def timed_steps(step, args, dev):
     every entry point launches on.  The K timed steps are bracketed by HIP
     events on that stream (outer events around all K, and a pair around each
     step); the host synchronises after the last one.  Returns (per-step ms in
-    launch order, ms per step between the outer events, settle record)."""
+    launch order, ms per step between the outer events, settle record); with
+    with_repeats, also the ms per step of args.repeats blocks of K steps: the
+    timed block, then the further blocks right behind it (each step bracketed
+    by events like the others, outer events per block)."""
     import torch
 
     stream = torch.cuda.current_stream(dev)
@@ -283,19 +290,36 @@ def timed_steps(step, args, dev):
         step(i)
         ev[i][1].record(stream)
     outer[1].record(stream)
+    blocks = []
+    if with_repeats:
+        bracket = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        for _ in range(args.repeats - 1):
+            o = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            o[0].record(stream)
+            for i in range(args.steps):
+                bracket[0].record(stream)
+                step(i)
+                bracket[1].record(stream)
+            o[1].record(stream)
+            blocks.append(o)
     torch.cuda.synchronize()
     if tel is not None:
         settle["telemetry"] = finish_telemetry(tel)
-    return [a.elapsed_time(b) for a, b in ev], outer[0].elapsed_time(outer[1]) / args.steps, settle
+    ms_per_step = outer[0].elapsed_time(outer[1]) / args.steps
+    res = ([a.elapsed_time(b) for a, b in ev], ms_per_step, settle)
+    if with_repeats:
+        return res + ([ms_per_step] + [a.elapsed_time(b) / args.steps for a, b in blocks],)
+    return res
 
 
-def graph_steps(step, args, dev):
+def graph_steps(step, args, dev, repeats=1):
     """The timed steps submitted as one HIP graph: args.steps calls of step(i)
     captured once (torch.cuda.CUDAGraph on torch's capture stream, which every
     entry point launches on), replayed untimed for --settle-ms, then one timed
-    replay right behind them, bracketed by HIP events.  Only entry points that
-    allocate nothing can be captured (the fused MGN kernels).  Returns (ms per
-    step, settle record)."""
+    replay right behind them, bracketed by HIP events, and repeats - 1 more
+    timed replays right behind that.  Only entry points that allocate nothing
+    can be captured (the fused MGN kernels).  Returns (ms per step of the first
+    timed replay, settle record, ms per step of every timed replay)."""
     import torch
 
     g = torch.cuda.CUDAGraph()
@@ -308,12 +332,14 @@ def graph_steps(step, args, dev):
     if args.settle_ms > 0:
         settle = _settle(lambda n: g.replay(), stream, args.settle_ms)
         settle["launches"] *= args.steps
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    g.replay()
-    e1.record(stream)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(repeats)]
+    for e0, e1 in evs:
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / args.steps, settle
+    blocks = [e0.elapsed_time(e1) / args.steps for e0, e1 in evs]
+    return blocks[0], settle, blocks
 
 
 def bench_bert(args):
@@ -763,6 +789,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--repeats", type=int, default=5,
+                    help="MGN workloads: blocks of --steps timed steps per submission (the first is the "
+                         "headline, the others follow it back to back; their median is reported beside it)")
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["bert", "dlrm", "nerf", "bert_addln", "bert_app", "nerf_a",
                                                                "queue", "mfma_peak", "gemm"],
@@ -869,13 +898,13 @@ def main():
         torch.cuda.synchronize()
         del ref_in, ref_out
 
-    launch_ms, eager_ms_per_step, settle = timed_steps(step, args, dev)
+    launch_ms, eager_ms_per_step, settle, eager_blocks = timed_steps(step, args, dev, with_repeats=True)
     avg_launch_ms = sum(launch_ms) / len(launch_ms)
     # The fused kernels allocate nothing, so the same steps can also be
     # submitted as one HIP graph; `value` comes from the faster submission.
-    graph_ms_per_step, graph_settle = None, None
+    graph_ms_per_step, graph_settle, graph_blocks = None, None, None
     if args.impl == "fused" and not args.eager:
-        graph_ms_per_step, graph_settle = graph_steps(step, args, dev)
+        graph_ms_per_step, graph_settle, graph_blocks = graph_steps(step, args, dev, args.repeats)
     use_graph = graph_ms_per_step is not None and graph_ms_per_step < eager_ms_per_step
     ms_per_step = graph_ms_per_step if use_graph else eager_ms_per_step
     bytes_, flops = algorithmic(M, K, ln, GATHER_NODES if gather else 0)
@@ -906,6 +935,9 @@ def main():
                   "and after the last step; value from the faster of eager and graph submission",
         "eager_ms_per_step": eager_ms_per_step,
         "graph_ms_per_step": graph_ms_per_step,
+        # the timed block and args.repeats - 1 more blocks of K steps right behind it, per submission
+        "repeats": {"blocks": args.repeats, "eager_ms_per_step": eager_blocks, "graph_ms_per_step": graph_blocks,
+                    "median_ms_per_step": statistics.median(graph_blocks if use_graph else eager_blocks)},
         "roofline": {
             "bound": "hbm", "achieved": achieved_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": load_traffic(args.workload, args.impl),
