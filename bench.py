@@ -856,7 +856,7 @@ def main():
     import torch
 
     import gpipes
-    from gpipes.synth import mgn_params, normal_fp16
+    from gpipes.synth import mgn_params
 
     dev = torch.device("cuda:0")
     M, K, ln = WORKLOADS[args.workload]
@@ -874,12 +874,14 @@ def main():
             print("the gather front end exists for the fused kernel only", file=sys.stderr)
             sys.exit(2)
         g = torch.Generator().manual_seed(0)
-        nf = normal_fp16(GATHER_NODES, 128, seed=1, device=dev)
-        xs = [normal_fp16(M, 128, seed=0, device=dev)]  # edge features
+        nf = gpipes.fill_normal(torch.empty((GATHER_NODES, 128), dtype=torch.float16, device=dev), seed=1)
+        xs = [gpipes.fill_normal(torch.empty((M, 128), dtype=torch.float16, device=dev), seed=0)]  # edge features
         src = torch.randint(0, GATHER_NODES, (M,), generator=g).to(dev)
         dst = torch.randint(0, GATHER_NODES, (M,), generator=g).to(dev)
     else:
-        xs = [normal_fp16(M, K, seed=i, device=dev, dtype=et) for i in range(nbuf)]
+        # X ~ N(0, 1) from the builder-owned generator (Philox-4x32-10 + Box-Muller,
+        # gp_fill_normal), seed = buffer index; oracle.normal gives the same values on the host
+        xs = [gpipes.fill_normal(torch.empty((M, K), dtype=et, device=dev), seed=i) for i in range(nbuf)]
     outs = [torch.empty((M, 128), dtype=et, device=dev) for _ in range(nbuf)]
 
     def step(i):
@@ -923,7 +925,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": args.dtype,
-        "data": "synthetic (X~N(0,1), nn.Linear default init, seed 0)",
+        "data": "synthetic (X~N(0,1) from gp_fill_normal, Philox-4x32-10 + Box-Muller, seed 0; "
+                "nn.Linear default init, seed 0)",
         "config": {"workload": f"mgn_{args.workload}_mlp", "M": M, "K": K,
                    **({"nodes": GATHER_NODES, "index": "int64"} if gather else {}),
                    "layers": f"{K}-128-128-128" + ("+LN" if ln else ""), "impl": args.impl,

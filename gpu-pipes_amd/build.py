@@ -38,7 +38,7 @@ HIP_FLAGS = [
 VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 
 SOURCES = ["mgn_fused.hip", "mgn_pipelined.hip", "stages.hip", "gemm.hip", "nerf_fused.hip", "dlrm_fused.hip", "status.hip",
-           "bert_addln_pipelined.hip", "bert_ffn_pipelined.hip", "nerf_a_pipelined.hip", "probe.hip", "capi.cpp", "ffn.cpp", "mlp.cpp", "arena.cpp"]
+           "bert_addln_pipelined.hip", "bert_ffn_pipelined.hip", "nerf_a_pipelined.hip", "probe.hip", "synth.hip", "capi.cpp", "ffn.cpp", "mlp.cpp", "arena.cpp"]
 SOURCE_FLAGS = {"gemm.hip": [], "nerf_fused.hip": [], "dlrm_fused.hip": []}
 
 
@@ -84,9 +84,17 @@ def build_library(verbose=False):
 
 def build_oracle(verbose=False):
     # x86-64-v3 (AVX2 + FMA) runs on any current server host; OpenMP over rows.
+    # synth.c (the input generator) without contraction: each of its steps
+    # must round as in the device generator.
     tmp = ORACLE_LIB + ".tmp"
-    _run(["gcc", "-O3", "-march=x86-64-v3", "-fopenmp", "-fPIC", "-shared",
-          os.path.join(ORACLE_DIR, "oracle.c"), "-o", tmp, "-lm"], verbose)
+    os.makedirs(BUILD, exist_ok=True)
+    objs = []
+    for src, extra in (("oracle.c", []), ("synth.c", ["-ffp-contract=off"])):
+        obj = os.path.join(BUILD, "oracle_" + os.path.splitext(src)[0] + ".o")
+        _run(["gcc", "-O3", "-march=x86-64-v3", "-fopenmp", "-fPIC"] + extra +
+             ["-c", os.path.join(ORACLE_DIR, src), "-o", obj], verbose)
+        objs.append(obj)
+    _run(["gcc", "-fopenmp", "-shared"] + objs + ["-o", tmp, "-lm"], verbose)
     os.replace(tmp, ORACLE_LIB)
     return ORACLE_LIB
 

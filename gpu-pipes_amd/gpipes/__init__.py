@@ -28,7 +28,7 @@ __all__ = [
     "gemm_out", "bert_ffn", "bert_ffn_out", "mlp_out", "dlrm_botmlp", "dlrm_botmlp_out", "dlrm_topmlp",
     "dlrm_topmlp_out", "nerf_full", "nerf_full_out", "nerf_full_out_noalloc", "bert_addln_ffn",
     "bert_addln_ffn_out", "nerf_a", "nerf_a_out", "pipe_handoff", "handoff_checksums", "phase_timers",
-    "probe_mfma",
+    "probe_mfma", "fill_normal",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -92,6 +92,8 @@ def _load():
     L.gp_bert_ffn_dtype_out.argtypes = [i64, i64, i64] + [vp] * 7 + [f32, i32, vp, i32, vp]
     L.gp_bert_ffn_impl_out.argtypes = [i64, i64, i64] + [vp] * 7 + [f32, i32, vp, i32, vp]
     L.gp_probe_mfma.argtypes = [i64, i32, i32, vp, i64, ctypes.POINTER(i64), vp]
+    L.gp_fill_normal.argtypes = [vp, i64, ctypes.c_uint64, ctypes.c_uint64, i32, vp]
+    L.gp_fill_normal.restype = i32
     L.gp_mlp_out.argtypes = [i64, i32, vp, vp, vp, vp, vp, vp, vp]
     L.gp_mlp_dtype_out.argtypes = [i64, i32, vp, vp, vp, vp, vp, vp, i32, vp]
     L.gp_mlp_dtype_out.restype = i32
@@ -410,6 +412,18 @@ def probe_mfma(iters, dtype=torch.float16, device=None, shape=32):
         _check(lib.gp_probe_mfma(int(iters), _DTYPES[dtype], int(shape), _ptr(out), out.numel(),
                                  ctypes.byref(flops), ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
     return flops.value
+
+
+def fill_normal(t, seed=0, offset=0):
+    """Fill a contiguous fp16 / bf16 CUDA tensor with elements offset, offset + 1, ... of the
+    N(0, 1) stream of `seed` (gp_fill_normal: Philox-4x32-10 + Box-Muller, the same values
+    as oracle.normal on the host), on the current stream; returns t."""
+    if not t.is_cuda or not t.is_contiguous():
+        raise GpipesError("fill_normal needs a contiguous CUDA tensor")
+    with torch.cuda.device(t.device):
+        _check(lib.gp_fill_normal(_ptr(t), t.numel(), int(seed), int(offset), _DTYPES.get(t.dtype, -1),
+                                  ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)))
+    return t
 
 
 def phase_timers():

@@ -464,6 +464,18 @@ int gp_pipe_route(int64_t M, const void* x, void* out, void* out2, int route, in
 int gp_probe_mfma(int64_t iters, int dtype, int shape, void* out, int64_t out_floats, int64_t* flops, void* stream);
 
 /*
+ * Synthetic inputs, no counterpart in the reference (whose inputs come from
+ * torch's host generator, apps/mgn_fullmlp/pipelined/val.py:15-21): fills
+ * dst[0 .. n) (GP_DTYPE_F16 or GP_DTYPE_BF16, 2-byte aligned) with elements
+ * offset .. offset + n - 1 of the N(0, 1) stream of `seed`: element e is
+ * normal e % 4 of Philox-4x32-10 counter e / 4 under key `seed`, by
+ * Box-Muller, rounded to nearest even.  A given (seed, e) gives the same value
+ * for any n, offset, launch shape and device, and the same as the oracle's
+ * host restatement.  Enqueued on `stream`; n = 0 is a no-op.
+ */
+int gp_fill_normal(void* dst, int64_t n, uint64_t seed, uint64_t offset, int dtype, void* stream);
+
+/*
  * Waits for `stream`, then reports whether the last launch on it that
  * reports device-side failures failed (GP_ERR_TIMEOUT) or completed (GP_OK).
  * Those are the launches of gp_mgn_fullmlp_out, gp_mgn_linears_out,

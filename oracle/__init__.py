@@ -37,6 +37,15 @@ def lib():
         L.oracle_bert_ffn.argtypes = [i64, i64, i64] + [vp] * 7 + [i32, f32, vp, vp]
         L.oracle_add.argtypes = [i64, vp, vp, vp]
         L.oracle_concat.argtypes = [i64, i64, i64, vp, vp, vp]
+        u64 = ctypes.c_uint64
+        L.oracle_philox4x32_10.argtypes = [vp, vp, vp]
+        L.oracle_log_unit.argtypes = [f32]
+        L.oracle_log_unit.restype = f32
+        L.oracle_sqrt_small.argtypes = [f32]
+        L.oracle_sqrt_small.restype = f32
+        L.oracle_sincos_quarter.argtypes = [f32, vp, vp]
+        L.oracle_normal_f32.argtypes = [i64, u64, u64, vp]
+        L.oracle_normal_16.argtypes = [i64, u64, u64, i32, vp]
         L.oracle_num_threads.restype = i32
         L.oracle_set_num_threads.argtypes = [i32]
         _lib = L
@@ -64,6 +73,41 @@ def f2h(f):
     f = _f32(f)
     out = np.empty(f.shape, np.uint16)
     lib().oracle_f2h_array(f.size, _p(f), _p(out))
+    return out
+
+
+def philox4x32_10(ctr, key):
+    """Philox-4x32-10 of a 4-word counter under a 2-word key (synth.c)."""
+    c = np.ascontiguousarray(ctr, dtype=np.uint32)
+    k = np.ascontiguousarray(key, dtype=np.uint32)
+    out = np.empty(4, np.uint32)
+    lib().oracle_philox4x32_10(_p(c), _p(k), _p(out))
+    return out
+
+
+def log_unit(u):
+    return lib().oracle_log_unit(float(u))
+
+
+def sqrt_small(v):
+    return lib().oracle_sqrt_small(float(v))
+
+
+def sincos_quarter(a):
+    s, c = ctypes.c_float(), ctypes.c_float()
+    lib().oracle_sincos_quarter(float(a), ctypes.byref(s), ctypes.byref(c))
+    return s.value, c.value
+
+
+def normal(n, seed=0, offset=0, dtype="f32"):
+    """Elements offset .. offset + n - 1 of the N(0, 1) stream of `seed`, as gp_fill_normal
+    makes them: float32 values ("f32"), or the raw fp16 / bf16 bits ("f16" / "bf16") as uint16."""
+    if dtype == "f32":
+        out = np.empty(n, np.float32)
+        lib().oracle_normal_f32(n, seed, offset, _p(out))
+    else:
+        out = np.empty(n, np.uint16)
+        lib().oracle_normal_16(n, seed, offset, 1 if dtype == "bf16" else 0, _p(out))
     return out
 
 

@@ -31,6 +31,14 @@ void oracle_bert_ffn(int64_t M, int64_t H, int64_t FF, const float* x, const flo
 void oracle_add(int64_t n, const float* a, const float* b, float* c);
 void oracle_concat(int64_t M, int64_t N0, int64_t N1, const float* a, const float* b, float* c);
 
+/* Synthetic inputs (synth.c): the host restatement of gp_fill_normal. */
+void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+float oracle_log_unit(float u);
+float oracle_sqrt_small(float v);
+void oracle_sincos_quarter(float a, float* s, float* c);
+void oracle_normal_f32(int64_t n, uint64_t seed, uint64_t offset, float* dst);
+void oracle_normal_16(int64_t n, uint64_t seed, uint64_t offset, int bf16, uint16_t* dst);
+
 int oracle_num_threads(void);
 void oracle_set_num_threads(int n);
 

@@ -286,3 +286,14 @@ def test_probe_argument_errors(iters, dtype, shape, out, flops, code):
                                   ctypes.byref(f) if flops else None, None)
     assert rc == code
     assert gpipes.lib.gp_last_error().decode() != ""
+
+
+@pytest.mark.parametrize("dst,n,dtype,code", [
+    (16, -1, 0, -1), (16, 8, 7, -1), (0, 8, 0, -1), (17, 8, 1, -3), (0, 0, 0, 0), (16, 0, 1, 0),
+])
+def test_fill_normal_argument_errors(dst, n, dtype, code):
+    """gp_fill_normal rejects bad arguments before any device call (and n = 0 is a no-op)."""
+    rc = gpipes.lib.gp_fill_normal(ctypes.c_void_p(dst) if dst else None, n, 0, 0, dtype, None)
+    assert rc == code
+    if code:
+        assert gpipes.lib.gp_last_error().decode() != ""
